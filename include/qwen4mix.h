@@ -1,0 +1,204 @@
+/* qwen4mix: the qwen4exp token-mixing path (QSA + Gated DeltaNet) on MI355X.
+ *
+ * C ABI of libqwen4mix.so. Every entry point takes raw device pointers, plain
+ * sizes, a dtype enum and the caller's HIP stream; the caller owns all memory
+ * (kernels never allocate), state is updated in place, and the return value is
+ * QM_OK or a negative QM_ERR_* code whose message qm_last_error() returns
+ * (thread-local). There is no fallback path: an unsupported shape is an error.
+ *
+ * The reference has no C ABI; its plugin surface for this path is the Python
+ * module interface of src/ttrunner_qwen38_flash_next/reference/. Each entry
+ * point below cites the reference function(s) whose arithmetic it replaces.
+ *
+ * Layouts (b = sequence, h = head, d = head_dim, P = page_size):
+ *   DeltaNet recurrent state  float32 [B, Hv, d_k, d_v]   (reference/cache.py:24)
+ *   DeltaNet conv ring        act     [B, conv_dim, K]    slot p % K holds the
+ *                              input of the token at position p
+ *   QSA K pool                bf16    [n_pages, Hkv, P, d]
+ *   QSA V pool                bf16    [n_pages, Hkv, d, P]  tokens within each
+ *                              32-token group stored in MFMA operand order
+ *                              (qm_v_slot() gives the column of a page row)
+ *   page table                int32   [B, max_pages]  logical page -> physical
+ *   indexer raw keys          act     [B, max_ctx, idx_dim]
+ *   indexer block cache       float32 [B, max_blocks, idx_dim]  pooled, normed,
+ *                              roped keys of complete blocks
+ *   rope tables               float32 [n_pos, rope_dim]  (cos, sin)
+ */
+#ifndef QWEN4MIX_H
+#define QWEN4MIX_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QM_OK 0
+#define QM_ERR_ARG (-1)
+#define QM_ERR_DTYPE (-2)
+#define QM_ERR_LAUNCH (-3)
+#define QM_ERR_WORKSPACE (-4)
+#define QM_ERR_UNSUPPORTED (-5)
+
+#define QM_ACT_F32 0
+#define QM_ACT_BF16 1
+
+/* Last error message of the calling thread ("" after success). */
+const char* qm_last_error(void);
+/* ABI version of this library. */
+int qm_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Gated DeltaNet                                                           */
+/* ------------------------------------------------------------------------ */
+
+typedef struct qm_dn_geom {
+  int batch;        /* sequences in the call                           */
+  int n_v_heads;    /* Hv (32)                                          */
+  int n_k_heads;    /* Hk (16); v-head j reads q/k head j % Hk          */
+  int head_dim;     /* d_k = d_v (128)                                   */
+  int conv_kernel;  /* K (4)                                             */
+  int act_dtype;    /* QM_ACT_F32 or QM_ACT_BF16                         */
+  float eps;        /* rms_norm_eps of the gated output norm             */
+} qm_dn_geom;
+
+/* Bytes of workspace qm_dn_decode needs; zero it once before first use (the
+ * kernel leaves it ready for the next call). */
+size_t qm_dn_decode_workspace(int batch, int n_v_heads, int head_dim);
+
+/* One decode step of the DeltaNet mixer core, fused into one launch.
+ * Replaces the seq == 1 body of Qwen4ExpModel._linear_attention between its
+ * projections and ssm_out (reference/model.py:189-243): causal_conv1d_step
+ * (reference/layers.py:141-147), the gates (reference/model.py:212-217), the
+ * tiled q/k expansion (:230-233), recurrent_gated_delta_rule
+ * (reference/layers.py:155-192) and rms_norm_gated (reference/layers.py:46-61).
+ *   qkv [B, conv_dim], z [B, Hv*d], a, b [B, Hv]: projection outputs (act)
+ *   a_neg, dt_bias [Hv] f32 (ssm_a, ssm_dt.bias); conv_w [conv_dim, K] act;
+ *   norm_w [d] f32; positions [B] int32 position of this token;
+ *   conv_ring, state: in/out; out [B, Hv*d] act (input of ssm_out). */
+int qm_dn_decode(const qm_dn_geom* g, const void* qkv, const void* z, const void* a, const void* b,
+                 const float* a_neg, const float* dt_bias, const void* conv_w, const float* norm_w,
+                 const int* positions, void* conv_ring, float* state, void* out, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream);
+
+/* The gated delta rule over T tokens on split, expanded inputs:
+ * recurrent_gated_delta_rule (reference/layers.py:155-192).
+ *   q, k [B, T, H, d], v [B, T, H, d] act; g, beta [B, T, H] f32;
+ *   state [B, H, d, d] f32 in/out; out [B, T, H, d] act. */
+int qm_dn_recurrent(int act_dtype, int batch, int seq, int heads, int head_dim, const void* q, const void* k,
+                    const void* v, const float* g, const float* beta, float* state, void* out,
+                    hipStream_t stream);
+
+/* The same rule in the chunked WY/UT form, 64-token chunks:
+ * chunk_gated_delta_rule (reference/layers.py:195-275). Same arguments and
+ * result (to float32 rounding) as qm_dn_recurrent. */
+int qm_dn_chunked(int act_dtype, int batch, int seq, int heads, int head_dim, const void* q, const void* k,
+                  const void* v, const float* g, const float* beta, float* state, void* out, hipStream_t stream);
+
+/* Bytes of workspace qm_dn_prefill needs for a chunk of `seq` tokens. */
+size_t qm_dn_prefill_workspace(const qm_dn_geom* g, int seq);
+
+/* The DeltaNet mixer core over a chunk of `seq` tokens (prefill): the seq > 1
+ * body of Qwen4ExpModel._linear_attention (reference/model.py:198-201,
+ * 205-243): causal conv over [history | chunk] (reference/layers.py:133-138)
+ * with the last K-1 inputs left in the ring, the gates, the delta rule
+ * (chunk_gated_delta_rule, reference/layers.py:195-275; token loop for short
+ * chunks) and rms_norm_gated. positions[b] = position of the chunk's first
+ * token. Shapes as qm_dn_decode with a [B, S, ...] token axis. */
+int qm_dn_prefill(const qm_dn_geom* g, int seq, const void* qkv, const void* z, const void* a, const void* b,
+                  const float* a_neg, const float* dt_bias, const void* conv_w, const float* norm_w,
+                  const int* positions, void* conv_ring, float* state, void* out, void* workspace,
+                  size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* QSA (Qwen Sparse Attention)                                              */
+/* ------------------------------------------------------------------------ */
+
+typedef struct qm_qsa_geom {
+  int batch;        /* sequences                                          */
+  int n_heads;      /* Hq (16)                                            */
+  int n_kv_heads;   /* Hkv (2); q-head h reads kv-head h / (Hq/Hkv)       */
+  int head_dim;     /* 256                                                */
+  int rope_dim;     /* rotated leading channels (64)                      */
+  int idx_heads;    /* indexer query heads (4)                            */
+  int idx_dim;      /* indexer head dim (128)                             */
+  int ratio;        /* indexer compress ratio = block size (64)           */
+  int budget;       /* indexer budget in tokens (2048): top budget/ratio  */
+  int page_size;    /* KV page size (64)                                  */
+  int max_pages;    /* page-table row length                              */
+  int max_ctx;      /* raw-key cache rows per sequence                    */
+  int max_blocks;   /* block-cache rows per sequence                      */
+  int act_dtype;    /* QM_ACT_F32 or QM_ACT_BF16                          */
+  float eps;        /* rms_norm_eps                                       */
+} qm_qsa_geom;
+
+/* Column of page row `row` in the transposed V pool page. */
+int qm_v_slot(int row);
+
+/* Per-token preparation for a decode step (or the S rows of a prefill chunk):
+ * q/k RMS norm and partial rope, q|gate split (reference/model.py:345-356);
+ * the current K/V appended at their page slots (reference/model.py:358-363;
+ * paging as tt/model.py:625-666); the indexer query rope(rms_norm(.))
+ * (reference/model.py:270-272); the raw indexer key appended
+ * (reference/model.py:274-279); and, for every block the new tokens complete,
+ * its pooled, normed, roped key written to the block cache
+ * (reference/model.py:289-294; block cache as tt/model.py:1043-1115).
+ *   seq: rows per sequence in this call (1 for decode)
+ *   qg [B, S, Hq, 2*d]; k_new, v_new [B, S, Hkv, d]; iq [B, S, idx_heads*idx_dim];
+ *   ik [B, S, idx_dim] (act); *_norm f32 weights; cos/sin [n_pos, rope_dim] f32;
+ *   positions [B] int32 = position of the first row; page_table [B, max_pages].
+ *   Outputs: q_out [B, S, Hq, d] f32 (normed, roped); iq_out [B, S, idx_heads,
+ *   idx_dim] f32; pools, raw keys and block cache updated in place.
+ *   qg may be NULL (no attention query: q_norm, q_out unused) and k_new/v_new
+ *   may both be NULL (no K/V append), which leaves the indexer part alone. */
+int qm_qsa_prep(const qm_qsa_geom* g, int seq, const void* qg, const void* k_new, const void* v_new,
+                const void* iq, const void* ik, const float* q_norm, const float* k_norm,
+                const float* iq_norm, const float* ik_norm, const float* cos, const float* sin,
+                const int* positions, const int* page_table, void* k_pool, void* v_pool, void* raw_keys,
+                float* block_keys, float* q_out, float* iq_out, hipStream_t stream);
+
+/* Pooled keys of blocks first_block .. first_block+n_blocks-1 recomputed from
+ * the raw-key cache (reference/model.py:289-294), for a history imported into
+ * the caches rather than appended through qm_qsa_prep (tt/model.py:1043-1115
+ * keeps the same block cache). raw_keys [B, max_ctx, idx_dim] act;
+ * block_keys [B, max_blocks, idx_dim] f32. */
+int qm_qsa_pool_blocks(const qm_qsa_geom* g, const void* raw_keys, const float* k_norm, const float* cos,
+                       const float* sin, int first_block, int n_blocks, float* block_keys, hipStream_t stream);
+
+/* Block scoring and top-k selection for each query row: scores
+ * sum_h relu(q_h . block_j) / sqrt(idx_dim) (reference/model.py:297-298) over
+ * the eligible blocks j*ratio + ratio - 1 <= p, top min(budget/ratio, eligible)
+ * with ties to the lower index (reference/model.py:300-313; the lower-index
+ * rule is this library's; torch leaves tie order unspecified).
+ *   iq [B, S, idx_heads, idx_dim] f32; block_keys as above; positions [B] first
+ *   row's position; ids [B, S, budget/ratio] int32 in rank order; n_sel [B, S];
+ *   scores_out [B, S, max_blocks] f32 or NULL (ineligible entries -inf). */
+int qm_qsa_select(const qm_qsa_geom* g, int seq, const float* iq, const float* block_keys,
+                  const int* positions, int* ids, int* n_sel, float* scores_out, hipStream_t stream);
+
+/* Bytes of workspace qm_qsa_attend needs for `seq` query rows and `splits`. */
+size_t qm_qsa_attend_workspace(const qm_qsa_geom* g, int seq, int splits);
+/* Split count (32-token groups per query at most) for queries up to max_position. */
+int qm_qsa_attend_splits(const qm_qsa_geom* g, int max_position);
+
+/* Paged GQA attention of `seq` query rows per sequence (row s at position
+ * positions[b] + s) over each row's selected blocks plus its tail block, then
+ * the sigmoid output gate (reference/model.py:365-382 with the mask of
+ * :306-326; paging as tt/model.py:1252-1323): fp32 softmax of q.k/sqrt(d) over
+ * the visible keys, times v, cast to act, times sigmoid(gate). K/V of every row
+ * must already be in the pages (qm_qsa_prep).
+ *   q [B, S, Hq, d] f32 (from qm_qsa_prep); qg [B, S, Hq, 2*d] act (the gate is
+ *   the second half of each head); ids, n_sel from qm_qsa_select;
+ *   out [B, S, Hq*d] act. */
+int qm_qsa_attend(const qm_qsa_geom* g, int seq, const float* q, const void* qg, const void* k_pool,
+                  const void* v_pool, const int* page_table, const int* positions, const int* ids,
+                  const int* n_sel, void* out, int splits, void* workspace, size_t workspace_bytes,
+                  hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN4MIX_H */

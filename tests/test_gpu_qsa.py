@@ -1,0 +1,275 @@
+"""QSA on the GPU against the oracle and the reference's goldens.
+
+Bar (north star): selected block indices and page gathers bit-exact; bf16
+outputs within 2e-2 max relative error (max |got - want| / max |want|).
+Selection parity is checked with the exact projection bits the reference saw
+(stored in the fixtures), so the comparison covers the kernels, not the GEMMs.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import selection as sel
+from oracle.cache import OracleHybridCache
+from oracle.config import OracleConfig
+from oracle.layers import RotaryEmbedding, apply_rotary, rms_norm
+from oracle.mixing import OracleMixer
+
+HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+sys.path.insert(0, HERE)
+import inputs as gi  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+OUT_TOL = 2e-2
+META = json.load(open(os.path.join(HERE, "golden_meta.json")))
+ROT = RotaryEmbedding(64, 1e7, [11, 11, 10])
+
+
+def rel_err(got, want):
+    got, want = got.detach().float().cpu(), want.detach().float().cpu()
+    return ((got - want).abs().max() / want.abs().max().clamp_min(1e-30)).item()
+
+
+def tables(n):
+    p = torch.arange(n)[None]
+    return ROT(p[None].expand(3, -1, -1))
+
+
+def _model_and_cache(gpu, store, dtype, max_ctx, cfg=None, page_table="random", batch=1):
+    qm = gpu
+    cfg = cfg or qm.MixConfig()
+    model = qm.Qwen4MixModel(cfg, store, device=DEV, max_ctx=max_ctx)
+    cache = qm.MixHybridCache(4, cfg, batch, max_ctx, DEV, dtype, page_table=page_table, seed=5)
+    return model, cache
+
+
+def _oracle_core(cfg, store, hidden, cos, sin, keys, values, idx_keys, pos, layer=3):
+    """The oracle's pre-projection QSA output and per-query selected blocks."""
+    m = OracleMixer(cfg, store)
+    q, k, v, gate = m.qkv_prep(hidden, layer, cos, sin)
+    K = torch.cat([keys, k], 2) if keys is not None else k
+    V = torch.cat([values, v], 2) if values is not None else v
+    kv_len = K.shape[2]
+    oc = OracleHybridCache(layer + 1)
+    oc[layer].indexer_keys = idx_keys
+    mask = m._indexer_mask(hidden, layer, cos, sin, oc, kv_len, pos)
+    n_t = hidden.shape[1]
+    kpos = torch.arange(kv_len)
+    qpos = torch.arange(n_t)[:, None] + pos
+    allowed = (kpos[None, :] <= qpos)[None, None] & mask
+    out = m.attention_core(q, K, V, allowed, hidden.dtype)
+    out = out.transpose(1, 2).reshape(hidden.shape[0], n_t, -1) * torch.sigmoid(gate)
+    chosen = []
+    for b in range(hidden.shape[0]):
+        rows = []
+        for i in range(n_t):
+            p = pos + i
+            n_el = (p + 1) // cfg.indexer_compress_ratio
+            rows.append(sorted(j for j in range(n_el) if bool(mask[b, 0, i, j * cfg.indexer_compress_ratio])))
+        chosen.append(rows)
+    return out, k, v, chosen
+
+
+def _projections(store, hidden, layer=3):
+    g = lambda s: store.get(f"blk.{layer}.{s}")  # noqa: E731
+    return [F.linear(hidden, g(n)).contiguous() for n in
+            ("attn_q.weight", "attn_k.weight", "attn_v.weight", "indexer.q_proj.weight", "indexer.k_proj.weight")]
+
+
+def _got_sets(lc):
+    ids, n = lc.last_ids.cpu(), lc.last_n_sel.cpu()
+    return [[sorted(ids[b, i, : n[b, i]].tolist()) for i in range(ids.shape[1])] for b in range(ids.shape[0])]
+
+
+@pytest.mark.parametrize("tag", ["cfg3", "cfg3b", "cfg1"])
+def test_indexer_stages_and_selection_match_reference(gpu, tag):
+    """Pooled block keys and indexer queries bit-exact vs the oracle, selected
+    set bit-exact vs the reference, fed the reference's own projection bits."""
+    m = META[tag]
+    z = np.load(os.path.join(HERE, f"{tag}.npz"))
+    dtype = torch.float32 if m["dtype"] == "torch.float32" else torch.bfloat16
+    pos = m["pos"]
+    store = gi.FakeStore(gi.qsa_weights(3, m["qsa_seeds"][0], dtype))
+    _, _, idx_keys = gi.qsa_past(m["qsa_seeds"][1], pos, dtype)
+    if dtype == torch.bfloat16:
+        iq = gi.from_bf16_bits(z["idx_q_raw"]).reshape(1, 1, -1)
+        ik = gi.from_bf16_bits(z["idx_k_raw"]).reshape(1, 1, -1)
+    else:
+        iq = torch.from_numpy(z["idx_q_raw"]).reshape(1, 1, -1)
+        ik = torch.from_numpy(z["idx_k_raw"]).reshape(1, 1, -1)
+    cos, sin = tables(pos + 1)
+    model, cache = _model_and_cache(gpu, store, dtype, pos + 64)
+    cache[3].indexer_keys = idx_keys.to(DEV)
+    print(f"indexer {tag} pos={pos}", flush=True)
+    model.qsa_core(None, None, None, iq.to(DEV), ik.to(DEV), 3, cache, pos, cos.to(DEV), sin.to(DEV), attend=False)
+    lc = cache[3]
+    # oracle stages on the same bits
+    om = OracleMixer(OracleConfig(), store)
+    q_want = apply_rotary(rms_norm(iq.reshape(1, 1, 4, 128), store.get("blk.3.indexer.q_norm.weight"), 1e-6),
+                          cos[:, -1:], sin[:, -1:], unsqueeze_dim=2)
+    assert torch.equal(lc.last_iq.cpu(), q_want.float()), "indexer query not bit-exact"
+    n_blocks = (pos + 1) // 64
+    pooled = om.indexer_pooled(torch.cat([idx_keys, ik], 1), 3, cos, sin, n_blocks)
+    got_pooled = lc.block_keys[:, :n_blocks].cpu()
+    assert torch.equal(got_pooled, pooled.float()), \
+        f"pooled keys differ in {(got_pooled != pooled).sum().item()} entries"
+    got = _got_sets(lc)[0][0]
+    assert got == sorted(z["selected"].tolist()), "selected blocks differ from the reference"
+
+
+@pytest.mark.parametrize("pos,dtype", [(192, torch.float32), (1984, torch.bfloat16), (4032, torch.bfloat16),
+                                       (8128, torch.bfloat16), (130, torch.bfloat16), (2047, torch.bfloat16),
+                                       (0, torch.bfloat16), (63, torch.bfloat16)])
+def test_decode_core_matches_oracle(gpu, pos, dtype):
+    cfg = OracleConfig()
+    store = gi.FakeStore(gi.qsa_weights(3, 61, dtype))
+    keys, values, idx_keys = gi.qsa_past(62, pos, dtype)
+    hidden = gi.normal(gi.rng(63), (1, 1, gi.HIDDEN)).to(dtype)
+    cos, sin = tables(pos + 1)
+    print(f"decode core pos={pos} dtype={dtype}", flush=True)
+    want, k_new, v_new, chosen = _oracle_core(cfg, store, hidden, cos, sin, keys if pos else None,
+                                              values if pos else None, idx_keys, pos)
+    model, cache = _model_and_cache(gpu, store, dtype, pos + 128)
+    if pos:
+        cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
+    qg, k, v, iq, ik = (t.to(DEV) for t in _projections(store, hidden))
+    got = model.qsa_core(qg, k, v, iq, ik, 3, cache, pos, cos.to(DEV), sin.to(DEV))
+    assert _got_sets(cache[3]) == chosen
+    assert rel_err(got, want) < OUT_TOL
+    # the appended token sits at its page slot, bit-exact (bf16 of the roped key)
+    P = 64
+    page = int(cache.page_table[0, pos // P])
+    assert torch.equal(cache[3].k_pool[page, :, pos % P].cpu(), k_new[0, :, 0].to(torch.bfloat16))
+    col = gpu.native.load().qm_v_slot(pos % P)
+    assert torch.equal(cache[3].v_pool[page, :, :, col].cpu(), v_new[0, :, 0].to(torch.bfloat16))
+
+
+def test_page_gather_round_trip_is_bit_exact(gpu):
+    store = gi.FakeStore(gi.qsa_weights(3, 64, torch.bfloat16))
+    keys, values, idx = gi.qsa_past(65, 1000, torch.bfloat16)
+    model, cache = _model_and_cache(gpu, store, torch.bfloat16, 1024)
+    cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx.to(DEV)
+    assert torch.equal(cache[3].keys.cpu(), keys.to(torch.bfloat16).float())
+    assert torch.equal(cache[3].values.cpu(), values)
+    assert torch.equal(cache[3].indexer_keys.cpu(), idx)
+    # the page table really is a permutation: no two logical pages share a page
+    pt = cache.page_table[0].cpu()
+    assert len(set(pt.tolist())) == pt.numel()
+
+
+@pytest.mark.parametrize("tag", ["cfg1", "cfg3", "cfg3b"])
+def test_decode_layer_matches_golden_reference(gpu, tag):
+    m = META[tag]
+    z = np.load(os.path.join(HERE, f"{tag}.npz"))
+    dtype = torch.float32 if m["dtype"] == "torch.float32" else torch.bfloat16
+    pos = m["pos"]
+    store = gi.FakeStore(gi.qsa_weights(3, m["qsa_seeds"][0], dtype))
+    keys, values, idx_keys = gi.qsa_past(m["qsa_seeds"][1], pos, dtype)
+    hidden = gi.hidden_states(m["hidden_seed"], 1, dtype)
+    cos, sin = tables(pos + 1)
+    model, cache = _model_and_cache(gpu, store, dtype, pos + 64)
+    cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
+    print(f"golden layer {tag}", flush=True)
+    y = model._full_attention(hidden.to(DEV), 3, cos.to(DEV), sin.to(DEV), cache, pos)
+    want = torch.from_numpy(z["qsa_out"])
+    flat = y.float().reshape(-1).cpu()
+    stride = max(1, flat.numel() // want.numel())
+    assert rel_err(flat[::stride][: want.numel()], want) < OUT_TOL
+
+
+def test_prefill_chunk_matches_golden_reference(gpu):
+    """Config 5: 128 queries at 32640..32767, per-query top-32 and causal tails."""
+    m = META["cfg5"]
+    z = np.load(os.path.join(HERE, "cfg5.npz"))
+    past, seq = m["past"], m["seq"]
+    dtype = torch.bfloat16
+    store = gi.FakeStore(gi.qsa_weights(3, m["qsa_seeds"][0], dtype))
+    keys, values, idx_keys = gi.qsa_past(m["qsa_seeds"][1], past, dtype)
+    hidden = gi.hidden_states(m["hidden_seed"], seq, dtype)
+    cos, sin = tables(past + seq)
+    model, cache = _model_and_cache(gpu, store, dtype, past + seq)
+    cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
+    qg, k, v, _, _ = _projections(store, hidden)
+    iq = gi.from_bf16_bits(z["idx_q_raw"]).reshape(1, seq, -1)
+    ik = gi.from_bf16_bits(z["idx_k_raw"]).reshape(1, seq, -1)
+    print("prefill chunk 32640+128", flush=True)
+    got = model.qsa_core(qg.to(DEV), k.to(DEV), v.to(DEV), iq.to(DEV), ik.to(DEV), 3, cache, past, cos.to(DEV),
+                         sin.to(DEV))
+    sets = _got_sets(cache[3])[0]
+    for i in range(seq):
+        want_ids = z["selected"][i]
+        assert sets[i] == sorted(want_ids[want_ids >= 0].tolist()), f"query {i}"
+    want = torch.from_numpy(z["qsa_core"])
+    flat = got.float().reshape(-1).cpu()
+    stride = max(1, flat.numel() // want.numel())
+    assert rel_err(flat[::stride][: want.numel()], want) < OUT_TOL
+
+
+def test_small_ratio_several_blocks_per_page(gpu):
+    """ratio 4 < page 64 (the reference checkpoint's ratio), budget 64 -> top-16."""
+    qm = gpu
+    cfg = OracleConfig(indexer_compress_ratio=4, indexer_budget=64)
+    mcfg = qm.MixConfig(indexer_compress_ratio=4, indexer_budget=64)
+    dtype = torch.bfloat16
+    store = gi.FakeStore(gi.qsa_weights(3, 66, dtype))
+    for pos in (3, 50, 130, 301):
+        keys, values, idx_keys = gi.qsa_past(67, pos, dtype)
+        hidden = gi.normal(gi.rng(68 + pos), (1, 1, gi.HIDDEN)).to(dtype)
+        cos, sin = tables(pos + 1)
+        want, _, _, chosen = _oracle_core(cfg, store, hidden, cos, sin, keys, values, idx_keys, pos)
+        model, cache = _model_and_cache(gpu, store, dtype, 384, cfg=mcfg)
+        cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
+        qg, k, v, iq, ik = (t.to(DEV) for t in _projections(store, hidden))
+        got = model.qsa_core(qg, k, v, iq, ik, 3, cache, pos, cos.to(DEV), sin.to(DEV))
+        assert _got_sets(cache[3]) == chosen, pos
+        assert rel_err(got, want) < OUT_TOL, pos
+
+
+def test_batch_of_two_with_own_pages(gpu):
+    dtype = torch.bfloat16
+    cfg = OracleConfig()
+    store = gi.FakeStore(gi.qsa_weights(3, 69, dtype))
+    pos = 3000
+    k1, v1, i1 = gi.qsa_past(70, pos, dtype)
+    k2, v2, i2 = gi.qsa_past(71, pos, dtype)
+    keys, values, idx = torch.cat([k1, k2]), torch.cat([v1, v2]), torch.cat([i1, i2])
+    hidden = gi.normal(gi.rng(72), (2, 1, gi.HIDDEN)).to(dtype)
+    cos, sin = tables(pos + 1)
+    want, _, _, chosen = _oracle_core(cfg, store, hidden, cos, sin, keys, values, idx, pos)
+    model, cache = _model_and_cache(gpu, store, dtype, pos + 64, batch=2)
+    cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx.to(DEV)
+    qg, k, v, iq, ik = (t.to(DEV) for t in _projections(store, hidden))
+    got = model.qsa_core(qg, k, v, iq, ik, 3, cache, pos, cos.to(DEV), sin.to(DEV))
+    assert _got_sets(cache[3]) == chosen
+    assert rel_err(got, want) < OUT_TOL
+
+
+def test_consecutive_decode_steps_cross_a_block_boundary(gpu):
+    """Steps 8126..8131 append tokens, complete block 126 at 8127 (pooled in the
+    same launch) and move the tail into block 127."""
+    dtype = torch.bfloat16
+    cfg = OracleConfig()
+    store = gi.FakeStore(gi.qsa_weights(3, 73, dtype))
+    start = 8126
+    keys, values, idx_keys = gi.qsa_past(74, start, dtype)
+    model, cache = _model_and_cache(gpu, store, dtype, 8192 + 64)
+    cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
+    om = OracleMixer(cfg, store)
+    ocache = OracleHybridCache(4)
+    ocache[3].keys, ocache[3].values, ocache[3].indexer_keys = keys, values, idx_keys
+    r = gi.rng(75)
+    for pos in range(start, start + 6):
+        hidden = gi.normal(r, (1, 1, gi.HIDDEN)).to(dtype)
+        cos, sin = tables(pos + 1)
+        want = om._full_attention(hidden, 3, cos, sin, ocache, pos)
+        got = model._full_attention(hidden.to(DEV), 3, cos.to(DEV), sin.to(DEV), cache, pos)
+        assert rel_err(got, want) < OUT_TOL, pos

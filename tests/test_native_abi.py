@@ -1,0 +1,86 @@
+"""The C ABI library (CPU-side checks: no kernel is launched here).
+
+* libqwen4mix.so loads and exports every function include/*.h declares, and
+  the ctypes binding declares exactly those;
+* host-side helpers that need no GPU: the V-page slot permutation is a bijection
+  of each 32-row group, the argument checks reject bad geometry before any
+  launch, the package's rope tables are bit-identical to the reference's.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import glob
+import json
+import os
+import re
+import sys
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(qm_\w+)\s*\(", text))
+    return names
+
+
+def test_library_exports_every_declared_symbol(qm):
+    lib = qm.native.load()
+    declared = _declared()
+    assert declared, "no declarations found"
+    for name in sorted(declared):
+        assert hasattr(lib, name), f"{name} not exported"
+    assert declared == set(qm.native.SIGNATURES), "binding and header disagree"
+    assert lib.qm_version() >= 1
+
+
+def test_v_slot_is_a_permutation_of_each_group(qm):
+    lib = qm.native.load()
+    for page in (32, 64, 128):
+        cols = [lib.qm_v_slot(r) for r in range(page)]
+        assert sorted(cols) == list(range(page))
+        assert all(c // 32 == r // 32 for r, c in enumerate(cols))
+
+
+def test_bad_geometry_is_rejected_without_a_launch(qm):
+    n = qm.native
+    lib = n.load()
+    g = n.DnGeom(1, 32, 16, 64, 4, n.QM_ACT_BF16, 1e-6)       # head_dim 64 unsupported
+    rc = lib.qm_dn_decode(ctypes.byref(g), *([None] * 12), None, 0, None)
+    assert rc == -5 and b"head_dim" in lib.qm_last_error()
+    g = n.DnGeom(1, 32, 16, 128, 4, 7, 1e-6)                  # unknown dtype
+    rc = lib.qm_dn_decode(ctypes.byref(g), *([ctypes.c_void_p(8)] * 12), ctypes.c_void_p(8), 1 << 20, None)
+    assert rc in (-2, -4)
+    q = n.QsaGeom(1, 16, 2, 128, 64, 4, 128, 64, 2048, 64, 4, 256, 4, n.QM_ACT_BF16, 1e-6)
+    assert lib.qm_qsa_select(ctypes.byref(q), 1, *([None] * 6), None) == -5
+    with pytest.raises(n.QmError, match="head_dim"):
+        n.call("qm_qsa_select", ctypes.byref(q), 1, *([None] * 6), None)
+
+
+def test_workspace_sizes_are_sane(qm):
+    n = qm.native
+    lib = n.load()
+    assert lib.qm_dn_decode_workspace(1, 32, 128) >= 32 * 128 * 4
+    q = n.QsaGeom(1, 16, 2, 256, 64, 4, 128, 64, 2048, 64, 128, 8192, 128, n.QM_ACT_BF16, 1e-6)
+    splits = lib.qm_qsa_attend_splits(ctypes.byref(q), 8128)
+    assert splits == 32 * 2 + 3
+    assert lib.qm_qsa_attend_workspace(ctypes.byref(q), 1, splits) >= splits * 2 * 8 * 256 * 4
+
+
+def test_rope_tables_bit_identical_to_reference(qm):
+    meta = json.load(open(os.path.join(ROOT, "tests", "golden", "golden_meta.json")))
+    if meta["torch"] != torch.__version__ or meta["cpu_capability"] != torch.backends.cpu.get_cpu_capability():
+        pytest.skip("different torch build than the golden generator")
+    from importlib import import_module
+    rope = import_module(qm.__name__ + ".rope")
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    import inputs as gi
+    cos, sin = rope.rope_tables_cpu(32768, 64, 1e7, [11, 11, 10])
+    assert gi.digest(cos) == meta["digests"]["rope"]["cos_sha"]
+    assert gi.digest(sin) == meta["digests"]["rope"]["sin_sha"]

@@ -1,0 +1,117 @@
+// Shared device helpers for the qwen4mix HIP kernels (gfx950 / CDNA4).
+//
+// Conventions used by every kernel in this library:
+//  * activations are either float32 or bfloat16 (ACT_F32 / ACT_BF16); every
+//    kernel is instantiated for both and the entry point dispatches on the enum;
+//  * wavefronts are 64 lanes; block reductions go through LDS;
+//  * arithmetic that must reproduce PyTorch's CPU rounding bit for bit (the QSA
+//    indexer path) uses the explicit *_rn helpers below so that the compiler
+//    cannot contract a multiply and an add into one FMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define QM_ACT_F32 0
+#define QM_ACT_BF16 1
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+struct bf16_t {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// round-to-nearest-even float32 -> bfloat16 (NaN kept quiet)
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Activation element access: load as float, store with rounding to the type.
+template <typename T> struct Act;
+template <> struct Act<float> {
+  __device__ __forceinline__ static float load(const float* p, long i) { return p[i]; }
+  __device__ __forceinline__ static void store(float* p, long i, float v) { p[i] = v; }
+  // value after a round trip through the activation dtype
+  __device__ __forceinline__ static float round(float v) { return v; }
+};
+template <> struct Act<bf16_t> {
+  __device__ __forceinline__ static float load(const bf16_t* p, long i) { return bf16_to_f32(p[i].bits); }
+  __device__ __forceinline__ static void store(bf16_t* p, long i, float v) { p[i].bits = f32_to_bf16(v); }
+  __device__ __forceinline__ static float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+};
+
+// Non-contracting float ops (each rounds once, like a CPU SIMD mul/add).
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
+// correctly rounded 1/sqrt(x), as torch's CPU rsqrt computes it (sqrt, then divide)
+__device__ __forceinline__ float rsqrt_rn(float x) { return __fdiv_rn(1.0f, __fsqrt_rn(x)); }
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+// torch.nn.functional.softplus with beta 1, threshold 20
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Sum over a block of NT threads (NT a multiple of 64); `red` holds NT/64 floats.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) s += red[i];
+  return s;
+}
+
+// Sum of squares of `n` floats in LDS, in the order torch's CPU `x.pow(2).mean(-1)`
+// reduces a contiguous float32 row: 8-lane vectors into 4 accumulators
+// (element e -> accumulator (e/8)%4, lane e%8, in increasing e), the 4
+// accumulators added in order lane-wise, then the 8 lanes added in order.
+// Requires n % 32 == 0. Called by all threads of the block; thread 0..31 work.
+// `scratch` holds 32 floats. Returns the sum (not the mean) in every thread.
+__device__ __forceinline__ float torch_row_sumsq(const float* x, int n, float* scratch) {
+  const int t = threadIdx.x;
+  __syncthreads();
+  if (t < 32) {
+    float acc = 0.f;
+    for (int e = t; e < n; e += 32) acc = add_rn(acc, mul_rn(x[e], x[e]));
+    scratch[t] = acc;
+  }
+  __syncthreads();
+  float lanes[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l)
+    lanes[l] = add_rn(add_rn(add_rn(scratch[l], scratch[8 + l]), scratch[16 + l]), scratch[24 + l]);
+  float tot = lanes[0];
+#pragma unroll
+  for (int l = 1; l < 8; ++l) tot = add_rn(tot, lanes[l]);
+  return tot;
+}
+
+#define QM_CHECK_LAUNCH()                                              \
+  do {                                                                 \
+    hipError_t e_ = hipGetLastError();                                 \
+    if (e_ != hipSuccess) return qm_fail(QM_ERR_LAUNCH, hipGetErrorString(e_)); \
+  } while (0)

@@ -1,0 +1,415 @@
+// Gated DeltaNet decode on gfx950: one token per sequence, one launch.
+//
+// Computes, for every sequence b and value head h (reference/model.py:189-243,
+// reference/layers.py:141-147, 155-192, 46-61):
+//   conv   : y = silu(sum_t w[c,t] * hist[c,t])  over [ring | x], tap 0 oldest
+//   gates  : beta = sigmoid(b), g = A * softplus(a + dt_bias)
+//   norms  : q^ = l2norm(q) / sqrt(d), k^ = l2norm(k)   (eps 1e-6)
+//   update : S <- S e^g ; pred = S^T k^ ; delta = (v - pred) beta ;
+//            S <- S + k^ delta^T ; o = S^T q^  (= q^T S_dec + (q^.k^) delta)
+//   norm   : out = rms_norm(o) * w * sigmoid(z)
+// with v-head h reading q/k head h % Hk (the tiled layout of the checkpoint).
+//
+// Work split: the delta rule is independent per state column (v index), so a
+// workgroup owns (sequence, head, 16-column tile): 128 rows x 16 columns of the
+// float32 state, 8 KB read + 8 KB written, kept in registers. 32 heads x 8
+// tiles = 256 workgroups per sequence, one per CU. The gated RMS norm needs the
+// whole 128-vector of a head: each workgroup parks its 16 outputs in the
+// workspace and the last of the head's 8 workgroups to arrive (an agent-scope
+// acq_rel counter) finishes the norm and resets the counter for the next call.
+//
+// The conv window is a ring of K slots per channel: the input of the token at
+// position p lives in slot p % K, so the K-1 history slots read by this step are
+// never the slot it writes, and no workgroup can observe another's write.
+
+#include "common.h"
+#include "qwen4mix_internal.h"
+
+namespace {
+
+constexpr int DN_D = 128;      // head dim (k and v)
+constexpr int DN_TILE = 16;    // state columns per workgroup
+constexpr int DN_NT = 256;     // threads per workgroup
+
+template <typename T>
+struct DnDecodeArgs {
+  const T* qkv; const T* z; const T* a; const T* b;
+  const float* a_neg; const float* dt_bias;
+  const T* conv_w; const float* norm_w;
+  const int* positions;
+  T* ring; float* state; T* out;
+  float* o_park; unsigned* counters;
+  int batch, hv, hk, conv_dim, K;
+  float eps;
+};
+
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  // blocks are dealt round-robin to the 8 XCDs; give each XCD a contiguous
+  // range of logical work so neighbouring column tiles share an L2
+  if (n % 8) return bid;
+  return (bid % 8) * (n / 8) + bid / 8;
+}
+
+template <typename T>
+__device__ __forceinline__ float conv_channel(const DnDecodeArgs<T>& A, int b, int ch, int pos, bool write_ring) {
+  const int K = A.K;
+  const T* w = A.conv_w + (long)ch * K;
+  T* ring = A.ring + ((long)b * A.conv_dim + ch) * K;
+  const float x = Act<T>::load(A.qkv, (long)b * A.conv_dim + ch);
+  float acc = 0.f;
+  for (int j = 0; j < K - 1; ++j) {
+    int slot = (pos - (K - 1) + j) % K;
+    if (slot < 0) slot += K;
+    acc = fmaf(Act<T>::load(w, j), Act<T>::load(ring, slot), acc);
+  }
+  acc = fmaf(Act<T>::load(w, K - 1), x, acc);
+  if (write_ring) Act<T>::store(ring, pos % K, x);
+  const float y = Act<T>::round(acc);
+  return Act<T>::round(silu_f(y));
+}
+
+template <typename T>
+__global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
+  constexpr int NTILE = DN_D / DN_TILE;
+  const int nwg = A.batch * A.hv * NTILE;
+  const int wg = xcd_remap(blockIdx.x, nwg);
+  const int tile = wg % NTILE;
+  const int h = (wg / NTILE) % A.hv;
+  const int b = wg / (NTILE * A.hv);
+  const int hk = h % A.hk;
+  const int col0 = tile * DN_TILE;
+  const int tid = threadIdx.x;
+
+  __shared__ float s_q[DN_D], s_k[DN_D], s_v[DN_TILE];
+  __shared__ float s_red[4][2 * DN_TILE];
+  __shared__ float s_delta[DN_TILE];
+  __shared__ float s_scal[8];
+  __shared__ float s_wred[DN_NT / 64];
+  __shared__ unsigned s_last;
+
+  // 1. the state tile first: its latency overlaps everything below
+  const int c4 = tid & 3, r = tid >> 2;
+  float4* S = reinterpret_cast<float4*>(A.state + ((long)(b * A.hv + h) * DN_D) * DN_D);
+  const int rowf4 = DN_D / 4;
+  float4 s0 = S[r * rowf4 + col0 / 4 + c4];
+  float4 s1 = S[(r + 64) * rowf4 + col0 / 4 + c4];
+
+  // 2. short conv on this head's q, k channels and its 16 v channels
+  const int pos = A.positions[b];
+  const int key_dim = A.hk * DN_D;
+  {
+    const bool is_q = tid < DN_D;
+    const int i = is_q ? tid : tid - DN_D;
+    const int ch = (is_q ? 0 : key_dim) + hk * DN_D + i;
+    const bool own_qk = (h == hk) && (tile == 0);   // one writer per q/k channel
+    const float y = conv_channel(A, b, ch, pos, own_qk);
+    if (is_q) s_q[i] = y; else s_k[i] = y;
+    if (tid < DN_TILE) {
+      const int vch = 2 * key_dim + h * DN_D + col0 + tid;
+      s_v[tid] = conv_channel(A, b, vch, pos, true);
+    }
+  }
+  __syncthreads();
+
+  // 3. l2 norms of q and k (fp32), and q.k
+  {
+    const int i = tid & (DN_D - 1);
+    const float qv = s_q[i], kv = s_k[i];
+    float sq = tid < DN_D ? qv * qv : 0.f;
+    float sk = tid < DN_D ? kv * kv : 0.f;
+    float sqk = tid < DN_D ? qv * kv : 0.f;
+    sq = block_sum<DN_NT>(sq, s_wred);
+    sk = block_sum<DN_NT>(sk, s_wred);
+    sqk = block_sum<DN_NT>(sqk, s_wred);
+    const float rq = rsqrt_rn(sq + 1e-6f), rk = rsqrt_rn(sk + 1e-6f);
+    const float inv_sqrt_d = 11.313708498984761f;   // sqrt(128)
+    __syncthreads();
+    if (tid < DN_D) {
+      s_q[tid] = div_rn(mul_rn(qv, rq), inv_sqrt_d);
+      s_k[tid] = mul_rn(kv, rk);
+    }
+    if (tid == 0) {
+      const float beta = Act<T>::round(sigmoid_f(Act<T>::load(A.b, (long)b * A.hv + h)));
+      const float ga = Act<T>::load(A.a, (long)b * A.hv + h) + A.dt_bias[h];
+      const float g = A.a_neg[h] * softplus_f(ga);
+      s_scal[0] = beta;
+      s_scal[1] = expf(g);
+      s_scal[2] = div_rn(sqk * rq * rk, inv_sqrt_d);   // q^.k^
+    }
+  }
+  __syncthreads();
+
+  // 4. decay, then per column: pred = S^T k^, qd = S^T q^
+  const float decay = s_scal[1];
+  const float kr0 = s_k[r], kr1 = s_k[r + 64];
+  const float qr0 = s_q[r], qr1 = s_q[r + 64];
+  float d0[4] = {s0.x * decay, s0.y * decay, s0.z * decay, s0.w * decay};
+  float d1[4] = {s1.x * decay, s1.y * decay, s1.z * decay, s1.w * decay};
+  float pk[4], pq[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    pk[c] = fmaf(d0[c], kr0, d1[c] * kr1);
+    pq[c] = fmaf(d0[c], qr0, d1[c] * qr1);
+  }
+#pragma unroll
+  for (int off = 4; off < 64; off <<= 1) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      pk[c] += __shfl_xor(pk[c], off, 64);
+      pq[c] += __shfl_xor(pq[c], off, 64);
+    }
+  }
+  const int lane = tid & 63, wid = tid >> 6;
+  if (lane < 4) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      s_red[wid][lane * 4 + c] = pk[c];
+      s_red[wid][DN_TILE + lane * 4 + c] = pq[c];
+    }
+  }
+  __syncthreads();
+  if (tid < DN_TILE) {
+    const float pred = s_red[0][tid] + s_red[1][tid] + s_red[2][tid] + s_red[3][tid];
+    const float qd = s_red[0][DN_TILE + tid] + s_red[1][DN_TILE + tid] + s_red[2][DN_TILE + tid] +
+                     s_red[3][DN_TILE + tid];
+    const float delta = (s_v[tid] - pred) * s_scal[0];
+    s_delta[tid] = delta;
+    const float o = Act<T>::round(fmaf(s_scal[2], delta, qd));
+    A.o_park[((long)b * A.hv + h) * DN_D + col0 + tid] = o;
+  }
+  __syncthreads();
+
+  // 5. rank-1 update and write-back
+  {
+    float4 n0, n1;
+    const float dl[4] = {s_delta[c4 * 4 + 0], s_delta[c4 * 4 + 1], s_delta[c4 * 4 + 2], s_delta[c4 * 4 + 3]};
+    n0.x = fmaf(kr0, dl[0], d0[0]); n0.y = fmaf(kr0, dl[1], d0[1]);
+    n0.z = fmaf(kr0, dl[2], d0[2]); n0.w = fmaf(kr0, dl[3], d0[3]);
+    n1.x = fmaf(kr1, dl[0], d1[0]); n1.y = fmaf(kr1, dl[1], d1[1]);
+    n1.z = fmaf(kr1, dl[2], d1[2]); n1.w = fmaf(kr1, dl[3], d1[3]);
+    S[r * rowf4 + col0 / 4 + c4] = n0;
+    S[(r + 64) * rowf4 + col0 / 4 + c4] = n1;
+  }
+
+  // 6. the last of the head's workgroups applies the gated RMS norm
+  if (tid == 0) {
+    unsigned* ctr = A.counters + (long)b * A.hv + h;
+    const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == NTILE - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const long hoff = ((long)b * A.hv + h) * DN_D;
+  const float ov = tid < DN_D ? __hip_atomic_load(A.o_park + hoff + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+  const float ss = block_sum<DN_NT>(ov * ov, s_wred);
+  if (tid < DN_D) {
+    const float rn = rsqrt_rn(ss / (float)DN_D + A.eps);
+    const float hnorm = A.norm_w[tid] * (ov * rn);
+    const float gz = sigmoid_f(Act<T>::load(A.z, (long)b * A.hv * DN_D + h * DN_D + tid));
+    Act<T>::store(A.out, (long)b * A.hv * DN_D + h * DN_D + tid, hnorm * gz);
+  }
+  if (tid == 0) __hip_atomic_store(A.counters + (long)b * A.hv + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Multi-token recurrence on already split and expanded q, k, v (the free
+// function recurrent_gated_delta_rule, reference/layers.py:155-192). Same
+// column split; the state tile stays in registers across the T tokens.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct DnRecurArgs {
+  const T* q; const T* k; const T* v;       // token rows of q_stride / v_stride elements
+  const float* g; const float* beta;        // [B, T, H]
+  float* state;                             // [B, H, D, D]
+  T* out;                                   // [B, T, H, D]
+  int batch, seq, heads, hk;                // head h reads q/k head h % hk
+  long q_stride, v_stride;
+};
+
+template <typename T>
+__global__ __launch_bounds__(DN_NT) void dn_recurrent_kernel(DnRecurArgs<T> A) {
+  constexpr int NTILE = DN_D / DN_TILE;
+  const int nwg = A.batch * A.heads * NTILE;
+  const int wg = xcd_remap(blockIdx.x, nwg);
+  const int tile = wg % NTILE;
+  const int h = (wg / NTILE) % A.heads;
+  const int b = wg / (NTILE * A.heads);
+  const int col0 = tile * DN_TILE;
+  const int tid = threadIdx.x;
+  const int c4 = tid & 3, r = tid >> 2;
+  const int lane = tid & 63, wid = tid >> 6;
+
+  __shared__ float s_q[DN_D], s_k[DN_D], s_v[DN_TILE];
+  __shared__ float s_red[4][2 * DN_TILE];
+  __shared__ float s_delta[DN_TILE];
+  __shared__ float s_scal[4];
+  __shared__ float s_wred[DN_NT / 64];
+
+  float4* S = reinterpret_cast<float4*>(A.state + ((long)(b * A.heads + h) * DN_D) * DN_D);
+  const int rowf4 = DN_D / 4;
+  float4 s0 = S[r * rowf4 + col0 / 4 + c4];
+  float4 s1 = S[(r + 64) * rowf4 + col0 / 4 + c4];
+  float st0[4] = {s0.x, s0.y, s0.z, s0.w};
+  float st1[4] = {s1.x, s1.y, s1.z, s1.w};
+  const float inv_sqrt_d = 11.313708498984761f;
+
+  for (int t = 0; t < A.seq; ++t) {
+    const long tok = (long)b * A.seq + t;
+    const long row = tok * A.heads + h;
+    const int i = tid & (DN_D - 1);
+    const long qoff = tok * A.q_stride + (long)(h % A.hk) * DN_D + i;
+    const float qv = Act<T>::load(A.q, qoff);
+    const float kv = Act<T>::load(A.k, qoff);
+    if (tid < DN_TILE) s_v[tid] = Act<T>::load(A.v, tok * A.v_stride + (long)h * DN_D + col0 + tid);
+    float sq = tid < DN_D ? qv * qv : 0.f;
+    float sk = tid < DN_D ? kv * kv : 0.f;
+    float sqk = tid < DN_D ? qv * kv : 0.f;
+    sq = block_sum<DN_NT>(sq, s_wred);
+    sk = block_sum<DN_NT>(sk, s_wred);
+    sqk = block_sum<DN_NT>(sqk, s_wred);
+    const float rq = rsqrt_rn(sq + 1e-6f), rk = rsqrt_rn(sk + 1e-6f);
+    if (tid < DN_D) {
+      s_q[tid] = div_rn(mul_rn(qv, rq), inv_sqrt_d);
+      s_k[tid] = mul_rn(kv, rk);
+    }
+    if (tid == 0) {
+      s_scal[0] = A.beta[row];
+      s_scal[1] = expf(A.g[row]);
+      s_scal[2] = div_rn(sqk * rq * rk, inv_sqrt_d);
+    }
+    __syncthreads();
+    const float decay = s_scal[1];
+    const float kr0 = s_k[r], kr1 = s_k[r + 64], qr0 = s_q[r], qr1 = s_q[r + 64];
+    float pk[4], pq[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      st0[c] *= decay;
+      st1[c] *= decay;
+      pk[c] = fmaf(st0[c], kr0, st1[c] * kr1);
+      pq[c] = fmaf(st0[c], qr0, st1[c] * qr1);
+    }
+#pragma unroll
+    for (int off = 4; off < 64; off <<= 1) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        pk[c] += __shfl_xor(pk[c], off, 64);
+        pq[c] += __shfl_xor(pq[c], off, 64);
+      }
+    }
+    if (lane < 4) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        s_red[wid][lane * 4 + c] = pk[c];
+        s_red[wid][DN_TILE + lane * 4 + c] = pq[c];
+      }
+    }
+    __syncthreads();
+    if (tid < DN_TILE) {
+      const float pred = s_red[0][tid] + s_red[1][tid] + s_red[2][tid] + s_red[3][tid];
+      const float qd = s_red[0][DN_TILE + tid] + s_red[1][DN_TILE + tid] + s_red[2][DN_TILE + tid] +
+                       s_red[3][DN_TILE + tid];
+      const float delta = (s_v[tid] - pred) * s_scal[0];
+      s_delta[tid] = delta;
+      Act<T>::store(A.out, row * DN_D + col0 + tid, fmaf(s_scal[2], delta, qd));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float dl = s_delta[c4 * 4 + c];
+      st0[c] = fmaf(kr0, dl, st0[c]);
+      st1[c] = fmaf(kr1, dl, st1[c]);
+    }
+  }
+  S[r * rowf4 + col0 / 4 + c4] = make_float4(st0[0], st0[1], st0[2], st0[3]);
+  S[(r + 64) * rowf4 + col0 / 4 + c4] = make_float4(st1[0], st1[1], st1[2], st1[3]);
+}
+
+template <typename T>
+int launch_dn_decode(const qm_dn_geom* g, const void* qkv, const void* z, const void* a, const void* b,
+                     const float* a_neg, const float* dt_bias, const void* conv_w, const float* norm_w,
+                     const int* positions, void* conv_ring, float* state, void* out, void* ws,
+                     hipStream_t stream) {
+  DnDecodeArgs<T> A;
+  A.qkv = static_cast<const T*>(qkv); A.z = static_cast<const T*>(z);
+  A.a = static_cast<const T*>(a); A.b = static_cast<const T*>(b);
+  A.a_neg = a_neg; A.dt_bias = dt_bias;
+  A.conv_w = static_cast<const T*>(conv_w); A.norm_w = norm_w;
+  A.positions = positions;
+  A.ring = static_cast<T*>(conv_ring); A.state = state; A.out = static_cast<T*>(out);
+  A.batch = g->batch; A.hv = g->n_v_heads; A.hk = g->n_k_heads;
+  A.conv_dim = 2 * g->n_k_heads * DN_D + g->n_v_heads * DN_D;
+  A.K = g->conv_kernel; A.eps = g->eps;
+  A.o_park = static_cast<float*>(ws);
+  A.counters = reinterpret_cast<unsigned*>(static_cast<char*>(ws) + qm_align256((size_t)g->batch * g->n_v_heads * DN_D * sizeof(float)));
+  const int nwg = g->batch * g->n_v_heads * (DN_D / DN_TILE);
+  hipLaunchKernelGGL(dn_decode_kernel<T>, dim3(nwg), dim3(DN_NT), 0, stream, A);
+  QM_CHECK_LAUNCH();
+  return QM_OK;
+}
+
+template <typename T>
+int launch_dn_recurrent(int batch, int seq, int heads, int hk, long q_stride, long v_stride, const void* q,
+                        const void* k, const void* v, const float* g, const float* beta, float* state, void* out,
+                        hipStream_t stream) {
+  DnRecurArgs<T> A;
+  A.q = static_cast<const T*>(q); A.k = static_cast<const T*>(k); A.v = static_cast<const T*>(v);
+  A.g = g; A.beta = beta; A.state = state; A.out = static_cast<T*>(out);
+  A.batch = batch; A.seq = seq; A.heads = heads; A.hk = hk; A.q_stride = q_stride; A.v_stride = v_stride;
+  const int nwg = batch * heads * (DN_D / DN_TILE);
+  hipLaunchKernelGGL(dn_recurrent_kernel<T>, dim3(nwg), dim3(DN_NT), 0, stream, A);
+  QM_CHECK_LAUNCH();
+  return QM_OK;
+}
+
+}  // namespace
+
+extern "C" size_t qm_dn_decode_workspace(int batch, int n_v_heads, int head_dim) {
+  if (batch <= 0 || n_v_heads <= 0 || head_dim <= 0) return 0;
+  return qm_align256((size_t)batch * n_v_heads * head_dim * sizeof(float)) +
+         qm_align256((size_t)batch * n_v_heads * sizeof(unsigned));
+}
+
+extern "C" int qm_dn_decode(const qm_dn_geom* g, const void* qkv, const void* z, const void* a, const void* b,
+                            const float* a_neg, const float* dt_bias, const void* conv_w, const float* norm_w,
+                            const int* positions, void* conv_ring, float* state, void* out, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream) {
+  if (!g) return qm_fail(QM_ERR_ARG, "qm_dn_decode: null geometry");
+  if (g->head_dim != DN_D) return qm_fail(QM_ERR_UNSUPPORTED, "qm_dn_decode: head_dim must be 128");
+  if (g->batch <= 0 || g->n_v_heads <= 0 || g->n_k_heads <= 0 || g->n_v_heads % g->n_k_heads)
+    return qm_fail(QM_ERR_ARG, "qm_dn_decode: need batch > 0 and n_v_heads a multiple of n_k_heads");
+  if (g->conv_kernel < 2 || g->conv_kernel > 8) return qm_fail(QM_ERR_ARG, "qm_dn_decode: conv_kernel must be 2..8");
+  if (!qkv || !z || !a || !b || !a_neg || !dt_bias || !conv_w || !norm_w || !positions || !conv_ring || !state || !out)
+    return qm_fail(QM_ERR_ARG, "qm_dn_decode: null tensor pointer");
+  if (!workspace || workspace_bytes < qm_dn_decode_workspace(g->batch, g->n_v_heads, g->head_dim))
+    return qm_fail(QM_ERR_WORKSPACE, "qm_dn_decode: workspace too small");
+  if (g->act_dtype == QM_ACT_F32)
+    return launch_dn_decode<float>(g, qkv, z, a, b, a_neg, dt_bias, conv_w, norm_w, positions, conv_ring, state, out,
+                                   workspace, stream);
+  if (g->act_dtype == QM_ACT_BF16)
+    return launch_dn_decode<bf16_t>(g, qkv, z, a, b, a_neg, dt_bias, conv_w, norm_w, positions, conv_ring, state, out,
+                                    workspace, stream);
+  return qm_fail(QM_ERR_DTYPE, "qm_dn_decode: act_dtype must be QM_ACT_F32 or QM_ACT_BF16");
+}
+
+extern "C" int qm_dn_recurrent(int act_dtype, int batch, int seq, int heads, int head_dim, const void* q,
+                               const void* k, const void* v, const float* g, const float* beta, float* state,
+                               void* out, hipStream_t stream) {
+  if (head_dim != DN_D) return qm_fail(QM_ERR_UNSUPPORTED, "qm_dn_recurrent: head_dim must be 128");
+  if (batch <= 0 || seq < 0 || heads <= 0) return qm_fail(QM_ERR_ARG, "qm_dn_recurrent: bad sizes");
+  if (!q || !k || !v || !g || !beta || !state || !out) return qm_fail(QM_ERR_ARG, "qm_dn_recurrent: null pointer");
+  if (seq == 0) return QM_OK;
+  return qm_dn_recurrent_strided(act_dtype, batch, seq, heads, heads, (long)heads * head_dim, (long)heads * head_dim,
+                                 q, k, v, g, beta, state, out, stream);
+}
+
+int qm_dn_recurrent_strided(int act_dtype, int batch, int seq, int heads, int hk, long q_stride, long v_stride,
+                            const void* q, const void* k, const void* v, const float* g, const float* beta,
+                            float* state, void* out, hipStream_t stream) {
+  if (act_dtype == QM_ACT_F32)
+    return launch_dn_recurrent<float>(batch, seq, heads, hk, q_stride, v_stride, q, k, v, g, beta, state, out, stream);
+  if (act_dtype == QM_ACT_BF16)
+    return launch_dn_recurrent<bf16_t>(batch, seq, heads, hk, q_stride, v_stride, q, k, v, g, beta, state, out,
+                                       stream);
+  return qm_fail(QM_ERR_DTYPE, "qm_dn_recurrent: act_dtype must be QM_ACT_F32 or QM_ACT_BF16");
+}

@@ -1,0 +1,23 @@
+// Internal declarations shared by the qwen4mix translation units.
+#pragma once
+
+#include <stddef.h>
+
+#include "qwen4mix.h"
+
+// Record `msg` as the calling thread's last error and return `code`.
+int qm_fail(int code, const char* msg);
+
+inline size_t qm_align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
+
+// The delta-rule token loop over strided q/k/v rows (q/k head h % hk): shared
+// by qm_dn_recurrent and the prefill path.
+int qm_dn_recurrent_strided(int act_dtype, int batch, int seq, int heads, int hk, long q_stride, long v_stride,
+                            const void* q, const void* k, const void* v, const float* g, const float* beta,
+                            float* state, void* out, hipStream_t stream);
+
+// The delta rule over a chunk of tokens for the prefill path: the WY/UT chunked
+// kernel where it applies, the token loop otherwise.
+int qm_dn_rule_chunk(int act_dtype, int batch, int seq, int heads, int hk, long q_stride, long v_stride,
+                     const void* q, const void* k, const void* v, const float* g, const float* beta, float* state,
+                     void* out, hipStream_t stream);

@@ -1,0 +1,260 @@
+"""The token-mixing layers of qwen4exp on MI355X, behind the reference's methods.
+
+``Qwen4MixModel`` carries the three methods of the reference's
+``Qwen4ExpModel`` that this path replaces, with the same names, signatures and
+return values, so an engine written against the reference can call them:
+
+* ``_linear_attention(hidden, layer, cache)``            reference/model.py:177-244
+* ``_indexer_mask(hidden, layer, cos, sin, cache, kv_len, query_offset)``
+                                                          reference/model.py:248-327
+* ``_full_attention(hidden, layer, cos, sin, cache, query_offset)``
+                                                          reference/model.py:331-383
+
+Weights come from ``store.get(f"blk.{layer}.{suffix}")`` as in
+reference/model.py:45-49 and are copied to the device once. The projections
+(``F.linear``) run as PyTorch-ROCm GEMMs; everything between them -- conv ring,
+gates, delta rule, norms, rope, paging, indexer scoring, top-k, attention,
+output gate -- runs in the HIP kernels of libqwen4mix.so. There is no other
+implementation to fall back to: a missing library or a failed call raises.
+
+``cache`` is a ``MixHybridCache`` (cache.py). ``hidden`` must be a float32 or
+bfloat16 tensor on the model's device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+import torch.nn.functional as F
+
+from . import native
+from .cache import MixHybridCache
+from .config import MixConfig
+from .rope import RopeTable
+
+
+class Qwen4MixModel:
+    def __init__(self, config, store, device=None, max_ctx: int = 8192):
+        self.config = config if isinstance(config, MixConfig) else MixConfig.from_reference(config)
+        self.store = store
+        self.device = torch.device(device if device is not None else "cuda")
+        self.max_ctx = max_ctx
+        self.rope = RopeTable(self.config.rope_dim, self.config.rope_theta, self.config.mrope_section, self.device)
+        self._dev = {}
+        self._ws = {}
+        native.load()
+
+    # -- weights (reference/model.py:45-49) -----------------------------------
+
+    def w(self, name: str) -> torch.Tensor:
+        return self.store.get(name)
+
+    def bw(self, layer: int, suffix: str) -> torch.Tensor:
+        return self.store.get(f"blk.{layer}.{suffix}")
+
+    def _dw(self, layer: int, suffix: str, dtype=None) -> torch.Tensor:
+        key = (layer, suffix, dtype)
+        t = self._dev.get(key)
+        if t is None:
+            src = self.bw(layer, suffix)
+            t = src.to(self.device, dtype if dtype is not None else src.dtype).contiguous()
+            self._dev[key] = t
+        return t
+
+    def _workspace(self, name: str, nbytes: int) -> torch.Tensor:
+        buf = self._ws.get(name)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            self._ws[name] = buf
+        return buf
+
+    def _positions(self, batch: int, pos: int) -> torch.Tensor:
+        return torch.full((batch,), pos, dtype=torch.int32, device=self.device)
+
+    # -- geometry ----------------------------------------------------------------
+
+    def dn_geom(self, batch: int, dtype) -> native.DnGeom:
+        c = self.config
+        return native.DnGeom(batch, c.linear_num_v_heads, c.linear_num_k_heads, c.linear_head_dim, c.conv_kernel,
+                             native.act_code(dtype), c.rms_norm_eps)
+
+    def qsa_geom(self, cache: MixHybridCache, dtype) -> native.QsaGeom:
+        c = self.config
+        return native.QsaGeom(cache.batch, c.num_attention_heads, c.num_kv_heads, c.head_dim, c.rope_dim,
+                              c.indexer_heads, c.indexer_head_dim, c.indexer_compress_ratio, c.indexer_budget,
+                              c.page_size, cache.max_pages, cache.max_ctx, cache.max_blocks, native.act_code(dtype),
+                              c.rms_norm_eps)
+
+    # -- Gated DeltaNet ------------------------------------------------------------
+
+    def dn_core(self, qkv, z, a, b, layer: int, lc, out=None):
+        """The mixer core between the projections (the HIP part of _linear_attention).
+
+        qkv [B, S, conv_dim], z [B, S, Hv*d], a, b [B, S, Hv] (act) -> [B, S, Hv*d].
+        ``lc`` is the layer's ``MixLayerCache``; its ring and state update in place.
+        """
+        c = self.config
+        batch, seq = qkv.shape[0], qkv.shape[1]
+        dt = qkv.dtype
+        lc.ensure_dn(batch, dt)
+        if out is None:
+            out = torch.empty(batch, seq, c.linear_value_dim, dtype=dt, device=self.device)
+        g = self.dn_geom(batch, dt)
+        pos = self._positions(batch, lc.n_tokens)
+        a_neg = self._dw(layer, "ssm_a", torch.float32)
+        dt_bias = self._dw(layer, "ssm_dt.bias", torch.float32)
+        conv_w = self._dw(layer, "ssm_conv1d.weight", dt)
+        norm_w = self._dw(layer, "ssm_norm.weight", torch.float32)
+        stream = native.stream_handle(self.device)
+        args = (native.ptr(qkv), native.ptr(z), native.ptr(a), native.ptr(b), native.ptr(a_neg), native.ptr(dt_bias),
+                native.ptr(conv_w), native.ptr(norm_w), native.ptr(pos), native.ptr(lc.conv_ring),
+                native.ptr(lc.recurrent_state), native.ptr(out))
+        if seq == 1:
+            nbytes = native.load().qm_dn_decode_workspace(batch, c.linear_num_v_heads, c.linear_head_dim)
+            ws = self._workspace("dn_decode", nbytes)
+            native.call("qm_dn_decode", ctypes.byref(g), *args, native.ptr(ws), ws.numel(), stream)
+        else:
+            nbytes = native.load().qm_dn_prefill_workspace(ctypes.byref(g), seq)
+            ws = self._workspace("dn_prefill", nbytes)
+            native.call("qm_dn_prefill", ctypes.byref(g), seq, *args, native.ptr(ws), ws.numel(), stream)
+        lc.n_tokens += seq
+        return out
+
+    def _linear_attention(self, hidden: torch.Tensor, layer: int, cache) -> torch.Tensor:
+        """reference/model.py:177-244."""
+        batch, seq, _ = hidden.shape
+        dt = hidden.dtype
+        if cache is None:
+            cache = MixHybridCache(layer + 1, self.config, batch, max(seq, 64), self.device, dt)
+        lc = cache[layer]
+        qkv = F.linear(hidden, self._dw(layer, "attn_qkv.weight", dt))
+        z = F.linear(hidden, self._dw(layer, "attn_gate.weight", dt))
+        b = F.linear(hidden, self._dw(layer, "ssm_beta.weight", dt))
+        a = F.linear(hidden, self._dw(layer, "ssm_alpha.weight", dt))
+        out = self.dn_core(qkv.contiguous(), z.contiguous(), a.contiguous(), b.contiguous(), layer, lc)
+        return F.linear(out, self._dw(layer, "ssm_out.weight", dt))
+
+    # -- QSA -------------------------------------------------------------------
+
+    def _rope(self, cos, sin, n_pos: int):
+        """Device (cos, sin) tables [n_pos, rope_dim] from the caller's, or our own."""
+        if cos is not None and cos.is_cuda and cos.dtype == torch.float32 and cos.shape[-2] >= n_pos:
+            c = cos[0] if cos.ndim == 3 else cos
+            s = sin[0] if sin.ndim == 3 else sin
+            return c.contiguous(), s.contiguous()
+        if cos is not None and not cos.is_cuda:
+            c = (cos[0] if cos.ndim == 3 else cos)[:n_pos].to(self.device, torch.float32).contiguous()
+            s = (sin[0] if sin.ndim == 3 else sin)[:n_pos].to(self.device, torch.float32).contiguous()
+            return c, s
+        return self.rope.get(n_pos)
+
+    def _sync_blocks(self, lc, g, cos_t, sin_t, upto_tokens: int, layer: int):
+        """Pool any complete block of an imported history that has no pooled key yet."""
+        ratio = self.config.indexer_compress_ratio
+        n_complete = min(upto_tokens // ratio, lc.block_keys.shape[1])
+        if n_complete > lc.blocks_valid:
+            native.call("qm_qsa_pool_blocks", ctypes.byref(g), native.ptr(lc.raw_keys),
+                        native.ptr(self._dw(layer, "indexer.k_norm.weight", torch.float32)), native.ptr(cos_t),
+                        native.ptr(sin_t), lc.blocks_valid, n_complete - lc.blocks_valid, native.ptr(lc.block_keys),
+                        native.stream_handle(self.device))
+            lc.blocks_valid = n_complete
+
+    def qsa_core(self, qg, k, v, iq, ik, layer: int, cache, query_offset: int, cos=None, sin=None, out=None,
+                 attend: bool = True):
+        """The HIP part of _full_attention: prep, select and attend on the projections.
+
+        qg [B, S, Hq*2*d], k, v [B, S, Hkv*d], iq [B, S, idx_heads*idx_dim],
+        ik [B, S, idx_dim] (act). Returns out [B, S, Hq*d] (act), or None when
+        ``attend`` is False (indexer and cache update only).
+        """
+        c = self.config
+        batch, seq = iq.shape[0], iq.shape[1]
+        dt = iq.dtype
+        lc = cache[layer]
+        lc.ensure_qsa(batch, dt)
+        if lc.raw_keys.dtype != dt:
+            raise ValueError(f"activations are {dt} but the cache was built for {lc.raw_keys.dtype}")
+        if query_offset + seq > cache.max_ctx:
+            raise ValueError(f"context {query_offset + seq} exceeds the cache's {cache.max_ctx}")
+        g = self.qsa_geom(cache, dt)
+        cos_t, sin_t = self._rope(cos, sin, query_offset + seq)
+        stream = native.stream_handle(self.device)
+        self._sync_blocks(lc, g, cos_t, sin_t, query_offset, layer)
+        pos = self._positions(batch, query_offset)
+        q_out = torch.empty(batch, seq, c.num_attention_heads, c.head_dim, dtype=torch.float32, device=self.device) \
+            if qg is not None else None
+        iq_out = torch.empty(batch, seq, c.indexer_heads, c.indexer_head_dim, dtype=torch.float32, device=self.device)
+        native.call("qm_qsa_prep", ctypes.byref(g), seq, native.ptr(qg), native.ptr(k), native.ptr(v),
+                    native.ptr(iq), native.ptr(ik), native.ptr(self._dw(layer, "attn_q_norm.weight", torch.float32)),
+                    native.ptr(self._dw(layer, "attn_k_norm.weight", torch.float32)),
+                    native.ptr(self._dw(layer, "indexer.q_norm.weight", torch.float32)),
+                    native.ptr(self._dw(layer, "indexer.k_norm.weight", torch.float32)), native.ptr(cos_t),
+                    native.ptr(sin_t), native.ptr(pos), native.ptr(lc.page_table), native.ptr(lc.k_pool),
+                    native.ptr(lc.v_pool), native.ptr(lc.raw_keys), native.ptr(lc.block_keys), native.ptr(q_out),
+                    native.ptr(iq_out), stream)
+        lc.blocks_valid = max(lc.blocks_valid, (query_offset + seq) // c.indexer_compress_ratio)
+        if k is not None:
+            lc.n_tokens = query_offset + seq
+        ids = torch.empty(batch, seq, c.block_topk, dtype=torch.int32, device=self.device)
+        n_sel = torch.empty(batch, seq, dtype=torch.int32, device=self.device)
+        native.call("qm_qsa_select", ctypes.byref(g), seq, native.ptr(iq_out), native.ptr(lc.block_keys),
+                    native.ptr(pos), native.ptr(ids), native.ptr(n_sel), None, stream)
+        lc.last_ids, lc.last_n_sel, lc.last_iq, lc.last_q = ids, n_sel, iq_out, q_out
+        if not attend:
+            return None
+        lib = native.load()
+        splits = lib.qm_qsa_attend_splits(ctypes.byref(g), query_offset + seq - 1)
+        ws = self._workspace("qsa_attend", lib.qm_qsa_attend_workspace(ctypes.byref(g), seq, splits))
+        if out is None:
+            out = torch.empty(batch, seq, c.num_attention_heads * c.head_dim, dtype=dt, device=self.device)
+        native.call("qm_qsa_attend", ctypes.byref(g), seq, native.ptr(q_out), native.ptr(qg), native.ptr(lc.k_pool),
+                    native.ptr(lc.v_pool), native.ptr(lc.page_table), native.ptr(pos), native.ptr(ids),
+                    native.ptr(n_sel), native.ptr(out), splits, native.ptr(ws), ws.numel(), stream)
+        return out
+
+    def _full_attention(self, hidden, layer: int, cos, sin, cache, query_offset: int) -> torch.Tensor:
+        """reference/model.py:331-383."""
+        batch, seq, _ = hidden.shape
+        dt = hidden.dtype
+        if cache is None:
+            cache = MixHybridCache(layer + 1, self.config, batch, max(query_offset + seq, 64), self.device, dt)
+        qg = F.linear(hidden, self._dw(layer, "attn_q.weight", dt)).contiguous()
+        k = F.linear(hidden, self._dw(layer, "attn_k.weight", dt)).contiguous()
+        v = F.linear(hidden, self._dw(layer, "attn_v.weight", dt)).contiguous()
+        iq = F.linear(hidden, self._dw(layer, "indexer.q_proj.weight", dt)).contiguous()
+        ik = F.linear(hidden, self._dw(layer, "indexer.k_proj.weight", dt)).contiguous()
+        out = self.qsa_core(qg, k, v, iq, ik, layer, cache, query_offset, cos, sin)
+        return F.linear(out, self._dw(layer, "attn_output.weight", dt))
+
+    def selection_mask(self, lc, kv_len: int, query_offset: int) -> torch.Tensor:
+        """Boolean (B, 1, S, kv_len) mask of the layer's last selection plus tails."""
+        c = self.config
+        ratio = c.indexer_compress_ratio
+        ids, n_sel = lc.last_ids.long(), lc.last_n_sel.long()
+        batch, seq, k = ids.shape
+        mask = torch.zeros(batch, seq, kv_len, dtype=torch.bool, device=self.device)
+        valid = torch.arange(k, device=self.device)[None, None] < n_sel[..., None]
+        tok = (ids[..., None] * ratio + torch.arange(ratio, device=self.device)).flatten(2)
+        keep = valid[..., None].expand(-1, -1, -1, ratio).flatten(2)
+        tok = torch.where(keep, tok, torch.zeros_like(tok))
+        mask.scatter_(2, tok, keep)
+        qpos = torch.arange(seq, device=self.device) + query_offset
+        tail_start = ((qpos + 1) // ratio) * ratio
+        kpos = torch.arange(kv_len, device=self.device)
+        tail = (kpos[None] >= tail_start[:, None]) & (kpos[None] <= qpos[:, None])
+        return (mask | tail[None]).unsqueeze(1)
+
+    def _indexer_mask(self, hidden, layer: int, cos, sin, cache, kv_len: int, query_offset: int) -> torch.Tensor:
+        """reference/model.py:248-327: appends the raw indexer keys of ``hidden``,
+        selects, and returns the boolean visibility mask."""
+        batch, seq, _ = hidden.shape
+        dt = hidden.dtype
+        if cache is None:
+            cache = MixHybridCache(layer + 1, self.config, batch, max(kv_len, 64), self.device, dt)
+        iq = F.linear(hidden, self._dw(layer, "indexer.q_proj.weight", dt)).contiguous()
+        ik = F.linear(hidden, self._dw(layer, "indexer.k_proj.weight", dt)).contiguous()
+        lc = cache[layer]
+        self.qsa_core(None, None, None, iq, ik, layer, cache, query_offset, cos, sin, attend=False)
+        lc.n_tokens = max(lc.n_tokens, query_offset + seq)
+        return self.selection_mask(lc, kv_len, query_offset)

@@ -1,0 +1,109 @@
+"""ctypes binding of libqwen4mix.so (declared in include/qwen4mix.h).
+
+There is one code path: if the library is missing or a call fails, this module
+raises. Nothing here computes anything itself.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libqwen4mix.so")
+
+QM_ACT_F32 = 0
+QM_ACT_BF16 = 1
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+
+
+class QmError(RuntimeError):
+    """A qwen4mix entry point returned an error code."""
+
+
+class DnGeom(ctypes.Structure):
+    _fields_ = [("batch", _i), ("n_v_heads", _i), ("n_k_heads", _i), ("head_dim", _i),
+                ("conv_kernel", _i), ("act_dtype", _i), ("eps", _f)]
+
+
+class QsaGeom(ctypes.Structure):
+    _fields_ = [("batch", _i), ("n_heads", _i), ("n_kv_heads", _i), ("head_dim", _i), ("rope_dim", _i),
+                ("idx_heads", _i), ("idx_dim", _i), ("ratio", _i), ("budget", _i), ("page_size", _i),
+                ("max_pages", _i), ("max_ctx", _i), ("max_blocks", _i), ("act_dtype", _i), ("eps", _f)]
+
+
+# name -> (restype, argtypes); every symbol include/qwen4mix.h declares
+SIGNATURES = {
+    "qm_last_error": (ctypes.c_char_p, []),
+    "qm_version": (_i, []),
+    "qm_dn_decode_workspace": (_sz, [_i, _i, _i]),
+    "qm_dn_decode": (_i, [ctypes.POINTER(DnGeom), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                          _vp, _sz, _vp]),
+    "qm_dn_recurrent": (_i, [_i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "qm_dn_chunked": (_i, [_i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "qm_v_slot": (_i, [_i]),
+    "qm_qsa_prep": (_i, [ctypes.POINTER(QsaGeom), _i] + [_vp] * 19 + [_vp]),
+    "qm_qsa_select": (_i, [ctypes.POINTER(QsaGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "qm_qsa_attend_workspace": (_sz, [ctypes.POINTER(QsaGeom), _i, _i]),
+    "qm_qsa_attend_splits": (_i, [ctypes.POINTER(QsaGeom), _i]),
+    "qm_qsa_attend": (_i, [ctypes.POINTER(QsaGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
+                           _sz, _vp]),
+    "qm_qsa_pool_blocks": (_i, [ctypes.POINTER(QsaGeom), _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
+    "qm_dn_prefill_workspace": (_sz, [ctypes.POINTER(DnGeom), _i]),
+    "qm_dn_prefill": (_i, [ctypes.POINTER(DnGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                           _vp, _vp, _sz, _vp]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the library (once) and bind every entry point; raise if absent."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            raise QmError(f"{path} is missing: build it with __graft_entry__.build() "
+                          "(there is no fallback implementation)")
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def call(name: str, *args) -> int:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.qm_last_error().decode(errors="replace")
+        raise QmError(f"{name} failed ({rc}): {msg}")
+    return rc
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device=None) -> int:
+    import torch
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def act_code(dtype) -> int:
+    import torch
+    if dtype == torch.float32:
+        return QM_ACT_F32
+    if dtype == torch.bfloat16:
+        return QM_ACT_BF16
+    raise QmError(f"unsupported activation dtype {dtype}; use float32 or bfloat16")

@@ -1,0 +1,294 @@
+"""Benchmark: qwen4exp token mixing at batch 1, position 8128 (QSA selection on
++ one Gated DeltaNet decode step), on one MI355X.
+
+One step = one QSA decode core at position 8128 of an 8192-token context
+(token prep + K/V page append, indexer scoring over 127 blocks, top-32
+selection, paged GQA attention over the 2049 selected keys, sigmoid gate) plus
+one DeltaNet decode core (conv ring, gates, delta-rule update of the
+[32,128,128] float32 state, gated norm). Inputs are synthetic (seeded), already
+resident in HBM, and rotated over enough independent layer instances that the
+data touched per rotation exceeds twice the 256 MB Infinity Cache.
+
+Prints one JSON line (see the driver contract); ``--sweep`` adds per-position
+lines (192, 1984, 4032, 8128) and the 128-token prefill chunk to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "attention µs/token at batch 1, pos 8128 (QSA sel on + DeltaNet); % HBM roofline"
+
+# algorithmic bytes (bf16 KV and activations, float32 DeltaNet state)
+KV_BYTES_PER_KEY = 2 * 256 * 2 * 2          # K and V of 2 kv heads
+BLOCK_KEY_BYTES = 128 * 4                   # this build keeps pooled keys in float32
+DN_BYTES = (2 * 32 * 128 * 128 * 4          # state read + write
+            + 4 * 8192 * 2                  # conv ring: 3 history columns read, 1 written
+            + 8192 * 4 * 2                  # conv weights
+            + 8192 * 2 + 4096 * 2 * 2       # qkv in, z in, out
+            + 32 * 2 * 2 + 32 * 4 * 2 + 128 * 4)
+
+
+def qsa_keys(pos: int, ratio: int = 64, topk: int = 32) -> int:
+    """Keys a query at `pos` attends: its selected blocks plus its tail."""
+    n_elig = (pos + 1) // ratio
+    return min(topk, n_elig) * ratio + (pos + 1 - n_elig * ratio)
+
+
+def qsa_bytes(pos: int, ratio: int = 64, topk: int = 32) -> int:
+    n_elig = (pos + 1) // ratio
+    keys = qsa_keys(pos, ratio, topk)
+    scored = n_elig if n_elig > topk else 0
+    io = 16 * 512 * 2 + 2 * 2 * 256 * 2 + 512 * 2 + 128 * 2 + 16 * 256 * 2   # qg, k, v, iq, ik, out
+    return keys * KV_BYTES_PER_KEY + scored * BLOCK_KEY_BYTES + io
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--position", type=int, default=8128)
+    ap.add_argument("--instances", type=int, default=0, help="rotated layer instances (0: auto, > 512 MB)")
+    ap.add_argument("--sweep", action="store_true", help="also time positions 192/1984/4032 and a prefill chunk")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+class Instance:
+    """One QSA layer + one DeltaNet layer with their own caches and inputs."""
+
+    def __init__(self, qm, model, pos, max_ctx, seed):
+        import torch
+        from importlib import import_module
+        plan = import_module(qm.__name__ + ".plan")
+        dev = model.device
+        c = model.config
+        g = torch.Generator(device=dev).manual_seed(seed)
+        bf = torch.bfloat16
+        self.cache = qm.MixHybridCache(4, c, 1, max_ctx, dev, bf, page_table="random", seed=seed)
+        lq, ld = self.cache[3], self.cache[0]
+        lq.ensure_qsa(1, bf)
+        ld.ensure_dn(1, bf)
+        # resident history: K/V pages, raw indexer keys, DeltaNet state and ring
+        lq.k_pool.copy_(torch.randn(lq.k_pool.shape, generator=g, device=dev).to(bf))
+        lq.v_pool.copy_(torch.randn(lq.v_pool.shape, generator=g, device=dev).to(bf))
+        lq.raw_keys.copy_(torch.randn(lq.raw_keys.shape, generator=g, device=dev).to(bf))
+        lq.n_tokens = pos
+        ld.recurrent_state.copy_(torch.randn(ld.recurrent_state.shape, generator=g, device=dev) * 0.02)
+        ld.conv_ring.copy_(torch.randn(ld.conv_ring.shape, generator=g, device=dev).to(bf))
+        ld.n_tokens = pos
+        cos, sin = model.rope.get(max_ctx)
+        geom = model.qsa_geom(self.cache, bf)
+        qm.native.call("qm_qsa_pool_blocks", ctypes.byref(geom), lq.raw_keys.data_ptr(),
+                       model._dw(3, "indexer.k_norm.weight", torch.float32).data_ptr(), cos.data_ptr(),
+                       sin.data_ptr(), 0, pos // c.indexer_compress_ratio, lq.block_keys.data_ptr(),
+                       qm.native.stream_handle(dev))
+        lq.blocks_valid = pos // c.indexer_compress_ratio
+        # this step's projection outputs
+        r = lambda *s: torch.randn(*s, generator=g, device=dev).to(bf)  # noqa: E731
+        self.qg, self.k, self.v = r(1, 1, 16 * 512), r(1, 1, 512), r(1, 1, 512)
+        self.iq, self.ik = r(1, 1, 512), r(1, 1, 128)
+        self.qkv, self.z, self.a, self.b = r(1, 1, 8192), r(1, 1, 4096), r(1, 1, 32), r(1, 1, 32)
+        self.qsa = plan.QsaDecodePlan(model, self.cache, 3, pos, bf)
+        self.dn = plan.DnDecodePlan(model, self.cache, 0, bf)
+        self.qsa.positions.fill_(pos)
+        self.dn.positions.fill_(pos)
+
+    def step(self, stream):
+        self.qsa.run(self.qg, self.k, self.v, self.iq, self.ik, stream)
+        self.dn.run(self.qkv, self.z, self.a, self.b, stream)
+
+
+def weights_store(dtype):
+    """Random-init weights of the layer architecture (only norms and DeltaNet
+    scalars are read by the timed core; projections are synthetic inputs)."""
+    import torch
+    w = {}
+    w["blk.0.ssm_a"] = -torch.rand(32) * 2 - 0.1
+    w["blk.0.ssm_dt.bias"] = torch.randn(32) * 0.1
+    w["blk.0.ssm_conv1d.weight"] = (torch.randn(8192, 4) * 0.5).to(dtype)
+    w["blk.0.ssm_norm.weight"] = torch.ones(128)
+    for s in ("attn_q_norm.weight", "attn_k_norm.weight"):
+        w[f"blk.3.{s}"] = torch.ones(256)
+    for s in ("indexer.q_norm.weight", "indexer.k_norm.weight"):
+        w[f"blk.3.{s}"] = torch.ones(128)
+
+    class Store:
+        def get(self, name):
+            return w[name]
+    return Store()
+
+
+def time_steps(instances, steps, warmup, stream):
+    import torch
+    n = len(instances)
+    for i in range(warmup):
+        instances[i % n].step(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        instances[i % n].step(stream)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def time_kernels(instances, reps, stream_obj):
+    """Average duration of each entry point's launches, HIP events on the launch stream."""
+    import torch
+    n = len(instances)
+    s = stream_obj.cuda_stream
+    parts = {"qsa_prep": lambda x: x.qsa.prep(x.qg, x.k, x.v, x.iq, x.ik, s),
+             "qsa_select": lambda x: x.qsa.select(s),
+             "qsa_attend": lambda x: x.qsa.attend(x.qg, s),
+             "dn_decode": lambda x: x.dn.run(x.qkv, x.z, x.a, x.b, s)}
+    out = {}
+    for name, fn in parts.items():
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for i in range(reps):
+            x = instances[i % n]
+            if name in ("qsa_select", "qsa_attend"):
+                x.qsa.prep(x.qg, x.k, x.v, x.iq, x.ik, s)
+                if name == "qsa_attend":
+                    x.qsa.select(s)
+            evs[i][0].record(stream_obj)
+            fn(x)
+            evs[i][1].record(stream_obj)
+        torch.cuda.synchronize()
+        ms = sorted(a.elapsed_time(b) for a, b in evs)
+        out[name] = statistics.median(ms) * 1000.0   # microseconds
+    return out
+
+
+def cpu_baseline(position: int, seconds: float):
+    """The oracle (torch CPU restatement of the reference layers) on this host."""
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    import inputs as gi
+    from oracle.cache import OracleHybridCache
+    from oracle.config import OracleConfig
+    from oracle.layers import RotaryEmbedding
+    from oracle.mixing import OracleMixer
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    dt = torch.bfloat16
+    cfg = OracleConfig()
+    qstore = gi.FakeStore(gi.qsa_weights(3, 90, dt))
+    dstore = gi.FakeStore(gi.dn_weights(0, 91, dt))
+    keys, values, idx = gi.qsa_past(92, position, dt)
+    conv, state = gi.dn_past(93, dt)
+    rot = RotaryEmbedding(64, 1e7, [11, 11, 10])
+    p = torch.arange(position + 1)[None]
+    cos, sin = rot(p[None].expand(3, -1, -1))
+    qm_, dm_ = OracleMixer(cfg, qstore), OracleMixer(cfg, dstore)
+    F = torch.nn.functional
+    hidden = gi.hidden_states(94, 1, dt)
+    proj_d = [F.linear(hidden, dstore.get(f"blk.0.{n}")) for n in
+              ("attn_qkv.weight", "attn_gate.weight", "ssm_beta.weight", "ssm_alpha.weight")]
+
+    def one():
+        # QSA core: q/k norm + rope, cache append, indexer mask, masked GQA softmax, gate
+        oc = OracleHybridCache(4)
+        oc[3].keys, oc[3].values, oc[3].indexer_keys = keys, values, idx
+        q, k, v, gate = qm_.qkv_prep(hidden, 3, cos, sin)
+        K, V = torch.cat([keys, k], 2), torch.cat([values, v], 2)
+        mask = qm_._indexer_mask(hidden, 3, cos, sin, oc, position + 1, position)
+        out = qm_.attention_core(q, K, V, mask, dt)
+        out = out.transpose(1, 2).reshape(1, 1, -1) * torch.sigmoid(gate)
+        # DeltaNet core
+        dc = OracleHybridCache(1)
+        dc[0].conv_state, dc[0].recurrent_state = conv, state
+        dm_.dn_core(*proj_d[:2], proj_d[2], proj_d[3], 0, dc)
+        return out
+
+    for _ in range(3):
+        one()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times) * 1e6
+    return {"value": round(med, 1), "unit": "µs/token", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} steps of the oracle's QSA core at pos {position} (indexer + dense masked "
+                      f"softmax, as the reference computes it) + DeltaNet decode core, bf16, median"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
+                                   "(see DESIGN.md for how the path would shard)"}))
+        sys.exit(2)
+    import torch
+    import __graft_entry__
+    qm = __graft_entry__.load_package()
+    qm.native.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    pos = args.position
+    max_ctx = ((pos + 1 + 63) // 64) * 64
+    max_ctx = max(max_ctx, 8192)
+    model = qm.Qwen4MixModel(qm.MixConfig(), weights_store(torch.bfloat16), device=dev, max_ctx=max_ctx)
+
+    touched = qsa_bytes(pos) + DN_BYTES
+    n_inst = args.instances or max(8, int(2 * 256e6 / touched) + 1)
+    insts = [Instance(qm, model, pos, max_ctx, 1000 + i) for i in range(n_inst)]
+    stream = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
+    print(f"[bench] {n_inst} instances, {n_inst * touched / 1e6:.0f} MB touched per rotation", file=sys.stderr)
+
+    sec = time_steps(insts, args.steps, args.warmup, stream.cuda_stream)
+    us_step = sec * 1e6
+    kern = time_kernels(insts, max(50, min(args.steps, 400)), stream)
+    bytes_step = touched
+    kb = {"qsa_attend": qsa_keys(pos) * KV_BYTES_PER_KEY, "dn_decode": DN_BYTES}
+    dominant = max(kb, key=lambda k: kern[k])
+    achieved = kb[dominant] / (kern[dominant] * 1e-6) / 1e9
+    print(f"[bench] step {us_step:.2f} us; kernels (us): " +
+          ", ".join(f"{k} {v:.2f}" for k, v in kern.items()), file=sys.stderr)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(pos, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(us_step, 3),
+        "unit": "µs/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random KV pages, indexer keys, DeltaNet state, projection outputs)",
+        "config": {"workload": f"QSA selection-on decode at pos {pos} (ctx {max_ctx}, top-32 of 64-token "
+                               f"blocks) + one Gated DeltaNet decode step, batch 1",
+                   "position": pos, "batch": 1, "instances_rotated": n_inst,
+                   "step_bytes": bytes_step,
+                   "step_hbm_frac": round(bytes_step / sec / 1e9 / HBM_PEAK_GBS, 4),
+                   "kernel_us": {k: round(v, 3) for k, v in kern.items()}},
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

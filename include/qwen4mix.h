@@ -149,7 +149,9 @@ int qm_v_slot(int row);
  *   qg [B, S, Hq, 2*d]; k_new, v_new [B, S, Hkv, d]; iq [B, S, idx_heads*idx_dim];
  *   ik [B, S, idx_dim] (act); *_norm f32 weights; cos/sin [n_pos, rope_dim] f32;
  *   positions [B] int32 = position of the first row; page_table [B, max_pages].
- *   Outputs: q_out [B, S, Hq, d] f32 (normed, roped); iq_out [B, S, idx_heads,
+ *   Outputs: q_out [B, S, 2, Hq, d] bf16: the normed, roped query as hi and lo
+ *   parts (hi = bf16(q), lo = bf16(q - hi)), the operand form of the attention
+ *   MFMA; iq_out [B, S, idx_heads,
  *   idx_dim] f32; pools, raw keys and block cache updated in place.
  *   qg may be NULL (no attention query: q_norm, q_out unused) and k_new/v_new
  *   may both be NULL (no K/V append), which leaves the indexer part alone. */
@@ -157,7 +159,7 @@ int qm_qsa_prep(const qm_qsa_geom* g, int seq, const void* qg, const void* k_new
                 const void* iq, const void* ik, const float* q_norm, const float* k_norm,
                 const float* iq_norm, const float* ik_norm, const float* cos, const float* sin,
                 const int* positions, const int* page_table, void* k_pool, void* v_pool, void* raw_keys,
-                float* block_keys, float* q_out, float* iq_out, hipStream_t stream);
+                float* block_keys, void* q_out, float* iq_out, hipStream_t stream);
 
 /* Pooled keys of blocks first_block .. first_block+n_blocks-1 recomputed from
  * the raw-key cache (reference/model.py:289-294), for a history imported into
@@ -167,6 +169,9 @@ int qm_qsa_prep(const qm_qsa_geom* g, int seq, const void* qg, const void* k_new
 int qm_qsa_pool_blocks(const qm_qsa_geom* g, const void* raw_keys, const float* k_norm, const float* cos,
                        const float* sin, int first_block, int n_blocks, float* block_keys, hipStream_t stream);
 
+/* int2 entries per query row of the attention item table (see qm_qsa_select). */
+int qm_qsa_items_stride(const qm_qsa_geom* g);
+
 /* Block scoring and top-k selection for each query row: scores
  * sum_h relu(q_h . block_j) / sqrt(idx_dim) (reference/model.py:297-298) over
  * the eligible blocks j*ratio + ratio - 1 <= p, top min(budget/ratio, eligible)
@@ -174,28 +179,34 @@ int qm_qsa_pool_blocks(const qm_qsa_geom* g, const void* raw_keys, const float* 
  * rule is this library's; torch leaves tie order unspecified).
  *   iq [B, S, idx_heads, idx_dim] f32; block_keys as above; positions [B] first
  *   row's position; ids [B, S, budget/ratio] int32 in rank order; n_sel [B, S];
- *   scores_out [B, S, max_blocks] f32 or NULL (ineligible entries -inf). */
-int qm_qsa_select(const qm_qsa_geom* g, int seq, const float* iq, const float* block_keys,
-                  const int* positions, int* ids, int* n_sel, float* scores_out, hipStream_t stream);
+ *   scores_out [B, S, max_blocks] f32 or NULL (ineligible entries -inf).
+ *   items [B, S, qm_qsa_items_stride(g)] int2 or NULL: the attention work list
+ *   of each row -- entry 0 holds the count, then one entry per 32-token group
+ *   of the selected blocks (rank order) and of the row's tail block: physical
+ *   pool row of the group's first token (page_table lookup, paging as
+ *   tt/model.py:1252-1323) and its visible rows [lo, hi) as lo | hi << 8.
+ *   page_table [B, max_pages] is needed when items is given. */
+int qm_qsa_select(const qm_qsa_geom* g, int seq, const float* iq, const float* block_keys, const int* positions,
+                  const int* page_table, int* ids, int* n_sel, void* items, float* scores_out,
+                  hipStream_t stream);
 
 /* Bytes of workspace qm_qsa_attend needs for `seq` query rows and `splits`. */
 size_t qm_qsa_attend_workspace(const qm_qsa_geom* g, int seq, int splits);
-/* Split count (32-token groups per query at most) for queries up to max_position. */
-int qm_qsa_attend_splits(const qm_qsa_geom* g, int max_position);
+/* Split count (workgroups per row and kv head) covering every query row at
+ * positions first_position .. last_position. */
+int qm_qsa_attend_splits(const qm_qsa_geom* g, int first_position, int last_position);
 
-/* Paged GQA attention of `seq` query rows per sequence (row s at position
- * positions[b] + s) over each row's selected blocks plus its tail block, then
- * the sigmoid output gate (reference/model.py:365-382 with the mask of
- * :306-326; paging as tt/model.py:1252-1323): fp32 softmax of q.k/sqrt(d) over
- * the visible keys, times v, cast to act, times sigmoid(gate). K/V of every row
- * must already be in the pages (qm_qsa_prep).
- *   q [B, S, Hq, d] f32 (from qm_qsa_prep); qg [B, S, Hq, 2*d] act (the gate is
- *   the second half of each head); ids, n_sel from qm_qsa_select;
+/* Paged GQA attention of `seq` query rows per sequence over each row's item
+ * list (its selected blocks plus its tail block), then the sigmoid output gate
+ * (reference/model.py:365-382 with the mask of :306-326): fp32 softmax of
+ * q.k/sqrt(d) over the visible keys, times v, cast to act, times
+ * sigmoid(gate). K/V of every row must already be in the pages (qm_qsa_prep).
+ *   q [B, S, 2, Hq, d] bf16 hi/lo (from qm_qsa_prep); qg [B, S, Hq, 2*d] act (the gate is
+ *   the second half of each head); items from qm_qsa_select;
  *   out [B, S, Hq*d] act. */
-int qm_qsa_attend(const qm_qsa_geom* g, int seq, const float* q, const void* qg, const void* k_pool,
-                  const void* v_pool, const int* page_table, const int* positions, const int* ids,
-                  const int* n_sel, void* out, int splits, void* workspace, size_t workspace_bytes,
-                  hipStream_t stream);
+int qm_qsa_attend(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool,
+                  const void* v_pool, const void* items, void* out, int splits, void* workspace,
+                  size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

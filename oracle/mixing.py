@@ -68,14 +68,24 @@ class OracleMixer:
 
     def _linear_attention(self, hidden, layer: int, cache):
         """reference/model.py:177-244."""
-        cfg = self.config
-        n_b, n_t, _ = hidden.shape
-        n_v, n_k, d = cfg.linear_num_v_heads, cfg.linear_num_k_heads, cfg.linear_head_dim
-
-        mixed = F.linear(hidden, self.bw(layer, "attn_qkv.weight")).transpose(1, 2)
-        z = F.linear(hidden, self.bw(layer, "attn_gate.weight")).reshape(n_b, n_t, -1, d)
+        mixed = F.linear(hidden, self.bw(layer, "attn_qkv.weight"))
+        z = F.linear(hidden, self.bw(layer, "attn_gate.weight"))
         b = F.linear(hidden, self.bw(layer, "ssm_beta.weight"))
         a = F.linear(hidden, self.bw(layer, "ssm_alpha.weight"))
+        out = self.dn_core(mixed, z, b, a, layer, cache)
+        return F.linear(out, self.bw(layer, "ssm_out.weight"))
+
+    def dn_core(self, mixed, z, b, a, layer: int, cache):
+        """reference/model.py:184-243 between the projections and ssm_out.
+
+        ``mixed`` [B, S, conv_dim], ``z`` [B, S, Hv*d], ``b``, ``a`` [B, S, Hv]
+        are the projection outputs; returns the gated-normed [B, S, Hv*d].
+        """
+        cfg = self.config
+        n_b, n_t, _ = mixed.shape
+        n_v, n_k, d = cfg.linear_num_v_heads, cfg.linear_num_k_heads, cfg.linear_head_dim
+        mixed = mixed.transpose(1, 2)
+        z = z.reshape(n_b, n_t, -1, d)
 
         conv_w = self.bw(layer, "ssm_conv1d.weight")
         hist = cfg.conv_kernel - 1
@@ -117,11 +127,10 @@ class OracleMixer:
         if cache is not None:
             cache[layer].recurrent_state = new_state
 
-        out = rms_norm_gated(
+        return rms_norm_gated(
             out.reshape(-1, d), z.reshape(-1, d), self.bw(layer, "ssm_norm.weight"),
             cfg.rms_norm_eps, cfg.output_gate_type,
         ).reshape(n_b, n_t, -1)
-        return F.linear(out, self.bw(layer, "ssm_out.weight"))
 
     # ------------------------------------------------------------------
     # QSA indexer, one stage at a time

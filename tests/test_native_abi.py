@@ -58,19 +58,20 @@ def test_bad_geometry_is_rejected_without_a_launch(qm):
     rc = lib.qm_dn_decode(ctypes.byref(g), *([ctypes.c_void_p(8)] * 12), ctypes.c_void_p(8), 1 << 20, None)
     assert rc in (-2, -4)
     q = n.QsaGeom(1, 16, 2, 128, 64, 4, 128, 64, 2048, 64, 4, 256, 4, n.QM_ACT_BF16, 1e-6)
-    assert lib.qm_qsa_select(ctypes.byref(q), 1, *([None] * 6), None) == -5
+    assert lib.qm_qsa_select(ctypes.byref(q), 1, *([None] * 8), None) == -5
     with pytest.raises(n.QmError, match="head_dim"):
-        n.call("qm_qsa_select", ctypes.byref(q), 1, *([None] * 6), None)
+        n.call("qm_qsa_select", ctypes.byref(q), 1, *([None] * 8), None)
 
 
 def test_workspace_sizes_are_sane(qm):
     n = qm.native
     lib = n.load()
-    assert lib.qm_dn_decode_workspace(1, 32, 128) >= 32 * 128 * 4
+    assert lib.qm_dn_decode_workspace(1, 32, 128) > 0 and lib.qm_dn_decode_workspace(0, 32, 128) == 0
     q = n.QsaGeom(1, 16, 2, 256, 64, 4, 128, 64, 2048, 64, 128, 8192, 128, n.QM_ACT_BF16, 1e-6)
-    splits = lib.qm_qsa_attend_splits(ctypes.byref(q), 8128)
-    assert splits == 32 * 2 + 3
+    splits = lib.qm_qsa_attend_splits(ctypes.byref(q), 8128, 8128)
+    assert splits == (32 * 2 + 1 + 1) // 2          # 64 block groups + 1 tail group, 2 per workgroup
     assert lib.qm_qsa_attend_workspace(ctypes.byref(q), 1, splits) >= splits * 2 * 8 * 256 * 4
+    assert lib.qm_qsa_items_stride(ctypes.byref(q)) == 1 + 64 + 3
 
 
 def test_rope_tables_bit_identical_to_reference(qm):

@@ -48,27 +48,71 @@ template <> struct Act<bf16_t> {
   __device__ __forceinline__ static float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 };
 
-// Non-contracting float ops (each rounds once, like a CPU SIMD mul/add).
-__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
-__device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
+// Non-contracting float ops: each rounds once, like a CPU SIMD mul/add. hipcc
+// compiles with -ffp-contract=fast, and __fmul_rn/__fadd_rn are plain operators,
+// so contraction is switched off inside these helpers explicitly: the fmul they
+// emit carries no `contract` flag and cannot be fused into a later add.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+// IEEE division and square root (HIP's default for float: correctly rounded)
+__device__ __forceinline__ float div_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a / b;
+}
 // correctly rounded 1/sqrt(x), as torch's CPU rsqrt computes it (sqrt, then divide)
-__device__ __forceinline__ float rsqrt_rn(float x) { return __fdiv_rn(1.0f, __fsqrt_rn(x)); }
+__device__ __forceinline__ float rsqrt_rn(float x) { return div_rn(1.0f, __builtin_sqrtf(x)); }
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 // torch.nn.functional.softplus with beta 1, threshold 20
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+// Cross-lane reductions on DPP / readlane / permlane (VALU, a few cycles each)
+// rather than __shfl_xor, whose ds_bpermute costs an LDS round trip per step
+// and serialises a reduction tree into a chain of LDS latencies.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+// sum / max over each row of 16 lanes, result in every lane of the row:
+// xor 1, xor 2 (quad_perm), then the half-row and row mirrors
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
   return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
   return v;
+}
+// v(lane) + v(lane ^ 32) and v(lane) + v(lane ^ 16), in every lane (a single
+// cross-row step each, so one ds_bpermute is cheap enough)
+__device__ __forceinline__ float xor32_sum(float v) { return v + __shfl_xor(v, 32, 64); }
+__device__ __forceinline__ float xor16_sum(float v) { return v + __shfl_xor(v, 16, 64); }
+__device__ __forceinline__ float xor32_max(float v) { return fmaxf(v, __shfl_xor(v, 32, 64)); }
+__device__ __forceinline__ float xor16_max(float v) { return fmaxf(v, __shfl_xor(v, 16, 64)); }
+// whole-wavefront sum / max, uniform result
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
 // Sum over a block of NT threads (NT a multiple of 64); `red` holds NT/64 floats.

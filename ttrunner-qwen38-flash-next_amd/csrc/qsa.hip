@@ -96,7 +96,7 @@ struct PrepArgs {
   const float* cos; const float* sin;
   const int* positions; const int* page_table;
   uint16_t* k_pool; uint16_t* v_pool; T* raw_keys; float* block_keys;
-  float* q_out; float* iq_out;
+  uint16_t* q_out; float* iq_out;
   int batch, seq, hq, hkv, rope, idx_heads, ratio, page_size, max_pages, max_ctx, max_blocks;
   float eps;
 };
@@ -120,7 +120,11 @@ __global__ __launch_bounds__(PREP_NT) void qsa_prep_kernel(PrepArgs<T> A) {
     const T* src = A.qg + ((long)row * A.hq + role) * (2 * QSA_D);
     s_x[tid] = Act<T>::load(src, tid);
     const float y = norm_rope_row<T>(s_x, s_y, s_scr, QSA_D, A.q_norm, A.eps, A.rope, cs, sn);
-    A.q_out[((long)row * A.hq + role) * QSA_D + tid] = y;
+    // the attention MFMA takes q as bf16: keep it as hi + lo so the product
+    // carries ~16 mantissa bits (rows [2 * row] hold hi, [2 * row + 1] lo)
+    const uint16_t hi = f32_to_bf16(y);
+    A.q_out[((long)(2 * row) * A.hq + role) * QSA_D + tid] = hi;
+    A.q_out[((long)(2 * row + 1) * A.hq + role) * QSA_D + tid] = f32_to_bf16(y - bf16_to_f32(hi));
     return;
   }
   if (role < A.hq + A.hkv) {
@@ -177,6 +181,7 @@ __global__ __launch_bounds__(IDX_D) void qsa_pool_kernel(PoolArgs<T> A) {
 // ---------------------------------------------------------------------------
 constexpr int SEL_NT = 256;
 constexpr int SEL_MAX_BLOCKS = 4096;    // eligible blocks one query may score
+constexpr int SEL_CHUNK = SEL_NT / 16 * 8;   // blocks scored per preloaded chunk (128)
 
 __device__ __forceinline__ unsigned long long sel_key(float s, int j) {
   unsigned u = __float_as_uint(s);
@@ -184,10 +189,15 @@ __device__ __forceinline__ unsigned long long sel_key(float s, int j) {
   return (static_cast<unsigned long long>(u) << 32) | static_cast<unsigned>(0x7fffffff - j);
 }
 
+// An attention work item: one 32-token group of one page, rows [lo, hi) visible.
+// .x = physical pool row of the group's first token (page * P + row0),
+// .y = lo | hi << 8. items[row][0].x holds the item count.
+__device__ __forceinline__ int2 make_item(int phys_row, int lo, int hi) { return make_int2(phys_row, lo | (hi << 8)); }
+
 struct SelArgs {
-  const float* iq; const float* block_keys; const int* positions;
-  int* ids; int* n_sel; float* scores_out;
-  int batch, seq, idx_heads, ratio, topk, max_blocks;
+  const float* iq; const float* block_keys; const int* positions; const int* page_table;
+  int* ids; int* n_sel; int2* items; float* scores_out;
+  int batch, seq, idx_heads, ratio, topk, max_blocks, page_size, max_pages, max_items;
 };
 
 __global__ __launch_bounds__(SEL_NT) void qsa_select_kernel(SelArgs A) {
@@ -196,148 +206,162 @@ __global__ __launch_bounds__(SEL_NT) void qsa_select_kernel(SelArgs A) {
   const int p = A.positions[b] + s;
   const int tid = threadIdx.x;
   const int n_elig = min((p + 1) / A.ratio, A.max_blocks);
+  const int n_sel = min(n_elig, A.topk);
   int* out_ids = A.ids + (long)row * A.topk;
 
   __shared__ float s_q[4 * IDX_D];
   __shared__ unsigned long long s_key[SEL_MAX_BLOCKS];
+  __shared__ int s_pages[SEL_MAX_BLOCKS];
+  __shared__ int s_sel[SEL_MAX_BLOCKS / 2];
 
-  if (A.scores_out) {
+  // the page-table row, needed to describe the attention items, comes in with the keys
+  const int n_lpages = min(A.max_pages, (p + A.page_size) / A.page_size);
+  if (A.items)
+    for (int i = tid; i < n_lpages; i += SEL_NT) s_pages[i] = A.page_table[(long)b * A.max_pages + i];
+  if (A.scores_out)
     for (int j = tid; j < A.max_blocks; j += SEL_NT)
       if (j >= n_elig) A.scores_out[(long)row * A.max_blocks + j] = -INFINITY;
-  }
-  if (n_elig <= A.topk && !A.scores_out) {
-    for (int i = tid; i < n_elig; i += SEL_NT) out_ids[i] = i;
-    if (tid == 0) A.n_sel[row] = n_elig;
-    return;
-  }
-  for (int i = tid; i < A.idx_heads * IDX_D; i += SEL_NT) s_q[i] = A.iq[(long)row * A.idx_heads * IDX_D + i];
-  __syncthreads();
 
-  // 16 lanes per block, 8 channels each
-  const int sub = tid & 15, grp = tid >> 4;
-  const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
-  for (int j0 = 0; j0 < n_elig; j0 += SEL_NT / 16) {
-    const int j = j0 + grp;
-    float dots[4] = {0.f, 0.f, 0.f, 0.f};
-    if (j < n_elig) {
-      const float4* kr = reinterpret_cast<const float4*>(bk + (long)j * IDX_D + sub * 8);
-      const float4 k0 = kr[0], k1 = kr[1];
-      const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-      for (int h = 0; h < A.idx_heads; ++h) {
-        const float* qh = s_q + h * IDX_D + sub * 8;
-        float acc = 0.f;
+  const bool score = n_elig > A.topk || A.scores_out;
+  if (score) {
+    for (int i = tid; i < 4 * IDX_D; i += SEL_NT)
+      s_q[i] = i < A.idx_heads * IDX_D ? A.iq[(long)row * A.idx_heads * IDX_D + i] : 0.f;
+    // 16 lanes per block, 8 channels each; a chunk of 128 blocks is loaded
+    // before any of it is used so the loads overlap
+    const int sub = tid & 15, grp = tid >> 4;
+    const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
+    for (int c0 = 0; c0 < n_elig; c0 += SEL_CHUNK) {
+      float4 kb[8][2];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc = fmaf(qh[e], kv[e], acc);
-        dots[h] = acc;
+      for (int i = 0; i < 8; ++i) {
+        const int j = c0 + grp + 16 * i;
+        if (j < n_elig) {
+          const float4* kr = reinterpret_cast<const float4*>(bk + (long)j * IDX_D + sub * 8);
+          kb[i][0] = kr[0];
+          kb[i][1] = kr[1];
+        } else {
+          kb[i][0] = kb[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+      __syncthreads();    // s_q visible
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int j = c0 + grp + 16 * i;
+        const float kv[8] = {kb[i][0].x, kb[i][0].y, kb[i][0].z, kb[i][0].w,
+                             kb[i][1].x, kb[i][1].y, kb[i][1].z, kb[i][1].w};
+        float dots[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {        // s_q rows past idx_heads are zero
+          const float* qh = s_q + h * IDX_D + sub * 8;
+          float acc = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc = fmaf(qh[e], kv[e], acc);
+          dots[h] = row16_sum(acc);
+        }
+        if (sub == 0 && j < n_elig) {
+          float sc = 0.f;
+#pragma unroll
+          for (int h = 0; h < 4; ++h)
+            if (h < A.idx_heads) sc = add_rn(sc, fmaxf(dots[h], 0.f));
+          sc = div_rn(sc, 11.313708498984761f);     // sqrt(128)
+          if (A.scores_out) A.scores_out[(long)row * A.max_blocks + j] = sc;
+          s_key[j] = sel_key(sc, j);
+        }
       }
     }
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1)
-#pragma unroll
-      for (int h = 0; h < 4; ++h) dots[h] += __shfl_xor(dots[h], off, 64);
-    if (sub == 0 && j < n_elig) {
-      float sc = 0.f;
-      for (int h = 0; h < A.idx_heads; ++h) sc = add_rn(sc, fmaxf(dots[h], 0.f));
-      sc = div_rn(sc, 11.313708498984761f);     // sqrt(128)
-      if (A.scores_out) A.scores_out[(long)row * A.max_blocks + j] = sc;
-      s_key[j] = sel_key(sc, j);
-    }
-  }
-  if (n_elig <= A.topk) {
-    for (int i = tid; i < n_elig; i += SEL_NT) out_ids[i] = i;
-    if (tid == 0) A.n_sel[row] = n_elig;
-    return;
   }
   __syncthreads();
-  // rank by counting: keys are distinct, rank = number of larger keys
-  for (int j = tid; j < n_elig; j += SEL_NT) {
-    const unsigned long long kj = s_key[j];
-    int rank = 0;
-    for (int i = 0; i < n_elig; ++i) rank += s_key[i] > kj ? 1 : 0;
-    if (rank < A.topk) out_ids[rank] = j;
+  if (n_elig <= A.topk) {
+    for (int i = tid; i < n_elig; i += SEL_NT) { out_ids[i] = i; s_sel[i] = i; }
+  } else {
+    // rank by counting: keys are distinct, rank = number of larger keys
+    // (keys past n_elig are padded with 0, which no real key is below)
+    for (int j = n_elig + tid; j < ((n_elig + 15) & ~15); j += SEL_NT) s_key[j] = 0ull;
+    __syncthreads();
+    for (int j = tid; j < n_elig; j += SEL_NT) {
+      const unsigned long long kj = s_key[j];
+      int rank = 0;
+      for (int i = 0; i < n_elig; i += 16) {
+        unsigned long long k16[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) k16[u] = s_key[i + u];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) rank += k16[u] > kj ? 1 : 0;
+      }
+      if (rank < A.topk) { out_ids[rank] = j; s_sel[rank] = j; }
+    }
   }
-  if (tid == 0) A.n_sel[row] = A.topk;
+  if (tid == 0) A.n_sel[row] = n_sel;
+  if (!A.items) return;
+  __syncthreads();
+  // attention items: the groups of every selected block in rank order, then the tail's
+  int2* items = A.items + (long)row * A.max_items;
+  const int gpb = A.ratio >= 32 ? A.ratio / 32 : 1;
+  const int n_blk_items = n_sel * gpb;
+  const int ts = ((p + 1) / A.ratio) * A.ratio;
+  const int n_tail = ts > p ? 0 : (p >> 5) - (ts >> 5) + 1;
+  const int n_items = n_blk_items + n_tail;
+  for (int it = tid; it < n_items; it += SEL_NT) {
+    int t0, lo, hi;
+    if (it < n_blk_items) {
+      const int bs = s_sel[it / gpb] * A.ratio;
+      if (A.ratio >= 32) { t0 = bs + (it % gpb) * 32; lo = 0; hi = 32; }
+      else { t0 = bs & ~31; lo = bs - t0; hi = lo + A.ratio; }
+    } else {
+      t0 = (ts & ~31) + (it - n_blk_items) * 32;
+      lo = max(ts - t0, 0);
+      hi = min(p + 1 - t0, 32);
+    }
+    const int page = s_pages[t0 / A.page_size];
+    items[1 + it] = make_item(page * A.page_size + t0 % A.page_size, lo, hi);
+  }
+  if (tid == 0) items[0] = make_int2(n_items, 0);
 }
 
 // ---------------------------------------------------------------------------
 // decode attention
 // ---------------------------------------------------------------------------
 constexpr int GQA = 8;          // query heads per kv head this kernel handles
+constexpr int ATT_WAVES = 2;    // waves (one 32-token item each) per workgroup
 
 struct AttnArgs {
-  const float* q; const uint16_t* k_pool; const uint16_t* v_pool;
-  const int* page_table; const int* positions; const int* ids; const int* n_sel;
+  const uint16_t* q; const uint16_t* k_pool; const uint16_t* v_pool;
+  const int2* items;
   float* part_o; float* part_ml;
-  int batch, seq, hq, hkv, ratio, page_size, max_pages, topk, splits;
+  int batch, seq, hq, hkv, page_size, max_items, splits;
   float scale;
 };
-
-// logical 32-token groups a query attends: selected blocks (in rank order),
-// then the groups of its tail block
-__device__ __forceinline__ int groups_per_block(int ratio) { return ratio >= 32 ? ratio / 32 : 1; }
-
-__device__ __forceinline__ void item_range(const AttnArgs& A, int row, int item, int nsel_b, int p, int* t0,
-                                           int* lo, int* hi) {
-  const int gpb = groups_per_block(A.ratio);
-  const int n_blk_items = nsel_b * gpb;
-  if (item < n_blk_items) {
-    const int j = A.ids[(long)row * A.topk + item / gpb];
-    if (j < 0 || (long)(j + 1) * A.ratio > (long)p + 1) {   // not an eligible block: skip, never address it
-      *t0 = -1; *lo = *hi = 0;
-      return;
-    }
-    const int bs = j * A.ratio;
-    if (A.ratio >= 32) {
-      *t0 = bs + (item % gpb) * 32; *lo = 0; *hi = 32;
-    } else {
-      *t0 = bs & ~31; *lo = bs - *t0; *hi = *lo + A.ratio;
-    }
-    return;
-  }
-  const int ts = ((p + 1) / A.ratio) * A.ratio;
-  const int g0 = ts & ~31;
-  *t0 = g0 + (item - n_blk_items) * 32;
-  *lo = max(ts - *t0, 0);
-  *hi = min(p + 1 - *t0, 32);
-}
-
-__device__ __forceinline__ int n_items_for(const AttnArgs& A, int nsel_b, int p) {
-  const int ts = ((p + 1) / A.ratio) * A.ratio;
-  const int tail = ts > p ? 0 : (p >> 5) - (ts >> 5) + 1;
-  return nsel_b * groups_per_block(A.ratio) + tail;
-}
 
 __device__ __forceinline__ bf16x8_t load_bf16x8(const uint16_t* p) {
   return *reinterpret_cast<const bf16x8_t*>(p);
 }
 
-__global__ __launch_bounds__(64) void qsa_attend_kernel(AttnArgs A) {
+// split s of (row, kv head g) handles items [s*W, s*W + W), one per wave; the
+// waves merge their (max, sum, output) in LDS and write one partial
+__global__ __launch_bounds__(64 * ATT_WAVES) void qsa_attend_kernel(AttnArgs A) {
   const int split = blockIdx.x, g = blockIdx.y, row = blockIdx.z;   // row = b * seq + s
-  const int b = row / A.seq;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int col = lane & 15;        // query head within the group (8..15 are padding)
   const int quad = lane >> 4;       // which 8-wide k slice / 4-row output slice
-  const int p = A.positions[b] + row % A.seq;
-  const int nsel_b = A.n_sel[row];
-  const int n_items = n_items_for(A, nsel_b, p);
-  const int per = (n_items + A.splits - 1) / A.splits;
-  const int it0 = split * per, it1 = min(n_items, it0 + per);
+  const int2* items = A.items + (long)row * A.max_items;
+  const int item = split * ATT_WAVES + wv;
 
-  // query fragments (B operand of S^T = K Q^T): hi and lo bf16 parts of
-  // q[head col][32 s + 8 quad .. +8]
+  __shared__ float s_m[ATT_WAVES][GQA], s_l[ATT_WAVES][GQA];
+  __shared__ float s_acc[ATT_WAVES][GQA][QSA_D];
+
+  // the item descriptor and the query are independent loads
+  const int n_items = items[0].x;
+  const int2 desc = items[1 + min(item, A.max_items - 2)];
   bf16x8_t qhi[8], qlo[8];
   {
-    const float* qrow = A.q + ((long)row * A.hq + g * GQA + (col < GQA ? col : 0)) * QSA_D;
+    const int hq = g * GQA + (col < GQA ? col : 0);
+    const uint16_t* qh = A.q + ((long)(2 * row) * A.hq + hq) * QSA_D + 8 * quad;
+    const uint16_t* ql = A.q + ((long)(2 * row + 1) * A.hq + hq) * QSA_D + 8 * quad;
+    const bf16x8_t zero = {};
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = col < GQA ? qrow[32 * s + 8 * quad + e] : 0.f;
-        const uint16_t hb = f32_to_bf16(x);
-        const float rem = x - bf16_to_f32(hb);
-        qhi[s][e] = __builtin_bit_cast(__bf16, hb);
-        qlo[s][e] = __builtin_bit_cast(__bf16, f32_to_bf16(rem));
-      }
+    for (int sk = 0; sk < 8; ++sk) {
+      qhi[sk] = col < GQA ? load_bf16x8(qh + 32 * sk) : zero;
+      qlo[sk] = col < GQA ? load_bf16x8(ql + 32 * sk) : zero;
     }
   }
 
@@ -346,21 +370,16 @@ __global__ __launch_bounds__(64) void qsa_attend_kernel(AttnArgs A) {
   for (int i = 0; i < 16; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  for (int item = it0; item < it1; ++item) {
-    int t0, lo, hi;
-    item_range(A, row, item, nsel_b, p, &t0, &lo, &hi);
-    if (t0 < 0) continue;
-    const int page = A.page_table[(long)b * A.max_pages + t0 / A.page_size];
-    const int row0 = t0 % A.page_size;
+  if (item < n_items) {
+    const int page = desc.x / A.page_size, row0 = desc.x % A.page_size;
+    const int lo = desc.y & 0xff, hi = desc.y >> 8;
     const uint16_t* kp = A.k_pool + (((long)page * A.hkv + g) * A.page_size + row0) * QSA_D;
     const uint16_t* vp = A.v_pool + ((long)page * A.hkv + g) * QSA_D * A.page_size + row0;
-
-    // issue every K and V load of the group up front
     bf16x8_t kf[2][8], vf[16];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int s = 0; s < 8; ++s) kf[t][s] = load_bf16x8(kp + (16 * t + col) * QSA_D + 32 * s + 8 * quad);
+      for (int sk = 0; sk < 8; ++sk) kf[t][sk] = load_bf16x8(kp + (16 * t + col) * QSA_D + 32 * sk + 8 * quad);
 #pragma unroll
     for (int db = 0; db < 16; ++db) vf[db] = load_bf16x8(vp + (long)(16 * db + col) * A.page_size + 8 * quad);
 
@@ -370,9 +389,9 @@ __global__ __launch_bounds__(64) void qsa_attend_kernel(AttnArgs A) {
     for (int t = 0; t < 2; ++t) {
       f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][s], qhi[s], c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][s], qlo[s], c, 0, 0, 0);
+      for (int sk = 0; sk < 8; ++sk) {
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][sk], qhi[sk], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][sk], qlo[sk], c, 0, 0, 0);
       }
       sc[t] = c;
     }
@@ -386,43 +405,56 @@ __global__ __launch_bounds__(64) void qsa_attend_kernel(AttnArgs A) {
         sc[t][v] = x;
         mx = fmaxf(mx, x);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __expf(m_run - m_new);
-    float psum = 0.f;
+    mx = xor32_max(xor16_max(mx));
+    m_run = mx;
     bf16x8_t pf;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float pv = __expf(sc[t][v] - m_new);
-        psum += pv;
+        const float pv = __expf(sc[t][v] - m_run);
+        l_run += pv;
         pf[4 * t + v] = __builtin_bit_cast(__bf16, f32_to_bf16(pv));
       }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
     // O^T[d][head] += V^T[d][tok] P^T[tok][head]
 #pragma unroll
-    for (int db = 0; db < 16; ++db) {
-      acc[db] *= alpha;
-      acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[db], pf, acc[db], 0, 0, 0);
-    }
+    for (int db = 0; db < 16; ++db) acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[db], pf, acc[db], 0, 0, 0);
   }
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run = xor32_sum(xor16_sum(l_run));
 
-  const long pbase = (((long)row * A.hkv + g) * A.splits + split) * GQA;
+  // merge the workgroup's waves
+  if (quad == 0 && col < GQA) { s_m[wv][col] = m_run; s_l[wv][col] = l_run; }
+  __syncthreads();
+  float M = -INFINITY;
   if (col < GQA) {
-    float* po = A.part_o + (pbase + col) * QSA_D;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w) M = fmaxf(M, s_m[w][col]);
+  }
+  const float wself = (col < GQA && m_run != -INFINITY) ? __expf(m_run - M) : 0.f;
+  if (col < GQA) {
 #pragma unroll
     for (int db = 0; db < 16; ++db)
-      *reinterpret_cast<float4*>(po + 16 * db + 4 * quad) =
-          make_float4(acc[db][0], acc[db][1], acc[db][2], acc[db][3]);
-    if (quad == 0) {
-      A.part_ml[(pbase + col) * 2 + 0] = m_run;
-      A.part_ml[(pbase + col) * 2 + 1] = l_run;
-    }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) s_acc[wv][col][16 * db + 4 * quad + v] = acc[db][v] * wself;
+  }
+  __syncthreads();
+  const long pbase = (((long)row * A.hkv + g) * A.splits + split) * GQA;
+  for (int i = threadIdx.x; i < GQA * QSA_D; i += 64 * ATT_WAVES) {
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w) o += s_acc[w][i / QSA_D][i % QSA_D];
+    A.part_o[pbase * QSA_D + i] = o;
+  }
+  if (threadIdx.x < GQA) {
+    const int hh = threadIdx.x;
+    float Mh = -INFINITY, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w) Mh = fmaxf(Mh, s_m[w][hh]);
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w)
+      if (s_m[w][hh] != -INFINITY) L += s_l[w][hh] * __expf(s_m[w][hh] - Mh);
+    A.part_ml[(pbase + hh) * 2 + 0] = Mh;
+    A.part_ml[(pbase + hh) * 2 + 1] = L;
   }
 }
 
@@ -432,26 +464,49 @@ struct CombineArgs {
   int hq, hkv, splits;
 };
 
+constexpr int MAX_SPLITS = 1024;
+
 template <typename T>
 __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T> A) {
-  const int hq = blockIdx.x, b = blockIdx.y;
+  const int hq = blockIdx.x, row = blockIdx.y;
   const int d = threadIdx.x;
   const int g = hq / GQA, hh = hq % GQA;
-  const long base = (((long)b * A.hkv + g) * A.splits) * GQA + hh;
-  float M = -INFINITY;
-  for (int s = 0; s < A.splits; ++s) M = fmaxf(M, A.part_ml[(base + (long)s * GQA) * 2]);
-  float L = 0.f, o = 0.f;
-  for (int s = 0; s < A.splits; ++s) {
-    const long ps = base + (long)s * GQA;
-    const float m = A.part_ml[ps * 2];
-    const float w = m == -INFINITY ? 0.f : __expf(m - M);
-    L += A.part_ml[ps * 2 + 1] * w;
-    o += A.part_o[ps * QSA_D + d] * w;
+  const long base = (((long)row * A.hkv + g) * A.splits) * GQA + hh;
+  __shared__ float s_w[MAX_SPLITS];
+  __shared__ float s_red[QSA_D / 64];
+  const float gate = Act<T>::load(A.qg, ((long)row * A.hq + hq) * (2 * QSA_D) + QSA_D + d);
+  // every split's (max, sum) in parallel, then the weights in LDS
+  float m = -INFINITY, l = 0.f;
+  for (int s = d; s < A.splits; s += QSA_D) {
+    const float ms = A.part_ml[(base + (long)s * GQA) * 2];
+    m = fmaxf(m, ms);
+    s_w[s] = ms;
   }
+  m = wave_max(m);
+  if ((d & 63) == 0) s_red[d >> 6] = m;
+  __syncthreads();
+  float M = s_red[0];
+#pragma unroll
+  for (int i = 1; i < QSA_D / 64; ++i) M = fmaxf(M, s_red[i]);
+  for (int s = d; s < A.splits; s += QSA_D) {
+    const float ms = s_w[s];
+    const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
+    l += A.part_ml[(base + (long)s * GQA) * 2 + 1] * w;
+    s_w[s] = w;
+  }
+  l = wave_sum(l);
+  __syncthreads();
+  if ((d & 63) == 0) s_red[d >> 6] = l;
+  __syncthreads();
+  float L = 0.f;
+#pragma unroll
+  for (int i = 0; i < QSA_D / 64; ++i) L += s_red[i];
+  float o = 0.f;
+#pragma unroll 8
+  for (int s = 0; s < A.splits; ++s) o += A.part_o[(base + (long)s * GQA) * QSA_D + d] * s_w[s];
   const float att = Act<T>::round(o / L);
-  const float gate = Act<T>::load(A.qg, ((long)b * A.hq + hq) * (2 * QSA_D) + QSA_D + d);
   const float sg = Act<T>::round(sigmoid_f(gate));
-  Act<T>::store(A.out, ((long)b * A.hq + hq) * QSA_D + d, att * sg);
+  Act<T>::store(A.out, ((long)row * A.hq + hq) * QSA_D + d, att * sg);
 }
 
 int check_geom(const qm_qsa_geom* g, const char* who) {
@@ -478,14 +533,15 @@ template <typename T>
 int launch_prep(const qm_qsa_geom* g, int seq, const void* qg, const void* k_new, const void* v_new, const void* iq,
                 const void* ik, const float* q_norm, const float* k_norm, const float* iq_norm, const float* ik_norm,
                 const float* cos, const float* sin, const int* positions, const int* page_table, void* k_pool,
-                void* v_pool, void* raw_keys, float* block_keys, float* q_out, float* iq_out, hipStream_t stream) {
+                void* v_pool, void* raw_keys, float* block_keys, void* q_out, float* iq_out, hipStream_t stream) {
   PrepArgs<T> A;
   A.qg = static_cast<const T*>(qg); A.k_new = static_cast<const T*>(k_new); A.v_new = static_cast<const T*>(v_new);
   A.iq = static_cast<const T*>(iq); A.ik = static_cast<const T*>(ik);
   A.q_norm = q_norm; A.k_norm = k_norm; A.iq_norm = iq_norm; A.ik_norm = ik_norm;
   A.cos = cos; A.sin = sin; A.positions = positions; A.page_table = page_table;
   A.k_pool = static_cast<uint16_t*>(k_pool); A.v_pool = static_cast<uint16_t*>(v_pool);
-  A.raw_keys = static_cast<T*>(raw_keys); A.block_keys = block_keys; A.q_out = q_out; A.iq_out = iq_out;
+  A.raw_keys = static_cast<T*>(raw_keys); A.block_keys = block_keys; A.q_out = static_cast<uint16_t*>(q_out);
+  A.iq_out = iq_out;
   A.batch = g->batch; A.seq = seq; A.hq = g->n_heads; A.hkv = g->n_kv_heads; A.rope = g->rope_dim;
   A.idx_heads = g->idx_heads; A.ratio = g->ratio; A.page_size = g->page_size; A.max_pages = g->max_pages;
   A.max_ctx = g->max_ctx; A.max_blocks = g->max_blocks; A.eps = g->eps;
@@ -499,6 +555,13 @@ size_t part_o_bytes(const qm_qsa_geom* g, int rows, int splits) {
   return qm_align256((size_t)rows * g->n_kv_heads * splits * GQA * QSA_D * sizeof(float));
 }
 
+// int2 entries per query row of the item table: a header, every group of the
+// top-k blocks, and the tail's groups
+int item_stride(const qm_qsa_geom* g) {
+  const int gpb = g->ratio >= 32 ? g->ratio / 32 : 1;
+  return 1 + (g->budget / g->ratio) * gpb + (g->ratio + 31) / 32 + 1;
+}
+
 }  // namespace
 
 extern "C" int qm_v_slot(int row) { return v_slot(row); }
@@ -507,7 +570,7 @@ extern "C" int qm_qsa_prep(const qm_qsa_geom* g, int seq, const void* qg, const 
                            const void* iq, const void* ik, const float* q_norm, const float* k_norm,
                            const float* iq_norm, const float* ik_norm, const float* cos, const float* sin,
                            const int* positions, const int* page_table, void* k_pool, void* v_pool, void* raw_keys,
-                           float* block_keys, float* q_out, float* iq_out, hipStream_t stream) {
+                           float* block_keys, void* q_out, float* iq_out, hipStream_t stream) {
   int rc = check_geom(g, "qm_qsa_prep: null geometry");
   if (rc) return rc;
   if (seq <= 0) return qm_fail(QM_ERR_ARG, "qm_qsa_prep: seq must be positive");
@@ -523,31 +586,57 @@ extern "C" int qm_qsa_prep(const qm_qsa_geom* g, int seq, const void* qg, const 
                              page_table, k_pool, v_pool, raw_keys, block_keys, q_out, iq_out, stream);
 }
 
+extern "C" int qm_qsa_items_stride(const qm_qsa_geom* g) {
+  if (!g || g->ratio <= 0 || g->budget < g->ratio) return 0;
+  return item_stride(g);
+}
+
 extern "C" int qm_qsa_select(const qm_qsa_geom* g, int seq, const float* iq, const float* block_keys,
-                             const int* positions, int* ids, int* n_sel, float* scores_out, hipStream_t stream) {
+                             const int* positions, const int* page_table, int* ids, int* n_sel, void* items,
+                             float* scores_out, hipStream_t stream) {
   int rc = check_geom(g, "qm_qsa_select: null geometry");
   if (rc) return rc;
   if (seq <= 0) return qm_fail(QM_ERR_ARG, "qm_qsa_select: seq must be positive");
   if (!iq || !block_keys || !positions || !ids || !n_sel) return qm_fail(QM_ERR_ARG, "qm_qsa_select: null pointer");
-  if (g->max_blocks > SEL_MAX_BLOCKS) return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_select: more than 4096 blocks");
+  if (items && !page_table) return qm_fail(QM_ERR_ARG, "qm_qsa_select: items need the page table");
+  if (g->max_blocks > SEL_MAX_BLOCKS || g->max_pages > SEL_MAX_BLOCKS || g->budget / g->ratio > SEL_MAX_BLOCKS / 2)
+    return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_select: more than 4096 blocks or pages");
   SelArgs A;
-  A.iq = iq; A.block_keys = block_keys; A.positions = positions; A.ids = ids; A.n_sel = n_sel;
-  A.scores_out = scores_out; A.batch = g->batch; A.seq = seq; A.idx_heads = g->idx_heads; A.ratio = g->ratio;
-  A.topk = g->budget / g->ratio; A.max_blocks = g->max_blocks;
+  A.iq = iq; A.block_keys = block_keys; A.positions = positions; A.page_table = page_table;
+  A.ids = ids; A.n_sel = n_sel; A.items = static_cast<int2*>(items); A.scores_out = scores_out;
+  A.batch = g->batch; A.seq = seq; A.idx_heads = g->idx_heads; A.ratio = g->ratio;
+  A.topk = g->budget / g->ratio; A.max_blocks = g->max_blocks; A.page_size = g->page_size;
+  A.max_pages = g->max_pages; A.max_items = item_stride(g);
   hipLaunchKernelGGL(qsa_select_kernel, dim3(g->batch * seq), dim3(SEL_NT), 0, stream, A);
   QM_CHECK_LAUNCH();
   return QM_OK;
 }
 
-extern "C" int qm_qsa_attend_splits(const qm_qsa_geom* g, int max_position) {
-  if (!g || g->ratio <= 0) return 1;
+namespace {
+int items_at(const qm_qsa_geom* g, int p) {
   const int gpb = g->ratio >= 32 ? g->ratio / 32 : 1;
   const int topk = g->budget / g->ratio;
-  const int n_elig = (max_position + 1) / g->ratio;
+  const int n_elig = (p + 1) / g->ratio;
   const int sel = n_elig < topk ? n_elig : topk;
-  const int tail_groups = (g->ratio + 31) / 32 + 1;
-  int items = sel * gpb + tail_groups;
-  return items < 1 ? 1 : items;
+  const int ts = ((p + 1) / g->ratio) * g->ratio;
+  const int tail = ts > p ? 0 : (p >> 5) - (ts >> 5) + 1;
+  return sel * gpb + tail;
+}
+}  // namespace
+
+extern "C" int qm_qsa_attend_splits(const qm_qsa_geom* g, int first_position, int last_position) {
+  if (!g || g->ratio <= 0 || g->budget < g->ratio || first_position < 0 || last_position < first_position) return 1;
+  int items = 0;
+  if (last_position - first_position > 4 * g->ratio) {
+    items = item_stride(g) - 1;   // every row of a long range reaches the bound
+  } else {
+    for (int p = first_position; p <= last_position; ++p) {
+      const int n = items_at(g, p);
+      items = n > items ? n : items;
+    }
+  }
+  const int splits = (items + ATT_WAVES - 1) / ATT_WAVES;
+  return splits < 1 ? 1 : splits;
 }
 
 extern "C" size_t qm_qsa_attend_workspace(const qm_qsa_geom* g, int seq, int splits) {
@@ -556,27 +645,26 @@ extern "C" size_t qm_qsa_attend_workspace(const qm_qsa_geom* g, int seq, int spl
   return part_o_bytes(g, rows, splits) + qm_align256((size_t)rows * g->n_kv_heads * splits * GQA * 2 * sizeof(float));
 }
 
-extern "C" int qm_qsa_attend(const qm_qsa_geom* g, int seq, const float* q, const void* qg, const void* k_pool,
-                             const void* v_pool, const int* page_table, const int* positions, const int* ids,
-                             const int* n_sel, void* out, int splits, void* workspace, size_t workspace_bytes,
-                             hipStream_t stream) {
+extern "C" int qm_qsa_attend(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool,
+                             const void* v_pool, const void* items, void* out, int splits, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream) {
   int rc = check_geom(g, "qm_qsa_attend: null geometry");
   if (rc) return rc;
-  if (!q || !qg || !k_pool || !v_pool || !page_table || !positions || !ids || !n_sel || !out)
-    return qm_fail(QM_ERR_ARG, "qm_qsa_attend: null pointer");
-  if (splits <= 0 || splits > 65535) return qm_fail(QM_ERR_ARG, "qm_qsa_attend: bad split count");
+  if (!q || !qg || !k_pool || !v_pool || !items || !out) return qm_fail(QM_ERR_ARG, "qm_qsa_attend: null pointer");
+  if (splits <= 0 || splits > MAX_SPLITS) return qm_fail(QM_ERR_ARG, "qm_qsa_attend: bad split count");
   if (seq <= 0 || (long)g->batch * seq > 65535) return qm_fail(QM_ERR_ARG, "qm_qsa_attend: bad seq");
   if (!workspace || workspace_bytes < qm_qsa_attend_workspace(g, seq, splits))
     return qm_fail(QM_ERR_WORKSPACE, "qm_qsa_attend: workspace too small");
   AttnArgs A;
-  A.q = q; A.k_pool = static_cast<const uint16_t*>(k_pool); A.v_pool = static_cast<const uint16_t*>(v_pool);
-  A.page_table = page_table; A.positions = positions; A.ids = ids; A.n_sel = n_sel;
+  A.q = static_cast<const uint16_t*>(q); A.k_pool = static_cast<const uint16_t*>(k_pool);
+  A.v_pool = static_cast<const uint16_t*>(v_pool); A.items = static_cast<const int2*>(items);
   A.part_o = static_cast<float*>(workspace);
   A.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_o_bytes(g, g->batch * seq, splits));
-  A.batch = g->batch; A.seq = seq; A.hq = g->n_heads; A.hkv = g->n_kv_heads; A.ratio = g->ratio; A.page_size = g->page_size;
-  A.max_pages = g->max_pages; A.topk = g->budget / g->ratio; A.splits = splits;
+  A.batch = g->batch; A.seq = seq; A.hq = g->n_heads; A.hkv = g->n_kv_heads; A.page_size = g->page_size;
+  A.max_items = item_stride(g); A.splits = splits;
   A.scale = 1.0f / 16.0f;   // 1/sqrt(256), exact
-  hipLaunchKernelGGL(qsa_attend_kernel, dim3(splits, g->n_kv_heads, g->batch * seq), dim3(64), 0, stream, A);
+  hipLaunchKernelGGL(qsa_attend_kernel, dim3(splits, g->n_kv_heads, g->batch * seq), dim3(64 * ATT_WAVES), 0, stream,
+                     A);
   QM_CHECK_LAUNCH();
   if (g->act_dtype == QM_ACT_F32) {
     CombineArgs<float> C{A.part_o, A.part_ml, static_cast<const float*>(qg), static_cast<float*>(out), g->n_heads,

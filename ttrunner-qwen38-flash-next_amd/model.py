@@ -182,7 +182,7 @@ class Qwen4MixModel:
         stream = native.stream_handle(self.device)
         self._sync_blocks(lc, g, cos_t, sin_t, query_offset, layer)
         pos = self._positions(batch, query_offset)
-        q_out = torch.empty(batch, seq, c.num_attention_heads, c.head_dim, dtype=torch.float32, device=self.device) \
+        q_out = torch.empty(batch, seq, 2, c.num_attention_heads, c.head_dim, dtype=torch.bfloat16, device=self.device) \
             if qg is not None else None
         iq_out = torch.empty(batch, seq, c.indexer_heads, c.indexer_head_dim, dtype=torch.float32, device=self.device)
         native.call("qm_qsa_prep", ctypes.byref(g), seq, native.ptr(qg), native.ptr(k), native.ptr(v),
@@ -196,21 +196,24 @@ class Qwen4MixModel:
         lc.blocks_valid = max(lc.blocks_valid, (query_offset + seq) // c.indexer_compress_ratio)
         if k is not None:
             lc.n_tokens = query_offset + seq
+        lib = native.load()
         ids = torch.empty(batch, seq, c.block_topk, dtype=torch.int32, device=self.device)
         n_sel = torch.empty(batch, seq, dtype=torch.int32, device=self.device)
+        items = torch.empty(batch, seq, 2 * lib.qm_qsa_items_stride(ctypes.byref(g)), dtype=torch.int32,
+                            device=self.device) if attend else None
         native.call("qm_qsa_select", ctypes.byref(g), seq, native.ptr(iq_out), native.ptr(lc.block_keys),
-                    native.ptr(pos), native.ptr(ids), native.ptr(n_sel), None, stream)
+                    native.ptr(pos), native.ptr(lc.page_table), native.ptr(ids), native.ptr(n_sel),
+                    native.ptr(items), None, stream)
         lc.last_ids, lc.last_n_sel, lc.last_iq, lc.last_q = ids, n_sel, iq_out, q_out
         if not attend:
             return None
-        lib = native.load()
-        splits = lib.qm_qsa_attend_splits(ctypes.byref(g), query_offset + seq - 1)
+        splits = lib.qm_qsa_attend_splits(ctypes.byref(g), query_offset, query_offset + seq - 1)
         ws = self._workspace("qsa_attend", lib.qm_qsa_attend_workspace(ctypes.byref(g), seq, splits))
         if out is None:
             out = torch.empty(batch, seq, c.num_attention_heads * c.head_dim, dtype=dt, device=self.device)
         native.call("qm_qsa_attend", ctypes.byref(g), seq, native.ptr(q_out), native.ptr(qg), native.ptr(lc.k_pool),
-                    native.ptr(lc.v_pool), native.ptr(lc.page_table), native.ptr(pos), native.ptr(ids),
-                    native.ptr(n_sel), native.ptr(out), splits, native.ptr(ws), ws.numel(), stream)
+                    native.ptr(lc.v_pool), native.ptr(items), native.ptr(out), splits, native.ptr(ws), ws.numel(),
+                    stream)
         return out
 
     def _full_attention(self, hidden, layer: int, cos, sin, cache, query_offset: int) -> torch.Tensor:

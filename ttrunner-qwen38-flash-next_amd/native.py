@@ -48,11 +48,11 @@ SIGNATURES = {
     "qm_dn_chunked": (_i, [_i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "qm_v_slot": (_i, [_i]),
     "qm_qsa_prep": (_i, [ctypes.POINTER(QsaGeom), _i] + [_vp] * 19 + [_vp]),
-    "qm_qsa_select": (_i, [ctypes.POINTER(QsaGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "qm_qsa_items_stride": (_i, [ctypes.POINTER(QsaGeom)]),
+    "qm_qsa_select": (_i, [ctypes.POINTER(QsaGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "qm_qsa_attend_workspace": (_sz, [ctypes.POINTER(QsaGeom), _i, _i]),
-    "qm_qsa_attend_splits": (_i, [ctypes.POINTER(QsaGeom), _i]),
-    "qm_qsa_attend": (_i, [ctypes.POINTER(QsaGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
-                           _sz, _vp]),
+    "qm_qsa_attend_splits": (_i, [ctypes.POINTER(QsaGeom), _i, _i]),
+    "qm_qsa_attend": (_i, [ctypes.POINTER(QsaGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _sz, _vp]),
     "qm_qsa_pool_blocks": (_i, [ctypes.POINTER(QsaGeom), _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "qm_dn_prefill_workspace": (_sz, [ctypes.POINTER(DnGeom), _i]),
     "qm_dn_prefill": (_i, [ctypes.POINTER(DnGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

@@ -149,19 +149,13 @@ def time_kernels(instances, reps, stream_obj):
     import torch
     n = len(instances)
     s = stream_obj.cuda_stream
-    parts = {"qsa_prep": lambda x: x.qsa.prep(x.qg, x.k, x.v, x.iq, x.ik, s),
-             "qsa_select": lambda x: x.qsa.select(s),
-             "qsa_attend": lambda x: x.qsa.attend(x.qg, s),
+    parts = {"qsa_decode": lambda x: x.qsa.decode(x.qg, x.k, x.v, x.iq, x.ik, s),
              "dn_decode": lambda x: x.dn.run(x.qkv, x.z, x.a, x.b, s)}
     out = {}
     for name, fn in parts.items():
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
         for i in range(reps):
             x = instances[i % n]
-            if name in ("qsa_select", "qsa_attend"):
-                x.qsa.prep(x.qg, x.k, x.v, x.iq, x.ik, s)
-                if name == "qsa_attend":
-                    x.qsa.select(s)
             evs[i][0].record(stream_obj)
             fn(x)
             evs[i][1].record(stream_obj)
@@ -254,7 +248,7 @@ def main():
     us_step = sec * 1e6
     kern = time_kernels(insts, max(50, min(args.steps, 400)), stream)
     bytes_step = touched
-    kb = {"qsa_attend": qsa_keys(pos) * KV_BYTES_PER_KEY, "dn_decode": DN_BYTES}
+    kb = {"qsa_decode": qsa_bytes(pos), "dn_decode": DN_BYTES}
     dominant = max(kb, key=lambda k: kern[k])
     achieved = kb[dominant] / (kern[dominant] * 1e-6) / 1e9
     print(f"[bench] step {us_step:.2f} us; kernels (us): " +

@@ -190,6 +190,39 @@ int qm_qsa_select(const qm_qsa_geom* g, int seq, const float* iq, const float* b
                   const int* page_table, int* ids, int* n_sel, void* items, float* scores_out,
                   hipStream_t stream);
 
+/* The decode (one token per sequence) front end in one launch: qm_qsa_prep's
+ * work for the query and key/value heads, plus, per sequence, the raw indexer
+ * key append, the indexer query, the pooled key of the block this token
+ * completes (if any) and qm_qsa_select -- the same results as qm_qsa_prep
+ * followed by qm_qsa_select with seq = 1 (reference/model.py:248-363). */
+int qm_qsa_decode_front(const qm_qsa_geom* g, const void* qg, const void* k_new, const void* v_new, const void* iq,
+                        const void* ik, const float* q_norm, const float* k_norm, const float* iq_norm,
+                        const float* ik_norm, const float* cos, const float* sin, const int* positions,
+                        const int* page_table, void* k_pool, void* v_pool, void* raw_keys, float* block_keys,
+                        void* q_out, float* iq_out, int* ids, int* n_sel, void* items, hipStream_t stream);
+
+/* Split count (workgroups per kv head) of qm_qsa_decode for queries up to max_position. */
+int qm_qsa_decode_splits(const qm_qsa_geom* g, int max_position);
+/* Bytes of workspace qm_qsa_decode needs; zero it once before first use (the
+ * kernel leaves its completion counters at zero for the next call). */
+size_t qm_qsa_decode_workspace(const qm_qsa_geom* g, int splits);
+
+/* One QSA decode step (one token per sequence) in a single launch: everything
+ * qm_qsa_decode_front + qm_qsa_attend compute -- token prep and K/V append,
+ * raw indexer key append and block pooling, indexer query, block scores and
+ * top-k, paged GQA attention over the selected blocks and the tail, sigmoid
+ * gate (reference/model.py:248-382). Every workgroup recomputes the selection
+ * it needs; the last workgroup of each kv head merges the split partials.
+ * Requires max_blocks, max_pages <= 2048 and budget/ratio <= 256.
+ *   out [B, Hq*d] act; ids [B, budget/ratio], n_sel [B], items, iq_out
+ *   [B, idx_heads, idx_dim] are optional inspection outputs (may be NULL). */
+int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k_new, const void* v_new, const void* iq,
+                  const void* ik, const float* q_norm, const float* k_norm, const float* iq_norm,
+                  const float* ik_norm, const float* cos, const float* sin, const int* positions,
+                  const int* page_table, void* k_pool, void* v_pool, void* raw_keys, float* block_keys, void* out,
+                  int splits, void* workspace, size_t workspace_bytes, int* ids, int* n_sel, void* items,
+                  float* iq_out, hipStream_t stream);
+
 /* Bytes of workspace qm_qsa_attend needs for `seq` query rows and `splits`. */
 size_t qm_qsa_attend_workspace(const qm_qsa_geom* g, int seq, int splits);
 /* Split count (workgroups per row and kv head) covering every query row at

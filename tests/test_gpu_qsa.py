@@ -273,3 +273,33 @@ def test_consecutive_decode_steps_cross_a_block_boundary(gpu):
         want = om._full_attention(hidden, 3, cos, sin, ocache, pos)
         got = model._full_attention(hidden.to(DEV), 3, cos.to(DEV), sin.to(DEV), cache, pos)
         assert rel_err(got, want) < OUT_TOL, pos
+
+
+@pytest.mark.parametrize("pos", [63, 127, 2047, 4095, 8127, 8128, 300])
+def test_fused_decode_front_equals_prep_then_select(gpu, pos):
+    """qm_qsa_decode_front (one launch) == qm_qsa_prep + qm_qsa_select, bit for
+    bit: pooled block keys (including the block this token completes), the
+    indexer query, selected ids and the attention item table."""
+    dtype = torch.bfloat16
+    store = gi.FakeStore(gi.qsa_weights(3, 80, dtype))
+    keys, values, idx_keys = gi.qsa_past(81, pos, dtype)
+    hidden = gi.normal(gi.rng(82 + pos), (1, 1, gi.HIDDEN)).to(dtype)
+    cos, sin = tables(pos + 1)
+    qg, k, v, iq, ik = (t.to(DEV) for t in _projections(store, hidden))
+    results = []
+    for fused in (True, False):
+        model, cache = _model_and_cache(gpu, store, dtype, pos + 128)
+        cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
+        if fused:
+            model.qsa_core(qg, k, v, iq, ik, 3, cache, pos, cos.to(DEV), sin.to(DEV))
+        else:
+            # the same step through the separate launches (the prefill path with seq 1)
+            model.qsa_core(None, k, v, iq, ik, 3, cache, pos, cos.to(DEV), sin.to(DEV), attend=False)
+        lc = cache[3]
+        results.append((lc.block_keys.cpu().clone(), lc.last_iq.cpu().clone(), lc.last_ids.cpu().clone(),
+                        lc.last_n_sel.cpu().clone(), lc.k_pool.cpu().clone()))
+    (bk1, iq1, ids1, n1, kp1), (bk2, iq2, ids2, n2, kp2) = results
+    assert torch.equal(bk1, bk2) and torch.equal(iq1, iq2)
+    assert torch.equal(n1, n2)
+    assert torch.equal(ids1[..., : int(n1.max())], ids2[..., : int(n2.max())])
+    assert torch.equal(kp1, kp2)

@@ -182,28 +182,51 @@ class Qwen4MixModel:
         stream = native.stream_handle(self.device)
         self._sync_blocks(lc, g, cos_t, sin_t, query_offset, layer)
         pos = self._positions(batch, query_offset)
-        q_out = torch.empty(batch, seq, 2, c.num_attention_heads, c.head_dim, dtype=torch.bfloat16, device=self.device) \
-            if qg is not None else None
+        q_out = torch.empty(batch, seq, 2, c.num_attention_heads, c.head_dim, dtype=torch.bfloat16,
+                            device=self.device) if qg is not None else None
         iq_out = torch.empty(batch, seq, c.indexer_heads, c.indexer_head_dim, dtype=torch.float32, device=self.device)
-        native.call("qm_qsa_prep", ctypes.byref(g), seq, native.ptr(qg), native.ptr(k), native.ptr(v),
-                    native.ptr(iq), native.ptr(ik), native.ptr(self._dw(layer, "attn_q_norm.weight", torch.float32)),
-                    native.ptr(self._dw(layer, "attn_k_norm.weight", torch.float32)),
-                    native.ptr(self._dw(layer, "indexer.q_norm.weight", torch.float32)),
-                    native.ptr(self._dw(layer, "indexer.k_norm.weight", torch.float32)), native.ptr(cos_t),
-                    native.ptr(sin_t), native.ptr(pos), native.ptr(lc.page_table), native.ptr(lc.k_pool),
-                    native.ptr(lc.v_pool), native.ptr(lc.raw_keys), native.ptr(lc.block_keys), native.ptr(q_out),
-                    native.ptr(iq_out), stream)
-        lc.blocks_valid = max(lc.blocks_valid, (query_offset + seq) // c.indexer_compress_ratio)
-        if k is not None:
-            lc.n_tokens = query_offset + seq
         lib = native.load()
         ids = torch.empty(batch, seq, c.block_topk, dtype=torch.int32, device=self.device)
         n_sel = torch.empty(batch, seq, dtype=torch.int32, device=self.device)
         items = torch.empty(batch, seq, 2 * lib.qm_qsa_items_stride(ctypes.byref(g)), dtype=torch.int32,
                             device=self.device) if attend else None
-        native.call("qm_qsa_select", ctypes.byref(g), seq, native.ptr(iq_out), native.ptr(lc.block_keys),
-                    native.ptr(pos), native.ptr(lc.page_table), native.ptr(ids), native.ptr(n_sel),
-                    native.ptr(items), None, stream)
+        norms = [native.ptr(self._dw(layer, n, torch.float32)) for n in
+                 ("attn_q_norm.weight", "attn_k_norm.weight", "indexer.q_norm.weight", "indexer.k_norm.weight")]
+        if seq == 1 and qg is not None and k is not None and attend and self.fused_decode_fits(cache):
+            # decode: the whole QSA step in one launch
+            splits = lib.qm_qsa_decode_splits(ctypes.byref(g), query_offset)
+            ws = self._workspace(f"qsa_decode_{layer}", lib.qm_qsa_decode_workspace(ctypes.byref(g), splits))
+            if out is None:
+                out = torch.empty(batch, seq, c.num_attention_heads * c.head_dim, dtype=dt, device=self.device)
+            native.call("qm_qsa_decode", ctypes.byref(g), native.ptr(qg), native.ptr(k), native.ptr(v),
+                        native.ptr(iq), native.ptr(ik), *norms, native.ptr(cos_t), native.ptr(sin_t),
+                        native.ptr(pos), native.ptr(lc.page_table), native.ptr(lc.k_pool), native.ptr(lc.v_pool),
+                        native.ptr(lc.raw_keys), native.ptr(lc.block_keys), native.ptr(out), splits,
+                        native.ptr(ws), ws.numel(), native.ptr(ids), native.ptr(n_sel), native.ptr(items),
+                        native.ptr(iq_out), stream)
+            lc.blocks_valid = max(lc.blocks_valid, (query_offset + seq) // c.indexer_compress_ratio)
+            lc.n_tokens = query_offset + seq
+            lc.last_ids, lc.last_n_sel, lc.last_iq, lc.last_q = ids, n_sel, iq_out, None
+            return out
+        if seq == 1 and qg is not None and k is not None and attend:
+            # decode: prep and selection in one launch
+            native.call("qm_qsa_decode_front", ctypes.byref(g), native.ptr(qg), native.ptr(k), native.ptr(v),
+                        native.ptr(iq), native.ptr(ik), *norms, native.ptr(cos_t), native.ptr(sin_t),
+                        native.ptr(pos), native.ptr(lc.page_table), native.ptr(lc.k_pool), native.ptr(lc.v_pool),
+                        native.ptr(lc.raw_keys), native.ptr(lc.block_keys), native.ptr(q_out), native.ptr(iq_out),
+                        native.ptr(ids), native.ptr(n_sel), native.ptr(items), stream)
+        else:
+            native.call("qm_qsa_prep", ctypes.byref(g), seq, native.ptr(qg), native.ptr(k), native.ptr(v),
+                        native.ptr(iq), native.ptr(ik), *norms, native.ptr(cos_t), native.ptr(sin_t),
+                        native.ptr(pos), native.ptr(lc.page_table), native.ptr(lc.k_pool), native.ptr(lc.v_pool),
+                        native.ptr(lc.raw_keys), native.ptr(lc.block_keys), native.ptr(q_out), native.ptr(iq_out),
+                        stream)
+            native.call("qm_qsa_select", ctypes.byref(g), seq, native.ptr(iq_out), native.ptr(lc.block_keys),
+                        native.ptr(pos), native.ptr(lc.page_table), native.ptr(ids), native.ptr(n_sel),
+                        native.ptr(items), None, stream)
+        lc.blocks_valid = max(lc.blocks_valid, (query_offset + seq) // c.indexer_compress_ratio)
+        if k is not None:
+            lc.n_tokens = query_offset + seq
         lc.last_ids, lc.last_n_sel, lc.last_iq, lc.last_q = ids, n_sel, iq_out, q_out
         if not attend:
             return None
@@ -215,6 +238,11 @@ class Qwen4MixModel:
                     native.ptr(lc.v_pool), native.ptr(items), native.ptr(out), splits, native.ptr(ws), ws.numel(),
                     stream)
         return out
+
+    def fused_decode_fits(self, cache) -> bool:
+        """Whether qm_qsa_decode (one launch) covers this cache's geometry."""
+        c = self.config
+        return cache.max_blocks <= 2048 and cache.max_pages <= 2048 and c.block_topk <= 256
 
     def _full_attention(self, hidden, layer: int, cos, sin, cache, query_offset: int) -> torch.Tensor:
         """reference/model.py:331-383."""

@@ -49,6 +49,10 @@ SIGNATURES = {
     "qm_v_slot": (_i, [_i]),
     "qm_qsa_prep": (_i, [ctypes.POINTER(QsaGeom), _i] + [_vp] * 19 + [_vp]),
     "qm_qsa_items_stride": (_i, [ctypes.POINTER(QsaGeom)]),
+    "qm_qsa_decode_splits": (_i, [ctypes.POINTER(QsaGeom), _i]),
+    "qm_qsa_decode_workspace": (_sz, [ctypes.POINTER(QsaGeom), _i]),
+    "qm_qsa_decode": (_i, [ctypes.POINTER(QsaGeom)] + [_vp] * 18 + [_i, _vp, _sz, _vp, _vp, _vp, _vp, _vp]),
+    "qm_qsa_decode_front": (_i, [ctypes.POINTER(QsaGeom)] + [_vp] * 22 + [_vp]),
     "qm_qsa_select": (_i, [ctypes.POINTER(QsaGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "qm_qsa_attend_workspace": (_sz, [ctypes.POINTER(QsaGeom), _i, _i]),
     "qm_qsa_attend_splits": (_i, [ctypes.POINTER(QsaGeom), _i, _i]),

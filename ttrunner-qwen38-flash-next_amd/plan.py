@@ -64,6 +64,10 @@ class QsaDecodePlan:
         self.splits = lib.qm_qsa_attend_splits(ctypes.byref(self.geom), max_position, max_position)
         self.ws = torch.zeros(lib.qm_qsa_attend_workspace(ctypes.byref(self.geom), 1, self.splits),
                               dtype=torch.uint8, device=dev)
+        self.fused = model.fused_decode_fits(cache)
+        self.dec_splits = lib.qm_qsa_decode_splits(ctypes.byref(self.geom), max_position)
+        self.dec_ws = torch.zeros(lib.qm_qsa_decode_workspace(ctypes.byref(self.geom), self.dec_splits),
+                                  dtype=torch.uint8, device=dev)
         self.positions = torch.zeros(batch, dtype=torch.int32, device=dev)
         self.q_out = torch.empty(batch, 1, 2, c.num_attention_heads, c.head_dim, dtype=torch.bfloat16, device=dev)
         self.iq_out = torch.empty(batch, 1, c.indexer_heads, c.indexer_head_dim, dtype=torch.float32, device=dev)
@@ -75,6 +79,18 @@ class QsaDecodePlan:
         self.w = {s: model._dw(layer, s, torch.float32) for s in
                   ("attn_q_norm.weight", "attn_k_norm.weight", "indexer.q_norm.weight", "indexer.k_norm.weight")}
         self.cos, self.sin = model.rope.get(max_position + 1)
+
+    def front(self, qg, k, v, iq, ik, stream):
+        """prep + select in one launch (qm_qsa_decode_front)."""
+        lc, w = self.lc, self.w
+        native.call("qm_qsa_decode_front", ctypes.byref(self.geom), qg.data_ptr(), k.data_ptr(), v.data_ptr(),
+                    iq.data_ptr(), ik.data_ptr(), w["attn_q_norm.weight"].data_ptr(),
+                    w["attn_k_norm.weight"].data_ptr(), w["indexer.q_norm.weight"].data_ptr(),
+                    w["indexer.k_norm.weight"].data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
+                    self.positions.data_ptr(), lc.page_table.data_ptr(), lc.k_pool.data_ptr(),
+                    lc.v_pool.data_ptr(), lc.raw_keys.data_ptr(), lc.block_keys.data_ptr(), self.q_out.data_ptr(),
+                    self.iq_out.data_ptr(), self.ids.data_ptr(), self.n_sel.data_ptr(), self.items.data_ptr(),
+                    stream)
 
     def prep(self, qg, k, v, iq, ik, stream):
         lc, w = self.lc, self.w
@@ -97,9 +113,22 @@ class QsaDecodePlan:
                     lc.k_pool.data_ptr(), lc.v_pool.data_ptr(), self.items.data_ptr(), self.out.data_ptr(),
                     self.splits, self.ws.data_ptr(), self.ws.numel(), stream)
 
+    def decode(self, qg, k, v, iq, ik, stream):
+        """The whole step in one launch (qm_qsa_decode)."""
+        lc, w = self.lc, self.w
+        native.call("qm_qsa_decode", ctypes.byref(self.geom), qg.data_ptr(), k.data_ptr(), v.data_ptr(),
+                    iq.data_ptr(), ik.data_ptr(), w["attn_q_norm.weight"].data_ptr(),
+                    w["attn_k_norm.weight"].data_ptr(), w["indexer.q_norm.weight"].data_ptr(),
+                    w["indexer.k_norm.weight"].data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
+                    self.positions.data_ptr(), lc.page_table.data_ptr(), lc.k_pool.data_ptr(),
+                    lc.v_pool.data_ptr(), lc.raw_keys.data_ptr(), lc.block_keys.data_ptr(), self.out.data_ptr(),
+                    self.dec_splits, self.dec_ws.data_ptr(), self.dec_ws.numel(), None, None, None, None, stream)
+
     def run(self, qg, k, v, iq, ik, stream=None):
         s = stream if stream is not None else native.stream_handle(self.model.device)
-        self.prep(qg, k, v, iq, ik, s)
-        self.select(s)
-        self.attend(qg, s)
+        if self.fused:
+            self.decode(qg, k, v, iq, ik, s)
+        else:
+            self.front(qg, k, v, iq, ik, s)
+            self.attend(qg, s)
         return self.out

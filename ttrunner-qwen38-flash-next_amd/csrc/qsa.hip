@@ -193,7 +193,6 @@ __global__ __launch_bounds__(IDX_D) void qsa_pool_kernel(PoolArgs<T> A) {
 // ---------------------------------------------------------------------------
 constexpr int SEL_NT = 256;
 constexpr int SEL_MAX_BLOCKS = 4096;    // eligible blocks one query may score
-constexpr int SEL_CHUNK = SEL_NT / 16 * 8;   // blocks scored per preloaded chunk (128)
 
 __device__ __forceinline__ unsigned long long sel_key(float s, int j) {
   unsigned u = __float_as_uint(s);
@@ -205,6 +204,143 @@ __device__ __forceinline__ unsigned long long sel_key(float s, int j) {
 // .x = physical pool row of the group's first token (page * P + row0),
 // .y = lo | hi << 8. items[row][0].x holds the item count.
 __device__ __forceinline__ int2 make_item(int phys_row, int lo, int hi) { return make_int2(phys_row, lo | (hi << 8)); }
+
+// Block scores, 32 blocks per pass of a 256-thread block: the 8 lanes of
+// block j = 32 * pass + t / 8 hold its 16-byte channel chunks part, part + 8,
+// part + 16, part + 24 (part = t % 8), so every load instruction reads whole
+// 128-byte lines, and the lanes add their partial dot products with three DPP
+// exchanges (all 8 lanes end with the same sum: float addition commutes). Each
+// lane keeps the matching chunks of the 4 query heads in registers.
+constexpr int SCORE_LANES = 8;
+constexpr int SCORE_PASS = 256 / SCORE_LANES;   // blocks per pass at 256 threads
+constexpr int SCORE_PRE = 4;                    // passes of keys held in registers ahead of use
+
+// (an invalid j loads row 0, always allocated, and zeroes the result: the
+// loads stay unconditional so later waits on them stay exact)
+__device__ __forceinline__ void load_block_part(float4 (&k)[4], const float* bk, int j, bool valid) {
+  const float4* src = reinterpret_cast<const float4*>(bk + (long)(valid ? j : 0) * IDX_D) + (threadIdx.x & 7);
+  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 v = src[8 * i];
+    k[i] = valid ? v : zero;
+  }
+}
+
+// sum over the first idx_heads heads of relu(q_h . k), divided by sqrt(128);
+// q holds this lane's chunks of the 4 query rows (rows past idx_heads unused)
+__device__ __forceinline__ float oct_block_score(const float4 (&q)[4][4], const float4 (&k)[4], int idx_heads) {
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      acc[h] = fmaf(q[h][i].x, k[i].x, acc[h]);
+      acc[h] = fmaf(q[h][i].y, k[i].y, acc[h]);
+      acc[h] = fmaf(q[h][i].z, k[i].z, acc[h]);
+      acc[h] = fmaf(q[h][i].w, k[i].w, acc[h]);
+    }
+#pragma unroll
+  for (int h = 0; h < 4; ++h) acc[h] = acc[h] + dpp_f<0xB1>(acc[h]);      // lane ^ 1
+#pragma unroll
+  for (int h = 0; h < 4; ++h) acc[h] = acc[h] + dpp_f<0x4E>(acc[h]);      // lane ^ 2
+#pragma unroll
+  for (int h = 0; h < 4; ++h) acc[h] = acc[h] + dpp_f<0x141>(acc[h]);     // 7 - lane within 8
+  float sc = 0.f;
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+    if (h < idx_heads) sc = add_rn(sc, fmaxf(acc[h], 0.f));
+  return div_rn(sc, 11.313708498984761f);     // sqrt(128)
+}
+
+// keys[j] = sel_key(score_j, j) for every eligible block j (and scores_out[j]
+// when given), then zeros up to a multiple of 32. kp[u] comes in holding pass
+// u's keys (load_block_part); later passes load SCORE_PRE passes ahead of use.
+// Block new_j's key is new_key (LDS), not the cache's. s_iq: 4 rows of 128.
+template <int NT>
+__device__ void score_blocks(const float* s_iq, const float* new_key, const float* bk, int n_elig, int new_j,
+                             int idx_heads, unsigned long long* keys, float* scores_out,
+                             float4 (&kp)[SCORE_PRE][4]) {
+  static_assert(NT / SCORE_LANES == SCORE_PASS, "8 lanes per block");
+  const int tid = threadIdx.x, jl = tid >> 3, part = tid & 7;
+  float4 q[4][4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[h][i] = reinterpret_cast<const float4*>(s_iq + h * IDX_D)[8 * i + part];
+  const int n_pass = (n_elig + SCORE_PASS - 1) / SCORE_PASS;
+  for (int ps0 = 0; ps0 < n_pass; ps0 += SCORE_PRE) {
+#pragma unroll
+    for (int u = 0; u < SCORE_PRE; ++u) {
+      const int ps = ps0 + u;
+      if (ps < n_pass) {
+        const int j = ps * SCORE_PASS + jl;
+        if (j == new_j) {
+          const float4* src = reinterpret_cast<const float4*>(new_key) + part;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) kp[u][i] = src[8 * i];
+        }
+        const float sc = oct_block_score(q, kp[u], idx_heads);
+        if (part == 0 && j < n_elig) {
+          keys[j] = sel_key(sc, j);
+          if (scores_out) scores_out[j] = sc;
+        }
+        const int jn = j + SCORE_PRE * SCORE_PASS;
+        if (ps + SCORE_PRE < n_pass) load_block_part(kp[u], bk, jn, jn < n_elig && jn != new_j);
+      }
+    }
+  }
+  const int npad = (n_elig + 31) & ~31;
+  for (int j = n_elig + tid; j < npad; j += NT) keys[j] = 0ull;
+}
+
+// prefetch of the first SCORE_PRE passes (issued before the scores are needed)
+__device__ __forceinline__ void prefetch_block_keys(float4 (&kp)[SCORE_PRE][4], const float* bk, int n_elig,
+                                                    int new_j, bool on) {
+  const int jl = threadIdx.x >> 3;
+#pragma unroll
+  for (int u = 0; u < SCORE_PRE; ++u) {
+    const int j = u * SCORE_PASS + jl;
+    load_block_part(kp[u], bk, j, on && j < n_elig && j != new_j);
+  }
+}
+
+// Top-k by counting: the keys are distinct, so the rank of key j is the number
+// of larger keys, and sel[rank] = j for rank < topk. `keys` is padded with
+// zeros (below every real key) to a multiple of 32. Up to NT/2 keys, two
+// adjacent lanes split the comparisons of one key and add their counts by DPP.
+template <int NT>
+__device__ void rank_topk(const unsigned long long* keys, int n, int topk, int* sel) {
+  const int tid = threadIdx.x;
+  const int npad = (n + 31) & ~31;
+  if (n <= NT / 2) {
+    const int j = tid >> 1, part = tid & 1, half = npad >> 1;
+    const unsigned long long kj = keys[j < n ? j : 0];
+    int rank = 0;
+    for (int i = part * half; i < part * half + half; i += 16) {
+      unsigned long long k16[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) k16[u] = keys[i + u];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) rank += k16[u] > kj ? 1 : 0;
+    }
+    rank += __builtin_amdgcn_update_dpp(0, rank, 0xB1, 0xF, 0xF, true);
+    if (part == 0 && j < n && rank < topk) sel[rank] = j;
+  } else {
+    for (int j = tid; j < n; j += NT) {
+      const unsigned long long kj = keys[j];
+      int rank = 0;
+      for (int i = 0; i < npad; i += 16) {
+        unsigned long long k16[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) k16[u] = keys[i + u];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) rank += k16[u] > kj ? 1 : 0;
+      }
+      if (rank < topk) sel[rank] = j;
+    }
+  }
+}
 
 struct SelArgs {
   const float* iq; const float* block_keys; const int* positions; const int* page_table;
@@ -239,71 +375,21 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
       if (j >= n_elig) A.scores_out[(long)row * A.max_blocks + j] = -INFINITY;
 
   if (n_elig > A.topk || A.scores_out) {
-    // 16 lanes per block, 8 channels each; a chunk of 128 blocks is loaded
-    // before any of it is used so the loads overlap
-    const int sub = tid & 15, grp = tid >> 4;
+    // the first two passes of block keys are in flight across the barrier
     const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
-    for (int c0 = 0; c0 < n_elig; c0 += SEL_CHUNK) {
-      float4 kb[8][2];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int j = c0 + grp + 16 * i;
-        const float4* kr = reinterpret_cast<const float4*>(
-            j == new_j ? S.newkey + sub * 8 : bk + (long)(j < n_elig ? j : 0) * IDX_D + sub * 8);
-        if (j < n_elig) {
-          kb[i][0] = kr[0];
-          kb[i][1] = kr[1];
-        } else {
-          kb[i][0] = kb[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-      }
-      __syncthreads();    // S.q and S.newkey visible
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int j = c0 + grp + 16 * i;
-        const float kv[8] = {kb[i][0].x, kb[i][0].y, kb[i][0].z, kb[i][0].w,
-                             kb[i][1].x, kb[i][1].y, kb[i][1].z, kb[i][1].w};
-        float dots[4];
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          const float* qh = S.q + h * IDX_D + sub * 8;
-          float acc = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc = fmaf(qh[e], kv[e], acc);
-          dots[h] = row16_sum(acc);
-        }
-        if (sub == 0 && j < n_elig) {
-          float sc = 0.f;
-#pragma unroll
-          for (int h = 0; h < 4; ++h)
-            if (h < A.idx_heads) sc = add_rn(sc, fmaxf(dots[h], 0.f));
-          sc = div_rn(sc, 11.313708498984761f);     // sqrt(128)
-          if (A.scores_out) A.scores_out[(long)row * A.max_blocks + j] = sc;
-          S.key[j] = sel_key(sc, j);
-        }
-      }
-    }
+    float4 kp[SCORE_PRE][4];
+    prefetch_block_keys(kp, bk, n_elig, new_j, true);
+    __syncthreads();    // S.q and S.newkey visible
+    score_blocks<SEL_NT>(S.q, S.newkey, bk, n_elig, new_j, A.idx_heads, S.key,
+                         A.scores_out ? A.scores_out + (long)row * A.max_blocks : nullptr, kp);
   }
   __syncthreads();
   if (n_elig <= A.topk) {
     for (int i = tid; i < n_elig; i += SEL_NT) { out_ids[i] = i; S.sel[i] = i; }
   } else {
-    // rank by counting: keys are distinct, rank = number of larger keys
-    // (keys past n_elig are padded with 0, which no real key is below)
-    for (int j = n_elig + tid; j < ((n_elig + 15) & ~15); j += SEL_NT) S.key[j] = 0ull;
+    rank_topk<SEL_NT>(S.key, n_elig, A.topk, S.sel);
     __syncthreads();
-    for (int j = tid; j < n_elig; j += SEL_NT) {
-      const unsigned long long kj = S.key[j];
-      int rank = 0;
-      for (int i = 0; i < n_elig; i += 16) {
-        unsigned long long k16[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) k16[u] = S.key[i + u];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) rank += k16[u] > kj ? 1 : 0;
-      }
-      if (rank < A.topk) { out_ids[rank] = j; S.sel[rank] = j; }
-    }
+    for (int i = tid; i < A.topk; i += SEL_NT) out_ids[i] = S.sel[i];
   }
   if (tid == 0) A.n_sel[row] = n_sel;
   if (!A.items) return;
@@ -583,107 +669,191 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T> A) {
 // ---------------------------------------------------------------------------
 // fused decode step: one launch per token
 // ---------------------------------------------------------------------------
-// Grid (split, kv head g, sequence b); each 256-thread workgroup:
-//   0. issues every load that depends only on the position: the indexer query
-//      and key, its 8 query heads, the token's key and value, the first chunk
-//      of block keys and the page-table row;
-//   1. norms and ropes the indexer query (and pools the block this token
-//      completes, if any) -- the same torch-order arithmetic as qsa_prep;
-//   2. scores the eligible blocks and ranks them (every workgroup redundantly:
-//      ~65 KB of L2-resident reads, cheaper than a cross-workgroup hand-off);
-//   3. attends its four 32-token items (one per wave) on bf16 MFMA; the item
-//      holding the current token takes that token's key/value from registers,
-//      and split 0 of each kv head appends them to the pages;
-//   4. writes its (max, sum, output) partial; the last workgroup of the kv head
-//      to finish (agent-scope counter) merges all partials, applies the
-//      sigmoid gate and resets the counter.
+// Grid (G, kv head g, sequence b) of 256-thread workgroups, G a power of two
+// at least the number of 4-item batches of attention work. The chip's dies
+// start a launch's workgroups up to a few microseconds apart, so the batches
+// are not tied to blockIdx: each workgroup takes a ticket from a per-(b, g)
+// counter as it starts, does batch (ticket mod G), and leaves at once when
+// that is past the last batch. The counter only grows, by exactly G per
+// launch, so the tickets of a launch cover every residue mod G. A working
+// workgroup then:
+//   0. issues its loads: those that do not depend on the position first (its
+//      8 query heads, the token's key and value, the indexer query and key,
+//      the norm weights), then the rope row, the page-table row, the first 128
+//      block keys and, when this token completes a block, its raw keys;
+//   1. RMS-norms and ropes the indexer query and the pooled block key (sums of
+//      squares in torch's order);
+//   2. scores the eligible blocks and ranks them (every working workgroup
+//      redundantly: ~65 KB of L2-resident reads, cheaper than a hand-off);
+//   3. issues the key/value loads of its first item, then norms and ropes the
+//      8 query heads and the key while those loads are in flight;
+//   4. attends its items, one 32-token group per wave at a time (items
+//      batch*4 + wave, then + 4G, ...), on bf16 MFMA with an online softmax;
+//      the item holding the current token takes its key/value from LDS;
+//   5. writes its (max, sum, output) partial; the last working workgroup of
+//      the kv head (a completion counter) merges all partials, applies
+//      the sigmoid gate and resets the counter. Batch 0 of each kv head also
+//      appends the token's key/value to its page slot, and batch 0 of kv head
+//      0 writes the per-sequence outputs (raw indexer key, pooled key).
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_NT = 64 * DEC_WAVES;
 constexpr int DEC_MAX_BLOCKS = 2048;
 constexpr int DEC_MAX_PAGES = 2048;
 constexpr int DEC_MAX_TOPK = 256;
-constexpr int DEC_MAX_SPLITS = 80;
+constexpr int DEC_MAX_SPLITS = 128;   // workgroups per (sequence, kv head)
+constexpr int DEC_MAX_RATIO = 64;     // raw keys of a completed block are held in registers
+constexpr int DEC_COMB = 18;          // partials merged per batch of loads in the combine
+
+// rows of the two norm passes, at these LDS offsets: the 4 indexer-query rows
+// and the pooled block key (128 wide) first, then the 8 query heads and the
+// key (256 wide)
+constexpr int NR_POOL = 4, NR_Q = 5, NR_K = 13, NR_ROWS = 14;
+constexpr int X_POOL = 4 * IDX_D, X_Q = X_POOL + IDX_D, X_K = X_Q + GQA * QSA_D, X_SIZE = X_K + QSA_D;
+constexpr int SLOTS_FRONT = NR_Q * 32, SLOTS_ALL = NR_ROWS * 32;   // 32 partial sums per row
+
+// Partials cross the dies as relaxed system-scope atomics: written through to,
+// and read back from, the device's point of coherence, so that publishing them
+// needs no L2 writeback (a release fence walks the die's whole L2, and the
+// fences of workgroups sharing a die queue behind each other) and reading them
+// no L2 invalidate. A writer waits for its stores to complete before it counts
+// itself in; the last workgroup reads only after it has seen the count.
+__device__ __forceinline__ void st_coherent(float* p, float a, float b) {
+  const unsigned long long v = (static_cast<unsigned long long>(__float_as_uint(b)) << 32) | __float_as_uint(a);
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float2 ld_coherent(const float* p) {
+  const unsigned long long v = __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_SYSTEM);
+  return make_float2(__uint_as_float(static_cast<unsigned>(v)), __uint_as_float(static_cast<unsigned>(v >> 32)));
+}
+// 16-byte versions through a buffer resource with the system-scope cache
+// policy (sc0 sc1); loads past the resource's byte range return zeros
+constexpr int BUF_DWORD3 = 0x00020000;     // raw 32-bit buffer, gfx9 encoding
+constexpr int CPOL_SYSTEM = 1 | 16;        // sc0 | sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const float* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, bytes, BUF_DWORD3);
+}
+__device__ __forceinline__ float4 ld_coherent4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, CPOL_SYSTEM));
+}
+__device__ __forceinline__ void st_coherent4(__amdgpu_buffer_rsrc_t r, int byte_off, float4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, byte_off, 0, CPOL_SYSTEM);
+}
+// counters of one (sequence, kv head) sit 128 bytes apart, one cache line each
+constexpr int DEC_CTR_STRIDE = 32;
+
+__device__ __forceinline__ int norm_row_offset(int r) {
+  return r < NR_POOL ? r * IDX_D : r == NR_POOL ? X_POOL : r < NR_K ? X_Q + (r - NR_Q) * QSA_D : X_K;
+}
 
 template <typename T>
 struct DecArgs {
   PrepArgs<T> P;
   float* part_o; float* part_ml; unsigned* counters; T* out;
   int* ids; int* n_sel; int2* items; float* iq_out;   // optional inspection outputs
-  int splits, topk, max_items;
+  int splits, topk, max_items, ticket_off;
 };
 
 struct DecShared {
+  float x[X_SIZE];                                // rows to norm
+  union {
+    unsigned long long key[DEC_MAX_BLOCKS];       // selection keys (step 2)
+    float acc[DEC_WAVES][GQA][QSA_D + 4];         // per-wave outputs (step 5), rows padded against bank conflicts
+  } u;
+  float part[SLOTS_ALL];
+  float rinv[16];
   float iq[4 * IDX_D];
   float newkey[IDX_D];
-  float x[GQA * QSA_D];
-  float y[GQA * QSA_D];
-  float part[GQA * 32];
-  float rinv[GQA];
-  float knew[QSA_D], vnew[QSA_D];
-  uint16_t qh[GQA * QSA_D], ql[GQA * QSA_D];
+  uint16_t knb[QSA_D], vnb[QSA_D];   // the token's roped key and its value, bf16
+  uint16_t qb[16][QSA_D];            // MFMA B operand: rows 0..7 bf16 hi of the 8 heads, 8..15 their lo parts
+  float chunk[DEC_MAX_RATIO / 16][IDX_D];
   int pages[DEC_MAX_PAGES];
   int sel[DEC_MAX_TOPK];
-  union {
-    unsigned long long key[DEC_MAX_BLOCKS];
-    float acc[DEC_WAVES][GQA][QSA_D];
-    float w[DEC_MAX_SPLITS][GQA];
-  } u;
+  float w[DEC_MAX_SPLITS][GQA];
   float m[DEC_WAVES][GQA], l[DEC_WAVES][GQA];
-  int last;
+  int ticket, last;
 };
 
-// y[r][e] = round_T(x[r][e] * rsqrt(mean_e x[r]^2 + eps) * w[e]) for R rows of n
-// (n % 32 == 0, R * 32 <= blockDim), with the row sums of squares reduced in
-// the order torch's CPU kernel uses (see torch_row_sumsq); then the first
-// `rope` channels of every row rotated with (cs, sn). Called by the whole block.
-template <typename T>
-__device__ void norm_rope_rows(DecShared& sh, float* out, int R, int n, const float* w, float eps, int rope,
-                               const float* cs, const float* sn) {
-  const int t = threadIdx.x;
-  __syncthreads();
-  if (t < R * 32) {
-    const int r = t >> 5, a = t & 31;
-    float acc = 0.f;
-    for (int e = a; e < n; e += 32) acc = add_rn(acc, mul_rn(sh.x[r * n + e], sh.x[r * n + e]));
-    sh.part[t] = acc;
+// item -> (first token t0, visible rows [lo, hi)) of a query at position p
+__device__ __forceinline__ void item_span(int it, int n_blk_items, int gpb, int ratio, int ts, int p, const int* sel,
+                                          int& t0, int& lo, int& hi) {
+  if (it < n_blk_items) {
+    const int bs = sel[it / gpb] * ratio;
+    if (ratio >= 32) { t0 = bs + (it % gpb) * 32; lo = 0; hi = 32; }
+    else { t0 = bs & ~31; lo = bs - t0; hi = lo + ratio; }
+  } else {
+    t0 = (ts & ~31) + (it - n_blk_items) * 32; lo = max(ts - t0, 0); hi = min(p + 1 - t0, 32);
   }
-  __syncthreads();
-  if (t < R) {
-    const float* pp = sh.part + t * 32;
+}
+
+// the 32 partial sums of squares of rows with slots [s0, s1) (slot = 32 row + a,
+// a = 0..31 summing channels a, a+32, ... in order), then each row's 1/rms
+__device__ __forceinline__ void norm_partials(DecShared& sh, int s0, int s1) {
+  for (int s = s0 + (int)threadIdx.x; s < s1; s += DEC_NT) {
+    const int r = s >> 5, a = s & 31;
+    const float* xr = sh.x + norm_row_offset(r);
+    float acc = 0.f;
+    if (r <= NR_POOL) {
+#pragma unroll
+      for (int e = 0; e < IDX_D; e += 32) acc = add_rn(acc, mul_rn(xr[a + e], xr[a + e]));
+    } else {
+#pragma unroll
+      for (int e = 0; e < QSA_D; e += 32) acc = add_rn(acc, mul_rn(xr[a + e], xr[a + e]));
+    }
+    sh.part[s] = acc;
+  }
+}
+__device__ __forceinline__ void norm_rinv(DecShared& sh, int r0, int r1, float eps) {
+  const int r = r0 + (int)threadIdx.x;
+  if (r < r1) {
+    const float* pp = sh.part + r * 32;
     float tot = 0.f;
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
       const float c = add_rn(add_rn(add_rn(pp[l], pp[8 + l]), pp[16 + l]), pp[24 + l]);
       tot = l == 0 ? c : add_rn(tot, c);
     }
-    sh.rinv[t] = rsqrt_rn(add_rn(div_rn(tot, (float)n), eps));
+    sh.rinv[r] = rsqrt_rn(add_rn(div_rn(tot, (float)(r <= NR_POOL ? IDX_D : QSA_D)), eps));
   }
-  __syncthreads();
-  for (int i = t; i < R * n; i += blockDim.x) {
-    const int r = i / n, e = i % n;
-    sh.y[i] = Act<T>::round(mul_rn(mul_rn(sh.x[i], sh.rinv[r]), w[e]));
-  }
-  __syncthreads();
-  const int half = rope / 2;
-  for (int i = t; i < R * n; i += blockDim.x) {
-    const int r = i / n, e = i % n;
-    float v = sh.y[i];
-    if (e < rope) {
-      const float rot = e < half ? -sh.y[r * n + e + half] : sh.y[r * n + e - half];
-      v = add_rn(mul_rn(v, cs[e]), mul_rn(rot, sn[e]));
-    }
-    out[i] = v;
-  }
-  __syncthreads();
 }
 
 template <typename T>
 __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   const PrepArgs<T>& A = D.P;
-  const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int g = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int col = lane & 15, quad = lane >> 4;
+  const int e128 = tid & 127, hh = tid >> 7;
+  const int bg = b * A.hkv + g;
   __shared__ DecShared sh;
+
+  // ---- 0. a ticket, then the loads
+  unsigned ticket = 0;
+  if (tid == 0)
+    ticket = __hip_atomic_fetch_add(D.counters + D.ticket_off + bg * DEC_CTR_STRIDE, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+  float iqv[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = tid + DEC_NT * k;
+    iqv[k] = i < A.idx_heads * IDX_D ? Act<T>::load(A.iq, (long)b * A.idx_heads * IDX_D + i) : 0.f;
+  }
+  const float ikv = Act<T>::load(A.ik, (long)b * IDX_D + e128);
+  float qx[GQA];
+#pragma unroll
+  for (int h = 0; h < GQA; ++h) qx[h] = Act<T>::load(A.qg, ((long)b * A.hq + g * GQA + h) * (2 * QSA_D) + tid);
+  const float kx = Act<T>::load(A.k_new, (long)bg * QSA_D + tid);
+  const float vx = Act<T>::load(A.v_new, (long)bg * QSA_D + tid);
+  // norm weights of this thread's channel and of its rope partner (channel
+  // +- rope/2); 256-wide rows rope channel tid (< rope <= 128), 128-wide rows
+  // channel e128. Every load is unconditional, indices clamped into range, so
+  // the waits on them stay exact instead of draining the memory counter.
+  const int rope = A.rope, half = A.rope >> 1;
+  const bool roped = e128 < rope;
+  const int pe = e128 < half ? e128 + half : e128 - half;
+  const int ec = min(e128, rope - 1);
+  const float w_q = A.q_norm[tid], w_k = A.k_norm[tid], w_iq = A.iq_norm[e128], w_ik = A.ik_norm[e128];
+  const float w_q2 = A.q_norm[pe], w_k2 = A.k_norm[pe], w_iq2 = A.iq_norm[pe], w_ik2 = A.ik_norm[pe];
 
   const int p = A.positions[b];
   const int ratio = A.ratio;
@@ -691,242 +861,215 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   const int topk = D.topk;
   const int n_sel = min(n_elig, topk);
   const int j_new = (p + 1) % ratio == 0 ? p / ratio : -1;
-  const bool leader = split == 0 && g == 0;       // writes the per-sequence side outputs
   const bool scoring = n_elig > topk;
-
-  // ---- 0. loads that depend only on p
-  float iqv[2];
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int i = tid + DEC_NT * k;
-    iqv[k] = i < A.idx_heads * IDX_D ? Act<T>::load(A.iq, (long)b * A.idx_heads * IDX_D + i) : 0.f;
-  }
-  const float ikv = tid < IDX_D ? Act<T>::load(A.ik, (long)b * IDX_D + tid) : 0.f;
-  float qx[GQA];
-#pragma unroll
-  for (int h = 0; h < GQA; ++h) qx[h] = Act<T>::load(A.qg, ((long)b * A.hq + g * GQA + h) * (2 * QSA_D) + tid);
-  const float kx = Act<T>::load(A.k_new, ((long)b * A.hkv + g) * QSA_D + tid);
-  const float vx = Act<T>::load(A.v_new, ((long)b * A.hkv + g) * QSA_D + tid);
-  const float* cs = A.cos + (long)p * A.rope;
-  const float* sn = A.sin + (long)p * A.rope;
-  const int sub = tid & 15, grp = tid >> 4;
-  const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
-  float4 kb[8][2];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int j = grp + 16 * i;
-    if (scoring && j < n_elig && j != j_new) {
-      const float4* kr = reinterpret_cast<const float4*>(bk + (long)j * IDX_D + sub * 8);
-      kb[i][0] = kr[0];
-      kb[i][1] = kr[1];
-    } else {
-      kb[i][0] = kb[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  }
+  const float cs = A.cos[(long)p * rope + ec], sn = A.sin[(long)p * rope + ec];
+  const long t0r = (long)max(j_new, 0) * ratio * rope + ec;
+  const float cs0 = A.cos[t0r], sn0 = A.sin[t0r];
   const int n_lpages = min(A.max_pages, (p + A.page_size) / A.page_size);
-  for (int i = tid; i < n_lpages; i += DEC_NT) sh.pages[i] = A.page_table[(long)b * A.max_pages + i];
-
-  // ---- 1. indexer query (and the block this token completes)
+  int pg[DEC_MAX_PAGES / DEC_NT];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) sh.x[tid + DEC_NT * k] = iqv[k];
-  norm_rope_rows<T>(sh, sh.iq, 4, IDX_D, A.iq_norm, A.eps, A.rope, cs, sn);
-  if (leader) {
-    if (D.iq_out)
-      for (int i = tid; i < A.idx_heads * IDX_D; i += DEC_NT) D.iq_out[(long)b * A.idx_heads * IDX_D + i] = sh.iq[i];
-    if (tid < IDX_D) A.raw_keys[((long)b * A.max_ctx + p) * IDX_D + tid] = A.ik[(long)b * IDX_D + tid];
-  }
-  if (A.idx_heads < 4)
-    for (int i = A.idx_heads * IDX_D + tid; i < 4 * IDX_D; i += DEC_NT) sh.iq[i] = 0.f;
+  for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k)
+    pg[k] = A.page_table[(long)b * A.max_pages + min(tid + DEC_NT * k, n_lpages - 1)];
+  const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
+  float4 kp[SCORE_PRE][4];
+  prefetch_block_keys(kp, bk, n_elig, j_new, scoring);
+  // raw keys of the block this token completes: thread (e128, hh) takes the
+  // 16-row chunks hh and hh + 2; the token's own row is ik (not yet stored)
+  float rk[2][16];
   if (j_new >= 0) {
-    // mean of the block's raw keys (16-row chunks in order), then norm + rope at its start
-    const int t0 = j_new * ratio;
-    if (tid < IDX_D) {
-      const T* raw = A.raw_keys + (long)b * A.max_ctx * IDX_D;
-      float total = 0.f;
-      for (int c0 = 0; c0 < ratio; c0 += 16) {
-        float acc = 0.f;
-        const int c1 = min(c0 + 16, ratio);
-        for (int i = c0; i < c1; ++i) {
-          const int tok = t0 + i;
-          acc = add_rn(acc, tok == p ? ikv : Act<T>::load(raw, (long)tok * IDX_D + tid));
-        }
-        total = c0 == 0 ? acc : add_rn(total, acc);
+    const T* raw = A.raw_keys + ((long)b * A.max_ctx + (long)j_new * ratio) * IDX_D + e128;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = 16 * (hh + 2 * c) + i;
+        rk[c][i] = r >= ratio ? 0.f : j_new * ratio + r == p ? ikv : Act<T>::load(raw, (long)r * IDX_D);
       }
-      sh.x[tid] = Act<T>::round(div_rn(total, (float)ratio));
-    }
-    norm_rope_rows<T>(sh, sh.newkey, 1, IDX_D, A.ik_norm, A.eps, A.rope, A.cos + (long)t0 * A.rope,
-                      A.sin + (long)t0 * A.rope);
-    if (leader && tid < IDX_D) A.block_keys[((long)b * A.max_blocks + j_new) * IDX_D + tid] = sh.newkey[tid];
   }
 
-  // ---- 2. block scores and top-k (ties to the lower index)
-  if (scoring) {
-    for (int c0 = 0; c0 < n_elig; c0 += SEL_CHUNK) {
-      if (c0 > 0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int j = c0 + grp + 16 * i;
-          if (j < n_elig && j != j_new) {
-            const float4* kr = reinterpret_cast<const float4*>(bk + (long)j * IDX_D + sub * 8);
-            kb[i][0] = kr[0];
-            kb[i][1] = kr[1];
-          } else {
-            kb[i][0] = kb[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-          }
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int j = c0 + grp + 16 * i;
-        if (j == j_new) {
-          kb[i][0] = *reinterpret_cast<const float4*>(sh.newkey + sub * 8);
-          kb[i][1] = *reinterpret_cast<const float4*>(sh.newkey + sub * 8 + 4);
-        }
-        const float kv[8] = {kb[i][0].x, kb[i][0].y, kb[i][0].z, kb[i][0].w,
-                             kb[i][1].x, kb[i][1].y, kb[i][1].z, kb[i][1].w};
-        float dots[4];
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          const float* qh = sh.iq + h * IDX_D + sub * 8;
-          float acc = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc = fmaf(qh[e], kv[e], acc);
-          dots[h] = row16_sum(acc);
-        }
-        if (sub == 0 && j < n_elig) {
-          float sc = 0.f;
-#pragma unroll
-          for (int h = 0; h < 4; ++h)
-            if (h < A.idx_heads) sc = add_rn(sc, fmaxf(dots[h], 0.f));
-          sh.u.key[j] = sel_key(div_rn(sc, 11.313708498984761f), j);
-        }
-      }
-    }
-    for (int j = n_elig + tid; j < ((n_elig + 15) & ~15); j += DEC_NT) sh.u.key[j] = 0ull;
-    __syncthreads();
-    for (int j = tid; j < n_elig; j += DEC_NT) {
-      const unsigned long long kj = sh.u.key[j];
-      int rank = 0;
-      for (int i = 0; i < n_elig; i += 16) {
-        unsigned long long k16[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) k16[u] = sh.u.key[i + u];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) rank += k16[u] > kj ? 1 : 0;
-      }
-      if (rank < topk) sh.sel[rank] = j;
-    }
-  } else {
-    for (int i = tid; i < n_elig; i += DEC_NT) sh.sel[i] = i;
-  }
-
-  // ---- the query heads, key and value of this token (normed, roped)
-#pragma unroll
-  for (int h = 0; h < GQA; ++h) sh.x[h * QSA_D + tid] = qx[h];
-  norm_rope_rows<T>(sh, sh.x, GQA, QSA_D, A.q_norm, A.eps, A.rope, cs, sn);   // roped rows land in x
-#pragma unroll
-  for (int h = 0; h < GQA; ++h) {
-    const float yv = sh.x[h * QSA_D + tid];
-    const uint16_t hi = f32_to_bf16(yv);
-    sh.qh[h * QSA_D + tid] = hi;
-    sh.ql[h * QSA_D + tid] = f32_to_bf16(yv - bf16_to_f32(hi));
-  }
-  __syncthreads();
-  sh.x[tid] = kx;
-  norm_rope_rows<T>(sh, sh.knew, 1, QSA_D, A.k_norm, A.eps, A.rope, cs, sn);
-  sh.vnew[tid] = vx;
-  const int pg_cur = sh.pages[p / A.page_size];
-  const int prow = p % A.page_size;
-  if (split == 0) {     // the token's key and value into its page slot, for later steps
-    A.k_pool[(((long)pg_cur * A.hkv + g) * A.page_size + prow) * QSA_D + tid] = f32_to_bf16(sh.knew[tid]);
-    A.v_pool[(((long)pg_cur * A.hkv + g) * QSA_D + tid) * A.page_size + v_slot(prow)] = f32_to_bf16(vx);
-  }
-  __syncthreads();
-
-  // ---- 3. attention over this workgroup's items, one 32-token group per wave
+  // the attention work of this position, and whether this workgroup has any
   const int gpb = ratio >= 32 ? ratio / 32 : 1;
   const int n_blk_items = n_sel * gpb;
   const int ts = ((p + 1) / ratio) * ratio;
   const int n_tail = ts > p ? 0 : (p >> 5) - (ts >> 5) + 1;
   const int n_items = n_blk_items + n_tail;
-  if (leader && D.items) {
-    int2* items = D.items + (long)b * D.max_items;
-    for (int it = tid; it < n_items; it += DEC_NT) {
-      int t0, lo, hi;
-      if (it < n_blk_items) {
-        const int bs = sh.sel[it / gpb] * ratio;
-        if (ratio >= 32) { t0 = bs + (it % gpb) * 32; lo = 0; hi = 32; }
-        else { t0 = bs & ~31; lo = bs - t0; hi = lo + ratio; }
-      } else {
-        t0 = (ts & ~31) + (it - n_blk_items) * 32; lo = max(ts - t0, 0); hi = min(p + 1 - t0, 32);
-      }
-      items[1 + it] = make_item(sh.pages[t0 / A.page_size] * A.page_size + t0 % A.page_size, lo, hi);
-    }
-    if (tid == 0) items[0] = make_int2(n_items, 0);
-  }
-  if (leader && D.ids) {
-    for (int i = tid; i < n_sel; i += DEC_NT) D.ids[(long)b * topk + i] = sh.sel[i];
-    if (tid == 0) D.n_sel[b] = n_sel;
-  }
+  const int n_work = min((n_items + DEC_WAVES - 1) / DEC_WAVES, D.splits);
 
-  const int item = split * DEC_WAVES + wv;
+  // ---- 1. the indexer query and the pooled block key
+  if (j_new >= 0) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int ch = hh + 2 * c;
+      if (16 * ch < ratio) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (16 * ch + i < ratio) acc = add_rn(acc, rk[c][i]);
+        sh.chunk[ch][e128] = acc;
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) sh.x[tid + DEC_NT * k] = iqv[k];
+#pragma unroll
+  for (int h = 0; h < GQA; ++h) sh.x[X_Q + h * QSA_D + tid] = qx[h];
+  sh.x[X_K + tid] = kx;
+  sh.vnb[tid] = f32_to_bf16(vx);
+#pragma unroll
+  for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k)
+    if (tid + DEC_NT * k < n_lpages) sh.pages[tid + DEC_NT * k] = pg[k];
+  __syncthreads();
+  float pmean = 0.f;
+  if (j_new >= 0) {
+    // block mean: the 16-row chunk sums in order, then divided by the count
+    if (tid < IDX_D) {
+      float total = sh.chunk[0][tid];
+      for (int ch = 1; 16 * ch < ratio; ++ch) total = add_rn(total, sh.chunk[ch][tid]);
+      pmean = Act<T>::round(div_rn(total, (float)ratio));
+      sh.x[X_POOL + tid] = pmean;
+    }
+    __syncthreads();
+  }
+  norm_partials(sh, 0, SLOTS_FRONT);
+  __syncthreads();
+  norm_rinv(sh, 0, NR_Q, A.eps);
+  __syncthreads();
+  // y = round_T(x * rinv * w); the first `rope` channels then rotate with their
+  // partner, recomputed here from its x rather than exchanged
+  auto nrm = [&](float xv, float ri, float w) { return Act<T>::round(mul_rn(mul_rn(xv, ri), w)); };
+  auto rot = [&](float y, float yp, float c, float s) {
+    return add_rn(mul_rn(y, c), mul_rn(e128 < half ? -yp : yp, s));
+  };
+  {
+    float ri[NR_Q], xp_iq[2], xp_pool = 0.f;
+#pragma unroll
+    for (int r = 0; r < NR_Q; ++r) ri[r] = sh.rinv[r];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) xp_iq[k] = sh.x[(hh + 2 * k) * IDX_D + pe];
+    if (j_new >= 0) xp_pool = sh.x[X_POOL + pe];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int r = hh + 2 * k;
+      float y = 0.f;
+      if (r < A.idx_heads) {
+        y = nrm(iqv[k], ri[r], w_iq);
+        if (roped) y = rot(y, nrm(xp_iq[k], ri[r], w_iq2), cs, sn);
+      }
+      sh.iq[r * IDX_D + e128] = y;
+    }
+    if (j_new >= 0 && tid < IDX_D) {
+      float y = nrm(pmean, ri[NR_POOL], w_ik);
+      if (roped) y = rot(y, nrm(xp_pool, ri[NR_POOL], w_ik2), cs0, sn0);
+      sh.newkey[tid] = y;
+    }
+  }
+  __syncthreads();
+
+  // ---- 2. block scores and top-k (ties to the lower index)
+  if (scoring) {
+    score_blocks<DEC_NT>(sh.iq, sh.newkey, bk, n_elig, j_new, A.idx_heads, sh.u.key, nullptr, kp);
+    __syncthreads();
+    rank_topk<DEC_NT>(sh.u.key, n_elig, topk, sh.sel);
+  } else {
+    for (int i = tid; i < n_elig; i += DEC_NT) sh.sel[i] = i;
+  }
+  // the ticket has long come back by now: workgroups past the last batch leave
+  if (tid == 0) sh.ticket = (int)(ticket & (unsigned)(D.splits - 1));
+  __syncthreads();
+  const int batch = sh.ticket;
+  if (batch >= n_work) return;
+  const bool leader = batch == 0 && g == 0;       // writes the per-sequence side outputs
+
+  // ---- 3. first item's keys/values in flight while the query heads and key are normed
+  const int stride = D.splits * DEC_WAVES;
+  int item = batch * DEC_WAVES + wv;
+  int t0 = 0, lo = 0, hi = 0;
+  bf16x8_t kf[2][8], vf[16];
+  auto issue = [&]() {
+    item_span(item, n_blk_items, gpb, ratio, ts, p, sh.sel, t0, lo, hi);
+    const int page = sh.pages[t0 / A.page_size], row0 = t0 % A.page_size;
+    const uint16_t* kp0 = A.k_pool + (((long)page * A.hkv + g) * A.page_size + row0) * QSA_D;
+    const uint16_t* vp0 = A.v_pool + ((long)page * A.hkv + g) * QSA_D * A.page_size + row0;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int sk = 0; sk < 8; ++sk) kf[t][sk] = load_bf16x8(kp0 + (16 * t + col) * QSA_D + 32 * sk + 8 * quad);
+#pragma unroll
+    for (int db = 0; db < 16; ++db) vf[db] = load_bf16x8(vp0 + (16 * db + col) * A.page_size + 8 * quad);
+  };
+  if (item < n_items) issue();
+  norm_partials(sh, SLOTS_FRONT, SLOTS_ALL);
+  __syncthreads();
+  norm_rinv(sh, NR_Q, NR_ROWS, A.eps);
+  __syncthreads();
+  {
+    float ri[NR_ROWS - NR_Q], xp_q[GQA], xp_k = 0.f;
+#pragma unroll
+    for (int r = 0; r < NR_ROWS - NR_Q; ++r) ri[r] = sh.rinv[NR_Q + r];
+#pragma unroll
+    for (int h = 0; h < GQA; ++h) xp_q[h] = 0.f;
+    if (tid < rope) {
+#pragma unroll
+      for (int h = 0; h < GQA; ++h) xp_q[h] = sh.x[X_Q + h * QSA_D + pe];
+      xp_k = sh.x[X_K + pe];
+    }
+#pragma unroll
+    for (int h = 0; h < GQA; ++h) {
+      float y = nrm(qx[h], ri[h], w_q);
+      if (tid < rope) y = rot(y, nrm(xp_q[h], ri[h], w_q2), cs, sn);
+      // the attention MFMA takes q as bf16: hi + lo carries ~16 mantissa bits
+      const uint16_t qhi = f32_to_bf16(y);
+      sh.qb[h][tid] = qhi;
+      sh.qb[GQA + h][tid] = f32_to_bf16(y - bf16_to_f32(qhi));
+    }
+    float y = nrm(kx, ri[NR_K - NR_Q], w_k);
+    if (tid < rope) y = rot(y, nrm(xp_k, ri[NR_K - NR_Q], w_k2), cs, sn);
+    sh.knb[tid] = f32_to_bf16(y);
+  }
+  __syncthreads();
+
+  // ---- 4. attention over this workgroup's items
+  bf16x8_t qf[8];
+#pragma unroll
+  for (int sk = 0; sk < 8; ++sk) qf[sk] = *reinterpret_cast<const bf16x8_t*>(&sh.qb[col][32 * sk + 8 * quad]);
   f32x4_t acc[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
-  if (item < n_items) {
-    int t0, lo, hi;
-    if (item < n_blk_items) {
-      const int bs = sh.sel[item / gpb] * ratio;
-      if (ratio >= 32) { t0 = bs + (item % gpb) * 32; lo = 0; hi = 32; }
-      else { t0 = bs & ~31; lo = bs - t0; hi = lo + ratio; }
-    } else {
-      t0 = (ts & ~31) + (item - n_blk_items) * 32; lo = max(ts - t0, 0); hi = min(p + 1 - t0, 32);
-    }
-    const int page = sh.pages[t0 / A.page_size], row0 = t0 % A.page_size;
-    const uint16_t* kp = A.k_pool + (((long)page * A.hkv + g) * A.page_size + row0) * QSA_D;
-    const uint16_t* vp = A.v_pool + ((long)page * A.hkv + g) * QSA_D * A.page_size + row0;
-    bf16x8_t kf[2][8], vf[16];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int sk = 0; sk < 8; ++sk) kf[t][sk] = load_bf16x8(kp + (16 * t + col) * QSA_D + 32 * sk + 8 * quad);
-#pragma unroll
-    for (int db = 0; db < 16; ++db) vf[db] = load_bf16x8(vp + (long)(16 * db + col) * A.page_size + 8 * quad);
-    // the current token's row comes from this launch, not from the pages
+  while (item < n_items) {
+    // the current token's row comes from this launch, not from the pages: its
+    // key replaces whole 8-channel vectors of one lane, its value one element
+    // (column kappa) of the lanes whose quad holds that column
     if (p >= t0 && p < t0 + 32) {
       const int r = p - t0;
-      if (col == (r & 15)) {
+      const bool krow = col == (r & 15);
 #pragma unroll
-        for (int sk = 0; sk < 8; ++sk)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const __bf16 kv = __builtin_bit_cast(__bf16, f32_to_bf16(sh.knew[32 * sk + 8 * quad + e]));
-            if (r >> 4) kf[1][sk][e] = kv; else kf[0][sk][e] = kv;
-          }
+      for (int sk = 0; sk < 8; ++sk) {
+        const bf16x8_t kv = *reinterpret_cast<const bf16x8_t*>(&sh.knb[32 * sk + 8 * quad]);
+        if (r >> 4) kf[1][sk] = krow ? kv : kf[1][sk];
+        else kf[0][sk] = krow ? kv : kf[0][sk];
       }
       const int kappa = v_slot(r);
-      if (quad == (kappa >> 3)) {
+      const int dw = (kappa & 7) >> 1, sh16 = 16 * (kappa & 1);
+      const bool vcol = quad == (kappa >> 3);
 #pragma unroll
-        for (int db = 0; db < 16; ++db) vf[db][kappa & 7] = __builtin_bit_cast(__bf16, f32_to_bf16(sh.vnew[16 * db + col]));
+      for (int db = 0; db < 16; ++db) {
+        const unsigned val = sh.vnb[16 * db + col];
+        u32x4_t u = __builtin_bit_cast(u32x4_t, vf[db]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (vcol && i == dw) u[i] = (u[i] & ~(0xffffu << sh16)) | (val << sh16);
+        vf[db] = __builtin_bit_cast(bf16x8_t, u);
       }
     }
-    bf16x8_t qhi[8], qlo[8];
-    const bf16x8_t zero = {};
-#pragma unroll
-    for (int sk = 0; sk < 8; ++sk) {
-      qhi[sk] = col < GQA ? *reinterpret_cast<const bf16x8_t*>(sh.qh + col * QSA_D + 32 * sk + 8 * quad) : zero;
-      qlo[sk] = col < GQA ? *reinterpret_cast<const bf16x8_t*>(sh.ql + col * QSA_D + 32 * sk + 8 * quad) : zero;
-    }
+    // S^T = K Q^T: columns 0..7 take q hi, 8..15 q lo; lane col then adds its
+    // partner column col ^ 8 (DPP row rotate by 8) for the full-precision score
     f32x4_t sc[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int sk = 0; sk < 8; ++sk) {
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][sk], qhi[sk], c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][sk], qlo[sk], c, 0, 0, 0);
-      }
+      for (int sk = 0; sk < 8; ++sk) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][sk], qf[sk], c, 0, 0, 0);
       sc[t] = c;
     }
     float mx = -INFINITY;
@@ -935,27 +1078,39 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int tok = 16 * t + 4 * quad + v;
-        const float x = (tok >= lo && tok < hi) ? sc[t][v] * (1.0f / 16.0f) : -INFINITY;
+        const float full = sc[t][v] + dpp_f<0x128>(sc[t][v]);
+        const float x = (tok >= lo && tok < hi) ? full * (1.0f / 16.0f) : -INFINITY;
         sc[t][v] = x;
         mx = fmaxf(mx, x);
       }
     mx = xor32_max(xor16_max(mx));
-    m_run = mx;
+    const float m_new = fmaxf(m_run, mx);
+    const bool carry = m_run != -INFINITY;      // false on a wave's first item
+    const float rescale = carry ? __expf(m_run - m_new) : 0.f;
+    m_run = m_new;
     bf16x8_t pf;
+    float lsum = 0.f;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float pv = __expf(sc[t][v] - m_run);
-        l_run += pv;
+        const float pv = col < GQA ? __expf(sc[t][v] - m_new) : 0.f;
+        lsum += pv;
         pf[4 * t + v] = __builtin_bit_cast(__bf16, f32_to_bf16(pv));
       }
+    l_run = l_run * rescale + lsum;
+    if (carry) {
+#pragma unroll
+      for (int db = 0; db < 16; ++db) acc[db] = acc[db] * rescale;
+    }
 #pragma unroll
     for (int db = 0; db < 16; ++db) acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[db], pf, acc[db], 0, 0, 0);
+    item += stride;
+    if (item < n_items) issue();
   }
   l_run = xor32_sum(xor16_sum(l_run));
 
-  // ---- 4. merge the waves, publish the partial, last workgroup combines
+  // ---- 5. merge the waves, publish the partial, last workgroup combines
   __syncthreads();        // sh.u.key no longer read: reuse it for the wave merge
   if (quad == 0 && col < GQA) { sh.m[wv][col] = m_run; sh.l[wv][col] = l_run; }
   __syncthreads();
@@ -966,17 +1121,24 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
     const float wself = m_run == -INFINITY ? 0.f : __expf(m_run - M);
 #pragma unroll
     for (int db = 0; db < 16; ++db)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) sh.u.acc[wv][col][16 * db + 4 * quad + v] = acc[db][v] * wself;
+      *reinterpret_cast<float4*>(&sh.u.acc[wv][col][16 * db + 4 * quad]) =
+          make_float4(acc[db][0] * wself, acc[db][1] * wself, acc[db][2] * wself, acc[db][3] * wself);
   }
   __syncthreads();
-  const long gbase = ((long)b * A.hkv + g) * D.splits;
-  const long pbase = (gbase + split) * GQA;
-  for (int i = tid; i < GQA * QSA_D; i += DEC_NT) {
-    float o = 0.f;
+  const long gbase = (long)bg * D.splits;
+  const int ch = tid >> 5, d0 = (tid & 31) * 8;     // this thread's head and 8 channels
+  {
+    float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
 #pragma unroll
-    for (int w = 0; w < DEC_WAVES; ++w) o += sh.u.acc[w][i / QSA_D][i % QSA_D];
-    D.part_o[pbase * QSA_D + i] = o;
+    for (int w = 0; w < DEC_WAVES; ++w) {
+      const float4 a0 = *reinterpret_cast<const float4*>(&sh.u.acc[w][ch][d0]);
+      const float4 a1 = *reinterpret_cast<const float4*>(&sh.u.acc[w][ch][d0 + 4]);
+      o0.x += a0.x; o0.y += a0.y; o0.z += a0.z; o0.w += a0.w;
+      o1.x += a1.x; o1.y += a1.y; o1.z += a1.z; o1.w += a1.w;
+    }
+    const __amdgpu_buffer_rsrc_t rw = coherent_rsrc(D.part_o + (gbase + batch) * GQA * QSA_D, GQA * QSA_D * 4);
+    st_coherent4(rw, (ch * QSA_D + d0) * 4, o0);
+    st_coherent4(rw, (ch * QSA_D + d0 + 4) * 4, o1);
   }
   if (tid < GQA) {
     float Mh = -INFINITY, L = 0.f;
@@ -985,43 +1147,109 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
 #pragma unroll
     for (int w = 0; w < DEC_WAVES; ++w)
       if (sh.m[w][tid] != -INFINITY) L += sh.l[w][tid] * __expf(sh.m[w][tid] - Mh);
-    D.part_ml[(pbase + tid) * 2 + 0] = Mh;
-    D.part_ml[(pbase + tid) * 2 + 1] = L;
+    st_coherent(D.part_ml + ((gbase + batch) * GQA + tid) * 2, Mh, L);
   }
-  __threadfence();
+  // the stores that outlive this step, issued last so that no earlier wait
+  // drains them: the token's key/value into its page slot (batch 0 of each kv
+  // head), and per sequence (the leader) its raw indexer key, the pooled key of
+  // a completed block and the optional inspection outputs
+  if (batch == 0) {
+    const int pg_cur = sh.pages[p / A.page_size], prow = p % A.page_size;
+    A.k_pool[(((long)pg_cur * A.hkv + g) * A.page_size + prow) * QSA_D + tid] = sh.knb[tid];
+    A.v_pool[(((long)pg_cur * A.hkv + g) * QSA_D + tid) * A.page_size + v_slot(prow)] = sh.vnb[tid];
+  }
+  if (leader) {
+    if (tid < IDX_D) {
+      Act<T>::store(A.raw_keys, ((long)b * A.max_ctx + p) * IDX_D + tid, ikv);
+      if (j_new >= 0) A.block_keys[((long)b * A.max_blocks + j_new) * IDX_D + tid] = sh.newkey[tid];
+    }
+    if (D.iq_out)
+      for (int i = tid; i < A.idx_heads * IDX_D; i += DEC_NT) D.iq_out[(long)b * A.idx_heads * IDX_D + i] = sh.iq[i];
+    if (D.items) {
+      int2* items = D.items + (long)b * D.max_items;
+      for (int it = tid; it < n_items; it += DEC_NT) {
+        int u0, ulo, uhi;
+        item_span(it, n_blk_items, gpb, ratio, ts, p, sh.sel, u0, ulo, uhi);
+        items[1 + it] = make_item(sh.pages[u0 / A.page_size] * A.page_size + u0 % A.page_size, ulo, uhi);
+      }
+      if (tid == 0) items[0] = make_int2(n_items, 0);
+    }
+    if (D.ids) {
+      for (int i = tid; i < n_sel; i += DEC_NT) D.ids[(long)b * topk + i] = sh.sel[i];
+      if (tid == 0) D.n_sel[b] = n_sel;
+    }
+  }
+  // every store of this workgroup complete (its partial at the point of
+  // coherence), then count it in; the last working workgroup merges
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(D.counters + (long)b * A.hkv + g, 1u, __ATOMIC_ACQ_REL,
+    const unsigned prev = __hip_atomic_fetch_add(D.counters + bg * DEC_CTR_STRIDE, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
-    sh.last = prev == (unsigned)(D.splits - 1);
+    sh.last = prev == (unsigned)(n_work - 1);
   }
   __syncthreads();
   if (!sh.last) return;
-  __threadfence();
-  // combine: weights per (split, head) in LDS, then every (head, d) sums its splits
-  if (tid < GQA) {
-    float M = -INFINITY;
-    for (int s = 0; s < D.splits; ++s) M = fmaxf(M, D.part_ml[((gbase + s) * GQA + tid) * 2]);
-    float L = 0.f;
-    for (int s = 0; s < D.splits; ++s) {
-      const float ms = D.part_ml[((gbase + s) * GQA + tid) * 2];
-      const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
-      L += D.part_ml[((gbase + s) * GQA + tid) * 2 + 1] * w;
-      sh.u.w[s][tid] = w;
-    }
-    sh.rinv[tid] = 1.0f / L;
-  }
-  __syncthreads();
+  // combine: thread (head ch, channels d0..d0+7); the head's 32 lanes share its partials
+  const int sl = tid & 31;
+  // partials of batches 0 .. n_work-1 (reads past them return zeros)
+  const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(D.part_o + gbase * GQA * QSA_D, n_work * GQA * QSA_D * 4);
+  const int obyte = (ch * QSA_D + d0) * 4;
+  float4 v[DEC_COMB][2];
 #pragma unroll
-  for (int h = 0; h < GQA; ++h) {
-    float o = 0.f;
-    for (int s = 0; s < D.splits; ++s) o += D.part_o[((gbase + s) * GQA + h) * QSA_D + tid] * sh.u.w[s][h];
-    const int hq = g * GQA + h;
-    const float att = Act<T>::round(o * sh.rinv[h]);
-    const float gate = Act<T>::round(sigmoid_f(Act<T>::load(A.qg, ((long)b * A.hq + hq) * (2 * QSA_D) + QSA_D + tid)));
-    Act<T>::store(D.out, ((long)b * A.hq + hq) * QSA_D + tid, att * gate);
+  for (int k = 0; k < DEC_COMB; ++k) {
+    v[k][0] = ld_coherent4(ro, obyte + k * GQA * QSA_D * 4);
+    v[k][1] = ld_coherent4(ro, obyte + k * GQA * QSA_D * 4 + 16);
   }
-  if (tid == 0) __hip_atomic_store(D.counters + (long)b * A.hkv + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float gate[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) gate[i] = Act<T>::load(A.qg, ((long)b * A.hq + g * GQA + ch) * (2 * QSA_D) + QSA_D + d0 + i);
+  float2 ml[DEC_MAX_SPLITS / 32];
+#pragma unroll
+  for (int k = 0; k < DEC_MAX_SPLITS / 32; ++k) {
+    const int s = sl + 32 * k;
+    ml[k] = s < n_work ? ld_coherent(D.part_ml + ((gbase + s) * GQA + ch) * 2) : make_float2(-INFINITY, 0.f);
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < DEC_MAX_SPLITS / 32; ++k) M = fmaxf(M, ml[k].x);
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, 32));
+  float L = 0.f;
+#pragma unroll
+  for (int k = 0; k < DEC_MAX_SPLITS / 32; ++k) {
+    const int s = sl + 32 * k;
+    const float w = ml[k].x == -INFINITY ? 0.f : __expf(ml[k].x - M);
+    L += ml[k].y * w;
+    if (s < n_work) sh.w[s][ch] = w;
+  }
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) L += __shfl_xor(L, o, 32);
+  __syncthreads();
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  auto accumulate = [&](int s0) {
+#pragma unroll
+    for (int k = 0; k < DEC_COMB; ++k) {
+      const float w = s0 + k < n_work ? sh.w[s0 + k][ch] : 0.f;
+      o[0] += v[k][0].x * w; o[1] += v[k][0].y * w; o[2] += v[k][0].z * w; o[3] += v[k][0].w * w;
+      o[4] += v[k][1].x * w; o[5] += v[k][1].y * w; o[6] += v[k][1].z * w; o[7] += v[k][1].w * w;
+    }
+  };
+  accumulate(0);
+  for (int s0 = DEC_COMB; s0 < n_work; s0 += DEC_COMB) {
+#pragma unroll
+    for (int k = 0; k < DEC_COMB; ++k) {
+      v[k][0] = ld_coherent4(ro, obyte + (s0 + k) * GQA * QSA_D * 4);
+      v[k][1] = ld_coherent4(ro, obyte + (s0 + k) * GQA * QSA_D * 4 + 16);
+    }
+    accumulate(s0);
+  }
+  const float rl = 1.0f / L;
+  const long obase = ((long)b * A.hq + g * GQA + ch) * QSA_D + d0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    Act<T>::store(D.out, obase + i, Act<T>::round(o[i] * rl) * Act<T>::round(sigmoid_f(gate[i])));
+  if (tid == 0) __hip_atomic_store(D.counters + bg * DEC_CTR_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 int check_geom(const qm_qsa_geom* g, const char* who) {
@@ -1268,14 +1496,26 @@ extern "C" int qm_qsa_decode_front(const qm_qsa_geom* g, const void* qg, const v
 
 extern "C" int qm_qsa_decode_splits(const qm_qsa_geom* g, int max_position) {
   if (!g || g->ratio <= 0 || g->budget < g->ratio || max_position < 0) return 1;
-  const int n = (items_at(g, max_position) + DEC_WAVES - 1) / DEC_WAVES;
-  return n < 1 ? 1 : n;
+  // item counts are not monotone in the position (the tail shrinks when a
+  // block completes): take the largest over the last `ratio` positions, which
+  // bounds every earlier one since the selected count never decreases
+  int items = 0;
+  for (int p = max_position - g->ratio < 0 ? 0 : max_position - g->ratio; p <= max_position; ++p) {
+    const int n = items_at(g, p);
+    items = n > items ? n : items;
+  }
+  // the batches rounded up to a power of two: the spare workgroups let the ones
+  // that start first take the work
+  const int n = (items + DEC_WAVES - 1) / DEC_WAVES;
+  int g2 = 1;
+  while (g2 < n && g2 < DEC_MAX_SPLITS) g2 <<= 1;
+  return g2;
 }
 
 extern "C" size_t qm_qsa_decode_workspace(const qm_qsa_geom* g, int splits) {
   if (!g || splits <= 0) return 0;
   return part_o_bytes(g, g->batch, splits) + qm_align256((size_t)g->batch * g->n_kv_heads * splits * GQA * 2 * 4) +
-         qm_align256((size_t)g->batch * g->n_kv_heads * sizeof(unsigned));
+         qm_align256((size_t)g->batch * g->n_kv_heads * 2 * DEC_CTR_STRIDE * sizeof(unsigned));
 }
 
 extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k_new, const void* v_new, const void* iq,
@@ -1290,15 +1530,18 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
       !positions || !page_table || !k_pool || !v_pool || !raw_keys || !block_keys || !out)
     return qm_fail(QM_ERR_ARG, "qm_qsa_decode: null pointer");
   if ((ids != nullptr) != (n_sel != nullptr)) return qm_fail(QM_ERR_ARG, "qm_qsa_decode: ids and n_sel go together");
-  if (g->max_blocks > DEC_MAX_BLOCKS || g->max_pages > DEC_MAX_PAGES || g->budget / g->ratio > DEC_MAX_TOPK)
-    return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_decode: more than 2048 blocks or pages, or top-k above 256 "
-                                       "(use qm_qsa_prep + qm_qsa_select + qm_qsa_attend)");
-  if (splits <= 0 || splits > DEC_MAX_SPLITS) return qm_fail(QM_ERR_ARG, "qm_qsa_decode: bad split count");
+  if (g->max_blocks > DEC_MAX_BLOCKS || g->max_pages > DEC_MAX_PAGES || g->budget / g->ratio > DEC_MAX_TOPK ||
+      g->ratio > DEC_MAX_RATIO)
+    return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_decode: more than 2048 blocks or pages, top-k above 256 or ratio "
+                                       "above 64 (use qm_qsa_prep + qm_qsa_select + qm_qsa_attend)");
+  if (splits <= 0 || splits > DEC_MAX_SPLITS || (splits & (splits - 1)))
+    return qm_fail(QM_ERR_ARG, "qm_qsa_decode: splits must be a power of two up to 128 (qm_qsa_decode_splits)");
   if (!workspace || workspace_bytes < qm_qsa_decode_workspace(g, splits))
     return qm_fail(QM_ERR_WORKSPACE, "qm_qsa_decode: workspace too small");
-  // counters first, at an offset that does not depend on the split count
+  // counters first (done counters, then ticket counters), at an offset that
+  // does not depend on the split count
   char* ws = static_cast<char*>(workspace);
-  const size_t c_bytes = qm_align256((size_t)g->batch * g->n_kv_heads * sizeof(unsigned));
+  const size_t c_bytes = qm_align256((size_t)g->batch * g->n_kv_heads * 2 * DEC_CTR_STRIDE * sizeof(unsigned));
   const size_t ml_bytes = qm_align256((size_t)g->batch * g->n_kv_heads * splits * GQA * 2 * 4);
   dim3 grid(splits, g->n_kv_heads, g->batch);
   auto fill = [&](auto& D) {
@@ -1307,6 +1550,7 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
     D.part_o = reinterpret_cast<float*>(ws + c_bytes + ml_bytes);
     D.ids = ids; D.n_sel = n_sel; D.items = static_cast<int2*>(items); D.iq_out = iq_out;
     D.splits = splits; D.topk = g->budget / g->ratio; D.max_items = item_stride(g);
+    D.ticket_off = g->batch * g->n_kv_heads * DEC_CTR_STRIDE;
   };
   if (g->act_dtype == QM_ACT_F32) {
     DecArgs<float> D;

@@ -242,7 +242,8 @@ class Qwen4MixModel:
     def fused_decode_fits(self, cache) -> bool:
         """Whether qm_qsa_decode (one launch) covers this cache's geometry."""
         c = self.config
-        return cache.max_blocks <= 2048 and cache.max_pages <= 2048 and c.block_topk <= 256
+        return (cache.max_blocks <= 2048 and cache.max_pages <= 2048 and c.block_topk <= 256
+                and c.indexer_compress_ratio <= 64)
 
     def _full_attention(self, hidden, layer: int, cos, sin, cache, query_offset: int) -> torch.Tensor:
         """reference/model.py:331-383."""

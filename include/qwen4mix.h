@@ -14,10 +14,14 @@
  *   DeltaNet recurrent state  float32 [B, Hv, d_k, d_v]   (reference/cache.py:24)
  *   DeltaNet conv ring        act     [B, conv_dim, K]    slot p % K holds the
  *                              input of the token at position p
- *   QSA K pool                bf16    [n_pages, Hkv, P, d]
- *   QSA V pool                bf16    [n_pages, Hkv, d, P]  tokens within each
- *                              32-token group stored in MFMA operand order
- *                              (qm_v_slot() gives the column of a page row)
+ *   QSA K pool                bf16    [n_pages, Hkv, P * d]  each page of a
+ *                              kv head in MFMA lane order: 16-token x
+ *                              32-channel tiles of 1 KB
+ *   QSA V pool                bf16    [n_pages, Hkv, P * d]  32-token x
+ *                              16-channel tiles of 1 KB, tokens of a group in
+ *                              the PV MFMA's order (qm_v_slot)
+ *                              (qm_qsa_page_index() maps (row, channel) of a
+ *                              page to its element offset in either pool)
  *   page table                int32   [B, max_pages]  logical page -> physical
  *   indexer raw keys          act     [B, max_ctx, idx_dim]
  *   indexer block cache       float32 [B, max_blocks, idx_dim]  pooled, normed,
@@ -134,8 +138,13 @@ typedef struct qm_qsa_geom {
   float eps;        /* rms_norm_eps                                       */
 } qm_qsa_geom;
 
-/* Column of page row `row` in the transposed V pool page. */
+/* Position of page row `row` among the 32 token slots of its V tile group. */
 int qm_v_slot(int row);
+/* Element offsets, within one page of one kv head, of (row, channel) in the
+ * K pool (k_index) and the V pool (v_index), for every row < page_size and
+ * channel < head_dim (row-major [page_size, head_dim] int arrays). Host only;
+ * for export, import and inspection of the pools. */
+int qm_qsa_page_index(int page_size, int head_dim, int* k_index, int* v_index);
 
 /* Per-token preparation for a decode step (or the S rows of a prefill chunk):
  * q/k RMS norm and partial rope, q|gate split (reference/model.py:345-356);

@@ -148,9 +148,8 @@ def test_decode_core_matches_oracle(gpu, pos, dtype):
     # the appended token sits at its page slot, bit-exact (bf16 of the roped key)
     P = 64
     page = int(cache.page_table[0, pos // P])
-    assert torch.equal(cache[3].k_pool[page, :, pos % P].cpu(), k_new[0, :, 0].to(torch.bfloat16))
-    col = gpu.native.load().qm_v_slot(pos % P)
-    assert torch.equal(cache[3].v_pool[page, :, :, col].cpu(), v_new[0, :, 0].to(torch.bfloat16))
+    assert torch.equal(cache[3].page_row("k", page, pos % P).cpu(), k_new[0, :, 0].to(torch.bfloat16))
+    assert torch.equal(cache[3].page_row("v", page, pos % P).cpu(), v_new[0, :, 0].to(torch.bfloat16))
 
 
 def test_page_gather_round_trip_is_bit_exact(gpu):

@@ -48,6 +48,33 @@ def test_v_slot_is_a_permutation_of_each_group(qm):
         assert all(c // 32 == r // 32 for r, c in enumerate(cols))
 
 
+def test_page_index_is_a_permutation_in_lane_order(qm):
+    """Each pool page is a permutation of its [P, d] rows, and every 1 KB tile
+    holds one MFMA operand: K tiles 16 tokens x 32 channels, V tiles 32 tokens
+    x 16 channels (lane order checked against the operand layout)."""
+    import numpy as np
+    lib = qm.native.load()
+    P, d = 64, 256
+    k = (ctypes.c_int * (P * d))()
+    v = (ctypes.c_int * (P * d))()
+    assert lib.qm_qsa_page_index(P, d, k, v) == 0
+    k = np.array(k).reshape(P, d)
+    v = np.array(v).reshape(P, d)
+    for idx in (k, v):
+        assert sorted(idx.ravel().tolist()) == list(range(P * d))
+    r, c = np.meshgrid(np.arange(P), np.arange(d), indexing="ij")
+    # K: tile (r // 16, c // 32); lane = r % 16 + 16 * ((c % 32) // 8); element c % 8
+    assert np.array_equal(k // 512, (r // 16) * 8 + c // 32)
+    assert np.array_equal((k % 512) // 8, r % 16 + 16 * ((c % 32) // 8))
+    assert np.array_equal(k % 8, c % 8)
+    # V: tile (r // 32, c // 16); lane = c % 16 + 16 * (slot // 8); element slot % 8
+    slot = np.array([lib.qm_v_slot(int(x)) % 32 for x in range(P)])[r]
+    assert np.array_equal(v // 512, (r // 32) * 16 + c // 16)
+    assert np.array_equal((v % 512) // 8, c % 16 + 16 * (slot // 8))
+    assert np.array_equal(v % 8, slot % 8)
+    assert lib.qm_qsa_page_index(48, d, (ctypes.c_int * (48 * d))(), (ctypes.c_int * (48 * d))()) == -1
+
+
 def test_bad_geometry_is_rejected_without_a_launch(qm):
     n = qm.native
     lib = n.load()

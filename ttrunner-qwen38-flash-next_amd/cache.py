@@ -8,8 +8,10 @@ reference field     device storage here
 ==================  ==============================================================
 conv_state          ``conv_ring`` [B, conv_dim, K] (act); slot p % K = input at p
 recurrent_state     ``recurrent_state`` [B, Hv, d, d] float32 (same tensor)
-keys / values       ``k_pool`` [n_pages, Hkv, P, d] / ``v_pool`` [n_pages, Hkv, d, P]
-                    bf16 under ``page_table`` [B, max_pages] int32
+keys / values       ``k_pool`` / ``v_pool`` [n_pages, Hkv, P * d] bf16 under
+                    ``page_table`` [B, max_pages] int32; each page of a kv head
+                    in the attention kernels' MFMA lane order
+                    (``qm_qsa_page_index`` maps (row, channel) to an offset)
 indexer_keys        ``raw_keys`` [B, max_ctx, idx_dim] (act) plus ``block_keys``
                     [B, max_blocks, idx_dim] float32 (pooled, normed, roped)
 ==================  ==============================================================
@@ -21,6 +23,8 @@ reuse and tests). The kernels never go through these properties.
 """
 
 from __future__ import annotations
+
+import ctypes
 
 import torch
 
@@ -64,8 +68,8 @@ class MixLayerCache:
         n_pages = o.n_pages
         # zero-filled: rows beyond a sequence's end are read (with weight 0) by
         # the tail group, so they must hold finite values
-        self.k_pool = torch.zeros(n_pages, cfg.num_kv_heads, P, d, dtype=torch.bfloat16, device=o.device)
-        self.v_pool = torch.zeros(n_pages, cfg.num_kv_heads, d, P, dtype=torch.bfloat16, device=o.device)
+        self.k_pool = torch.zeros(n_pages, cfg.num_kv_heads, P * d, dtype=torch.bfloat16, device=o.device)
+        self.v_pool = torch.zeros(n_pages, cfg.num_kv_heads, P * d, dtype=torch.bfloat16, device=o.device)
         self.raw_keys = torch.zeros(batch, o.max_ctx, cfg.indexer_head_dim, dtype=dtype, device=o.device)
         self.block_keys = torch.zeros(batch, o.max_blocks, cfg.indexer_head_dim, dtype=torch.float32,
                                       device=o.device)
@@ -100,13 +104,24 @@ class MixLayerCache:
         pages = self.page_table[:, tok // P].long()          # [B, n]
         return pages, (tok % P).long()
 
+    def _rows(self, pool, index):
+        """The pool as [n_pages, Hkv, P, d] rows (a gathered copy)."""
+        cfg = self._owner.config
+        n, h = pool.shape[:2]
+        return pool[:, :, index].view(n, h, cfg.page_size, cfg.head_dim)
+
+    def _store_rows(self, pool, index, rows_view):
+        n, h = pool.shape[:2]
+        pool[:, :, index] = rows_view.reshape(n, h, -1)
+
     @property
     def keys(self):
         if self.k_pool is None or self.n_tokens == 0:
             return None
         pages, rows = self._token_slots(self.n_tokens)
+        ref = self._rows(self.k_pool, self._owner.k_index)
         # [B, n, Hkv, d] -> [B, Hkv, n, d]
-        return self.k_pool[pages, :, rows[None].expand_as(pages)].permute(0, 2, 1, 3).float()
+        return ref[pages, :, rows[None].expand_as(pages)].permute(0, 2, 1, 3).float()
 
     @keys.setter
     def keys(self, value):
@@ -114,8 +129,9 @@ class MixLayerCache:
         batch, _, n, _ = value.shape
         self.ensure_qsa(batch, self._owner.dtype)
         pages, rows = self._token_slots(n)
-        v = value.to(self.k_pool.device).permute(0, 2, 1, 3).to(torch.bfloat16)   # [B, n, Hkv, d]
-        self.k_pool[pages, :, rows[None].expand_as(pages)] = v
+        ref = self._rows(self.k_pool, self._owner.k_index)
+        ref[pages, :, rows[None].expand_as(pages)] = value.to(ref.device).permute(0, 2, 1, 3).to(torch.bfloat16)
+        self._store_rows(self.k_pool, self._owner.k_index, ref)
         self.n_tokens = n
 
     @property
@@ -123,20 +139,26 @@ class MixLayerCache:
         if self.v_pool is None or self.n_tokens == 0:
             return None
         pages, rows = self._token_slots(self.n_tokens)
-        cols = self._owner.v_cols(rows)
-        # [B, n, Hkv, d]
-        out = self.v_pool[pages, :, :, cols[None].expand_as(pages)]
-        return out.permute(0, 2, 1, 3).to(self._owner.dtype)
+        ref = self._rows(self.v_pool, self._owner.v_index)
+        # [B, n, Hkv, d] -> [B, Hkv, n, d]
+        return ref[pages, :, rows[None].expand_as(pages)].permute(0, 2, 1, 3).to(self._owner.dtype)
 
     @values.setter
     def values(self, value):
         batch, _, n, _ = value.shape
         self.ensure_qsa(batch, self._owner.dtype)
         pages, rows = self._token_slots(n)
-        cols = self._owner.v_cols(rows)
-        v = value.to(self.v_pool.device).permute(0, 2, 1, 3).to(torch.bfloat16)   # [B, n, Hkv, d]
-        self.v_pool[pages, :, :, cols[None].expand_as(pages)] = v
+        ref = self._rows(self.v_pool, self._owner.v_index)
+        ref[pages, :, rows[None].expand_as(pages)] = value.to(ref.device).permute(0, 2, 1, 3).to(torch.bfloat16)
+        self._store_rows(self.v_pool, self._owner.v_index, ref)
         self.n_tokens = n
+
+    def page_row(self, pool: str, page: int, row: int) -> torch.Tensor:
+        """Row `row` of physical page `page` of the K or V pool, [Hkv, d]."""
+        o = self._owner
+        base = self.k_pool if pool == "k" else self.v_pool
+        index = (o.k_index if pool == "k" else o.v_index).view(o.config.page_size, -1)[row]
+        return base[page][:, index]
 
     @property
     def indexer_keys(self):
@@ -189,13 +211,15 @@ class MixHybridCache:
         else:
             raise ValueError(f"unknown page_table {page_table!r}")
         self.page_table = pt.to(self.device)
-        slots = torch.tensor([native.load().qm_v_slot(r) for r in range(P)], dtype=torch.long)
-        self._v_slot = slots.to(self.device)
+        d = config.head_dim
+        k_index = (ctypes.c_int * (P * d))()
+        v_index = (ctypes.c_int * (P * d))()
+        native.call("qm_qsa_page_index", P, d, k_index, v_index)
+        # offset in a page of (row, channel), row-major over [P, d]
+        self.k_index = torch.tensor(list(k_index), dtype=torch.long, device=self.device)
+        self.v_index = torch.tensor(list(v_index), dtype=torch.long, device=self.device)
         self.layers = [MixLayerCache(self) for _ in range(num_layers)]
         self.position_ids = None
-
-    def v_cols(self, rows: torch.Tensor) -> torch.Tensor:
-        return self._v_slot[rows]
 
     def __getitem__(self, idx: int) -> MixLayerCache:
         return self.layers[idx]

@@ -18,6 +18,8 @@
 // the way torch's vectorised CPU sum does (see torch_row_sumsq), rsqrt is
 // 1/sqrt, and every multiply and add of the rope is rounded separately.
 
+#include <type_traits>
+
 #include "common.h"
 #include "qwen4mix_internal.h"
 
@@ -32,6 +34,22 @@ constexpr int PREP_NT = 256;
 __host__ __device__ __forceinline__ int v_slot(int row) {
   const int t = row & 31;
   return (row & ~31) + 8 * ((t & 15) >> 2) + 4 * (t >> 4) + (t & 3);
+}
+
+// Page layouts (one page of one kv head = P x 256 bf16): both pools keep their
+// MFMA operands in lane order, so every wave-wide 16-byte load reads 1 KB of
+// contiguous memory.
+//   K: 16-token tiles x 8 steps of 32 channels; (tile, step) holds the A
+//      operand of one 16x16x32 MFMA, lane = token % 16 + 16 * channel octet.
+//   V: 32-token groups x 16 blocks of 16 channels; (group, block) holds the A
+//      operand of the PV MFMA, lane = channel % 16 + 16 * slot octet, the
+//      tokens of a group in v_slot order.
+__host__ __device__ __forceinline__ int k_page_index(int row, int dim) {
+  return ((((row >> 4) * 8 + (dim >> 5)) * 64 + (row & 15) + 16 * ((dim & 31) >> 3)) << 3) + (dim & 7);
+}
+__host__ __device__ __forceinline__ int v_page_index(int row, int dim) {
+  const int s = v_slot(row) & 31;
+  return ((((row >> 5) * 16 + (dim >> 4)) * 64 + (dim & 15) + 16 * (s >> 3)) << 3) + (s & 7);
 }
 
 // y = rope(round_T(rms_norm(x) * w)) for one row of `n` channels held in LDS
@@ -131,10 +149,9 @@ __device__ void prep_head(const PrepArgs<T>& A, int b, int s, int role) {
   const float y = norm_rope_row<T>(s_x, s_y, s_scr, QSA_D, A.k_norm, A.eps, A.rope, cs, sn);
   const int page = A.page_table[(long)b * A.max_pages + pos / A.page_size];
   const int prow = pos % A.page_size;
-  const long kbase = (((long)page * A.hkv + g) * A.page_size + prow) * QSA_D;
-  A.k_pool[kbase + tid] = f32_to_bf16(y);
-  const long vbase = (((long)page * A.hkv + g) * QSA_D + tid) * A.page_size + v_slot(prow);
-  A.v_pool[vbase] = f32_to_bf16(Act<T>::load(A.v_new, src + tid));
+  const long pbase = ((long)page * A.hkv + g) * A.page_size * QSA_D;
+  A.k_pool[pbase + k_page_index(prow, tid)] = f32_to_bf16(y);
+  A.v_pool[pbase + v_page_index(prow, tid)] = f32_to_bf16(Act<T>::load(A.v_new, src + tid));
 }
 
 template <typename T>
@@ -530,15 +547,16 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void qsa_attend_kernel(AttnArgs A) 
   if (item < n_items) {
     const int page = desc.x / A.page_size, row0 = desc.x % A.page_size;
     const int lo = desc.y & 0xff, hi = desc.y >> 8;
-    const uint16_t* kp = A.k_pool + (((long)page * A.hkv + g) * A.page_size + row0) * QSA_D;
-    const uint16_t* vp = A.v_pool + ((long)page * A.hkv + g) * QSA_D * A.page_size + row0;
+    const long pbase = ((long)page * A.hkv + g) * A.page_size * QSA_D;
+    const uint16_t* kp = A.k_pool + pbase + (row0 >> 4) * 8 * 512 + lane * 8;
+    const uint16_t* vp = A.v_pool + pbase + (row0 >> 5) * 16 * 512 + lane * 8;
     bf16x8_t kf[2][8], vf[16];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int sk = 0; sk < 8; ++sk) kf[t][sk] = load_bf16x8(kp + (16 * t + col) * QSA_D + 32 * sk + 8 * quad);
+      for (int sk = 0; sk < 8; ++sk) kf[t][sk] = load_bf16x8(kp + (t * 8 + sk) * 512);
 #pragma unroll
-    for (int db = 0; db < 16; ++db) vf[db] = load_bf16x8(vp + (long)(16 * db + col) * A.page_size + 8 * quad);
+    for (int db = 0; db < 16; ++db) vf[db] = load_bf16x8(vp + db * 512);
 
     // scores: rows = tokens 16t + 4 quad + v, column = head col
     f32x4_t sc[2];
@@ -667,42 +685,47 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T> A) {
 }
 
 // ---------------------------------------------------------------------------
-// fused decode step: one launch per token
+// decode step: two launches per token
 // ---------------------------------------------------------------------------
-// Grid (G, kv head g, sequence b) of 256-thread workgroups, G a power of two
-// at least the number of 4-item batches of attention work. The chip's dies
-// start a launch's workgroups up to a few microseconds apart, so the batches
-// are not tied to blockIdx: each workgroup takes a ticket from a per-(b, g)
-// counter as it starts, does batch (ticket mod G), and leaves at once when
-// that is past the last batch. The counter only grows, by exactly G per
-// launch, so the tickets of a launch cover every residue mod G. A working
-// workgroup then:
-//   0. issues its loads: those that do not depend on the position first (its
-//      8 query heads, the token's key and value, the indexer query and key,
-//      the norm weights), then the rope row, the page-table row, the first 128
-//      block keys and, when this token completes a block, its raw keys;
+// qsa_decode_kernel, grid (G, kv head g, sequence b) of 256-thread workgroups,
+// G at least the position's number of 32-token attention items. One workgroup
+// attends one item: spreading the key/value reads over one item per compute
+// unit is what lets them run near the memory system's speed (a unit reading
+// four items' 128 KB takes twice as long as four units reading 32 KB each).
+// Items are not tied to blockIdx: each workgroup takes a ticket from a
+// per-(b, g) counter as it starts and does item `ticket`, so the workgroups
+// that start first (the dies start a launch's workgroups microseconds apart)
+// take the work and spare ones leave; qsa_decode_combine resets the counter.
+// A workgroup:
+//   0. takes its ticket and issues its loads: those that do not depend on the
+//      position first (its 8 query heads, the token's key and value, the
+//      indexer query and key, the norm weights), then the rope row, the
+//      page-table row, the first 128 block keys and, when this token completes
+//      a block, that block's raw keys;
 //   1. RMS-norms and ropes the indexer query and the pooled block key (sums of
 //      squares in torch's order);
-//   2. scores the eligible blocks and ranks them (every working workgroup
-//      redundantly: ~65 KB of L2-resident reads, cheaper than a hand-off);
-//   3. issues the key/value loads of its first item, then norms and ropes the
-//      8 query heads and the key while those loads are in flight;
-//   4. attends its items, one 32-token group per wave at a time (items
-//      batch*4 + wave, then + 4G, ...), on bf16 MFMA with an online softmax;
-//      the item holding the current token takes its key/value from LDS;
-//   5. writes its (max, sum, output) partial; the last working workgroup of
-//      the kv head (a completion counter) merges all partials, applies
-//      the sigmoid gate and resets the counter. Batch 0 of each kv head also
-//      appends the token's key/value to its page slot, and batch 0 of kv head
-//      0 writes the per-sequence outputs (raw indexer key, pooled key).
+//   2. scores the eligible blocks and ranks them (redundantly in every
+//      workgroup whose item is a selected block's: ~65 KB of L2-resident reads,
+//      cheaper than a hand-off between workgroups);
+//   3. issues its item's key/value loads (waves 0-1: the two 16-token key
+//      tiles; wave w: value channels 64w..64w+63), then norms and ropes the 8
+//      query heads and the key while they are in flight;
+//   4. scores the item on bf16 MFMA (waves 0-1), shares the scores through LDS,
+//      and every wave forms the softmax weights and its 64 output channels;
+//      the current token's key/value come from LDS, not the pages;
+//   5. writes the item's (max, sum, unnormalised output) partial. The workgroup
+//      of item 0 also appends the token's key/value to its page slot, and for
+//      kv head 0 writes the per-sequence outputs (raw indexer key, pooled key).
+// qsa_decode_combine, grid (query head, sequence), merges the items' partials
+// of its head, applies the sigmoid gate and resets the ticket counter.
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_NT = 64 * DEC_WAVES;
 constexpr int DEC_MAX_BLOCKS = 2048;
 constexpr int DEC_MAX_PAGES = 2048;
 constexpr int DEC_MAX_TOPK = 256;
-constexpr int DEC_MAX_SPLITS = 128;   // workgroups per (sequence, kv head)
+constexpr int DEC_MAX_ITEMS = 1024;   // workgroups per (sequence, kv head)
 constexpr int DEC_MAX_RATIO = 64;     // raw keys of a completed block are held in registers
-constexpr int DEC_COMB = 18;          // partials merged per batch of loads in the combine
+constexpr int DEC_CTR_STRIDE = 32;    // counters 128 bytes apart, one cache line each
 
 // rows of the two norm passes, at these LDS offsets: the 4 indexer-query rows
 // and the pooled block key (128 wide) first, then the 8 query heads and the
@@ -711,37 +734,6 @@ constexpr int NR_POOL = 4, NR_Q = 5, NR_K = 13, NR_ROWS = 14;
 constexpr int X_POOL = 4 * IDX_D, X_Q = X_POOL + IDX_D, X_K = X_Q + GQA * QSA_D, X_SIZE = X_K + QSA_D;
 constexpr int SLOTS_FRONT = NR_Q * 32, SLOTS_ALL = NR_ROWS * 32;   // 32 partial sums per row
 
-// Partials cross the dies as relaxed system-scope atomics: written through to,
-// and read back from, the device's point of coherence, so that publishing them
-// needs no L2 writeback (a release fence walks the die's whole L2, and the
-// fences of workgroups sharing a die queue behind each other) and reading them
-// no L2 invalidate. A writer waits for its stores to complete before it counts
-// itself in; the last workgroup reads only after it has seen the count.
-__device__ __forceinline__ void st_coherent(float* p, float a, float b) {
-  const unsigned long long v = (static_cast<unsigned long long>(__float_as_uint(b)) << 32) | __float_as_uint(a);
-  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ float2 ld_coherent(const float* p) {
-  const unsigned long long v = __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_SYSTEM);
-  return make_float2(__uint_as_float(static_cast<unsigned>(v)), __uint_as_float(static_cast<unsigned>(v >> 32)));
-}
-// 16-byte versions through a buffer resource with the system-scope cache
-// policy (sc0 sc1); loads past the resource's byte range return zeros
-constexpr int BUF_DWORD3 = 0x00020000;     // raw 32-bit buffer, gfx9 encoding
-constexpr int CPOL_SYSTEM = 1 | 16;        // sc0 | sc1
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const float* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, bytes, BUF_DWORD3);
-}
-__device__ __forceinline__ float4 ld_coherent4(__amdgpu_buffer_rsrc_t r, int byte_off) {
-  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, CPOL_SYSTEM));
-}
-__device__ __forceinline__ void st_coherent4(__amdgpu_buffer_rsrc_t r, int byte_off, float4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, byte_off, 0, CPOL_SYSTEM);
-}
-// counters of one (sequence, kv head) sit 128 bytes apart, one cache line each
-constexpr int DEC_CTR_STRIDE = 32;
-
 __device__ __forceinline__ int norm_row_offset(int r) {
   return r < NR_POOL ? r * IDX_D : r == NR_POOL ? X_POOL : r < NR_K ? X_Q + (r - NR_Q) * QSA_D : X_K;
 }
@@ -749,29 +741,26 @@ __device__ __forceinline__ int norm_row_offset(int r) {
 template <typename T>
 struct DecArgs {
   PrepArgs<T> P;
-  float* part_o; float* part_ml; unsigned* counters; T* out;
+  float* part_o; float* part_ml; unsigned* tickets;
   int* ids; int* n_sel; int2* items; float* iq_out;   // optional inspection outputs
-  int splits, topk, max_items, ticket_off;
+  int splits, topk, max_items;
 };
 
 struct DecShared {
   float x[X_SIZE];                                // rows to norm
-  union {
-    unsigned long long key[DEC_MAX_BLOCKS];       // selection keys (step 2)
-    float acc[DEC_WAVES][GQA][QSA_D + 4];         // per-wave outputs (step 5), rows padded against bank conflicts
-  } u;
+  unsigned long long key[DEC_MAX_BLOCKS];         // selection keys
   float part[SLOTS_ALL];
   float rinv[16];
   float iq[4 * IDX_D];
   float newkey[IDX_D];
-  uint16_t knb[QSA_D], vnb[QSA_D];   // the token's roped key and its value, bf16
-  uint16_t qb[16][QSA_D];            // MFMA B operand: rows 0..7 bf16 hi of the 8 heads, 8..15 their lo parts
+  alignas(16) uint16_t knb[QSA_D];                // the token's roped key and its value, bf16
+  alignas(16) uint16_t vnb[QSA_D];
+  alignas(16) uint16_t qb[16][QSA_D];             // MFMA B operand: rows 0..7 bf16 hi of the heads, 8..15 lo
   float chunk[DEC_MAX_RATIO / 16][IDX_D];
   int pages[DEC_MAX_PAGES];
   int sel[DEC_MAX_TOPK];
-  float w[DEC_MAX_SPLITS][GQA];
-  float m[DEC_WAVES][GQA], l[DEC_WAVES][GQA];
-  int ticket, last;
+  alignas(16) float s[GQA][32];                   // the item's scores, head-major
+  int ticket;
 };
 
 // item -> (first token t0, visible rows [lo, hi)) of a query at position p
@@ -785,6 +774,21 @@ __device__ __forceinline__ void item_span(int it, int n_blk_items, int gpb, int 
     t0 = (ts & ~31) + (it - n_blk_items) * 32; lo = max(ts - t0, 0); hi = min(p + 1 - t0, 32);
   }
 }
+
+// attention items of a query at position p (the selected blocks' 32-token
+// groups, then the tail's)
+struct ItemCount {
+  int n_elig, n_sel, gpb, n_blk_items, ts, n_items;
+  __host__ __device__ ItemCount(int p, int ratio, int topk, int max_blocks) {
+    n_elig = min((p + 1) / ratio, max_blocks);
+    n_sel = min(n_elig, topk);
+    gpb = ratio >= 32 ? ratio / 32 : 1;
+    n_blk_items = n_sel * gpb;
+    ts = ((p + 1) / ratio) * ratio;
+    const int n_tail = ts > p ? 0 : (p >> 5) - (ts >> 5) + 1;
+    n_items = n_blk_items + n_tail;
+  }
+};
 
 // the 32 partial sums of squares of rows with slots [s0, s1) (slot = 32 row + a,
 // a = 0..31 summing channels a, a+32, ... in order), then each row's 1/rms
@@ -830,8 +834,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   // ---- 0. a ticket, then the loads
   unsigned ticket = 0;
   if (tid == 0)
-    ticket = __hip_atomic_fetch_add(D.counters + D.ticket_off + bg * DEC_CTR_STRIDE, 1u, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
+    ticket = __hip_atomic_fetch_add(D.tickets + bg * DEC_CTR_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   float iqv[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
@@ -857,11 +860,10 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
 
   const int p = A.positions[b];
   const int ratio = A.ratio;
-  const int n_elig = min((p + 1) / ratio, A.max_blocks);
   const int topk = D.topk;
-  const int n_sel = min(n_elig, topk);
+  const ItemCount ic(p, ratio, topk, A.max_blocks);
+  const int n_elig = ic.n_elig, n_items = ic.n_items;
   const int j_new = (p + 1) % ratio == 0 ? p / ratio : -1;
-  const bool scoring = n_elig > topk;
   const float cs = A.cos[(long)p * rope + ec], sn = A.sin[(long)p * rope + ec];
   const long t0r = (long)max(j_new, 0) * ratio * rope + ec;
   const float cs0 = A.cos[t0r], sn0 = A.sin[t0r];
@@ -871,6 +873,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k)
     pg[k] = A.page_table[(long)b * A.max_pages + min(tid + DEC_NT * k, n_lpages - 1)];
   const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
+  const bool scoring = n_elig > topk;
   float4 kp[SCORE_PRE][4];
   prefetch_block_keys(kp, bk, n_elig, j_new, scoring);
   // raw keys of the block this token completes: thread (e128, hh) takes the
@@ -887,15 +890,8 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
       }
   }
 
-  // the attention work of this position, and whether this workgroup has any
-  const int gpb = ratio >= 32 ? ratio / 32 : 1;
-  const int n_blk_items = n_sel * gpb;
-  const int ts = ((p + 1) / ratio) * ratio;
-  const int n_tail = ts > p ? 0 : (p >> 5) - (ts >> 5) + 1;
-  const int n_items = n_blk_items + n_tail;
-  const int n_work = min((n_items + DEC_WAVES - 1) / DEC_WAVES, D.splits);
-
-  // ---- 1. the indexer query and the pooled block key
+  // ---- 1. the indexer query and the pooled block key; the ticket decides
+  // whether this workgroup has an item at all
   if (j_new >= 0) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -918,7 +914,11 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
 #pragma unroll
   for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k)
     if (tid + DEC_NT * k < n_lpages) sh.pages[tid + DEC_NT * k] = pg[k];
+  if (tid == 0) sh.ticket = (int)ticket;
   __syncthreads();
+  const int item = sh.ticket;
+  if (item >= min(n_items, D.splits)) return;
+  const bool blk_item = item < ic.n_blk_items;
   float pmean = 0.f;
   if (j_new >= 0) {
     // block mean: the 16-row chunk sums in order, then divided by the count
@@ -965,39 +965,33 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   }
   __syncthreads();
 
-  // ---- 2. block scores and top-k (ties to the lower index)
-  if (scoring) {
-    score_blocks<DEC_NT>(sh.iq, sh.newkey, bk, n_elig, j_new, A.idx_heads, sh.u.key, nullptr, kp);
+  // ---- 2. block scores and top-k (ties to the lower index); the item of a
+  // tail workgroup does not depend on them
+  if (scoring && (blk_item || item == 0)) {
+    score_blocks<DEC_NT>(sh.iq, sh.newkey, bk, n_elig, j_new, A.idx_heads, sh.key, nullptr, kp);
     __syncthreads();
-    rank_topk<DEC_NT>(sh.u.key, n_elig, topk, sh.sel);
-  } else {
+    rank_topk<DEC_NT>(sh.key, n_elig, topk, sh.sel);
+  } else if (!scoring) {
     for (int i = tid; i < n_elig; i += DEC_NT) sh.sel[i] = i;
   }
-  // the ticket has long come back by now: workgroups past the last batch leave
-  if (tid == 0) sh.ticket = (int)(ticket & (unsigned)(D.splits - 1));
   __syncthreads();
-  const int batch = sh.ticket;
-  if (batch >= n_work) return;
-  const bool leader = batch == 0 && g == 0;       // writes the per-sequence side outputs
 
-  // ---- 3. first item's keys/values in flight while the query heads and key are normed
-  const int stride = D.splits * DEC_WAVES;
-  int item = batch * DEC_WAVES + wv;
-  int t0 = 0, lo = 0, hi = 0;
-  bf16x8_t kf[2][8], vf[16];
-  auto issue = [&]() {
-    item_span(item, n_blk_items, gpb, ratio, ts, p, sh.sel, t0, lo, hi);
-    const int page = sh.pages[t0 / A.page_size], row0 = t0 % A.page_size;
-    const uint16_t* kp0 = A.k_pool + (((long)page * A.hkv + g) * A.page_size + row0) * QSA_D;
-    const uint16_t* vp0 = A.v_pool + ((long)page * A.hkv + g) * QSA_D * A.page_size + row0;
+  // ---- 3. the item's keys/values in flight while the query heads and key are normed
+  int t0, lo, hi;
+  item_span(item, ic.n_blk_items, ic.gpb, ratio, ic.ts, p, sh.sel, t0, lo, hi);
+  const int page = sh.pages[t0 / A.page_size], row0 = t0 % A.page_size;
+  const long pbase = ((long)page * A.hkv + g) * A.page_size * QSA_D;
+  bf16x8_t kf[8], vf[4];
+  if (wv < 2) {
+    const uint16_t* kt = A.k_pool + pbase + ((row0 >> 4) + wv) * 8 * 512 + lane * 8;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int sk = 0; sk < 8; ++sk) kf[sk] = load_bf16x8(kt + sk * 512);
+  }
+  {
+    const uint16_t* vt = A.v_pool + pbase + ((row0 >> 5) * 16 + 4 * wv) * 512 + lane * 8;
 #pragma unroll
-      for (int sk = 0; sk < 8; ++sk) kf[t][sk] = load_bf16x8(kp0 + (16 * t + col) * QSA_D + 32 * sk + 8 * quad);
-#pragma unroll
-    for (int db = 0; db < 16; ++db) vf[db] = load_bf16x8(vp0 + (16 * db + col) * A.page_size + 8 * quad);
-  };
-  if (item < n_items) issue();
+    for (int i = 0; i < 4; ++i) vf[i] = load_bf16x8(vt + i * 512);
+  }
   norm_partials(sh, SLOTS_FRONT, SLOTS_ALL);
   __syncthreads();
   norm_rinv(sh, NR_Q, NR_ROWS, A.eps);
@@ -1028,228 +1022,201 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   }
   __syncthreads();
 
-  // ---- 4. attention over this workgroup's items
-  bf16x8_t qf[8];
-#pragma unroll
-  for (int sk = 0; sk < 8; ++sk) qf[sk] = *reinterpret_cast<const bf16x8_t*>(&sh.qb[col][32 * sk + 8 * quad]);
-  f32x4_t acc[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-  while (item < n_items) {
-    // the current token's row comes from this launch, not from the pages: its
-    // key replaces whole 8-channel vectors of one lane, its value one element
-    // (column kappa) of the lanes whose quad holds that column
-    if (p >= t0 && p < t0 + 32) {
-      const int r = p - t0;
-      const bool krow = col == (r & 15);
+  // ---- 4. scores of the item's two 16-token tiles (waves 0, 1)
+  const bool cur = p >= t0 && p < t0 + 32;          // the item holds the current token
+  const int rcur = p - t0;
+  if (wv < 2) {
+    if (cur && (rcur >> 4) == wv) {
+      // the current token's key replaces whole 8-channel vectors of one lane
+      const bool krow = col == (rcur & 15);
 #pragma unroll
       for (int sk = 0; sk < 8; ++sk) {
         const bf16x8_t kv = *reinterpret_cast<const bf16x8_t*>(&sh.knb[32 * sk + 8 * quad]);
-        if (r >> 4) kf[1][sk] = krow ? kv : kf[1][sk];
-        else kf[0][sk] = krow ? kv : kf[0][sk];
-      }
-      const int kappa = v_slot(r);
-      const int dw = (kappa & 7) >> 1, sh16 = 16 * (kappa & 1);
-      const bool vcol = quad == (kappa >> 3);
-#pragma unroll
-      for (int db = 0; db < 16; ++db) {
-        const unsigned val = sh.vnb[16 * db + col];
-        u32x4_t u = __builtin_bit_cast(u32x4_t, vf[db]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (vcol && i == dw) u[i] = (u[i] & ~(0xffffu << sh16)) | (val << sh16);
-        vf[db] = __builtin_bit_cast(bf16x8_t, u);
+        kf[sk] = krow ? kv : kf[sk];
       }
     }
     // S^T = K Q^T: columns 0..7 take q hi, 8..15 q lo; lane col then adds its
     // partner column col ^ 8 (DPP row rotate by 8) for the full-precision score
-    f32x4_t sc[2];
+    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int sk = 0; sk < 8; ++sk) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[t][sk], qf[sk], c, 0, 0, 0);
-      sc[t] = c;
+    for (int sk = 0; sk < 8; ++sk) {
+      const bf16x8_t qf = *reinterpret_cast<const bf16x8_t*>(&sh.qb[col][32 * sk + 8 * quad]);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[sk], qf, c, 0, 0, 0);
     }
-    float mx = -INFINITY;
+    float4 sv;
+    float* svp = reinterpret_cast<float*>(&sv);
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int tok = 16 * t + 4 * quad + v;
-        const float full = sc[t][v] + dpp_f<0x128>(sc[t][v]);
-        const float x = (tok >= lo && tok < hi) ? full * (1.0f / 16.0f) : -INFINITY;
-        sc[t][v] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = xor32_max(xor16_max(mx));
-    const float m_new = fmaxf(m_run, mx);
-    const bool carry = m_run != -INFINITY;      // false on a wave's first item
-    const float rescale = carry ? __expf(m_run - m_new) : 0.f;
-    m_run = m_new;
-    bf16x8_t pf;
-    float lsum = 0.f;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float pv = col < GQA ? __expf(sc[t][v] - m_new) : 0.f;
-        lsum += pv;
-        pf[4 * t + v] = __builtin_bit_cast(__bf16, f32_to_bf16(pv));
-      }
-    l_run = l_run * rescale + lsum;
-    if (carry) {
-#pragma unroll
-      for (int db = 0; db < 16; ++db) acc[db] = acc[db] * rescale;
+    for (int v = 0; v < 4; ++v) {
+      const int tok = 16 * wv + 4 * quad + v;
+      const float full = c[v] + dpp_f<0x128>(c[v]);
+      svp[v] = (tok >= lo && tok < hi) ? full * (1.0f / 16.0f) : -INFINITY;
     }
-#pragma unroll
-    for (int db = 0; db < 16; ++db) acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[db], pf, acc[db], 0, 0, 0);
-    item += stride;
-    if (item < n_items) issue();
-  }
-  l_run = xor32_sum(xor16_sum(l_run));
-
-  // ---- 5. merge the waves, publish the partial, last workgroup combines
-  __syncthreads();        // sh.u.key no longer read: reuse it for the wave merge
-  if (quad == 0 && col < GQA) { sh.m[wv][col] = m_run; sh.l[wv][col] = l_run; }
-  __syncthreads();
-  if (col < GQA) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < DEC_WAVES; ++w) M = fmaxf(M, sh.m[w][col]);
-    const float wself = m_run == -INFINITY ? 0.f : __expf(m_run - M);
-#pragma unroll
-    for (int db = 0; db < 16; ++db)
-      *reinterpret_cast<float4*>(&sh.u.acc[wv][col][16 * db + 4 * quad]) =
-          make_float4(acc[db][0] * wself, acc[db][1] * wself, acc[db][2] * wself, acc[db][3] * wself);
+    if (col < GQA) *reinterpret_cast<float4*>(&sh.s[col][16 * wv + 4 * quad]) = sv;
   }
   __syncthreads();
+  // softmax weights: lane (col, quad) takes tokens 16t + 4quad + v of head col
+  // (t = 0, 1), the k order the PV MFMA's B operand wants
+  const int hcol = col & 7;
+  const float4 s0 = *reinterpret_cast<const float4*>(&sh.s[hcol][4 * quad]);
+  const float4 s1 = *reinterpret_cast<const float4*>(&sh.s[hcol][16 + 4 * quad]);
+  const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+  mx = xor32_max(xor16_max(mx));
+  bf16x8_t pf;
+  float lsum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float pv = __expf(sv[i] - mx);
+    lsum += pv;
+    pf[i] = __builtin_bit_cast(__bf16, col < GQA ? f32_to_bf16(pv) : (uint16_t)0);
+  }
+  lsum = xor32_sum(xor16_sum(lsum));
+  if (cur) {
+    // the current token's value: one element (column kappa) of the lanes whose
+    // quad holds that column
+    const int kappa = v_slot(rcur);
+    const int dw = (kappa & 7) >> 1, sh16 = 16 * (kappa & 1);
+    const bool vcol = quad == (kappa >> 3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned val = sh.vnb[16 * (4 * wv + i) + col];
+      u32x4_t u = __builtin_bit_cast(u32x4_t, vf[i]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (vcol && j == dw) u[j] = (u[j] & ~(0xffffu << sh16)) | (val << sh16);
+      vf[i] = __builtin_bit_cast(bf16x8_t, u);
+    }
+  }
+  // O^T[d][head] = V^T[d][tok] P^T[tok][head] for this wave's 64 channels
   const long gbase = (long)bg * D.splits;
-  const int ch = tid >> 5, d0 = (tid & 31) * 8;     // this thread's head and 8 channels
-  {
-    float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
+  float* po = D.part_o + ((gbase + item) * GQA + hcol) * QSA_D;
 #pragma unroll
-    for (int w = 0; w < DEC_WAVES; ++w) {
-      const float4 a0 = *reinterpret_cast<const float4*>(&sh.u.acc[w][ch][d0]);
-      const float4 a1 = *reinterpret_cast<const float4*>(&sh.u.acc[w][ch][d0 + 4]);
-      o0.x += a0.x; o0.y += a0.y; o0.z += a0.z; o0.w += a0.w;
-      o1.x += a1.x; o1.y += a1.y; o1.z += a1.z; o1.w += a1.w;
-    }
-    const __amdgpu_buffer_rsrc_t rw = coherent_rsrc(D.part_o + (gbase + batch) * GQA * QSA_D, GQA * QSA_D * 4);
-    st_coherent4(rw, (ch * QSA_D + d0) * 4, o0);
-    st_coherent4(rw, (ch * QSA_D + d0 + 4) * 4, o1);
+  for (int i = 0; i < 4; ++i) {
+    const f32x4_t o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[i], pf, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    if (col < GQA) *reinterpret_cast<float4*>(po + 16 * (4 * wv + i) + 4 * quad) = make_float4(o[0], o[1], o[2], o[3]);
   }
-  if (tid < GQA) {
-    float Mh = -INFINITY, L = 0.f;
-#pragma unroll
-    for (int w = 0; w < DEC_WAVES; ++w) Mh = fmaxf(Mh, sh.m[w][tid]);
-#pragma unroll
-    for (int w = 0; w < DEC_WAVES; ++w)
-      if (sh.m[w][tid] != -INFINITY) L += sh.l[w][tid] * __expf(sh.m[w][tid] - Mh);
-    st_coherent(D.part_ml + ((gbase + batch) * GQA + tid) * 2, Mh, L);
-  }
-  // the stores that outlive this step, issued last so that no earlier wait
-  // drains them: the token's key/value into its page slot (batch 0 of each kv
-  // head), and per sequence (the leader) its raw indexer key, the pooled key of
-  // a completed block and the optional inspection outputs
-  if (batch == 0) {
+  if (wv == 0 && quad == 0 && col < GQA)
+    *reinterpret_cast<float2*>(D.part_ml + ((gbase + item) * GQA + col) * 2) = make_float2(mx, lsum);
+
+  // ---- 5. the stores that outlive this step: the token's key/value into its
+  // page slot (item 0 of each kv head), and per sequence (item 0 of kv head 0)
+  // its raw indexer key, the pooled key of a completed block and the optional
+  // inspection outputs
+  if (item == 0) {
     const int pg_cur = sh.pages[p / A.page_size], prow = p % A.page_size;
-    A.k_pool[(((long)pg_cur * A.hkv + g) * A.page_size + prow) * QSA_D + tid] = sh.knb[tid];
-    A.v_pool[(((long)pg_cur * A.hkv + g) * QSA_D + tid) * A.page_size + v_slot(prow)] = sh.vnb[tid];
-  }
-  if (leader) {
-    if (tid < IDX_D) {
-      Act<T>::store(A.raw_keys, ((long)b * A.max_ctx + p) * IDX_D + tid, ikv);
-      if (j_new >= 0) A.block_keys[((long)b * A.max_blocks + j_new) * IDX_D + tid] = sh.newkey[tid];
-    }
-    if (D.iq_out)
-      for (int i = tid; i < A.idx_heads * IDX_D; i += DEC_NT) D.iq_out[(long)b * A.idx_heads * IDX_D + i] = sh.iq[i];
-    if (D.items) {
-      int2* items = D.items + (long)b * D.max_items;
-      for (int it = tid; it < n_items; it += DEC_NT) {
-        int u0, ulo, uhi;
-        item_span(it, n_blk_items, gpb, ratio, ts, p, sh.sel, u0, ulo, uhi);
-        items[1 + it] = make_item(sh.pages[u0 / A.page_size] * A.page_size + u0 % A.page_size, ulo, uhi);
+    const long cbase = ((long)pg_cur * A.hkv + g) * A.page_size * QSA_D;
+    A.k_pool[cbase + k_page_index(prow, tid)] = sh.knb[tid];
+    A.v_pool[cbase + v_page_index(prow, tid)] = sh.vnb[tid];
+    if (g == 0) {
+      if (tid < IDX_D) {
+        Act<T>::store(A.raw_keys, ((long)b * A.max_ctx + p) * IDX_D + tid, ikv);
+        if (j_new >= 0) A.block_keys[((long)b * A.max_blocks + j_new) * IDX_D + tid] = sh.newkey[tid];
       }
-      if (tid == 0) items[0] = make_int2(n_items, 0);
+      if (D.iq_out)
+        for (int i = tid; i < A.idx_heads * IDX_D; i += DEC_NT) D.iq_out[(long)b * A.idx_heads * IDX_D + i] = sh.iq[i];
+      if (D.items) {
+        int2* items = D.items + (long)b * D.max_items;
+        for (int it = tid; it < n_items; it += DEC_NT) {
+          int u0, ulo, uhi;
+          item_span(it, ic.n_blk_items, ic.gpb, ratio, ic.ts, p, sh.sel, u0, ulo, uhi);
+          items[1 + it] = make_item(sh.pages[u0 / A.page_size] * A.page_size + u0 % A.page_size, ulo, uhi);
+        }
+        if (tid == 0) items[0] = make_int2(n_items, 0);
+      }
+      if (D.ids) {
+        for (int i = tid; i < ic.n_sel; i += DEC_NT) D.ids[(long)b * topk + i] = sh.sel[i];
+        if (tid == 0) D.n_sel[b] = ic.n_sel;
+      }
     }
-    if (D.ids) {
-      for (int i = tid; i < n_sel; i += DEC_NT) D.ids[(long)b * topk + i] = sh.sel[i];
-      if (tid == 0) D.n_sel[b] = n_sel;
-    }
   }
-  // every store of this workgroup complete (its partial at the point of
-  // coherence), then count it in; the last working workgroup merges
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(D.counters + bg * DEC_CTR_STRIDE, 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    sh.last = prev == (unsigned)(n_work - 1);
+}
+
+template <typename T>
+struct DecCombineArgs {
+  const float* part_o; const float* part_ml; unsigned* tickets;
+  const int* positions; const T* qg; T* out;
+  int hq, hkv, splits, ratio, topk, max_blocks;
+};
+
+constexpr int DC_NT = 256;
+
+// one query head of one sequence: out = round(sum_i w_i o_i / sum_i w_i l_i)
+// * round(sigmoid(gate)), w_i = exp(m_i - max m) over the position's items
+template <typename T>
+__global__ __launch_bounds__(DC_NT) void qsa_decode_combine_kernel(DecCombineArgs<T> C) {
+  const int hq = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x, grp = tid >> 6, lane = tid & 63;
+  const int g = hq / GQA, h = hq % GQA;
+  const int bg = b * C.hkv + g;
+  __shared__ float s_w[DEC_MAX_ITEMS];
+  __shared__ float s_red[DC_NT / 64];
+  __shared__ float4 s_o[DC_NT / 64][64];
+  const float gate = Act<T>::load(C.qg, ((long)b * C.hq + hq) * (2 * QSA_D) + QSA_D + tid);
+  const int p = C.positions[b];
+  const int n = min(ItemCount(p, C.ratio, C.topk, C.max_blocks).n_items, C.splits);
+  const long base = (long)bg * C.splits;
+  // every item's (max, sum), and the weighted outputs: thread (grp, lane)
+  // takes channels 4 lane .. 4 lane + 3 of items grp, grp + 4, ...
+  const float* pml = C.part_ml + (base * GQA + h) * 2;
+  const float* po = C.part_o + (base * GQA + h) * QSA_D + 4 * lane;
+  float m_i[DEC_MAX_ITEMS / DC_NT], l_i[DEC_MAX_ITEMS / DC_NT];
+#pragma unroll
+  for (int k = 0; k < DEC_MAX_ITEMS / DC_NT; ++k) {
+    const int i = tid + DC_NT * k;
+    const float2 ml = i < n ? *reinterpret_cast<const float2*>(pml + (long)i * GQA * 2) : make_float2(-INFINITY, 0.f);
+    m_i[k] = ml.x;
+    l_i[k] = ml.y;
   }
-  __syncthreads();
-  if (!sh.last) return;
-  // combine: thread (head ch, channels d0..d0+7); the head's 32 lanes share its partials
-  const int sl = tid & 31;
-  // partials of batches 0 .. n_work-1 (reads past them return zeros)
-  const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(D.part_o + gbase * GQA * QSA_D, n_work * GQA * QSA_D * 4);
-  const int obyte = (ch * QSA_D + d0) * 4;
-  float4 v[DEC_COMB][2];
+  constexpr int U = 16;
+  float4 ov[U];
 #pragma unroll
-  for (int k = 0; k < DEC_COMB; ++k) {
-    v[k][0] = ld_coherent4(ro, obyte + k * GQA * QSA_D * 4);
-    v[k][1] = ld_coherent4(ro, obyte + k * GQA * QSA_D * 4 + 16);
-  }
-  float gate[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) gate[i] = Act<T>::load(A.qg, ((long)b * A.hq + g * GQA + ch) * (2 * QSA_D) + QSA_D + d0 + i);
-  float2 ml[DEC_MAX_SPLITS / 32];
-#pragma unroll
-  for (int k = 0; k < DEC_MAX_SPLITS / 32; ++k) {
-    const int s = sl + 32 * k;
-    ml[k] = s < n_work ? ld_coherent(D.part_ml + ((gbase + s) * GQA + ch) * 2) : make_float2(-INFINITY, 0.f);
+  for (int u = 0; u < U; ++u) {
+    const int i = grp + 4 * u;
+    ov[u] = i < n ? *reinterpret_cast<const float4*>(po + (long)i * GQA * QSA_D) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   float M = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < DEC_MAX_SPLITS / 32; ++k) M = fmaxf(M, ml[k].x);
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, 32));
+  for (int k = 0; k < DEC_MAX_ITEMS / DC_NT; ++k) M = fmaxf(M, m_i[k]);
+  M = wave_max(M);
+  if (lane == 0) s_red[grp] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
   float L = 0.f;
 #pragma unroll
-  for (int k = 0; k < DEC_MAX_SPLITS / 32; ++k) {
-    const int s = sl + 32 * k;
-    const float w = ml[k].x == -INFINITY ? 0.f : __expf(ml[k].x - M);
-    L += ml[k].y * w;
-    if (s < n_work) sh.w[s][ch] = w;
+  for (int k = 0; k < DEC_MAX_ITEMS / DC_NT; ++k) {
+    const int i = tid + DC_NT * k;
+    const float w = i < n ? __expf(m_i[k] - M) : 0.f;
+    if (i < n) s_w[i] = w;
+    L += l_i[k] * w;
   }
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) L += __shfl_xor(L, o, 32);
+  L = wave_sum(L);
   __syncthreads();
-  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  auto accumulate = [&](int s0) {
+  if (lane == 0) s_red[grp] = L;
+  __syncthreads();
+  L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int i0 = 0;; i0 += 4 * U) {
 #pragma unroll
-    for (int k = 0; k < DEC_COMB; ++k) {
-      const float w = s0 + k < n_work ? sh.w[s0 + k][ch] : 0.f;
-      o[0] += v[k][0].x * w; o[1] += v[k][0].y * w; o[2] += v[k][0].z * w; o[3] += v[k][0].w * w;
-      o[4] += v[k][1].x * w; o[5] += v[k][1].y * w; o[6] += v[k][1].z * w; o[7] += v[k][1].w * w;
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + grp + 4 * u;
+      const float w = i < n ? s_w[i] : 0.f;
+      acc.x += ov[u].x * w; acc.y += ov[u].y * w; acc.z += ov[u].z * w; acc.w += ov[u].w * w;
     }
-  };
-  accumulate(0);
-  for (int s0 = DEC_COMB; s0 < n_work; s0 += DEC_COMB) {
+    if (i0 + 4 * U >= n) break;
 #pragma unroll
-    for (int k = 0; k < DEC_COMB; ++k) {
-      v[k][0] = ld_coherent4(ro, obyte + (s0 + k) * GQA * QSA_D * 4);
-      v[k][1] = ld_coherent4(ro, obyte + (s0 + k) * GQA * QSA_D * 4 + 16);
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + 4 * U + grp + 4 * u;
+      ov[u] = i < n ? *reinterpret_cast<const float4*>(po + (long)i * GQA * QSA_D) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    accumulate(s0);
   }
-  const float rl = 1.0f / L;
-  const long obase = ((long)b * A.hq + g * GQA + ch) * QSA_D + d0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    Act<T>::store(D.out, obase + i, Act<T>::round(o[i] * rl) * Act<T>::round(sigmoid_f(gate[i])));
-  if (tid == 0) __hip_atomic_store(D.counters + bg * DEC_CTR_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  s_o[grp][lane] = acc;
+  __syncthreads();
+  const float* so = reinterpret_cast<const float*>(s_o);
+  const float o = (so[tid] + so[256 + tid]) + (so[512 + tid] + so[768 + tid]);
+  Act<T>::store(C.out, ((long)b * C.hq + hq) * QSA_D + tid, Act<T>::round(o / L) * Act<T>::round(sigmoid_f(gate)));
+  if (h == 0 && tid == 0) C.tickets[bg * DEC_CTR_STRIDE] = 0u;
 }
 
 int check_geom(const qm_qsa_geom* g, const char* who) {
@@ -1332,6 +1299,17 @@ size_t part_o_bytes(const qm_qsa_geom* g, int rows, int splits) {
 }  // namespace
 
 extern "C" int qm_v_slot(int row) { return v_slot(row); }
+
+extern "C" int qm_qsa_page_index(int page_size, int head_dim, int* k_index, int* v_index) {
+  if (page_size <= 0 || page_size % 32 || head_dim != QSA_D || !k_index || !v_index)
+    return qm_fail(QM_ERR_ARG, "qm_qsa_page_index: page_size must be a multiple of 32 and head_dim 256");
+  for (int r = 0; r < page_size; ++r)
+    for (int d = 0; d < head_dim; ++d) {
+      k_index[r * head_dim + d] = k_page_index(r, d);
+      v_index[r * head_dim + d] = v_page_index(r, d);
+    }
+  return QM_OK;
+}
 
 extern "C" int qm_qsa_prep(const qm_qsa_geom* g, int seq, const void* qg, const void* k_new, const void* v_new,
                            const void* iq, const void* ik, const float* q_norm, const float* k_norm,
@@ -1499,23 +1477,28 @@ extern "C" int qm_qsa_decode_splits(const qm_qsa_geom* g, int max_position) {
   // item counts are not monotone in the position (the tail shrinks when a
   // block completes): take the largest over the last `ratio` positions, which
   // bounds every earlier one since the selected count never decreases
-  int items = 0;
+  int items = 1;
   for (int p = max_position - g->ratio < 0 ? 0 : max_position - g->ratio; p <= max_position; ++p) {
     const int n = items_at(g, p);
     items = n > items ? n : items;
   }
-  // the batches rounded up to a power of two: the spare workgroups let the ones
-  // that start first take the work
-  const int n = (items + DEC_WAVES - 1) / DEC_WAVES;
-  int g2 = 1;
-  while (g2 < n && g2 < DEC_MAX_SPLITS) g2 <<= 1;
-  return g2;
+  return items < DEC_MAX_ITEMS ? items : DEC_MAX_ITEMS;
 }
+
+namespace {
+// workspace of qm_qsa_decode: ticket counters (one cache line each), then the
+// items' (max, sum) and their unnormalised outputs
+size_t dec_ticket_bytes(const qm_qsa_geom* g) {
+  return qm_align256((size_t)g->batch * g->n_kv_heads * DEC_CTR_STRIDE * sizeof(unsigned));
+}
+size_t dec_ml_bytes(const qm_qsa_geom* g, int splits) {
+  return qm_align256((size_t)g->batch * g->n_kv_heads * splits * GQA * 2 * sizeof(float));
+}
+}  // namespace
 
 extern "C" size_t qm_qsa_decode_workspace(const qm_qsa_geom* g, int splits) {
   if (!g || splits <= 0) return 0;
-  return part_o_bytes(g, g->batch, splits) + qm_align256((size_t)g->batch * g->n_kv_heads * splits * GQA * 2 * 4) +
-         qm_align256((size_t)g->batch * g->n_kv_heads * 2 * DEC_CTR_STRIDE * sizeof(unsigned));
+  return dec_ticket_bytes(g) + dec_ml_bytes(g, splits) + part_o_bytes(g, g->batch, splits);
 }
 
 extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k_new, const void* v_new, const void* iq,
@@ -1534,39 +1517,32 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
       g->ratio > DEC_MAX_RATIO)
     return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_decode: more than 2048 blocks or pages, top-k above 256 or ratio "
                                        "above 64 (use qm_qsa_prep + qm_qsa_select + qm_qsa_attend)");
-  if (splits <= 0 || splits > DEC_MAX_SPLITS || (splits & (splits - 1)))
-    return qm_fail(QM_ERR_ARG, "qm_qsa_decode: splits must be a power of two up to 128 (qm_qsa_decode_splits)");
+  if (splits <= 0 || splits > DEC_MAX_ITEMS)
+    return qm_fail(QM_ERR_ARG, "qm_qsa_decode: splits must be 1..1024 (qm_qsa_decode_splits)");
+  if (g->batch > 65535) return qm_fail(QM_ERR_ARG, "qm_qsa_decode: batch above 65535");
   if (!workspace || workspace_bytes < qm_qsa_decode_workspace(g, splits))
     return qm_fail(QM_ERR_WORKSPACE, "qm_qsa_decode: workspace too small");
-  // counters first (done counters, then ticket counters), at an offset that
-  // does not depend on the split count
   char* ws = static_cast<char*>(workspace);
-  const size_t c_bytes = qm_align256((size_t)g->batch * g->n_kv_heads * 2 * DEC_CTR_STRIDE * sizeof(unsigned));
-  const size_t ml_bytes = qm_align256((size_t)g->batch * g->n_kv_heads * splits * GQA * 2 * 4);
-  dim3 grid(splits, g->n_kv_heads, g->batch);
-  auto fill = [&](auto& D) {
-    D.counters = reinterpret_cast<unsigned*>(ws);
-    D.part_ml = reinterpret_cast<float*>(ws + c_bytes);
-    D.part_o = reinterpret_cast<float*>(ws + c_bytes + ml_bytes);
+  unsigned* tickets = reinterpret_cast<unsigned*>(ws);
+  float* part_ml = reinterpret_cast<float*>(ws + dec_ticket_bytes(g));
+  float* part_o = reinterpret_cast<float*>(ws + dec_ticket_bytes(g) + dec_ml_bytes(g, splits));
+  const dim3 grid(splits, g->n_kv_heads, g->batch), cgrid(g->n_heads, g->batch);
+  auto run = [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    DecArgs<T> D;
+    D.P = prep_args<T>(g, 1, qg, k_new, v_new, iq, ik, q_norm, k_norm, iq_norm, ik_norm, cos, sin, positions,
+                       page_table, k_pool, v_pool, raw_keys, block_keys, nullptr, nullptr);
+    D.part_o = part_o; D.part_ml = part_ml; D.tickets = tickets;
     D.ids = ids; D.n_sel = n_sel; D.items = static_cast<int2*>(items); D.iq_out = iq_out;
     D.splits = splits; D.topk = g->budget / g->ratio; D.max_items = item_stride(g);
-    D.ticket_off = g->batch * g->n_kv_heads * DEC_CTR_STRIDE;
+    hipLaunchKernelGGL(qsa_decode_kernel<T>, grid, dim3(DEC_NT), 0, stream, D);
+    QM_CHECK_LAUNCH();
+    DecCombineArgs<T> C{part_o, part_ml, tickets, positions, static_cast<const T*>(qg), static_cast<T*>(out),
+                        g->n_heads, g->n_kv_heads, splits, g->ratio, g->budget / g->ratio, g->max_blocks};
+    hipLaunchKernelGGL(qsa_decode_combine_kernel<T>, cgrid, dim3(DC_NT), 0, stream, C);
+    QM_CHECK_LAUNCH();
+    return QM_OK;
   };
-  if (g->act_dtype == QM_ACT_F32) {
-    DecArgs<float> D;
-    D.P = prep_args<float>(g, 1, qg, k_new, v_new, iq, ik, q_norm, k_norm, iq_norm, ik_norm, cos, sin, positions,
-                           page_table, k_pool, v_pool, raw_keys, block_keys, nullptr, nullptr);
-    D.out = static_cast<float*>(out);
-    fill(D);
-    hipLaunchKernelGGL(qsa_decode_kernel<float>, grid, dim3(DEC_NT), 0, stream, D);
-  } else {
-    DecArgs<bf16_t> D;
-    D.P = prep_args<bf16_t>(g, 1, qg, k_new, v_new, iq, ik, q_norm, k_norm, iq_norm, ik_norm, cos, sin, positions,
-                            page_table, k_pool, v_pool, raw_keys, block_keys, nullptr, nullptr);
-    D.out = static_cast<bf16_t*>(out);
-    fill(D);
-    hipLaunchKernelGGL(qsa_decode_kernel<bf16_t>, grid, dim3(DEC_NT), 0, stream, D);
-  }
-  QM_CHECK_LAUNCH();
-  return QM_OK;
+  if (g->act_dtype == QM_ACT_F32) return run(static_cast<float*>(nullptr));
+  return run(static_cast<bf16_t*>(nullptr));
 }

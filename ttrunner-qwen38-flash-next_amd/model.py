@@ -193,7 +193,7 @@ class Qwen4MixModel:
         norms = [native.ptr(self._dw(layer, n, torch.float32)) for n in
                  ("attn_q_norm.weight", "attn_k_norm.weight", "indexer.q_norm.weight", "indexer.k_norm.weight")]
         if seq == 1 and qg is not None and k is not None and attend and self.fused_decode_fits(cache):
-            # decode: the whole QSA step in one launch
+            # decode: the whole QSA step in qm_qsa_decode (attend + combine launches)
             splits = lib.qm_qsa_decode_splits(ctypes.byref(g), query_offset)
             ws = self._workspace(f"qsa_decode_{layer}", lib.qm_qsa_decode_workspace(ctypes.byref(g), splits))
             if out is None:
@@ -240,7 +240,7 @@ class Qwen4MixModel:
         return out
 
     def fused_decode_fits(self, cache) -> bool:
-        """Whether qm_qsa_decode (one launch) covers this cache's geometry."""
+        """Whether qm_qsa_decode covers this cache's geometry."""
         c = self.config
         return (cache.max_blocks <= 2048 and cache.max_pages <= 2048 and c.block_topk <= 256
                 and c.indexer_compress_ratio <= 64)

@@ -47,6 +47,7 @@ SIGNATURES = {
     "qm_dn_recurrent": (_i, [_i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "qm_dn_chunked": (_i, [_i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "qm_v_slot": (_i, [_i]),
+    "qm_qsa_page_index": (_i, [_i, _i, _vp, _vp]),
     "qm_qsa_prep": (_i, [ctypes.POINTER(QsaGeom), _i] + [_vp] * 19 + [_vp]),
     "qm_qsa_items_stride": (_i, [ctypes.POINTER(QsaGeom)]),
     "qm_qsa_decode_splits": (_i, [ctypes.POINTER(QsaGeom), _i]),

@@ -114,7 +114,7 @@ class QsaDecodePlan:
                     self.splits, self.ws.data_ptr(), self.ws.numel(), stream)
 
     def decode(self, qg, k, v, iq, ik, stream):
-        """The whole step in one launch (qm_qsa_decode)."""
+        """The whole step (qm_qsa_decode: an attention launch and a combine launch)."""
         lc, w = self.lc, self.w
         native.call("qm_qsa_decode", ctypes.byref(self.geom), qg.data_ptr(), k.data_ptr(), v.data_ptr(),
                     iq.data_ptr(), ik.data_ptr(), w["attn_q_norm.weight"].data_ptr(),

@@ -716,8 +716,9 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T> A) {
 //   5. writes the item's (max, sum, unnormalised output) partial. The workgroup
 //      of item 0 also appends the token's key/value to its page slot, and for
 //      kv head 0 writes the per-sequence outputs (raw indexer key, pooled key).
-// qsa_decode_combine, grid (query head, sequence), merges the items' partials
-// of its head, applies the sigmoid gate and resets the ticket counter.
+// qsa_decode_combine, grid (64-channel quarter, query head, sequence), merges
+// the items' partials of its head, applies the sigmoid gate and resets the
+// ticket counter.
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_NT = 64 * DEC_WAVES;
 constexpr int DEC_MAX_BLOCKS = 2048;
@@ -1140,83 +1141,74 @@ struct DecCombineArgs {
   int hq, hkv, splits, ratio, topk, max_blocks;
 };
 
-constexpr int DC_NT = 256;
+constexpr int DC_NT = 64;          // one wave per (64-channel quarter, query head, sequence)
+constexpr int DC_CHUNK = 96;       // partial outputs in flight per lane
 
-// one query head of one sequence: out = round(sum_i w_i o_i / sum_i w_i l_i)
-// * round(sigmoid(gate)), w_i = exp(m_i - max m) over the position's items
+// out[d] = round(sum_i w_i o_i[d] / sum_i w_i l_i) * round(sigmoid(gate[d])),
+// w_i = exp(m_i - max m) over the position's items; lane = channel, and every
+// item's value of that channel is loaded before any is used (one round trip
+// for up to DC_CHUNK items). Loads are unconditional and do not wait for the
+// position: indices are clamped to the workspace's `splits` items (every one
+// holds finite values: the workspace starts zeroed and only ever receives
+// partials) and values past the position's item count are weighted by zero.
 template <typename T>
 __global__ __launch_bounds__(DC_NT) void qsa_decode_combine_kernel(DecCombineArgs<T> C) {
-  const int hq = blockIdx.x, b = blockIdx.y;
-  const int tid = threadIdx.x, grp = tid >> 6, lane = tid & 63;
+  const int quarter = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x, d = 64 * quarter + lane;
   const int g = hq / GQA, h = hq % GQA;
   const int bg = b * C.hkv + g;
-  __shared__ float s_w[DEC_MAX_ITEMS];
-  __shared__ float s_red[DC_NT / 64];
-  __shared__ float4 s_o[DC_NT / 64][64];
-  const float gate = Act<T>::load(C.qg, ((long)b * C.hq + hq) * (2 * QSA_D) + QSA_D + tid);
+  __shared__ __attribute__((aligned(16))) float s_w[DEC_MAX_ITEMS + DC_CHUNK];
+  const float gate = Act<T>::load(C.qg, ((long)b * C.hq + hq) * (2 * QSA_D) + QSA_D + d);
   const int p = C.positions[b];
   const int n = min(ItemCount(p, C.ratio, C.topk, C.max_blocks).n_items, C.splits);
+  const int n_round = (n + DC_CHUNK - 1) / DC_CHUNK * DC_CHUNK;
   const long base = (long)bg * C.splits;
-  // every item's (max, sum), and the weighted outputs: thread (grp, lane)
-  // takes channels 4 lane .. 4 lane + 3 of items grp, grp + 4, ...
   const float* pml = C.part_ml + (base * GQA + h) * 2;
-  const float* po = C.part_o + (base * GQA + h) * QSA_D + 4 * lane;
-  float m_i[DEC_MAX_ITEMS / DC_NT], l_i[DEC_MAX_ITEMS / DC_NT];
+  const float* po = C.part_o + (base * GQA + h) * QSA_D + d;
+  constexpr long ISTRIDE = (long)GQA * QSA_D;     // floats between two items' outputs of a head
+  const int last = C.splits - 1;
+  float ov[DC_CHUNK];
 #pragma unroll
-  for (int k = 0; k < DEC_MAX_ITEMS / DC_NT; ++k) {
-    const int i = tid + DC_NT * k;
-    const float2 ml = i < n ? *reinterpret_cast<const float2*>(pml + (long)i * GQA * 2) : make_float2(-INFINITY, 0.f);
-    m_i[k] = ml.x;
-    l_i[k] = ml.y;
-  }
-  constexpr int U = 16;
-  float4 ov[U];
+  for (int u = 0; u < DC_CHUNK; ++u) ov[u] = po[min(u, last) * ISTRIDE];
+  float2 ml[DEC_MAX_ITEMS / DC_NT];
+  const int n_ml = (C.splits + DC_NT - 1) / DC_NT;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int i = grp + 4 * u;
-    ov[u] = i < n ? *reinterpret_cast<const float4*>(po + (long)i * GQA * QSA_D) : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  for (int k = 0; k < DEC_MAX_ITEMS / DC_NT; ++k)
+    if (k < n_ml) ml[k] = *reinterpret_cast<const float2*>(pml + (long)min(lane + DC_NT * k, last) * GQA * 2);
   float M = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < DEC_MAX_ITEMS / DC_NT; ++k) M = fmaxf(M, m_i[k]);
+  for (int k = 0; k < DEC_MAX_ITEMS / DC_NT; ++k)
+    if (k < n_ml && lane + DC_NT * k < n) M = fmaxf(M, ml[k].x);
   M = wave_max(M);
-  if (lane == 0) s_red[grp] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
   float L = 0.f;
 #pragma unroll
   for (int k = 0; k < DEC_MAX_ITEMS / DC_NT; ++k) {
-    const int i = tid + DC_NT * k;
-    const float w = i < n ? __expf(m_i[k] - M) : 0.f;
-    if (i < n) s_w[i] = w;
-    L += l_i[k] * w;
+    const int i = lane + DC_NT * k;
+    if (k < n_ml && i < n) {
+      const float w = __expf(ml[k].x - M);
+      s_w[i] = w;
+      L += ml[k].y * w;
+    }
   }
   L = wave_sum(L);
+  for (int i = n + lane; i < n_round; i += DC_NT) s_w[i] = 0.f;    // weights past the items: zero
   __syncthreads();
-  if (lane == 0) s_red[grp] = L;
-  __syncthreads();
-  L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int i0 = 0;; i0 += 4 * U) {
+  float o = 0.f;
+  for (int i0 = 0;; i0 += DC_CHUNK) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = i0 + grp + 4 * u;
-      const float w = i < n ? s_w[i] : 0.f;
-      acc.x += ov[u].x * w; acc.y += ov[u].y * w; acc.z += ov[u].z * w; acc.w += ov[u].w * w;
+    for (int u = 0; u < DC_CHUNK; u += 4) {
+      const float4 w = *reinterpret_cast<const float4*>(&s_w[i0 + u]);
+      o += ov[u] * w.x;
+      o += ov[u + 1] * w.y;
+      o += ov[u + 2] * w.z;
+      o += ov[u + 3] * w.w;
     }
-    if (i0 + 4 * U >= n) break;
+    if (i0 + DC_CHUNK >= n) break;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = i0 + 4 * U + grp + 4 * u;
-      ov[u] = i < n ? *reinterpret_cast<const float4*>(po + (long)i * GQA * QSA_D) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    for (int u = 0; u < DC_CHUNK; ++u) ov[u] = po[min(i0 + DC_CHUNK + u, last) * ISTRIDE];
   }
-  s_o[grp][lane] = acc;
-  __syncthreads();
-  const float* so = reinterpret_cast<const float*>(s_o);
-  const float o = (so[tid] + so[256 + tid]) + (so[512 + tid] + so[768 + tid]);
-  Act<T>::store(C.out, ((long)b * C.hq + hq) * QSA_D + tid, Act<T>::round(o / L) * Act<T>::round(sigmoid_f(gate)));
-  if (h == 0 && tid == 0) C.tickets[bg * DEC_CTR_STRIDE] = 0u;
+  Act<T>::store(C.out, ((long)b * C.hq + hq) * QSA_D + d, Act<T>::round(o / L) * Act<T>::round(sigmoid_f(gate)));
+  if (h == 0 && quarter == 0 && lane == 0) C.tickets[bg * DEC_CTR_STRIDE] = 0u;
 }
 
 int check_geom(const qm_qsa_geom* g, const char* who) {
@@ -1526,7 +1518,7 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
   unsigned* tickets = reinterpret_cast<unsigned*>(ws);
   float* part_ml = reinterpret_cast<float*>(ws + dec_ticket_bytes(g));
   float* part_o = reinterpret_cast<float*>(ws + dec_ticket_bytes(g) + dec_ml_bytes(g, splits));
-  const dim3 grid(splits, g->n_kv_heads, g->batch), cgrid(g->n_heads, g->batch);
+  const dim3 grid(splits, g->n_kv_heads, g->batch), cgrid(QSA_D / DC_NT, g->n_heads, g->batch);
   auto run = [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
     DecArgs<T> D;

@@ -27,6 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK = 2.5e15          # dense bf16 FLOP/s
 METRIC = "attention µs/token at batch 1, pos 8128 (QSA sel on + DeltaNet); % HBM roofline"
 
 # algorithmic bytes (bf16 KV and activations, float32 DeltaNet state)
@@ -53,6 +54,18 @@ def qsa_bytes(pos: int, ratio: int = 64, topk: int = 32) -> int:
     return keys * KV_BYTES_PER_KEY + scored * BLOCK_KEY_BYTES + io
 
 
+def measured_traffic(pos: int, kernel: str):
+    """HBM bytes per launch of `kernel` at `pos` from the committed counter runs
+    (FETCH_SIZE + WRITE_SIZE scaled by a copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_decode_pos{pos}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        doc = json.load(f)
+    entry = doc.get("per_launch", {}).get(kernel)
+    return None if entry is None else entry["bytes"]
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -63,6 +76,9 @@ def parse():
     ap.add_argument("--sweep", action="store_true", help="also time positions 192/1984/4032 and a prefill chunk")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="after timing, copy a buffer of this many MiB device to device three times (a kernel of "
+                         "known traffic that scales hardware byte counters)")
     return ap.parse_args()
 
 
@@ -220,6 +236,101 @@ def cpu_baseline(position: int, seconds: float):
                       f"softmax, as the reference computes it) + DeltaNet decode core, bf16, median"}
 
 
+SWEEP_POSITIONS = (192, 1984, 4032, 8128)
+PREFILL_START, PREFILL_LEN, PREFILL_CTX = 32640, 128, 32768
+
+
+def qsa_chunk_flops(start: int, n: int, ratio: int = 64, topk: int = 32) -> int:
+    """Attention MACs x 2 of a prefill chunk: every query's selected keys plus its tail."""
+    keys = sum(qsa_keys(p, ratio, topk) for p in range(start, start + n))
+    return 16 * keys * 256 * 2 * 2
+
+
+def run_decode(qm, dev, pos, steps, warmup, instances=0):
+    """Time `steps` decode steps at `pos` over rotated instances; also each entry point."""
+    import torch
+    max_ctx = max(((pos + 1 + 63) // 64) * 64, 8192)
+    model = qm.Qwen4MixModel(qm.MixConfig(), weights_store(torch.bfloat16), device=dev, max_ctx=max_ctx)
+    touched = qsa_bytes(pos) + DN_BYTES
+    n_inst = instances or max(8, int(2 * 256e6 / touched) + 1)
+    insts = [Instance(qm, model, pos, max_ctx, 1000 + i) for i in range(n_inst)]
+    stream = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
+    sec = time_steps(insts, steps, warmup, stream.cuda_stream)
+    kern = time_kernels(insts, max(50, min(steps, 400)), stream)
+    del insts
+    torch.cuda.synchronize()
+    return {"pos": pos, "us_step": sec * 1e6, "kernel_us": kern, "instances": n_inst, "touched": touched,
+            "max_ctx": max_ctx}
+
+
+class PrefillInstance:
+    """One 128-token chunk at positions 32640..32767 of a 32768-token context:
+    QSA layer (per-query top-32 selection + causal paged attention) and DeltaNet
+    layer (chunked delta rule continuing a seeded state and ring)."""
+
+    def __init__(self, qm, model, seed):
+        import torch
+        dev = model.device
+        c = model.config
+        g = torch.Generator(device=dev).manual_seed(seed)
+        bf = torch.bfloat16
+        r = lambda *sh: torch.randn(*sh, generator=g, device=dev).to(bf)  # noqa: E731
+        self.cache = qm.MixHybridCache(4, c, 1, PREFILL_CTX, dev, bf, page_table="random", seed=seed)
+        lq, ld = self.cache[3], self.cache[0]
+        lq.ensure_qsa(1, bf)
+        ld.ensure_dn(1, bf)
+        lq.k_pool.copy_(r(*lq.k_pool.shape))
+        lq.v_pool.copy_(r(*lq.v_pool.shape))
+        lq.raw_keys.copy_(r(*lq.raw_keys.shape))
+        lq.n_tokens = PREFILL_START
+        lq.blocks_valid = 0
+        ld.recurrent_state.copy_(torch.randn(ld.recurrent_state.shape, generator=g, device=dev) * 0.02)
+        ld.conv_ring.copy_(r(*ld.conv_ring.shape))
+        ld.n_tokens = PREFILL_START
+        S = PREFILL_LEN
+        self.qg, self.k, self.v = r(1, S, 16 * 512), r(1, S, 512), r(1, S, 512)
+        self.iq, self.ik = r(1, S, 512), r(1, S, 128)
+        self.qkv, self.z, self.a, self.b = r(1, S, 8192), r(1, S, 4096), r(1, S, 32), r(1, S, 32)
+        self.model = model
+
+    def qsa(self):
+        self.cache[3].n_tokens = PREFILL_START
+        return self.model.qsa_core(self.qg, self.k, self.v, self.iq, self.ik, 3, self.cache, PREFILL_START)
+
+    def dn(self):
+        self.cache[0].n_tokens = PREFILL_START
+        return self.model.dn_core(self.qkv, self.z, self.a, self.b, 0, self.cache[0])
+
+
+def run_prefill(qm, dev, reps=20, n_inst=4):
+    import torch
+    model = qm.Qwen4MixModel(qm.MixConfig(), weights_store(torch.bfloat16), device=dev, max_ctx=PREFILL_CTX)
+    insts = [PrefillInstance(qm, model, 2000 + i) for i in range(n_inst)]
+    for x in insts:          # first calls pool the block cache and size the workspaces
+        x.qsa()
+        x.dn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    out = {}
+    for name in ("qsa", "dn"):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for i in range(reps):
+            x = insts[i % n_inst]
+            evs[i][0].record(stream)
+            getattr(x, name)()
+            evs[i][1].record(stream)
+        torch.cuda.synchronize()
+        out[name] = statistics.median(sorted(a.elapsed_time(b) for a, b in evs))   # ms
+    del insts
+    torch.cuda.synchronize()
+    flops = qsa_chunk_flops(PREFILL_START, PREFILL_LEN)
+    return {"positions": f"{PREFILL_START}-{PREFILL_START + PREFILL_LEN - 1} of {PREFILL_CTX}",
+            "qsa_ms": round(out["qsa"], 4), "dn_ms": round(out["dn"], 4),
+            "qsa_attention_gflop": round(flops / 1e9, 3),
+            "qsa_mfma_util": round(flops / (out["qsa"] * 1e-3) / MFMA_BF16_PEAK, 5)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -233,26 +344,42 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     pos = args.position
-    max_ctx = ((pos + 1 + 63) // 64) * 64
-    max_ctx = max(max_ctx, 8192)
-    model = qm.Qwen4MixModel(qm.MixConfig(), weights_store(torch.bfloat16), device=dev, max_ctx=max_ctx)
-
-    touched = qsa_bytes(pos) + DN_BYTES
-    n_inst = args.instances or max(8, int(2 * 256e6 / touched) + 1)
-    insts = [Instance(qm, model, pos, max_ctx, 1000 + i) for i in range(n_inst)]
-    stream = torch.cuda.current_stream(dev)
-    torch.cuda.synchronize()
+    head = run_decode(qm, dev, pos, args.steps, args.warmup, args.instances)
+    max_ctx, n_inst, touched = head["max_ctx"], head["instances"], head["touched"]
     print(f"[bench] {n_inst} instances, {n_inst * touched / 1e6:.0f} MB touched per rotation", file=sys.stderr)
-
-    sec = time_steps(insts, args.steps, args.warmup, stream.cuda_stream)
-    us_step = sec * 1e6
-    kern = time_kernels(insts, max(50, min(args.steps, 400)), stream)
+    us_step = head["us_step"]
+    sec = us_step * 1e-6
+    kern = head["kernel_us"]
     bytes_step = touched
     kb = {"qsa_decode": qsa_bytes(pos), "dn_decode": DN_BYTES}
     dominant = max(kb, key=lambda k: kern[k])
     achieved = kb[dominant] / (kern[dominant] * 1e-6) / 1e9
     print(f"[bench] step {us_step:.2f} us; kernels (us): " +
           ", ".join(f"{k} {v:.2f}" for k, v in kern.items()), file=sys.stderr)
+    if args.copy_mb > 0:
+        src = torch.ones(args.copy_mb << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    sweep = None
+    if args.sweep:
+        sweep = {"decode": [], "prefill_chunk": None}
+        for p in SWEEP_POSITIONS:
+            r = head if p == pos else run_decode(qm, dev, p, args.steps, args.warmup)
+            qb = qsa_bytes(p)
+            line = {"pos": p, "us_step": round(r["us_step"], 3),
+                    "qsa_us": round(r["kernel_us"]["qsa_decode"], 3), "dn_us": round(r["kernel_us"]["dn_decode"], 3),
+                    "qsa_gbs": round(qb / (r["kernel_us"]["qsa_decode"] * 1e-6) / 1e9, 1),
+                    "dn_gbs": round(DN_BYTES / (r["kernel_us"]["dn_decode"] * 1e-6) / 1e9, 1),
+                    "step_hbm_frac": round((qb + DN_BYTES) / (r["us_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+            sweep["decode"].append(line)
+            print(f"[sweep] {json.dumps(line)}", file=sys.stderr)
+        sweep["prefill_chunk"] = run_prefill(qm, dev)
+        print(f"[sweep] prefill {json.dumps(sweep['prefill_chunk'])}", file=sys.stderr)
 
     cpu = None
     if not args.no_cpu:
@@ -278,9 +405,12 @@ def main():
                    "step_hbm_frac": round(bytes_step / sec / 1e9 / HBM_PEAK_GBS, 4),
                    "kernel_us": {k: round(v, 3) for k, v in kern.items()}},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(pos, dominant)},
         "cpu_baseline": cpu,
     }
+    if sweep is not None:
+        line["sweep"] = sweep
     print(json.dumps(line))
 
 

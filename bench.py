@@ -160,6 +160,32 @@ def time_steps(instances, steps, warmup, stream):
     return (time.perf_counter() - t0) / steps
 
 
+def time_graph_steps(instances, steps, warmup):
+    """The same steps replayed from one HIP graph: the whole rotation (every
+    instance's step, three launches each) captured once, as a serving loop
+    captures a forward pass, then replayed until `steps` steps have run."""
+    import torch
+    side = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            for x in instances:
+                x.step(side.cuda_stream)
+    torch.cuda.synchronize()
+    n = len(instances)
+    reps = max(1, round(steps / n))
+    for _ in range(max(1, warmup // n)):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / (reps * n)
+    del g
+    return sec
+
+
 def time_kernels(instances, reps, stream_obj):
     """Average duration of each entry point's launches, HIP events on the launch stream."""
     import torch
@@ -246,7 +272,7 @@ def qsa_chunk_flops(start: int, n: int, ratio: int = 64, topk: int = 32) -> int:
     return 16 * keys * 256 * 2 * 2
 
 
-def run_decode(qm, dev, pos, steps, warmup, instances=0):
+def run_decode(qm, dev, pos, steps, warmup, instances=0, graphs=True):
     """Time `steps` decode steps at `pos` over rotated instances; also each entry point."""
     import torch
     max_ctx = max(((pos + 1 + 63) // 64) * 64, 8192)
@@ -258,10 +284,11 @@ def run_decode(qm, dev, pos, steps, warmup, instances=0):
     torch.cuda.synchronize()
     sec = time_steps(insts, steps, warmup, stream.cuda_stream)
     kern = time_kernels(insts, max(50, min(steps, 400)), stream)
+    gsec = time_graph_steps(insts, steps, warmup) if graphs else None
     del insts
     torch.cuda.synchronize()
     return {"pos": pos, "us_step": sec * 1e6, "kernel_us": kern, "instances": n_inst, "touched": touched,
-            "max_ctx": max_ctx}
+            "max_ctx": max_ctx, "graph_us_step": None if gsec is None else gsec * 1e6}
 
 
 class PrefillInstance:
@@ -354,7 +381,7 @@ def main():
     kb = {"qsa_decode": qsa_bytes(pos), "dn_decode": DN_BYTES}
     dominant = max(kb, key=lambda k: kern[k])
     achieved = kb[dominant] / (kern[dominant] * 1e-6) / 1e9
-    print(f"[bench] step {us_step:.2f} us; kernels (us): " +
+    print(f"[bench] step {us_step:.2f} us (graph replay {head['graph_us_step']:.2f} us); kernels (us): " +
           ", ".join(f"{k} {v:.2f}" for k, v in kern.items()), file=sys.stderr)
     if args.copy_mb > 0:
         src = torch.ones(args.copy_mb << 20, dtype=torch.uint8, device=dev)

@@ -108,9 +108,10 @@ __global__ __launch_bounds__(DN_HEAD_NT) void dn_decode_kernel(DnDecodeArgs<T> A
   const int c4 = tid & 31, r0 = tid >> 5;
   constexpr int NW = DN_HEAD_NT / 64;
 
-  __shared__ float s_q[DN_D], s_k[DN_D], s_v[DN_D], s_o[DN_D], s_delta[DN_D];
-  __shared__ float s_red[NW][2 * DN_D];
-  __shared__ float s_w3[NW][3];
+  __shared__ float s_q[DN_D], s_k[DN_D], s_v[DN_D], s_o[DN_D];
+  __shared__ __attribute__((aligned(16))) float s_delta[DN_D];
+  __shared__ __attribute__((aligned(16))) float s_red[NW][2 * DN_D];
+  __shared__ float s_w3[2][3];
   __shared__ float s_scal[4];
 
   // everything that depends on nothing is requested first: the state, this
@@ -119,10 +120,13 @@ __global__ __launch_bounds__(DN_HEAD_NT) void dn_decode_kernel(DnDecodeArgs<T> A
   float4 st[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) st[i] = S[(r0 + 32 * i) * (DN_D / 4) + c4];
-  float zv = 0.f, nw = 0.f;
-  if (tid < DN_D) {
-    zv = Act<T>::load(A.z, (long)b * A.hv * DN_D + h * DN_D + tid);
-    nw = A.norm_w[tid];
+  // wave 0 finishes the head: z and the norm weight of channels lane, lane + 64
+  float zv0 = 0.f, zv1 = 0.f, nw0 = 0.f, nw1 = 0.f;
+  if (wid == 0) {
+    zv0 = Act<T>::load(A.z, (long)b * A.hv * DN_D + h * DN_D + lane);
+    zv1 = Act<T>::load(A.z, (long)b * A.hv * DN_D + h * DN_D + lane + 64);
+    nw0 = A.norm_w[lane];
+    nw1 = A.norm_w[lane + 64];
   }
   float gate_b = 0.f, gate_a = 0.f, a_neg = 0.f, dtb = 0.f;
   if (tid == 0) {
@@ -132,7 +136,8 @@ __global__ __launch_bounds__(DN_HEAD_NT) void dn_decode_kernel(DnDecodeArgs<T> A
     dtb = A.dt_bias[h];
   }
 
-  // short conv on the head's 128 q, 128 k and 128 v channels
+  // short conv on the head's 128 q, 128 k and 128 v channels; meanwhile thread
+  // 0 turns this head's gate inputs into beta and the decay
   const int pos = A.positions[b];
   const int key_dim = A.hk * DN_D;
   if (tid < 3 * DN_D) {
@@ -142,34 +147,23 @@ __global__ __launch_bounds__(DN_HEAD_NT) void dn_decode_kernel(DnDecodeArgs<T> A
     const float y = conv_channel(A, b, ch, pos, writer);
     (part == 0 ? s_q : part == 1 ? s_k : s_v)[i] = y;
   }
-  __syncthreads();
-
-  // l2 norms of q and k and their dot product, one three-way block reduction
-  {
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f;
-    if (tid < DN_D) {
-      const float qv = s_q[tid], kv = s_k[tid];
-      a0 = qv * qv; a1 = kv * kv; a2 = qv * kv;
-    }
-    a0 = wave_sum(a0); a1 = wave_sum(a1); a2 = wave_sum(a2);
-    if (lane == 0) { s_w3[wid][0] = a0; s_w3[wid][1] = a1; s_w3[wid][2] = a2; }
-    __syncthreads();
-    if (tid < DN_D) {
-      float sq = 0.f, sk = 0.f, sqk = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) { sq += s_w3[w][0]; sk += s_w3[w][1]; sqk += s_w3[w][2]; }
-      const float rq = rsqrt_rn(sq + 1e-6f), rk = rsqrt_rn(sk + 1e-6f);
-      const float sqrt_d = 11.313708498984761f;
-      s_q[tid] = div_rn(mul_rn(s_q[tid], rq), sqrt_d);
-      s_k[tid] = mul_rn(s_k[tid], rk);
-      if (tid == 0) {
-        s_scal[0] = Act<T>::round(sigmoid_f(gate_b));
-        s_scal[1] = expf(a_neg * softplus_f(gate_a + dtb));
-        s_scal[2] = div_rn(sqk * rq * rk, sqrt_d);
-      }
-    }
+  if (tid == 0) {
+    s_scal[0] = Act<T>::round(sigmoid_f(gate_b));
+    s_scal[1] = expf(a_neg * softplus_f(gate_a + dtb));
   }
   __syncthreads();
+
+  // l2 norms of q and k and their dot product: waves 0-1 hold the 128 channels
+  if (tid < DN_D) {
+    const float qv = s_q[tid], kv = s_k[tid];
+    const float a0 = wave_sum(qv * qv), a1 = wave_sum(kv * kv), a2 = wave_sum(qv * kv);
+    if (lane == 0) { s_w3[wid][0] = a0; s_w3[wid][1] = a1; s_w3[wid][2] = a2; }
+  }
+  __syncthreads();
+  const float sq = s_w3[0][0] + s_w3[1][0], sk = s_w3[0][1] + s_w3[1][1], sqk = s_w3[0][2] + s_w3[1][2];
+  const float rq = rsqrt_rn(sq + 1e-6f), rk = rsqrt_rn(sk + 1e-6f);
+  const float sqrt_d = 11.313708498984761f;
+  const float qk = div_rn(sqk * rq * rk, sqrt_d);       // q^ . k^
 
   // decay, then per column pred = S^T k^ and qd = S^T q^
   const float decay = s_scal[1];
@@ -178,8 +172,8 @@ __global__ __launch_bounds__(DN_HEAD_NT) void dn_decode_kernel(DnDecodeArgs<T> A
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = r0 + 32 * i;
-    kr[i] = s_k[row];
-    const float qr = s_q[row];
+    kr[i] = mul_rn(s_k[row], rk);
+    const float qr = div_rn(mul_rn(s_q[row], rq), sqrt_d);
     st[i].x *= decay; st[i].y *= decay; st[i].z *= decay; st[i].w *= decay;
     pk[0] = fmaf(st[i].x, kr[i], pk[0]); pk[1] = fmaf(st[i].y, kr[i], pk[1]);
     pk[2] = fmaf(st[i].z, kr[i], pk[2]); pk[3] = fmaf(st[i].w, kr[i], pk[3]);
@@ -192,11 +186,8 @@ __global__ __launch_bounds__(DN_HEAD_NT) void dn_decode_kernel(DnDecodeArgs<T> A
     pq[c] = xor32_sum(pq[c]);
   }
   if (lane < 32) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      s_red[wid][4 * c4 + c] = pk[c];
-      s_red[wid][DN_D + 4 * c4 + c] = pq[c];
-    }
+    *reinterpret_cast<float4*>(&s_red[wid][4 * c4]) = make_float4(pk[0], pk[1], pk[2], pk[3]);
+    *reinterpret_cast<float4*>(&s_red[wid][DN_D + 4 * c4]) = make_float4(pq[0], pq[1], pq[2], pq[3]);
   }
   __syncthreads();
   if (tid < DN_D) {
@@ -205,7 +196,7 @@ __global__ __launch_bounds__(DN_HEAD_NT) void dn_decode_kernel(DnDecodeArgs<T> A
     for (int w = 0; w < NW; ++w) { pred += s_red[w][tid]; qd += s_red[w][DN_D + tid]; }
     const float delta = (s_v[tid] - pred) * s_scal[0];
     s_delta[tid] = delta;
-    s_o[tid] = Act<T>::round(fmaf(s_scal[2], delta, qd));
+    s_o[tid] = Act<T>::round(fmaf(qk, delta, qd));
   }
   __syncthreads();
 
@@ -221,19 +212,14 @@ __global__ __launch_bounds__(DN_HEAD_NT) void dn_decode_kernel(DnDecodeArgs<T> A
     }
   }
 
-  // gated RMS norm over the head's 128 outputs
-  {
-    const float ov = tid < DN_D ? s_o[tid] : 0.f;
-    float ss = wave_sum(ov * ov);
-    if (lane == 0) s_w3[wid][0] = ss;     // s_w3 is free again: last read before the previous barrier
-    __syncthreads();
-    if (tid < DN_D) {
-      ss = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) ss += s_w3[w][0];
-      const float rn = rsqrt_rn(ss / (float)DN_D + A.eps);
-      Act<T>::store(A.out, (long)b * A.hv * DN_D + h * DN_D + tid, (nw * (ov * rn)) * sigmoid_f(zv));
-    }
+  // gated RMS norm over the head's 128 outputs, by wave 0 (two channels a lane)
+  if (wid == 0) {
+    const float o0 = s_o[lane], o1 = s_o[lane + 64];
+    const float ss = wave_sum(o0 * o0 + o1 * o1);
+    const float rn = rsqrt_rn(ss / (float)DN_D + A.eps);
+    const long ob = (long)b * A.hv * DN_D + h * DN_D;
+    Act<T>::store(A.out, ob + lane, (nw0 * (o0 * rn)) * sigmoid_f(zv0));
+    Act<T>::store(A.out, ob + lane + 64, (nw1 * (o1 * rn)) * sigmoid_f(zv1));
   }
 }
 

@@ -95,11 +95,17 @@ int qm_dn_recurrent(int act_dtype, int batch, int seq, int heads, int head_dim, 
                     const void* v, const float* g, const float* beta, float* state, void* out,
                     hipStream_t stream);
 
+/* Bytes of workspace qm_dn_chunked needs: one fp32 record of 147712 bytes per
+ * (sequence, head, 64-token chunk). 0 for an unsupported head_dim. */
+size_t qm_dn_chunked_workspace(int batch, int seq, int heads, int head_dim);
+
 /* The same rule in the chunked WY/UT form, 64-token chunks:
  * chunk_gated_delta_rule (reference/layers.py:195-275). Same arguments and
- * result (to float32 rounding) as qm_dn_recurrent. */
+ * result (to float32 rounding) as qm_dn_recurrent, plus a workspace of
+ * qm_dn_chunked_workspace() bytes (no initial contents needed). */
 int qm_dn_chunked(int act_dtype, int batch, int seq, int heads, int head_dim, const void* q, const void* k,
-                  const void* v, const float* g, const float* beta, float* state, void* out, hipStream_t stream);
+                  const void* v, const float* g, const float* beta, float* state, void* out, void* workspace,
+                  size_t workspace_bytes, hipStream_t stream);
 
 /* Bytes of workspace qm_dn_prefill needs for a chunk of `seq` tokens. */
 size_t qm_dn_prefill_workspace(const qm_dn_geom* g, int seq);

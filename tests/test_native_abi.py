@@ -40,6 +40,17 @@ def test_library_exports_every_declared_symbol(qm):
     assert lib.qm_version() >= 1
 
 
+def test_binding_argument_counts_match_the_header(qm):
+    """Each ctypes argtypes list has as many entries as the C declaration has
+    parameters (a miscounted list would shift every later argument)."""
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        for name, params in re.findall(r"\b(qm_\w+)\s*\(([^)]*)\)\s*;", text):
+            params = params.strip()
+            n = 0 if params in ("", "void") else params.count(",") + 1
+            assert len(qm.native.SIGNATURES[name][1]) == n, f"{name}: header {n}, binding differs"
+
+
 def test_v_slot_is_a_permutation_of_each_group(qm):
     lib = qm.native.load()
     for page in (32, 64, 128):

@@ -74,6 +74,13 @@ __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
+// Workgroups are dealt round-robin to the 8 XCDs; this gives each XCD a
+// contiguous range of logical work items so that neighbours share an L2.
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  if (n % 8) return bid;
+  return (bid % 8) * (n / 8) + bid / 8;
+}
+
 // Cross-lane reductions on DPP / readlane / permlane (VALU, a few cycles each)
 // rather than __shfl_xor, whose ds_bpermute costs an LDS round trip per step
 // and serialises a reduction tree into a chain of LDS latencies.

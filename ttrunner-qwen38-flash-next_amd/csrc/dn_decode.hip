@@ -43,13 +43,6 @@ struct DnDecodeArgs {
   float eps;
 };
 
-__device__ __forceinline__ int xcd_remap(int bid, int n) {
-  // blocks are dealt round-robin to the 8 XCDs; give each XCD a contiguous
-  // range of logical work so neighbouring column tiles share an L2
-  if (n % 8) return bid;
-  return (bid % 8) * (n / 8) + bid / 8;
-}
-
 // K = 4: the ring row and the weight row of a channel are one 8-byte (bf16) or
 // 16-byte (fp32) load each, issued together with the input
 template <typename T> struct Vec4;

@@ -4,11 +4,12 @@
 // 198-201, 205-217, 230-243): the causal conv over [history | chunk] with the
 // last K-1 inputs carried to the ring, the gates, the delta rule over the chunk,
 // and the gated RMS norm. Launches:
-//   dn_conv_chunk   one thread per (sequence, channel): slides the K-tap window
-//                   down the chunk in registers, then writes the ring; the same
-//                   grid computes beta and g for every (token, head)
-//   delta rule      qm_dn_chunk_wy (WY/UT chunked form) when the chunk fills
-//                   64-token sub-chunks, else the token loop
+//   dn_conv_chunk   a workgroup per (sequence, 16 tokens, 256 channels): each
+//                   thread loads its channel's window inputs at once, then
+//                   writes 16 outputs; the first token block writes the ring;
+//                   the same grid computes beta and g for every (token, head)
+//   delta rule      the WY/UT chunked kernels (dn_chunk.hip) for chunks of 16
+//                   tokens or more, the token loop for shorter ones
 //   dn_gated_norm   one wavefront per (token, head) row of 128
 #include "common.h"
 #include "qwen4mix_internal.h"
@@ -21,43 +22,70 @@ template <typename T>
 struct ConvChunkArgs {
   const T* qkv; const T* a; const T* b; const float* a_neg; const float* dt_bias; const T* conv_w;
   const int* positions; T* ring; T* conv_out; float* g_out; float* beta_out;
-  int batch, seq, conv_dim, K, hv;
+  int batch, seq, conv_dim, hv, n_conv_wg;
 };
 
-template <typename T>
-__global__ __launch_bounds__(256) void dn_conv_chunk_kernel(ConvChunkArgs<T> A) {
-  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long n_conv = (long)A.batch * A.conv_dim;
-  if (gid < n_conv) {
-    const int b = gid / A.conv_dim, ch = gid % A.conv_dim;
-    const int K = A.K;
+constexpr int CONV_CH = 256;   // channels per workgroup (one per thread)
+constexpr int CONV_TOK = 16;   // tokens per workgroup
+
+// Workgroups [0, n_conv_wg) cover (sequence, 16-token block, 256 channels):
+// a thread loads its channel's K-1 + 16 inputs up front (history from the ring
+// before the chunk's first token), then writes the 16 outputs. The workgroup of
+// the first token block alone reads the ring, and it also writes the last K-1
+// inputs back to their slots after those reads, so no other workgroup races on
+// the ring. The remaining workgroups compute beta and g per (token, head).
+template <typename T, int K>
+__global__ __launch_bounds__(CONV_CH) void dn_conv_chunk_kernel(ConvChunkArgs<T> A) {
+  const int tid = threadIdx.x;
+  if ((int)blockIdx.x < A.n_conv_wg) {
+    const int n_cb = (A.conv_dim + CONV_CH - 1) / CONV_CH;
+    const int n_tb = (A.seq + CONV_TOK - 1) / CONV_TOK;
+    const int cb = blockIdx.x % n_cb, tb = (blockIdx.x / n_cb) % n_tb, b = blockIdx.x / (n_cb * n_tb);
+    const int ch = cb * CONV_CH + tid;
+    if (ch >= A.conv_dim) return;
     const int pos0 = A.positions[b];
+    const int t0 = tb * CONV_TOK;
+    const int nt = min(CONV_TOK, A.seq - t0);
     T* ring = A.ring + ((long)b * A.conv_dim + ch) * K;
-    float w[8], win[8];
+    const T* x = A.qkv + (long)b * A.seq * A.conv_dim + ch;
+    // every load is unconditional (clamped index, then a select), so the
+    // compiler issues them all before the first wait
+    float w[K], hist[K - 1], win[CONV_TOK + K - 1];
+#pragma unroll
     for (int j = 0; j < K; ++j) w[j] = Act<T>::load(A.conv_w, (long)ch * K + j);
-    // win[0..K-2] = inputs of positions pos0-K+1 .. pos0-1 (oldest first)
+#pragma unroll
     for (int j = 0; j < K - 1; ++j) {
       int slot = (pos0 - (K - 1) + j) % K;
       if (slot < 0) slot += K;
-      win[j] = Act<T>::load(ring, slot);
+      hist[j] = Act<T>::load(ring, slot);
     }
-    for (int t = 0; t < A.seq; ++t) {
-      const long idx = ((long)b * A.seq + t) * A.conv_dim + ch;
-      const float x = Act<T>::load(A.qkv, idx);
-      win[K - 1] = x;
-      float acc = 0.f;
-      for (int j = 0; j < K; ++j) acc = fmaf(w[j], win[j], acc);
-      Act<T>::store(A.conv_out, idx, Act<T>::round(silu_f(Act<T>::round(acc))));
-      for (int j = 0; j < K - 1; ++j) win[j] = win[j + 1];
+    // win[i] = input of token t0 - (K-1) + i; tokens before the chunk come
+    // from the ring (only in the first token block)
+#pragma unroll
+    for (int i = 0; i < CONV_TOK + K - 1; ++i) {
+      const int t = t0 - (K - 1) + i;
+      const int tc = min(max(t, 0), A.seq - 1);
+      const float val = Act<T>::load(x, (long)tc * A.conv_dim);
+      win[i] = (i < K - 1 && t < 0) ? hist[i < K - 1 ? i : 0] : val;
     }
-    // the last K-1 inputs of the chunk (or of history, when S < K-1) go to their slots
-    for (int t = max(0, A.seq - (K - 1)); t < A.seq; ++t) {
-      const long idx = ((long)b * A.seq + t) * A.conv_dim + ch;
-      Act<T>::store(ring, (pos0 + t) % K, Act<T>::load(A.qkv, idx));
+#pragma unroll
+    for (int i = 0; i < CONV_TOK; ++i) {
+      if (i < nt) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < K; ++j) acc = fmaf(w[j], win[i + j], acc);
+        Act<T>::store(A.conv_out, ((long)b * A.seq + t0 + i) * A.conv_dim + ch,
+                      Act<T>::round(silu_f(Act<T>::round(acc))));
+      }
+    }
+    if (tb == 0) {
+      // the last K-1 inputs of the chunk (or all of them, when S < K-1) go to their slots
+      for (int t = max(0, A.seq - (K - 1)); t < A.seq; ++t)
+        Act<T>::store(ring, (pos0 + t) % K, Act<T>::load(x, (long)t * A.conv_dim));
     }
     return;
   }
-  const long gg = gid - n_conv;
+  const long gg = (long)(blockIdx.x - A.n_conv_wg) * CONV_CH + tid;
   if (gg < (long)A.batch * A.seq * A.hv) {
     const int h = gg % A.hv;
     const float beta = Act<T>::round(sigmoid_f(Act<T>::load(A.b, gg)));
@@ -84,7 +112,7 @@ __global__ __launch_bounds__(256) void dn_gated_norm_kernel(const T* o, const T*
 }
 
 struct PrefillWs {
-  size_t conv, g, beta, core, total;
+  size_t conv, g, beta, core, rule, total;
 };
 
 PrefillWs prefill_layout(const qm_dn_geom* g, int seq) {
@@ -95,7 +123,8 @@ PrefillWs prefill_layout(const qm_dn_geom* g, int seq) {
   w.g = w.conv + qm_align256((size_t)g->batch * seq * conv_dim * act);
   w.beta = w.g + qm_align256((size_t)g->batch * seq * g->n_v_heads * 4);
   w.core = w.beta + qm_align256((size_t)g->batch * seq * g->n_v_heads * 4);
-  w.total = w.core + qm_align256((size_t)g->batch * seq * g->n_v_heads * g->head_dim * act);
+  w.rule = w.core + qm_align256((size_t)g->batch * seq * g->n_v_heads * g->head_dim * act);
+  w.total = w.rule + qm_align256(qm_dn_rule_chunk_workspace(g->batch, seq, g->n_v_heads));
   return w;
 }
 
@@ -115,14 +144,25 @@ int launch_prefill(const qm_dn_geom* g, int seq, const void* qkv, const void* z,
   C.qkv = static_cast<const T*>(qkv); C.a = static_cast<const T*>(a); C.b = static_cast<const T*>(b);
   C.a_neg = a_neg; C.dt_bias = dt_bias; C.conv_w = static_cast<const T*>(conv_w); C.positions = positions;
   C.ring = static_cast<T*>(conv_ring); C.conv_out = conv_out; C.g_out = g_out; C.beta_out = beta_out;
-  C.batch = g->batch; C.seq = seq; C.conv_dim = conv_dim; C.K = g->conv_kernel; C.hv = g->n_v_heads;
-  const long work = (long)g->batch * conv_dim + (long)g->batch * seq * g->n_v_heads;
-  hipLaunchKernelGGL(dn_conv_chunk_kernel<T>, dim3((work + 255) / 256), dim3(256), 0, stream, C);
+  C.batch = g->batch; C.seq = seq; C.conv_dim = conv_dim; C.hv = g->n_v_heads;
+  C.n_conv_wg = g->batch * ((conv_dim + CONV_CH - 1) / CONV_CH) * ((seq + CONV_TOK - 1) / CONV_TOK);
+  const long n_gate = (long)g->batch * seq * g->n_v_heads;
+  const dim3 grid(C.n_conv_wg + (unsigned)((n_gate + CONV_CH - 1) / CONV_CH));
+  switch (g->conv_kernel) {
+    case 2: hipLaunchKernelGGL((dn_conv_chunk_kernel<T, 2>), grid, dim3(CONV_CH), 0, stream, C); break;
+    case 3: hipLaunchKernelGGL((dn_conv_chunk_kernel<T, 3>), grid, dim3(CONV_CH), 0, stream, C); break;
+    case 4: hipLaunchKernelGGL((dn_conv_chunk_kernel<T, 4>), grid, dim3(CONV_CH), 0, stream, C); break;
+    case 5: hipLaunchKernelGGL((dn_conv_chunk_kernel<T, 5>), grid, dim3(CONV_CH), 0, stream, C); break;
+    case 6: hipLaunchKernelGGL((dn_conv_chunk_kernel<T, 6>), grid, dim3(CONV_CH), 0, stream, C); break;
+    case 7: hipLaunchKernelGGL((dn_conv_chunk_kernel<T, 7>), grid, dim3(CONV_CH), 0, stream, C); break;
+    default: hipLaunchKernelGGL((dn_conv_chunk_kernel<T, 8>), grid, dim3(CONV_CH), 0, stream, C); break;
+  }
   QM_CHECK_LAUNCH();
 
   const int key_dim = g->n_k_heads * DN_D;
   int rc = qm_dn_rule_chunk(g->act_dtype, g->batch, seq, g->n_v_heads, g->n_k_heads, conv_dim, conv_dim, conv_out,
-                            conv_out + key_dim, conv_out + 2 * key_dim, g_out, beta_out, state, core, stream);
+                            conv_out + key_dim, conv_out + 2 * key_dim, g_out, beta_out, state, core, base + L.rule,
+                            L.total - L.rule, stream);
   if (rc) return rc;
 
   const long rows = (long)g->batch * seq * g->n_v_heads;

@@ -17,7 +17,9 @@ int qm_dn_recurrent_strided(int act_dtype, int batch, int seq, int heads, int hk
                             float* state, void* out, hipStream_t stream);
 
 // The delta rule over a chunk of tokens for the prefill path: the WY/UT chunked
-// kernel where it applies, the token loop otherwise.
+// kernels (64-token chunks) for chunks of 16 tokens or more, the token loop for
+// shorter ones. `ws` holds qm_dn_rule_chunk_workspace(batch, seq, heads) bytes.
+size_t qm_dn_rule_chunk_workspace(int batch, int seq, int heads);
 int qm_dn_rule_chunk(int act_dtype, int batch, int seq, int heads, int hk, long q_stride, long v_stride,
                      const void* q, const void* k, const void* v, const float* g, const float* beta, float* state,
-                     void* out, hipStream_t stream);
+                     void* out, void* ws, size_t ws_bytes, hipStream_t stream);

@@ -30,8 +30,13 @@ def _rule(query, key, value, g, beta, initial_state, name: str):
     else:
         state = initial_state.to(dev, torch.float32).clone().contiguous()
     out = torch.empty(batch, seq, heads, d, dtype=dt, device=dev)
-    native.call(name, native.act_code(dt), batch, seq, heads, d, native.ptr(q), native.ptr(k), native.ptr(v),
-                native.ptr(g32), native.ptr(b32), native.ptr(state), native.ptr(out), native.stream_handle(dev))
+    args = [native.act_code(dt), batch, seq, heads, d, native.ptr(q), native.ptr(k), native.ptr(v),
+            native.ptr(g32), native.ptr(b32), native.ptr(state), native.ptr(out)]
+    if name == "qm_dn_chunked":
+        n_ws = native.load().qm_dn_chunked_workspace(batch, seq, heads, d)
+        ws = torch.empty(max(n_ws, 1), dtype=torch.uint8, device=dev)
+        args += [native.ptr(ws), n_ws]
+    native.call(name, *args, native.stream_handle(dev))
     return out, state
 
 

@@ -45,7 +45,8 @@ SIGNATURES = {
     "qm_dn_decode": (_i, [ctypes.POINTER(DnGeom), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                           _vp, _sz, _vp]),
     "qm_dn_recurrent": (_i, [_i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "qm_dn_chunked": (_i, [_i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "qm_dn_chunked_workspace": (_sz, [_i, _i, _i, _i]),
+    "qm_dn_chunked": (_i, [_i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "qm_v_slot": (_i, [_i]),
     "qm_qsa_page_index": (_i, [_i, _i, _vp, _vp]),
     "qm_qsa_prep": (_i, [ctypes.POINTER(QsaGeom), _i] + [_vp] * 19 + [_vp]),

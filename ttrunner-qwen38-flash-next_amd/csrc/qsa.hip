@@ -678,10 +678,284 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T> A) {
   for (int i = 0; i < QSA_D / 64; ++i) L += s_red[i];
   float o = 0.f;
 #pragma unroll 8
-  for (int s = 0; s < A.splits; ++s) o += A.part_o[(base + (long)s * GQA) * QSA_D + d] * s_w[s];
+  for (int s = 0; s < A.splits; ++s)
+    if (s_w[s] != 0.f) o += A.part_o[(base + (long)s * GQA) * QSA_D + d] * s_w[s];
   const float att = Act<T>::round(o / L);
   const float sg = Act<T>::round(sigmoid_f(gate));
   Act<T>::store(A.out, ((long)row * A.hq + hq) * QSA_D + d, att * sg);
+}
+
+// ---------------------------------------------------------------------------
+// chunk attention (prefill), block-major
+// ---------------------------------------------------------------------------
+// The attention of a chunk of S query rows reads each key/value block once:
+//   qsa_chunk_index   one workgroup per sequence: the (row, slot) entries
+//                     (slot i < topk: the row's i-th selected block; slot topk:
+//                     its tail block, keys ts..p) counting-sorted by block, then
+//                     cut into work items of up to 8 entries of one block; slots
+//                     a row does not use get an empty partial (max -inf)
+//   qsa_chunk_attend  persistent workgroups per (kv head, sequence): a work
+//                     item's block (ratio tokens: 16 KB of key and 16 KB of
+//                     value pieces per 32 tokens, contiguous in the page's lane
+//                     order) is staged in LDS once, and each wave scores it for
+//                     two entries x 8 query heads on bf16 MFMA, writing one
+//                     partial (max, sum, output) per (row, slot, head)
+//   qsa_combine       merges a row's topk + 1 slots and applies the gate
+constexpr int CK_NT2 = 256;
+constexpr int CI_MAX_BLOCKS = 4096;
+constexpr int CA_PER_ITEM = 8;    // entries per work item: two per wave
+constexpr int CI_NT = 1024;       // index workgroup
+
+struct ChunkIndexArgs {
+  const int* positions; const int* ids; const int* n_sel;
+  unsigned* ent; int4* work; int* n_work; float* part_ml;
+  int seq, hkv, ratio, topk, max_work;
+};
+
+// every entry's block, eight per thread at a time with all loads issued first;
+// j[k] = -1 for an unused slot, -2 past the end
+template <int NT>
+__device__ __forceinline__ void entry_blocks(const ChunkIndexArgs& A, int b, int pos0, int base, int (&j)[8],
+                                             int (&s)[8], int (&i)[8]) {
+  const int nslot = A.topk + 1, n_ent = A.seq * nslot;
+  int nsel[8], idv[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int e = min(base + k * NT + (int)threadIdx.x, n_ent - 1);
+    s[k] = e / nslot;
+    i[k] = e - s[k] * nslot;
+    const long row = (long)b * A.seq + s[k];
+    nsel[k] = A.n_sel[row];
+    idv[k] = A.ids[row * A.topk + min(i[k], A.topk - 1)];
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int p = pos0 + s[k];
+    const int ts = ((p + 1) / A.ratio) * A.ratio;
+    const int tail = ts <= p ? ts / A.ratio : -1;
+    const int jj = i[k] < A.topk ? (i[k] < nsel[k] ? idv[k] : -1) : tail;
+    j[k] = base + k * NT + (int)threadIdx.x < n_ent ? jj : -2;
+  }
+}
+
+__global__ __launch_bounds__(CI_NT) void qsa_chunk_index_kernel(ChunkIndexArgs A) {
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int nslot = A.topk + 1;
+  const int n_ent = A.seq * nslot;
+  const int pos0 = A.positions[b];
+  // blocks any entry can name: selected blocks are complete ones before the
+  // row, a tail block holds the row itself
+  const int NB = min((pos0 + A.seq - 1) / A.ratio + 1, CI_MAX_BLOCKS);
+  __shared__ int cnt[CI_MAX_BLOCKS], off[CI_MAX_BLOCKS], woff[CI_MAX_BLOCKS];
+  __shared__ int wsum[2][CI_NT / 64];
+  for (int j = tid; j < NB; j += CI_NT) cnt[j] = 0;
+  __syncthreads();
+  for (int base = 0; base < n_ent; base += 8 * CI_NT) {
+    int j[8], s[8], i[8];
+    entry_blocks<CI_NT>(A, b, pos0, base, j, s, i);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (j[k] >= 0) {
+        atomicAdd(&cnt[j[k]], 1);
+      } else if (j[k] == -1) {
+        const long row = (long)b * A.seq + s[k];
+        for (int gh = 0; gh < A.hkv * GQA; ++gh) {
+          const long pb = ((row * A.hkv + gh / GQA) * nslot + i[k]) * GQA + gh % GQA;
+          A.part_ml[pb * 2 + 0] = -INFINITY;
+          A.part_ml[pb * 2 + 1] = 0.f;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // exclusive scans of the entry counts and of the work items per block
+  const int per = (NB + CI_NT - 1) / CI_NT;
+  const int j0 = tid * per, j1 = min(NB, j0 + per);
+  int c_tot = 0, w_tot = 0;
+  for (int j = j0; j < j1; ++j) {
+    c_tot += cnt[j];
+    w_tot += (cnt[j] + CA_PER_ITEM - 1) / CA_PER_ITEM;
+  }
+  int ci = c_tot, wi = w_tot;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int a = __shfl_up(ci, o, 64), c = __shfl_up(wi, o, 64);
+    if (lane >= o) { ci += a; wi += c; }
+  }
+  if (lane == 63) { wsum[0][wv] = ci; wsum[1][wv] = wi; }
+  __syncthreads();
+  int cb = ci - c_tot, wb = wi - w_tot;
+  for (int w = 0; w < wv; ++w) { cb += wsum[0][w]; wb += wsum[1][w]; }
+  for (int j = j0; j < j1; ++j) {
+    off[j] = cb;
+    woff[j] = wb;
+    cb += cnt[j];
+    wb += (cnt[j] + CA_PER_ITEM - 1) / CA_PER_ITEM;
+  }
+  __syncthreads();
+  // work items, then the entries (cnt becomes each block's fill cursor)
+  for (int j = tid; j < NB; j += CI_NT) {
+    const int c = cnt[j];
+    for (int k = 0; k * CA_PER_ITEM < c; ++k)
+      A.work[(long)b * A.max_work + woff[j] + k] =
+          make_int4(j, off[j] + k * CA_PER_ITEM, min(CA_PER_ITEM, c - k * CA_PER_ITEM), 0);
+  }
+  if (tid == CI_NT - 1) {
+    int tot = 0;
+    for (int w = 0; w < CI_NT / 64; ++w) tot += wsum[1][w];
+    A.n_work[b] = tot;
+  }
+  __syncthreads();
+  for (int j = tid; j < NB; j += CI_NT) cnt[j] = 0;
+  __syncthreads();
+  for (int base = 0; base < n_ent; base += 8 * CI_NT) {
+    int j[8], s[8], i[8];
+    entry_blocks<CI_NT>(A, b, pos0, base, j, s, i);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (j[k] >= 0) {
+        const int c = atomicAdd(&cnt[j[k]], 1);
+        A.ent[(long)b * n_ent + off[j[k]] + c] = (static_cast<unsigned>(s[k]) << 16) |
+                                                  (i[k] == A.topk ? 1u << 9 : 0u) | static_cast<unsigned>(i[k]);
+      }
+    }
+  }
+}
+
+struct ChunkAttnArgs {
+  const uint16_t* q;                      // [rows, 2 (hi, lo), hq, 256] bf16
+  const uint16_t* k_pool; const uint16_t* v_pool;
+  const int* positions; const int* page_table;
+  const unsigned* ent; const int4* work; const int* n_work;
+  float* part_o; float* part_ml;
+  int seq, hq, hkv, page_size, max_pages, ratio, topk, max_work;
+  float scale;
+};
+
+__global__ __launch_bounds__(CK_NT2, 2) void qsa_chunk_attend_kernel(ChunkAttnArgs A) {
+  const int g = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int col = lane & 15, quad = lane >> 4;
+  const int il = col >> 3, hh = col & 7;
+  const int nslot = A.topk + 1;
+  const int gpb = A.ratio / 32;
+  const int pos0 = A.positions[b];
+  const int n_work = A.n_work[b];
+  const int* ptab = A.page_table + (long)b * A.max_pages;
+  const long head_stride = (long)A.page_size * QSA_D;
+  __shared__ uint16_t kv[2][32][64 * 8];  // per 32-token group: 16 key then 16 value 1 KB pieces
+
+  for (int w = blockIdx.x; w < n_work; w += gridDim.x) {
+    const int4 item = A.work[(long)b * A.max_work + w];
+    const int j = item.x, start = item.y, n = item.z;
+    // this lane's entry (column group il of the wave) and its query
+    const int e = 2 * wv + il;
+    const bool ok = e < n;
+    const unsigned pk = A.ent[(long)b * A.seq * nslot + start + min(e, n - 1)];
+    const int s = pk >> 16, slot = pk & 511;
+    const bool tail = (pk >> 9) & 1u;
+    const long row = (long)b * A.seq + s;
+    const int p = pos0 + s;
+    bf16x8_t qhi[8], qlo[8];
+    {
+      const int hqi = g * GQA + hh;
+      const uint16_t* qh = A.q + ((2 * row) * A.hq + hqi) * QSA_D + 8 * quad;
+      const uint16_t* ql = A.q + ((2 * row + 1) * A.hq + hqi) * QSA_D + 8 * quad;
+#pragma unroll
+      for (int sk = 0; sk < 8; ++sk) {
+        qhi[sk] = load_bf16x8(qh + 32 * sk);
+        qlo[sk] = load_bf16x8(ql + 32 * sk);
+      }
+    }
+    // stage the block's groups
+    for (int gi = 0; gi < gpb; ++gi) {
+      const int t0 = j * A.ratio + gi * 32;
+      const long pb = ((long)ptab[t0 / A.page_size] * A.hkv + g) * head_stride;
+      const int row0 = t0 % A.page_size;
+      const uint16_t* ks = A.k_pool + pb + (row0 >> 4) * 8 * 512;
+      const uint16_t* vs = A.v_pool + pb + (row0 >> 5) * 16 * 512;
+      uint4 kr[4], vr[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        kr[k] = *reinterpret_cast<const uint4*>(ks + (k * CK_NT2 + tid) * 8);
+        vr[k] = *reinterpret_cast<const uint4*>(vs + (k * CK_NT2 + tid) * 8);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        *reinterpret_cast<uint4*>(&kv[gi][0][0] + (k * CK_NT2 + tid) * 8) = kr[k];
+        *reinterpret_cast<uint4*>(&kv[gi][16][0] + (k * CK_NT2 + tid) * 8) = vr[k];
+      }
+    }
+    __syncthreads();
+
+    if (2 * wv < n) {
+      f32x4_t acc[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      float m_run = -INFINITY, l_run = 0.f;
+      for (int gi = 0; gi < gpb; ++gi) {
+        const uint16_t* kvg = &kv[gi][0][0];
+        f32x4_t sc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int sk = 0; sk < 8; ++sk) {
+            const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(kvg + ((t * 8 + sk) * 64 + lane) * 8);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qhi[sk], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qlo[sk], c, 0, 0, 0);
+          }
+          sc[t] = c;
+        }
+        // keys of a tail entry stop at the row's own position
+        const int kbase = j * A.ratio + gi * 32;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int kp = kbase + 16 * t + 4 * quad + v;
+            const float x = (ok && (!tail || kp <= p)) ? sc[t][v] * A.scale : -INFINITY;
+            sc[t][v] = x;
+            mx = fmaxf(mx, x);
+          }
+        mx = xor32_max(xor16_max(mx));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_run == -INFINITY ? 0.f : __expf(m_run - m_new);
+        bf16x8_t pf;
+        float lsum = 0.f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float pv = sc[t][v] == -INFINITY ? 0.f : __expf(sc[t][v] - m_new);
+            lsum += pv;
+            pf[4 * t + v] = __builtin_bit_cast(__bf16, f32_to_bf16(pv));
+          }
+        l_run = l_run * alpha + lsum;
+        m_run = m_new;
+#pragma unroll
+        for (int db = 0; db < 16; ++db) {
+          acc[db] = acc[db] * alpha;
+          const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(kvg + ((16 + db) * 64 + lane) * 8);
+          acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, acc[db], 0, 0, 0);
+        }
+      }
+      l_run = xor32_sum(xor16_sum(l_run));
+      if (ok) {
+        const long pb = ((row * A.hkv + g) * nslot + slot) * GQA + hh;
+        float* po = A.part_o + pb * QSA_D + 4 * quad;
+#pragma unroll
+        for (int db = 0; db < 16; ++db)
+          *reinterpret_cast<float4*>(po + 16 * db) = make_float4(acc[db][0], acc[db][1], acc[db][2], acc[db][3]);
+        if (quad == 0) {
+          A.part_ml[pb * 2 + 0] = m_run;
+          A.part_ml[pb * 2 + 1] = l_run;
+        }
+      }
+    }
+    __syncthreads();
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1406,6 +1680,94 @@ extern "C" int qm_qsa_attend(const qm_qsa_geom* g, int seq, const void* q, const
   } else {
     CombineArgs<bf16_t> C{A.part_o, A.part_ml, static_cast<const bf16_t*>(qg), static_cast<bf16_t*>(out), g->n_heads,
                           g->n_kv_heads, splits};
+    hipLaunchKernelGGL(qsa_combine_kernel<bf16_t>, dim3(g->n_heads, g->batch * seq), dim3(QSA_D), 0, stream, C);
+  }
+  QM_CHECK_LAUNCH();
+  return QM_OK;
+}
+
+namespace {
+struct ChunkWs {
+  size_t o, ml, ent, work, n_work, total;
+};
+
+ChunkWs chunk_ws_layout(const qm_qsa_geom* g, int seq) {
+  const int nslot = g->budget / g->ratio + 1;
+  const size_t rows = (size_t)g->batch * seq;
+  ChunkWs w;
+  w.o = 0;
+  w.ml = w.o + qm_align256(rows * g->n_kv_heads * nslot * GQA * QSA_D * sizeof(float));
+  w.ent = w.ml + qm_align256(rows * g->n_kv_heads * nslot * GQA * 2 * sizeof(float));
+  w.work = w.ent + qm_align256(rows * nslot * sizeof(unsigned));
+  w.n_work = w.work + qm_align256(rows * nslot * sizeof(int4));
+  w.total = w.n_work + qm_align256((size_t)g->batch * sizeof(int));
+  return w;
+}
+
+int check_chunk_geom(const qm_qsa_geom* g, const char* who) {
+  int rc = check_geom(g, who);
+  if (rc) return rc;
+  if (g->ratio != 32 && g->ratio != 64)
+    return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_attend_chunk: indexer ratio must be 32 or 64");
+  if (g->max_blocks > CI_MAX_BLOCKS || g->max_ctx > CI_MAX_BLOCKS * g->ratio)
+    return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_attend_chunk: more than 4096 blocks");
+  if (g->budget / g->ratio + 1 > 511) return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_attend_chunk: top-k above 510");
+  return QM_OK;
+}
+}  // namespace
+
+extern "C" size_t qm_qsa_attend_chunk_workspace(const qm_qsa_geom* g, int seq) {
+  if (!g || g->ratio <= 0 || g->budget < g->ratio || seq <= 0 || g->batch <= 0) return 0;
+  return chunk_ws_layout(g, seq).total;
+}
+
+extern "C" int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool,
+                                   const void* v_pool, const int* positions, const int* page_table, const int* ids,
+                                   const int* n_sel, void* out, void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream) {
+  int rc = check_chunk_geom(g, "qm_qsa_attend_chunk: null geometry");
+  if (rc) return rc;
+  if (!q || !qg || !k_pool || !v_pool || !positions || !page_table || !ids || !n_sel || !out)
+    return qm_fail(QM_ERR_ARG, "qm_qsa_attend_chunk: null pointer");
+  if (seq <= 0 || seq > 65535 || (long)g->batch * seq > 65535)
+    return qm_fail(QM_ERR_ARG, "qm_qsa_attend_chunk: bad seq");
+  const ChunkWs L = chunk_ws_layout(g, seq);
+  if (!workspace || workspace_bytes < L.total)
+    return qm_fail(QM_ERR_WORKSPACE, "qm_qsa_attend_chunk: workspace too small");
+  char* base = static_cast<char*>(workspace);
+  const int topk = g->budget / g->ratio;
+  const int nslot = topk + 1;
+  float* part_o = reinterpret_cast<float*>(base + L.o);
+  float* part_ml = reinterpret_cast<float*>(base + L.ml);
+  unsigned* ent = reinterpret_cast<unsigned*>(base + L.ent);
+  int4* work = reinterpret_cast<int4*>(base + L.work);
+  int* n_work = reinterpret_cast<int*>(base + L.n_work);
+
+  ChunkIndexArgs I;
+  I.positions = positions; I.ids = ids; I.n_sel = n_sel; I.ent = ent; I.work = work; I.n_work = n_work;
+  I.part_ml = part_ml; I.seq = seq; I.hkv = g->n_kv_heads; I.ratio = g->ratio; I.topk = topk;
+  I.max_work = seq * nslot;
+  hipLaunchKernelGGL(qsa_chunk_index_kernel, dim3(g->batch), dim3(CI_NT), 0, stream, I);
+  QM_CHECK_LAUNCH();
+
+  ChunkAttnArgs A;
+  A.q = static_cast<const uint16_t*>(q); A.k_pool = static_cast<const uint16_t*>(k_pool);
+  A.v_pool = static_cast<const uint16_t*>(v_pool); A.positions = positions; A.page_table = page_table;
+  A.ent = ent; A.work = work; A.n_work = n_work; A.part_o = part_o; A.part_ml = part_ml;
+  A.seq = seq; A.hq = g->n_heads; A.hkv = g->n_kv_heads; A.page_size = g->page_size; A.max_pages = g->max_pages;
+  A.ratio = g->ratio; A.topk = topk; A.max_work = seq * nslot;
+  A.scale = 1.0f / 16.0f;   // 1/sqrt(256), exact
+  int nwg = 512 / (g->n_kv_heads * g->batch);
+  nwg = nwg < 1 ? 1 : nwg > seq * nslot ? seq * nslot : nwg;
+  hipLaunchKernelGGL(qsa_chunk_attend_kernel, dim3(nwg, g->n_kv_heads, g->batch), dim3(CK_NT2), 0, stream, A);
+  QM_CHECK_LAUNCH();
+  if (g->act_dtype == QM_ACT_F32) {
+    CombineArgs<float> C{part_o, part_ml, static_cast<const float*>(qg), static_cast<float*>(out), g->n_heads,
+                         g->n_kv_heads, nslot};
+    hipLaunchKernelGGL(qsa_combine_kernel<float>, dim3(g->n_heads, g->batch * seq), dim3(QSA_D), 0, stream, C);
+  } else {
+    CombineArgs<bf16_t> C{part_o, part_ml, static_cast<const bf16_t*>(qg), static_cast<bf16_t*>(out), g->n_heads,
+                          g->n_kv_heads, nslot};
     hipLaunchKernelGGL(qsa_combine_kernel<bf16_t>, dim3(g->n_heads, g->batch * seq), dim3(QSA_D), 0, stream, C);
   }
   QM_CHECK_LAUNCH();

@@ -188,8 +188,9 @@ class Qwen4MixModel:
         lib = native.load()
         ids = torch.empty(batch, seq, c.block_topk, dtype=torch.int32, device=self.device)
         n_sel = torch.empty(batch, seq, dtype=torch.int32, device=self.device)
+        chunked = seq > 1 and attend and self.chunk_attend_fits(cache)
         items = torch.empty(batch, seq, 2 * lib.qm_qsa_items_stride(ctypes.byref(g)), dtype=torch.int32,
-                            device=self.device) if attend else None
+                            device=self.device) if attend and not chunked else None
         norms = [native.ptr(self._dw(layer, n, torch.float32)) for n in
                  ("attn_q_norm.weight", "attn_k_norm.weight", "indexer.q_norm.weight", "indexer.k_norm.weight")]
         if seq == 1 and qg is not None and k is not None and attend and self.fused_decode_fits(cache):
@@ -230,6 +231,15 @@ class Qwen4MixModel:
         lc.last_ids, lc.last_n_sel, lc.last_iq, lc.last_q = ids, n_sel, iq_out, q_out
         if not attend:
             return None
+        if seq > 1 and self.chunk_attend_fits(cache):
+            # a chunk of rows: each selected key block is read once for all rows that attend it
+            ws = self._workspace("qsa_attend", lib.qm_qsa_attend_chunk_workspace(ctypes.byref(g), seq))
+            if out is None:
+                out = torch.empty(batch, seq, c.num_attention_heads * c.head_dim, dtype=dt, device=self.device)
+            native.call("qm_qsa_attend_chunk", ctypes.byref(g), seq, native.ptr(q_out), native.ptr(qg),
+                        native.ptr(lc.k_pool), native.ptr(lc.v_pool), native.ptr(pos), native.ptr(lc.page_table),
+                        native.ptr(ids), native.ptr(n_sel), native.ptr(out), native.ptr(ws), ws.numel(), stream)
+            return out
         splits = lib.qm_qsa_attend_splits(ctypes.byref(g), query_offset, query_offset + seq - 1)
         ws = self._workspace("qsa_attend", lib.qm_qsa_attend_workspace(ctypes.byref(g), seq, splits))
         if out is None:
@@ -238,6 +248,12 @@ class Qwen4MixModel:
                     native.ptr(lc.v_pool), native.ptr(items), native.ptr(out), splits, native.ptr(ws), ws.numel(),
                     stream)
         return out
+
+    def chunk_attend_fits(self, cache) -> bool:
+        """Whether qm_qsa_attend_chunk covers this cache's geometry."""
+        c = self.config
+        return (c.indexer_compress_ratio in (32, 64) and cache.max_blocks <= 4096
+                and cache.max_ctx <= 4096 * c.indexer_compress_ratio and c.block_topk <= 510)
 
     def fused_decode_fits(self, cache) -> bool:
         """Whether qm_qsa_decode covers this cache's geometry."""

@@ -213,6 +213,37 @@ def test_prefill_chunk_matches_golden_reference(gpu):
     assert rel_err(flat[::stride][: want.numel()], want) < OUT_TOL
 
 
+@pytest.mark.parametrize("past,seq,batch,dtype", [(0, 37, 1, torch.bfloat16), (2000, 96, 1, torch.bfloat16),
+                                                   (4030, 70, 2, torch.float32), (8100, 128, 1, torch.bfloat16)])
+def test_prefill_chunk_attention_matches_oracle(gpu, past, seq, batch, dtype):
+    """The block-major chunk attention (qm_qsa_attend_chunk) against the oracle,
+    and against the per-row item attention (qm_qsa_attend) on the same chunk:
+    a ragged last tile, chunks that complete blocks part-way (rows whose tail
+    block another row has selected), a batch of two with its own pages."""
+    cfg = OracleConfig()
+    store = gi.FakeStore(gi.qsa_weights(3, 90, dtype))
+    pasts = [gi.qsa_past(91 + b, past, dtype) for b in range(batch)]
+    keys, values, idx_keys = (torch.cat([p[i] for p in pasts]) for i in range(3))
+    hidden = gi.normal(gi.rng(93), (batch, seq, gi.HIDDEN)).to(dtype)
+    cos, sin = tables(past + seq)
+    print(f"prefill chunk past={past} seq={seq} batch={batch} {dtype}", flush=True)
+    want, _, _, chosen = _oracle_core(cfg, store, hidden, cos, sin, keys if past else None,
+                                      values if past else None, idx_keys, past)
+    outs = []
+    for chunked in (True, False):
+        model, cache = _model_and_cache(gpu, store, dtype, past + seq + 64, batch=batch)
+        if not chunked:
+            model.chunk_attend_fits = lambda cache: False
+        if past:
+            cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
+        qg, k, v, iq, ik = (t.to(DEV) for t in _projections(store, hidden))
+        got = model.qsa_core(qg, k, v, iq, ik, 3, cache, past, cos.to(DEV), sin.to(DEV))
+        assert _got_sets(cache[3]) == chosen
+        assert rel_err(got, want) < OUT_TOL, "chunked" if chunked else "items"
+        outs.append(got.float())
+    assert rel_err(outs[0], outs[1]) < 1e-2
+
+
 def test_small_ratio_several_blocks_per_page(gpu):
     """ratio 4 < page 64 (the reference checkpoint's ratio), budget 64 -> top-16."""
     qm = gpu

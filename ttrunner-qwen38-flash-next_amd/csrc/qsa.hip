@@ -633,16 +633,22 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void qsa_attend_kernel(AttnArgs A) 
   }
 }
 
-template <typename T>
+// Partial outputs are either fp32 and unnormalised (o = sum p v) or bf16 and
+// normalised by their own sum (o / l, the chunk path's 16-bit partials).
+template <typename T, typename PO = float>
 struct CombineArgs {
-  const float* part_o; const float* part_ml; const T* qg; T* out;
+  const PO* part_o; const float* part_ml; const T* qg; T* out;
   int hq, hkv, splits;
 };
 
+__device__ __forceinline__ float part_value(const float* p, long i) { return p[i]; }
+__device__ __forceinline__ float part_value(const uint16_t* p, long i) { return bf16_to_f32(p[i]); }
+
 constexpr int MAX_SPLITS = 1024;
 
-template <typename T>
-__global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T> A) {
+template <typename T, typename PO = float>
+__global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T, PO> A) {
+  constexpr bool normed = sizeof(PO) == 2;
   const int hq = blockIdx.x, row = blockIdx.y;
   const int d = threadIdx.x;
   const int g = hq / GQA, hh = hq % GQA;
@@ -666,8 +672,9 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T> A) {
   for (int s = d; s < A.splits; s += QSA_D) {
     const float ms = s_w[s];
     const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
-    l += A.part_ml[(base + (long)s * GQA) * 2 + 1] * w;
-    s_w[s] = w;
+    const float lw = A.part_ml[(base + (long)s * GQA) * 2 + 1] * w;
+    l += lw;
+    s_w[s] = normed ? lw : w;
   }
   l = wave_sum(l);
   __syncthreads();
@@ -677,9 +684,13 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T> A) {
 #pragma unroll
   for (int i = 0; i < QSA_D / 64; ++i) L += s_red[i];
   float o = 0.f;
+  // loads are unconditional so that eight are in flight at once; a slot of
+  // zero weight (never written, or under the max by ~88) adds exactly 0
 #pragma unroll 8
-  for (int s = 0; s < A.splits; ++s)
-    if (s_w[s] != 0.f) o += A.part_o[(base + (long)s * GQA) * QSA_D + d] * s_w[s];
+  for (int s = 0; s < A.splits; ++s) {
+    const float v = part_value(A.part_o, (base + (long)s * GQA) * QSA_D + d);
+    o += s_w[s] != 0.f ? v * s_w[s] : 0.f;
+  }
   const float att = Act<T>::round(o / L);
   const float sg = Act<T>::round(sigmoid_f(gate));
   Act<T>::store(A.out, ((long)row * A.hq + hq) * QSA_D + d, att * sg);
@@ -699,10 +710,12 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T> A) {
 //                     value pieces per 32 tokens, contiguous in the page's lane
 //                     order) is staged in LDS once, and each wave scores it for
 //                     two entries x 8 query heads on bf16 MFMA, writing one
-//                     partial (max, sum, output) per (row, slot, head)
+//                     partial per (row, slot, head): fp32 max and sum, and the
+//                     output normalised by the sum, in bf16
 //   qsa_combine       merges a row's topk + 1 slots and applies the gate
 constexpr int CK_NT2 = 256;
 constexpr int CI_MAX_BLOCKS = 4096;
+constexpr int CA_NT = 256;        // attention workgroup: four waves
 constexpr int CA_PER_ITEM = 8;    // entries per work item: two per wave
 constexpr int CI_NT = 1024;       // index workgroup
 
@@ -827,12 +840,12 @@ struct ChunkAttnArgs {
   const uint16_t* k_pool; const uint16_t* v_pool;
   const int* positions; const int* page_table;
   const unsigned* ent; const int4* work; const int* n_work;
-  float* part_o; float* part_ml;
+  uint16_t* part_o; float* part_ml;      // part_o: bf16, normalised by l
   int seq, hq, hkv, page_size, max_pages, ratio, topk, max_work;
   float scale;
 };
 
-__global__ __launch_bounds__(CK_NT2, 2) void qsa_chunk_attend_kernel(ChunkAttnArgs A) {
+__global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArgs A) {
   const int g = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int col = lane & 15, quad = lane >> 4;
@@ -843,10 +856,11 @@ __global__ __launch_bounds__(CK_NT2, 2) void qsa_chunk_attend_kernel(ChunkAttnAr
   const int n_work = A.n_work[b];
   const int* ptab = A.page_table + (long)b * A.max_pages;
   const long head_stride = (long)A.page_size * QSA_D;
+  const int4* work = A.work + (long)b * A.max_work;
   __shared__ uint16_t kv[2][32][64 * 8];  // per 32-token group: 16 key then 16 value 1 KB pieces
 
   for (int w = blockIdx.x; w < n_work; w += gridDim.x) {
-    const int4 item = A.work[(long)b * A.max_work + w];
+    const int4 item = work[w];
     const int j = item.x, start = item.y, n = item.z;
     // this lane's entry (column group il of the wave) and its query
     const int e = 2 * wv + il;
@@ -867,91 +881,99 @@ __global__ __launch_bounds__(CK_NT2, 2) void qsa_chunk_attend_kernel(ChunkAttnAr
         qlo[sk] = load_bf16x8(ql + 32 * sk);
       }
     }
-    // stage the block's groups
-    for (int gi = 0; gi < gpb; ++gi) {
-      const int t0 = j * A.ratio + gi * 32;
-      const long pb = ((long)ptab[t0 / A.page_size] * A.hkv + g) * head_stride;
-      const int row0 = t0 % A.page_size;
-      const uint16_t* ks = A.k_pool + pb + (row0 >> 4) * 8 * 512;
-      const uint16_t* vs = A.v_pool + pb + (row0 >> 5) * 16 * 512;
-      uint4 kr[4], vr[4];
+    // stage the block's groups: per group 16 KB of key and 16 KB of value pieces
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        kr[k] = *reinterpret_cast<const uint4*>(ks + (k * CK_NT2 + tid) * 8);
-        vr[k] = *reinterpret_cast<const uint4*>(vs + (k * CK_NT2 + tid) * 8);
-      }
+    for (int gi = 0; gi < 2; ++gi) {
+      if (gi < gpb) {
+        const int t0 = j * A.ratio + gi * 32;
+        const long pb = ((long)ptab[t0 / A.page_size] * A.hkv + g) * head_stride;
+        const int row0 = t0 % A.page_size;
+        const uint16_t* ks = A.k_pool + pb + (row0 >> 4) * 8 * 512;
+        const uint16_t* vs = A.v_pool + pb + (row0 >> 5) * 16 * 512;
+        uint4 kr[4], vr[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        *reinterpret_cast<uint4*>(&kv[gi][0][0] + (k * CK_NT2 + tid) * 8) = kr[k];
-        *reinterpret_cast<uint4*>(&kv[gi][16][0] + (k * CK_NT2 + tid) * 8) = vr[k];
+        for (int k = 0; k < 4; ++k) {
+          kr[k] = *reinterpret_cast<const uint4*>(ks + (k * CA_NT + tid) * 8);
+          vr[k] = *reinterpret_cast<const uint4*>(vs + (k * CA_NT + tid) * 8);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          *reinterpret_cast<uint4*>(&kv[gi][0][0] + (k * CA_NT + tid) * 8) = kr[k];
+          *reinterpret_cast<uint4*>(&kv[gi][16][0] + (k * CA_NT + tid) * 8) = vr[k];
+        }
       }
     }
     __syncthreads();
 
     if (2 * wv < n) {
-      f32x4_t acc[16];
+      // scores of the block's groups, then one softmax over its keys
+      f32x4_t sc[2][2];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      float m_run = -INFINITY, l_run = 0.f;
-      for (int gi = 0; gi < gpb; ++gi) {
+      for (int gi = 0; gi < 2; ++gi) {
         const uint16_t* kvg = &kv[gi][0][0];
-        f32x4_t sc[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+          if (gi < gpb) {
 #pragma unroll
-          for (int sk = 0; sk < 8; ++sk) {
-            const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(kvg + ((t * 8 + sk) * 64 + lane) * 8);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qhi[sk], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qlo[sk], c, 0, 0, 0);
+            for (int sk = 0; sk < 8; ++sk) {
+              const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(kvg + ((t * 8 + sk) * 64 + lane) * 8);
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qhi[sk], c, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qlo[sk], c, 0, 0, 0);
+            }
           }
-          sc[t] = c;
-        }
-        // keys of a tail entry stop at the row's own position
-        const int kbase = j * A.ratio + gi * 32;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int kp = kbase + 16 * t + 4 * quad + v;
-            const float x = (ok && (!tail || kp <= p)) ? sc[t][v] * A.scale : -INFINITY;
-            sc[t][v] = x;
-            mx = fmaxf(mx, x);
-          }
-        mx = xor32_max(xor16_max(mx));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = m_run == -INFINITY ? 0.f : __expf(m_run - m_new);
-        bf16x8_t pf;
-        float lsum = 0.f;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const float pv = sc[t][v] == -INFINITY ? 0.f : __expf(sc[t][v] - m_new);
-            lsum += pv;
-            pf[4 * t + v] = __builtin_bit_cast(__bf16, f32_to_bf16(pv));
-          }
-        l_run = l_run * alpha + lsum;
-        m_run = m_new;
-#pragma unroll
-        for (int db = 0; db < 16; ++db) {
-          acc[db] = acc[db] * alpha;
-          const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(kvg + ((16 + db) * 64 + lane) * 8);
-          acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, acc[db], 0, 0, 0);
+          sc[gi][t] = c;
         }
       }
-      l_run = xor32_sum(xor16_sum(l_run));
-      if (ok) {
-        const long pb = ((row * A.hkv + g) * nslot + slot) * GQA + hh;
-        float* po = A.part_o + pb * QSA_D + 4 * quad;
+      float mx = -INFINITY;
 #pragma unroll
-        for (int db = 0; db < 16; ++db)
-          *reinterpret_cast<float4*>(po + 16 * db) = make_float4(acc[db][0], acc[db][1], acc[db][2], acc[db][3]);
-        if (quad == 0) {
-          A.part_ml[pb * 2 + 0] = m_run;
-          A.part_ml[pb * 2 + 1] = l_run;
+      for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            // keys of a tail entry stop at the row's own position
+            const int kp = j * A.ratio + gi * 32 + 16 * t + 4 * quad + v;
+            const float x = (ok && gi < gpb && (!tail || kp <= p)) ? sc[gi][t][v] * A.scale : -INFINITY;
+            sc[gi][t][v] = x;
+            mx = fmaxf(mx, x);
+          }
+      mx = xor32_max(xor16_max(mx));
+      float lsum = 0.f;
+      bf16x8_t pf[2];
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float pv = sc[gi][t][v] == -INFINITY ? 0.f : __expf(sc[gi][t][v] - mx);
+            lsum += pv;
+            pf[gi][4 * t + v] = __builtin_bit_cast(__bf16, f32_to_bf16(pv));
+          }
+      const float l = xor32_sum(xor16_sum(lsum));
+      const float rl = 1.0f / l;
+      const long pb = ((row * A.hkv + g) * nslot + slot) * GQA + hh;
+      uint16_t* po = A.part_o + pb * QSA_D + 4 * quad;
+#pragma unroll
+      for (int db = 0; db < 16; ++db) {
+        f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int gi = 0; gi < 2; ++gi) {
+          if (gi < gpb) {
+            const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(&kv[gi][16 + db][0] + lane * 8);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[gi], c, 0, 0, 0);
+          }
         }
+        if (ok) {
+          const unsigned lo = f32_to_bf16(c[0] * rl) | (static_cast<unsigned>(f32_to_bf16(c[1] * rl)) << 16);
+          const unsigned hi = f32_to_bf16(c[2] * rl) | (static_cast<unsigned>(f32_to_bf16(c[3] * rl)) << 16);
+          *reinterpret_cast<uint2*>(po + 16 * db) = make_uint2(lo, hi);
+        }
+      }
+      if (ok && quad == 0) {
+        A.part_ml[pb * 2 + 0] = mx;
+        A.part_ml[pb * 2 + 1] = l;
       }
     }
     __syncthreads();
@@ -1696,7 +1718,7 @@ ChunkWs chunk_ws_layout(const qm_qsa_geom* g, int seq) {
   const size_t rows = (size_t)g->batch * seq;
   ChunkWs w;
   w.o = 0;
-  w.ml = w.o + qm_align256(rows * g->n_kv_heads * nslot * GQA * QSA_D * sizeof(float));
+  w.ml = w.o + qm_align256(rows * g->n_kv_heads * nslot * GQA * QSA_D * sizeof(uint16_t));
   w.ent = w.ml + qm_align256(rows * g->n_kv_heads * nslot * GQA * 2 * sizeof(float));
   w.work = w.ent + qm_align256(rows * nslot * sizeof(unsigned));
   w.n_work = w.work + qm_align256(rows * nslot * sizeof(int4));
@@ -1737,7 +1759,7 @@ extern "C" int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q,
   char* base = static_cast<char*>(workspace);
   const int topk = g->budget / g->ratio;
   const int nslot = topk + 1;
-  float* part_o = reinterpret_cast<float*>(base + L.o);
+  uint16_t* part_o = reinterpret_cast<uint16_t*>(base + L.o);
   float* part_ml = reinterpret_cast<float*>(base + L.ml);
   unsigned* ent = reinterpret_cast<unsigned*>(base + L.ent);
   int4* work = reinterpret_cast<int4*>(base + L.work);
@@ -1759,16 +1781,16 @@ extern "C" int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q,
   A.scale = 1.0f / 16.0f;   // 1/sqrt(256), exact
   int nwg = 512 / (g->n_kv_heads * g->batch);
   nwg = nwg < 1 ? 1 : nwg > seq * nslot ? seq * nslot : nwg;
-  hipLaunchKernelGGL(qsa_chunk_attend_kernel, dim3(nwg, g->n_kv_heads, g->batch), dim3(CK_NT2), 0, stream, A);
+  hipLaunchKernelGGL(qsa_chunk_attend_kernel, dim3(nwg, g->n_kv_heads, g->batch), dim3(CA_NT), 0, stream, A);
   QM_CHECK_LAUNCH();
   if (g->act_dtype == QM_ACT_F32) {
-    CombineArgs<float> C{part_o, part_ml, static_cast<const float*>(qg), static_cast<float*>(out), g->n_heads,
+    CombineArgs<float, uint16_t> C{part_o, part_ml, static_cast<const float*>(qg), static_cast<float*>(out), g->n_heads,
                          g->n_kv_heads, nslot};
-    hipLaunchKernelGGL(qsa_combine_kernel<float>, dim3(g->n_heads, g->batch * seq), dim3(QSA_D), 0, stream, C);
+    hipLaunchKernelGGL((qsa_combine_kernel<float, uint16_t>), dim3(g->n_heads, g->batch * seq), dim3(QSA_D), 0, stream, C);
   } else {
-    CombineArgs<bf16_t> C{part_o, part_ml, static_cast<const bf16_t*>(qg), static_cast<bf16_t*>(out), g->n_heads,
+    CombineArgs<bf16_t, uint16_t> C{part_o, part_ml, static_cast<const bf16_t*>(qg), static_cast<bf16_t*>(out), g->n_heads,
                           g->n_kv_heads, nslot};
-    hipLaunchKernelGGL(qsa_combine_kernel<bf16_t>, dim3(g->n_heads, g->batch * seq), dim3(QSA_D), 0, stream, C);
+    hipLaunchKernelGGL((qsa_combine_kernel<bf16_t, uint16_t>), dim3(g->n_heads, g->batch * seq), dim3(QSA_D), 0, stream, C);
   }
   QM_CHECK_LAUNCH();
   return QM_OK;

@@ -3,7 +3,7 @@
 // chunk_gated_delta_rule (reference/layers.py:195-275). The chunk-local algebra
 // is independent across chunks and the state recurrence is not, so the rule
 // runs as two launches:
-//   dn_chunk_prep   one workgroup per (sequence, head, chunk): l2-normalises q
+//   dn_chunk_prep   four workgroups per (sequence, head, chunk): l2-normalises q
 //                   and k, takes the cumulative log-decay (in double, as torch's
 //                   CPU cumsum accumulates), forms L = (k beta k^T) * decay
 //                   below the diagonal and (q k^T) * decay on and below it,
@@ -32,6 +32,7 @@ constexpr int CK_LD = CK_D + 4;   // LDS row stride of [token][dim] tiles, float
 constexpr int CK_LT = CK_C + 4;   // LDS row stride of [.][token] tiles, floats
 constexpr int CK_COLS = 16;       // d_v columns per scan workgroup
 constexpr int CK_MIN_SEQ = 16;    // shorter prefill chunks take the token loop
+constexpr int CK_PARTS = 4;       // prep workgroups per chunk
 
 // One fp32 record per (sequence, head, chunk):
 //   w   [64][128]   T (k beta e^cum)
@@ -114,8 +115,11 @@ struct PrepShared {
 template <typename T>
 __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A) {
   __shared__ PrepShared sh;
-  const int c = blockIdx.x % A.n_chunks;
-  const int bh = blockIdx.x / A.n_chunks;
+  // CK_PARTS workgroups per chunk: each forms L and T (cheap, shared), then
+  // writes its quarter of qk, q_dec, k_dec^T and of the w / u columns
+  const int part = blockIdx.x % CK_PARTS;
+  const int c = (blockIdx.x / CK_PARTS) % A.n_chunks;
+  const int bh = blockIdx.x / CK_PARTS / A.n_chunks;
   const int h = bh % A.heads, b = bh / A.heads;
   const int t0 = c * CK_C;
   const int n_valid = min(CK_C, A.seq - t0);
@@ -143,7 +147,7 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
     sh.ecum[lane] = ec;
     sh.bec[lane] = bv * ec;
     sh.kds[lane] = expf(last - cum);
-    if (lane == 0) rec[CK_ECL] = expf(last);
+    if (lane == 0 && part == 0) rec[CK_ECL] = expf(last);
   }
 
   // q, k, v rows: four threads per token, 32 dims each as four runs of 8
@@ -224,8 +228,9 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
 #pragma unroll
     for (int i = 0; i < 16; ++i) sh.Tm[16 * I + i][16 * I + col] = x[i];
   } else {
-    // qk = (q k^T) * exp(cum_i - cum_j) for j <= i
-    for (int ti = wid - 1; ti < 10; ti += 3) {
+    // qk = (q k^T) * exp(cum_i - cum_j) for j <= i: this part's tiles part, part + 4, part + 8
+    const int ti = part + 4 * (wid - 1);
+    if (ti < 10) {
       int I, J;
       tile_ij(ti, I, J);
       const f32x4_t acc = gram_tile(&sh.q[16 * I + r16][4 * g4], &sh.k[16 * J + r16][4 * g4]);
@@ -240,7 +245,7 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
 
   // q e^cum as [token][dim] and (k e^(cum_last - cum))^T as [dim][token]
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
+  for (int it = 2 * part; it < 2 * part + 2; ++it) {
     const int idx = tid + CK_NT * it;
     const int t = idx >> 5, d = 4 * (idx & 31);
     const float4 x = lds4(&sh.q[t][d]);
@@ -248,7 +253,7 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
     *reinterpret_cast<float4*>(rec + CK_QD + t * CK_D + d) = make_float4(x.x * e, x.y * e, x.z * e, x.w * e);
   }
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
+  for (int it = 2 * part; it < 2 * part + 2; ++it) {
     const int idx = tid + CK_NT * it;
     const int t = 4 * (idx & 15), d = idx >> 4;
     *reinterpret_cast<float4*>(rec + CK_KDT + d * CK_C + t) =
@@ -277,10 +282,11 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
     __syncthreads();
   }
 
-  // w = T (k beta e^cum) and u = T (v beta); wave wid takes column tiles 2wid, 2wid+1 of each
-  for (int job = 0; job < 4; ++job) {
-    const bool is_u = job >= 2;
-    const int col = 16 * (2 * wid + (job & 1)) + r16;
+  // w = T (k beta e^cum) and u = T (v beta): this part's column tiles 2 part,
+  // 2 part + 1 of each, one per wave
+  {
+    const bool is_u = wid >= 2;
+    const int col = 16 * (2 * part + (wid & 1)) + r16;
     float bo[4][4];
 #pragma unroll
     for (int K = 0; K < 4; ++K) {
@@ -398,7 +404,7 @@ int launch_chunked(int batch, int seq, int heads, int hk, long q_stride, long v_
   P.g = g; P.beta = beta; P.ws = ws;
   P.batch = batch; P.seq = seq; P.heads = heads; P.hk = hk; P.n_chunks = n_chunks;
   P.q_stride = q_stride; P.v_stride = v_stride;
-  hipLaunchKernelGGL(dn_chunk_prep_kernel<T>, dim3(batch * heads * n_chunks), dim3(CK_NT), 0, stream, P);
+  hipLaunchKernelGGL(dn_chunk_prep_kernel<T>, dim3(batch * heads * n_chunks * CK_PARTS), dim3(CK_NT), 0, stream, P);
   QM_CHECK_LAUNCH();
   ChunkScanArgs<T> S;
   S.ws = ws; S.state = state; S.out = static_cast<T*>(out);

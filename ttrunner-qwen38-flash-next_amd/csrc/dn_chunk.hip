@@ -3,7 +3,7 @@
 // chunk_gated_delta_rule (reference/layers.py:195-275). The chunk-local algebra
 // is independent across chunks and the state recurrence is not, so the rule
 // runs as two launches:
-//   dn_chunk_prep   four workgroups per (sequence, head, chunk): l2-normalises q
+//   dn_chunk_prep   one or four workgroups per (sequence, head, chunk): l2-normalises q
 //                   and k, takes the cumulative log-decay (in double, as torch's
 //                   CPU cumsum accumulates), forms L = (k beta k^T) * decay
 //                   below the diagonal and (q k^T) * decay on and below it,
@@ -32,7 +32,7 @@ constexpr int CK_LD = CK_D + 4;   // LDS row stride of [token][dim] tiles, float
 constexpr int CK_LT = CK_C + 4;   // LDS row stride of [.][token] tiles, floats
 constexpr int CK_COLS = 16;       // d_v columns per scan workgroup
 constexpr int CK_MIN_SEQ = 16;    // shorter prefill chunks take the token loop
-constexpr int CK_PARTS = 4;       // prep workgroups per chunk
+constexpr int CK_PARTS = 4;       // prep workgroups per chunk when chunks are few
 
 // One fp32 record per (sequence, head, chunk):
 //   w   [64][128]   T (k beta e^cum)
@@ -100,6 +100,7 @@ struct ChunkPrepArgs {
   const float* g; const float* beta;    // [B, S, H]
   float* ws;                            // [B, H, n_chunks] records
   int batch, seq, heads, hk, n_chunks;  // head h reads q/k head h % hk
+  int parts;                            // workgroups per chunk: 1 or CK_PARTS
   long q_stride, v_stride;
 };
 
@@ -115,11 +116,12 @@ struct PrepShared {
 template <typename T>
 __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A) {
   __shared__ PrepShared sh;
-  // CK_PARTS workgroups per chunk: each forms L and T (cheap, shared), then
-  // writes its quarter of qk, q_dec, k_dec^T and of the w / u columns
-  const int part = blockIdx.x % CK_PARTS;
-  const int c = (blockIdx.x / CK_PARTS) % A.n_chunks;
-  const int bh = blockIdx.x / CK_PARTS / A.n_chunks;
+  // A.parts workgroups per chunk: each forms L and T, then writes its share
+  // (all of it, or a quarter) of qk, q_dec, k_dec^T and of the w / u columns
+  const int part = blockIdx.x % A.parts;
+  const int c = (blockIdx.x / A.parts) % A.n_chunks;
+  const int bh = blockIdx.x / A.parts / A.n_chunks;
+  const int span = CK_PARTS / A.parts;       // quarters this workgroup writes
   const int h = bh % A.heads, b = bh / A.heads;
   const int t0 = c * CK_C;
   const int n_valid = min(CK_C, A.seq - t0);
@@ -228,9 +230,12 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
 #pragma unroll
     for (int i = 0; i < 16; ++i) sh.Tm[16 * I + i][16 * I + col] = x[i];
   } else {
-    // qk = (q k^T) * exp(cum_i - cum_j) for j <= i: this part's tiles part, part + 4, part + 8
-    const int ti = part + 4 * (wid - 1);
-    if (ti < 10) {
+    // qk = (q k^T) * exp(cum_i - cum_j) for j <= i: tile ti belongs to quarter
+    // ti % 4; this workgroup's tiles go round-robin to waves 1-3
+    int k = 0;
+    for (int ti = 0; ti < 10; ++ti) {
+      if ((ti & 3) / span != part) continue;
+      if (k++ % 3 != wid - 1) continue;
       int I, J;
       tile_ij(ti, I, J);
       const f32x4_t acc = gram_tile(&sh.q[16 * I + r16][4 * g4], &sh.k[16 * J + r16][4 * g4]);
@@ -244,16 +249,14 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   }
 
   // q e^cum as [token][dim] and (k e^(cum_last - cum))^T as [dim][token]
-#pragma unroll
-  for (int it = 2 * part; it < 2 * part + 2; ++it) {
+  for (int it = 2 * span * part; it < 2 * span * (part + 1); ++it) {
     const int idx = tid + CK_NT * it;
     const int t = idx >> 5, d = 4 * (idx & 31);
     const float4 x = lds4(&sh.q[t][d]);
     const float e = sh.ecum[t];
     *reinterpret_cast<float4*>(rec + CK_QD + t * CK_D + d) = make_float4(x.x * e, x.y * e, x.z * e, x.w * e);
   }
-#pragma unroll
-  for (int it = 2 * part; it < 2 * part + 2; ++it) {
+  for (int it = 2 * span * part; it < 2 * span * (part + 1); ++it) {
     const int idx = tid + CK_NT * it;
     const int t = 4 * (idx & 15), d = idx >> 4;
     *reinterpret_cast<float4*>(rec + CK_KDT + d * CK_C + t) =
@@ -282,11 +285,11 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
     __syncthreads();
   }
 
-  // w = T (k beta e^cum) and u = T (v beta): this part's column tiles 2 part,
-  // 2 part + 1 of each, one per wave
-  {
+  // w = T (k beta e^cum) and u = T (v beta): quarter r holds column tiles 2r
+  // and 2r + 1 of each, one (matrix, tile) per wave
+  for (int kq = 0; kq < span; ++kq) {
     const bool is_u = wid >= 2;
-    const int col = 16 * (2 * part + (wid & 1)) + r16;
+    const int col = 16 * (2 * (span * part + kq) + (wid & 1)) + r16;
     float bo[4][4];
 #pragma unroll
     for (int K = 0; K < 4; ++K) {
@@ -318,6 +321,37 @@ struct ChunkScanArgs {
   int batch, seq, heads, n_chunks;
 };
 
+// A wave's operands of one chunk, none of which depends on the state: its 16
+// rows of w and q_dec, its row block of qk (blocks j <= wave used), its two
+// 16-row blocks of k_dec^T, its 4 values of u, and e^cum_last.
+struct ScanOps {
+  float4 w[8], qd[8], qk[4], kd[2][4];
+  float u[4], ecl;
+};
+
+__device__ __forceinline__ void load_scan_ops(const float* rec, int wid, int g4, int r16, int col0, ScanOps& o) {
+  const float* wr = rec + CK_W + (16 * wid + r16) * CK_D + 4 * g4;
+  const float* qr = rec + CK_QD + (16 * wid + r16) * CK_D + 4 * g4;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    o.w[j] = ld4(wr + 16 * j);
+    o.qd[j] = ld4(qr + 16 * j);
+  }
+  const float* qkr = rec + CK_QK + (16 * wid + r16) * CK_C + 4 * g4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o.qk[j] = ld4(qkr + 16 * j);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const float* kr = rec + CK_KDT + (32 * wid + 16 * t + r16) * CK_C + 4 * g4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.kd[t][j] = ld4(kr + 16 * j);
+  }
+  const float* ur = rec + CK_U + (16 * wid + 4 * g4) * CK_D + col0 + r16;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) o.u[v] = ur[v * CK_D];
+  o.ecl = rec[CK_ECL];
+}
+
 template <typename T>
 __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A) {
   __shared__ float sST[CK_COLS][CK_LD];  // the state slice, transposed: [column][d_k]
@@ -330,7 +364,11 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
   const int col0 = sl * CK_COLS;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int g4 = lane >> 4, r16 = lane & 15;
+  const float* recs = A.ws + (long)bh * A.n_chunks * CK_REC;
 
+  // the first chunk's operands are in flight with the state
+  ScanOps cur;
+  load_scan_ops(recs, wid, g4, r16, col0, cur);
   // wave wid keeps d_k rows 32wid .. 32wid+31 of the slice as two result tiles
   float* S = A.state + (long)bh * CK_D * CK_D + col0 + r16;
   f32x4_t st[2];
@@ -343,26 +381,29 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
   }
 
   for (int ci = 0; ci < A.n_chunks; ++ci) {
-    const float* rec = A.ws + ((long)bh * A.n_chunks + ci) * CK_REC;
+    // the next chunk's operands fly during this one (the last chunk reloads its own)
+    ScanOps nxt;
+    load_scan_ops(recs + (long)min(ci + 1, A.n_chunks - 1) * CK_REC, wid, g4, r16, col0, nxt);
     __syncthreads();
     // rows 16wid.. of w S and q_dec S
     f32x4_t aw = {0.f, 0.f, 0.f, 0.f}, ao = {0.f, 0.f, 0.f, 0.f};
-    const float* wr = rec + CK_W + (16 * wid + r16) * CK_D + 4 * g4;
-    const float* qr = rec + CK_QD + (16 * wid + r16) * CK_D + 4 * g4;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float4 sb = lds4(&sST[r16][16 * j + 4 * g4]);
-      aw = mfma4x4(ld4(wr + 16 * j), sb, aw);
-      ao = mfma4x4(ld4(qr + 16 * j), sb, ao);
+      aw = mfma4x4(cur.w[j], sb, aw);
+      ao = mfma4x4(cur.qd[j], sb, ao);
     }
-    const float* ur = rec + CK_U + (16 * wid + 4 * g4) * CK_D + col0 + r16;
     *reinterpret_cast<float4*>(&sVT[r16][16 * wid + 4 * g4]) =
-        make_float4(ur[0] - aw[0], ur[CK_D] - aw[1], ur[2 * CK_D] - aw[2], ur[3 * CK_D] - aw[3]);
+        make_float4(cur.u[0] - aw[0], cur.u[1] - aw[1], cur.u[2] - aw[2], cur.u[3] - aw[3]);
     __syncthreads();
 
     // out rows 16wid..: q_dec S + qk v_new over the causal blocks j <= wid
-    const float* qkr = rec + CK_QK + (16 * wid + r16) * CK_C + 4 * g4;
-    for (int j = 0; j <= wid; ++j) ao = mfma4x4(ld4(qkr + 16 * j), lds4(&sVT[r16][16 * j + 4 * g4]), ao);
+    float4 vb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vb[j] = lds4(&sVT[r16][16 * j + 4 * g4]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (j <= wid) ao = mfma4x4(cur.qk[j], vb[j], ao);
     const int tok0 = ci * CK_C + 16 * wid + 4 * g4;
 #pragma unroll
     for (int v = 0; v < 4; ++v)
@@ -370,20 +411,16 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
         Act<T>::store(A.out, (((long)b * A.seq + tok0 + v) * A.heads + h) * CK_D + col0 + r16, ao[v]);
 
     // S = S e^cum_last + k_dec^T v_new on this wave's rows
-    const float ecl = rec[CK_ECL];
-    float4 vb[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) vb[j] = lds4(&sVT[r16][16 * j + 4 * g4]);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int row = 32 * wid + 16 * t;
-      const float* kr = rec + CK_KDT + (row + r16) * CK_C + 4 * g4;
-      f32x4_t acc = {st[t][0] * ecl, st[t][1] * ecl, st[t][2] * ecl, st[t][3] * ecl};
+      f32x4_t acc = {st[t][0] * cur.ecl, st[t][1] * cur.ecl, st[t][2] * cur.ecl, st[t][3] * cur.ecl};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc = mfma4x4(ld4(kr + 16 * j), vb[j], acc);
+      for (int j = 0; j < 4; ++j) acc = mfma4x4(cur.kd[t][j], vb[j], acc);
       st[t] = acc;
       *reinterpret_cast<float4*>(&sST[r16][row + 4 * g4]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     }
+    cur = nxt;
   }
 
 #pragma unroll
@@ -404,7 +441,10 @@ int launch_chunked(int batch, int seq, int heads, int hk, long q_stride, long v_
   P.g = g; P.beta = beta; P.ws = ws;
   P.batch = batch; P.seq = seq; P.heads = heads; P.hk = hk; P.n_chunks = n_chunks;
   P.q_stride = q_stride; P.v_stride = v_stride;
-  hipLaunchKernelGGL(dn_chunk_prep_kernel<T>, dim3(batch * heads * n_chunks * CK_PARTS), dim3(CK_NT), 0, stream, P);
+  // few chunks: four workgroups per chunk so that the launch fills the chip;
+  // many: one each, since every workgroup repeats the L and T work
+  P.parts = (long)batch * heads * n_chunks < 256 ? CK_PARTS : 1;
+  hipLaunchKernelGGL(dn_chunk_prep_kernel<T>, dim3(batch * heads * n_chunks * P.parts), dim3(CK_NT), 0, stream, P);
   QM_CHECK_LAUNCH();
   ChunkScanArgs<T> S;
   S.ws = ws; S.state = state; S.out = static_cast<T*>(out);

@@ -88,17 +88,27 @@ __device__ float pool_block(int j, int ratio, int rope, float eps, const float* 
   const int tid = threadIdx.x;
   const int t0 = j * ratio;
   if (tid < IDX_D) {
+    // 64 rows' loads are issued together: each row's source is chosen by
+    // address, and rows past the block are clamped and not added
     float total = 0.f;
-    for (int c0 = 0; c0 < ratio; c0 += 16) {
-      float acc = 0.f;
-      const int c1 = min(c0 + 16, ratio);
-      for (int i = c0; i < c1; ++i) {
-        const int tok = t0 + i;
-        const float v = tok >= new0 ? Act<T>::load(fresh, (long)(tok - new0) * IDX_D + tid)
-                                    : Act<T>::load(cache, (long)tok * IDX_D + tid);
-        acc = add_rn(acc, v);
+    for (int r0 = 0; r0 < ratio; r0 += 64) {
+      float v[64];
+#pragma unroll
+      for (int i = 0; i < 64; ++i) {
+        const int tok = t0 + min(r0 + i, ratio - 1);
+        const T* src = tok >= new0 ? fresh + (long)(tok - new0) * IDX_D : cache + (long)tok * IDX_D;
+        v[i] = Act<T>::load(src, tid);
       }
-      total = c0 == 0 ? acc : add_rn(total, acc);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int c0 = r0 + 16 * c;
+        if (c0 < ratio) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc = c0 + i < ratio ? add_rn(acc, v[16 * c + i]) : acc;
+          total = c0 == 0 ? acc : add_rn(total, acc);
+        }
+      }
     }
     s_x[tid] = Act<T>::round(div_rn(total, (float)ratio));
   }
@@ -120,8 +130,11 @@ struct PrepArgs {
   float eps;
 };
 
-// Roles 0..Hq-1: attention query head `role` (RMS norm, rope, bf16 hi/lo).
-// Roles Hq..Hq+Hkv-1: key/value head (norm + rope the key, append both).
+// qsa_prep_kernel grid: (row, role). Roles 0..Hq-1: attention query head
+// `role` (RMS norm, rope, bf16 hi/lo). Roles Hq..Hq+Hkv-1: key/value head
+// (norm + rope the key, append both). Then one role per indexer query head,
+// and a last one that appends the raw indexer key and pools a block the row
+// completes.
 template <typename T>
 __device__ void prep_head(const PrepArgs<T>& A, int b, int s, int role) {
   __shared__ float s_x[QSA_D], s_y[QSA_D], s_scr[32];
@@ -158,7 +171,9 @@ template <typename T>
 __global__ __launch_bounds__(PREP_NT) void qsa_prep_kernel(PrepArgs<T> A) {
   const int row = blockIdx.x;               // b * seq + s
   const int b = row / A.seq, s = row % A.seq;
-  const int role = blockIdx.y;
+  // workgroups start in blockIdx order: the last role (raw key append and the
+  // pooling of a completed block, the longest) goes at y = 0
+  const int role = (blockIdx.y + gridDim.y - 1) % gridDim.y;
   const int tid = threadIdx.x;
   const int pos0 = A.positions[b];
   const int pos = pos0 + s;
@@ -171,14 +186,12 @@ __global__ __launch_bounds__(PREP_NT) void qsa_prep_kernel(PrepArgs<T> A) {
     prep_head<T>(A, b, s, role);
     return;
   }
-  if (role == A.hq + A.hkv) {
-    // -------- indexer query heads, one after another
-    for (int h = 0; h < A.idx_heads; ++h) {
-      __syncthreads();
-      if (tid < IDX_D) s_x[tid] = Act<T>::load(A.iq, ((long)row * A.idx_heads + h) * IDX_D + tid);
-      const float y = norm_rope_row<T>(s_x, s_y, s_scr, IDX_D, A.iq_norm, A.eps, A.rope, cs, sn);
-      if (tid < IDX_D) A.iq_out[((long)row * A.idx_heads + h) * IDX_D + tid] = y;
-    }
+  if (role < A.hq + A.hkv + A.idx_heads) {
+    // -------- one indexer query head
+    const int h = role - A.hq - A.hkv;
+    if (tid < IDX_D) s_x[tid] = Act<T>::load(A.iq, ((long)row * A.idx_heads + h) * IDX_D + tid);
+    const float y = norm_rope_row<T>(s_x, s_y, s_scr, IDX_D, A.iq_norm, A.eps, A.rope, cs, sn);
+    if (tid < IDX_D) A.iq_out[((long)row * A.idx_heads + h) * IDX_D + tid] = y;
     return;
   }
   // -------- raw indexer key append, and the pooled key of a completed block
@@ -1561,7 +1574,7 @@ int launch_prep(const qm_qsa_geom* g, int seq, const void* qg, const void* k_new
                 void* v_pool, void* raw_keys, float* block_keys, void* q_out, float* iq_out, hipStream_t stream) {
   PrepArgs<T> A = prep_args<T>(g, seq, qg, k_new, v_new, iq, ik, q_norm, k_norm, iq_norm, ik_norm, cos, sin,
                                positions, page_table, k_pool, v_pool, raw_keys, block_keys, q_out, iq_out);
-  dim3 grid(g->batch * seq, g->n_heads + g->n_kv_heads + 2);
+  dim3 grid(g->batch * seq, g->n_heads + g->n_kv_heads + g->idx_heads + 1);
   hipLaunchKernelGGL(qsa_prep_kernel<T>, grid, dim3(PREP_NT), 0, stream, A);
   QM_CHECK_LAUNCH();
   return QM_OK;

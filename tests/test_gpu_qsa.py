@@ -128,7 +128,9 @@ def test_indexer_stages_and_selection_match_reference(gpu, tag):
 
 @pytest.mark.parametrize("pos,dtype", [(192, torch.float32), (1984, torch.bfloat16), (4032, torch.bfloat16),
                                        (8128, torch.bfloat16), (130, torch.bfloat16), (2047, torch.bfloat16),
-                                       (0, torch.bfloat16), (63, torch.bfloat16)])
+                                       (0, torch.bfloat16), (63, torch.bfloat16),
+                                       # more than 128 eligible blocks: top-k by radix select
+                                       (9000, torch.bfloat16), (20000, torch.bfloat16)])
 def test_decode_core_matches_oracle(gpu, pos, dtype):
     cfg = OracleConfig()
     store = gi.FakeStore(gi.qsa_weights(3, 61, dtype))
@@ -305,7 +307,7 @@ def test_consecutive_decode_steps_cross_a_block_boundary(gpu):
         assert rel_err(got, want) < OUT_TOL, pos
 
 
-@pytest.mark.parametrize("pos", [63, 127, 2047, 4095, 8127, 8128, 300])
+@pytest.mark.parametrize("pos", [63, 127, 2047, 4095, 8127, 8128, 300, 9000, 20031])
 def test_fused_decode_front_equals_prep_then_select(gpu, pos):
     """qm_qsa_decode_front (one launch) == qm_qsa_prep + qm_qsa_select, bit for
     bit: pooled block keys (including the block this token completes), the

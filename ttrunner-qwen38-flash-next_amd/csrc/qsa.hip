@@ -221,7 +221,8 @@ __global__ __launch_bounds__(IDX_D) void qsa_pool_kernel(PoolArgs<T> A) {
 // ---------------------------------------------------------------------------
 // selection
 // ---------------------------------------------------------------------------
-constexpr int SEL_NT = 256;
+constexpr int SEL_NT = 256;             // the decode front kernel (its prep roles need 256)
+constexpr int SELP_NT = 1024;           // qsa_select_kernel: one row per workgroup
 constexpr int SEL_MAX_BLOCKS = 4096;    // eligible blocks one query may score
 
 __device__ __forceinline__ unsigned long long sel_key(float s, int j) {
@@ -241,8 +242,7 @@ __device__ __forceinline__ int2 make_item(int phys_row, int lo, int hi) { return
 // 128-byte lines, and the lanes add their partial dot products with three DPP
 // exchanges (all 8 lanes end with the same sum: float addition commutes). Each
 // lane keeps the matching chunks of the 4 query heads in registers.
-constexpr int SCORE_LANES = 8;
-constexpr int SCORE_PASS = 256 / SCORE_LANES;   // blocks per pass at 256 threads
+constexpr int SCORE_LANES = 8;                  // NT / 8 blocks per pass of NT threads
 constexpr int SCORE_PRE = 4;                    // passes of keys held in registers ahead of use
 
 // (an invalid j loads row 0, always allocated, and zeroes the result: the
@@ -291,7 +291,7 @@ template <int NT>
 __device__ void score_blocks(const float* s_iq, const float* new_key, const float* bk, int n_elig, int new_j,
                              int idx_heads, unsigned long long* keys, float* scores_out,
                              float4 (&kp)[SCORE_PRE][4]) {
-  static_assert(NT / SCORE_LANES == SCORE_PASS, "8 lanes per block");
+  constexpr int SCORE_PASS = NT / SCORE_LANES;
   const int tid = threadIdx.x, jl = tid >> 3, part = tid & 7;
   float4 q[4][4];
 #pragma unroll
@@ -325,8 +325,10 @@ __device__ void score_blocks(const float* s_iq, const float* new_key, const floa
 }
 
 // prefetch of the first SCORE_PRE passes (issued before the scores are needed)
+template <int NT>
 __device__ __forceinline__ void prefetch_block_keys(float4 (&kp)[SCORE_PRE][4], const float* bk, int n_elig,
                                                     int new_j, bool on) {
+  constexpr int SCORE_PASS = NT / SCORE_LANES;
   const int jl = threadIdx.x >> 3;
 #pragma unroll
   for (int u = 0; u < SCORE_PRE; ++u) {
@@ -335,15 +337,22 @@ __device__ __forceinline__ void prefetch_block_keys(float4 (&kp)[SCORE_PRE][4], 
   }
 }
 
-// Top-k by counting: the keys are distinct, so the rank of key j is the number
-// of larger keys, and sel[rank] = j for rank < topk. `keys` is padded with
-// zeros (below every real key) to a multiple of 32. Up to NT/2 keys, two
-// adjacent lanes split the comparisons of one key and add their counts by DPP.
-template <int NT>
-__device__ void rank_topk(const unsigned long long* keys, int n, int topk, int* sel) {
+// Top-k of distinct 64-bit keys; sel[rank] = j for rank < topk (rank = the
+// number of larger keys). `keys` is padded with zeros (below every real key) to
+// a multiple of 32. Up to 128 keys (n <= NT/2), by counting: two adjacent lanes
+// split the comparisons of one key and add their counts by DPP. Beyond, by
+// radix select: eight passes of an 8-bit histogram (LDS atomics, then a suffix
+// scan over the 256 digits) pin the topk-th largest key T exactly, the keys
+// >= T are gathered, and only they are ranked among themselves. `scr` holds
+// rank_scratch(MAXK) ints of LDS; topk <= MAXK.
+constexpr int rank_scratch(int maxk) { return 256 + 40 + maxk; }
+
+template <int NT, int MAXK>
+__device__ void rank_topk(const unsigned long long* keys, int n, int topk, int* sel, int* scr) {
+  static_assert(NT >= 256 && NT % 64 == 0 && NT <= 1024, "one digit per thread");
   const int tid = threadIdx.x;
   const int npad = (n + 31) & ~31;
-  if (n <= NT / 2) {
+  if (n <= NT / 2 && n <= 128) {
     const int j = tid >> 1, part = tid & 1, half = npad >> 1;
     const unsigned long long kj = keys[j < n ? j : 0];
     int rank = 0;
@@ -356,19 +365,63 @@ __device__ void rank_topk(const unsigned long long* keys, int n, int topk, int* 
     }
     rank += __builtin_amdgcn_update_dpp(0, rank, 0xB1, 0xF, 0xF, true);
     if (part == 0 && j < n && rank < topk) sel[rank] = j;
-  } else {
+    return;
+  }
+  int* hist = scr;                        // [256]
+  int* wtot = scr + 256;                  // [16]
+  int* state = scr + 256 + 32;            // prefix lo, prefix hi, remaining, count
+  int* cand = scr + 256 + 40;             // [topk]
+  const int lane = tid & 63, wv = tid >> 6;
+  unsigned long long prefix = 0ull;
+  int r = topk;
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    if (tid < 256) hist[tid] = 0;
+    __syncthreads();
     for (int j = tid; j < n; j += NT) {
-      const unsigned long long kj = keys[j];
-      int rank = 0;
-      for (int i = 0; i < npad; i += 16) {
-        unsigned long long k16[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) k16[u] = keys[i + u];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) rank += k16[u] > kj ? 1 : 0;
-      }
-      if (rank < topk) sel[rank] = j;
+      const unsigned long long k = keys[j];
+      const bool match = shift == 56 || ((k ^ prefix) >> (shift + 8)) == 0ull;
+      if (match) atomicAdd(&hist[(k >> shift) & 255], 1);
     }
+    __syncthreads();
+    // suffix sums over the digits: thread t takes digit 255 - t
+    int h = 0, incl = 0;
+    if (tid < 256) {
+      h = hist[255 - tid];
+      incl = h;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int x = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += x;
+      }
+      if (lane == 63) wtot[wv] = incl;
+    }
+    __syncthreads();
+    if (tid < 256) {
+      for (int w = 0; w < wv; ++w) incl += wtot[w];
+      const int above = incl - h;          // keys of the prefix with a larger digit
+      if (above < r && incl >= r) {
+        const unsigned long long np = prefix | (static_cast<unsigned long long>(255 - tid) << shift);
+        state[0] = static_cast<int>(np & 0xffffffffull);
+        state[1] = static_cast<int>(np >> 32);
+        state[2] = r - above;
+      }
+    }
+    __syncthreads();
+    prefix = (static_cast<unsigned long long>(static_cast<unsigned>(state[1])) << 32) |
+             static_cast<unsigned>(state[0]);
+    r = state[2];
+  }
+  // prefix is now the topk-th largest key: gather the keys >= it, then rank them
+  if (tid == 0) state[3] = 0;
+  __syncthreads();
+  for (int j = tid; j < n; j += NT)
+    if (keys[j] >= prefix) cand[atomicAdd(&state[3], 1)] = j;
+  __syncthreads();
+  for (int c = tid; c < topk; c += NT) {
+    const unsigned long long kc = keys[cand[c]];
+    int rank = 0;
+    for (int i = 0; i < topk; ++i) rank += keys[cand[i]] > kc ? 1 : 0;
+    sel[rank] = cand[c];
   }
 }
 
@@ -384,12 +437,14 @@ struct SelShared {
   unsigned long long key[SEL_MAX_BLOCKS];
   int pages[SEL_MAX_BLOCKS];
   int sel[SEL_MAX_BLOCKS / 2];
+  int rscr[rank_scratch(SEL_MAX_BLOCKS / 2)];
 };
 
 // Selection for one query row at position p, by a whole SEL_NT-thread block.
 // The indexer query must already be in S.q (heads past idx_heads zero). Block
 // keys come from the cache, except block new_j (>= 0 when this very launch
 // completed it), whose key is in S.newkey.
+template <int NT>
 __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p, int new_j) {
   const int tid = threadIdx.x;
   const int n_elig = min((p + 1) / A.ratio, A.max_blocks);
@@ -399,27 +454,27 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
   // the page-table row, needed to describe the attention items, comes in with the keys
   const int n_lpages = min(A.max_pages, (p + A.page_size) / A.page_size);
   if (A.items)
-    for (int i = tid; i < n_lpages; i += SEL_NT) S.pages[i] = A.page_table[(long)b * A.max_pages + i];
+    for (int i = tid; i < n_lpages; i += NT) S.pages[i] = A.page_table[(long)b * A.max_pages + i];
   if (A.scores_out)
-    for (int j = tid; j < A.max_blocks; j += SEL_NT)
+    for (int j = tid; j < A.max_blocks; j += NT)
       if (j >= n_elig) A.scores_out[(long)row * A.max_blocks + j] = -INFINITY;
 
   if (n_elig > A.topk || A.scores_out) {
     // the first two passes of block keys are in flight across the barrier
     const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
     float4 kp[SCORE_PRE][4];
-    prefetch_block_keys(kp, bk, n_elig, new_j, true);
+    prefetch_block_keys<NT>(kp, bk, n_elig, new_j, true);
     __syncthreads();    // S.q and S.newkey visible
-    score_blocks<SEL_NT>(S.q, S.newkey, bk, n_elig, new_j, A.idx_heads, S.key,
+    score_blocks<NT>(S.q, S.newkey, bk, n_elig, new_j, A.idx_heads, S.key,
                          A.scores_out ? A.scores_out + (long)row * A.max_blocks : nullptr, kp);
   }
   __syncthreads();
   if (n_elig <= A.topk) {
-    for (int i = tid; i < n_elig; i += SEL_NT) { out_ids[i] = i; S.sel[i] = i; }
+    for (int i = tid; i < n_elig; i += NT) { out_ids[i] = i; S.sel[i] = i; }
   } else {
-    rank_topk<SEL_NT>(S.key, n_elig, A.topk, S.sel);
+    rank_topk<NT, SEL_MAX_BLOCKS / 2>(S.key, n_elig, A.topk, S.sel, S.rscr);
     __syncthreads();
-    for (int i = tid; i < A.topk; i += SEL_NT) out_ids[i] = S.sel[i];
+    for (int i = tid; i < A.topk; i += NT) out_ids[i] = S.sel[i];
   }
   if (tid == 0) A.n_sel[row] = n_sel;
   if (!A.items) return;
@@ -431,7 +486,7 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
   const int ts = ((p + 1) / A.ratio) * A.ratio;
   const int n_tail = ts > p ? 0 : (p >> 5) - (ts >> 5) + 1;
   const int n_items = n_blk_items + n_tail;
-  for (int it = tid; it < n_items; it += SEL_NT) {
+  for (int it = tid; it < n_items; it += NT) {
     int t0, lo, hi;
     if (it < n_blk_items) {
       const int bs = S.sel[it / gpb] * A.ratio;
@@ -448,15 +503,15 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
   if (tid == 0) items[0] = make_int2(n_items, 0);
 }
 
-__global__ __launch_bounds__(SEL_NT) void qsa_select_kernel(SelArgs A) {
+__global__ __launch_bounds__(SELP_NT) void qsa_select_kernel(SelArgs A) {
   const int row = blockIdx.x;
   const int b = row / A.seq, s = row % A.seq;
   const int p = A.positions[b] + s;
   __shared__ SelShared S;
-  for (int i = threadIdx.x; i < 4 * IDX_D; i += SEL_NT)
+  for (int i = threadIdx.x; i < 4 * IDX_D; i += SELP_NT)
     S.q[i] = i < A.idx_heads * IDX_D ? A.iq[(long)row * A.idx_heads * IDX_D + i] : 0.f;
   __syncthreads();
-  select_row(A, S, row, b, p, -1);
+  select_row<SELP_NT>(A, S, row, b, p, -1);
 }
 
 // Decode (one token per sequence) front end in one launch: the query, key and
@@ -502,7 +557,7 @@ __global__ __launch_bounds__(SEL_NT) void qsa_front_kernel(PrepArgs<T> A, SelArg
     if (tid < IDX_D) S.newkey[tid] = y;
   }
   __syncthreads();
-  select_row(SA, S, b, b, p, new_j);
+  select_row<SEL_NT>(SA, S, b, b, p, new_j);
 }
 
 // ---------------------------------------------------------------------------
@@ -1069,6 +1124,7 @@ struct DecShared {
   float chunk[DEC_MAX_RATIO / 16][IDX_D];
   int pages[DEC_MAX_PAGES];
   int sel[DEC_MAX_TOPK];
+  int rscr[rank_scratch(DEC_MAX_TOPK)];
   alignas(16) float s[GQA][32];                   // the item's scores, head-major
   int ticket;
 };
@@ -1185,7 +1241,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
   const bool scoring = n_elig > topk;
   float4 kp[SCORE_PRE][4];
-  prefetch_block_keys(kp, bk, n_elig, j_new, scoring);
+  prefetch_block_keys<DEC_NT>(kp, bk, n_elig, j_new, scoring);
   // raw keys of the block this token completes: thread (e128, hh) takes the
   // 16-row chunks hh and hh + 2; the token's own row is ik (not yet stored)
   float rk[2][16];
@@ -1280,7 +1336,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   if (scoring && (blk_item || item == 0)) {
     score_blocks<DEC_NT>(sh.iq, sh.newkey, bk, n_elig, j_new, A.idx_heads, sh.key, nullptr, kp);
     __syncthreads();
-    rank_topk<DEC_NT>(sh.key, n_elig, topk, sh.sel);
+    rank_topk<DEC_NT, DEC_MAX_TOPK>(sh.key, n_elig, topk, sh.sel, sh.rscr);
   } else if (!scoring) {
     for (int i = tid; i < n_elig; i += DEC_NT) sh.sel[i] = i;
   }
@@ -1648,7 +1704,7 @@ extern "C" int qm_qsa_select(const qm_qsa_geom* g, int seq, const float* iq, con
   if (g->max_blocks > SEL_MAX_BLOCKS || g->max_pages > SEL_MAX_BLOCKS || g->budget / g->ratio > SEL_MAX_BLOCKS / 2)
     return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_select: more than 4096 blocks or pages");
   SelArgs A = sel_args(g, seq, iq, block_keys, positions, page_table, ids, n_sel, items, scores_out);
-  hipLaunchKernelGGL(qsa_select_kernel, dim3(g->batch * seq), dim3(SEL_NT), 0, stream, A);
+  hipLaunchKernelGGL(qsa_select_kernel, dim3(g->batch * seq), dim3(SELP_NT), 0, stream, A);
   QM_CHECK_LAUNCH();
   return QM_OK;
 }

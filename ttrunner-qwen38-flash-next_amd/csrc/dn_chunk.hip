@@ -35,12 +35,15 @@ constexpr int CK_MIN_SEQ = 16;    // shorter prefill chunks take the token loop
 constexpr int CK_PARTS = 4;       // prep workgroups per chunk when chunks are few
 
 // One fp32 record per (sequence, head, chunk):
-//   w   [64][128]   T (k beta e^cum)
-//   u   [64][128]   T (v beta)
-//   qd  [64][128]   q e^cum (q l2-normalised and scaled by d^-1/2)
-//   kdT [128][64]   (k e^(cum_last - cum))^T
-//   qk  [64][64]    (q k^T) * decay on and below the diagonal
+//   w   [64][128]   T (k beta e^cum)                               fragment order
+//   u   [64][128]   T (v beta)                                     row-major
+//   qd  [64][128]   q e^cum (q l2-normalised and scaled by d^-1/2) fragment order
+//   kdT [128][64]   (k e^(cum_last - cum))^T                       fragment order
+//   qk  [64][64]    (q k^T) * decay on and below the diagonal      fragment order
 //   ecl [64]        e^cum_last in element 0
+// Fragment order (frag_index) stores each 16x16 block as the A operands of its
+// four 16x16x4 MFMA steps in lane order: every wave-wide float4 load of the
+// scan reads 1 KB of contiguous memory.
 constexpr long CK_W = 0;
 constexpr long CK_U = CK_W + CK_C * CK_D;
 constexpr long CK_QD = CK_U + CK_C * CK_D;
@@ -49,6 +52,12 @@ constexpr long CK_QK = CK_KDT + CK_C * CK_D;
 constexpr long CK_ECL = CK_QK + CK_C * CK_C;
 constexpr long CK_REC = CK_ECL + 64;
 static_assert((CK_REC * 4) % 256 == 0, "records stay 256-byte aligned");
+
+// offset of element (row, col) of a [rows][ncol] matrix in fragment order:
+// 16x16 block, then lane 16 * ((col % 16) / 4) + row % 16, then col % 4
+__device__ __forceinline__ int frag_index(int row, int col, int ncol) {
+  return ((((row >> 4) * (ncol >> 4) + (col >> 4)) * 64 + ((col & 15) >> 2) * 16 + (row & 15)) << 2) + (col & 3);
+}
 
 __device__ __forceinline__ f32x4_t mfma4(float a, float b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -243,7 +252,7 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int i = 16 * I + 4 * g4 + v;
-        rec[CK_QK + i * CK_C + j] = i >= j ? acc[v] * expf(sh.cum[i] - sh.cum[j]) : 0.f;
+        rec[CK_QK + frag_index(i, j, CK_C)] = i >= j ? acc[v] * expf(sh.cum[i] - sh.cum[j]) : 0.f;
       }
     }
   }
@@ -254,12 +263,12 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
     const int t = idx >> 5, d = 4 * (idx & 31);
     const float4 x = lds4(&sh.q[t][d]);
     const float e = sh.ecum[t];
-    *reinterpret_cast<float4*>(rec + CK_QD + t * CK_D + d) = make_float4(x.x * e, x.y * e, x.z * e, x.w * e);
+    *reinterpret_cast<float4*>(rec + CK_QD + frag_index(t, d, CK_D)) = make_float4(x.x * e, x.y * e, x.z * e, x.w * e);
   }
   for (int it = 2 * span * part; it < 2 * span * (part + 1); ++it) {
     const int idx = tid + CK_NT * it;
     const int t = 4 * (idx & 15), d = idx >> 4;
-    *reinterpret_cast<float4*>(rec + CK_KDT + d * CK_C + t) =
+    *reinterpret_cast<float4*>(rec + CK_KDT + frag_index(d, t, CK_C)) =
         make_float4(sh.k[t][d] * sh.kds[t], sh.k[t + 1][d] * sh.kds[t + 1], sh.k[t + 2][d] * sh.kds[t + 2],
                     sh.k[t + 3][d] * sh.kds[t + 3]);
   }
@@ -308,7 +317,10 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
         acc = mfma4x4(lds4(&sh.Tm[16 * I + r16][16 * K + 4 * g4]), make_float4(bo[K][0], bo[K][1], bo[K][2], bo[K][3]),
                       acc);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) dst[(16 * I + 4 * g4 + v) * CK_D + col] = acc[v];
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * I + 4 * g4 + v;
+        dst[is_u ? row * CK_D + col : frag_index(row, col, CK_D)] = acc[v];
+      }
     }
   }
 }
@@ -330,22 +342,18 @@ struct ScanOps {
 };
 
 __device__ __forceinline__ void load_scan_ops(const float* rec, int wid, int g4, int r16, int col0, ScanOps& o) {
-  const float* wr = rec + CK_W + (16 * wid + r16) * CK_D + 4 * g4;
-  const float* qr = rec + CK_QD + (16 * wid + r16) * CK_D + 4 * g4;
+  const int lane4 = (16 * g4 + r16) * 4;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    o.w[j] = ld4(wr + 16 * j);
-    o.qd[j] = ld4(qr + 16 * j);
+    o.w[j] = ld4(rec + CK_W + (wid * 8 + j) * 256 + lane4);
+    o.qd[j] = ld4(rec + CK_QD + (wid * 8 + j) * 256 + lane4);
   }
-  const float* qkr = rec + CK_QK + (16 * wid + r16) * CK_C + 4 * g4;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) o.qk[j] = ld4(qkr + 16 * j);
+  for (int j = 0; j < 4; ++j) o.qk[j] = ld4(rec + CK_QK + (wid * 4 + j) * 256 + lane4);
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const float* kr = rec + CK_KDT + (32 * wid + 16 * t + r16) * CK_C + 4 * g4;
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o.kd[t][j] = ld4(kr + 16 * j);
-  }
+    for (int j = 0; j < 4; ++j) o.kd[t][j] = ld4(rec + CK_KDT + ((2 * wid + t) * 4 + j) * 256 + lane4);
   const float* ur = rec + CK_U + (16 * wid + 4 * g4) * CK_D + col0 + r16;
 #pragma unroll
   for (int v = 0; v < 4; ++v) o.u[v] = ur[v * CK_D];
@@ -366,9 +374,11 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
   const int g4 = lane >> 4, r16 = lane & 15;
   const float* recs = A.ws + (long)bh * A.n_chunks * CK_REC;
 
-  // the first chunk's operands are in flight with the state
-  ScanOps cur;
-  load_scan_ops(recs, wid, g4, r16, col0, cur);
+  // operands two chunks ahead: three register sets, the loop unrolled by
+  // three so that no set is copied while its loads are in flight
+  ScanOps o0, o1, o2;
+  load_scan_ops(recs, wid, g4, r16, col0, o0);
+  load_scan_ops(recs + (long)min(1, A.n_chunks - 1) * CK_REC, wid, g4, r16, col0, o1);
   // wave wid keeps d_k rows 32wid .. 32wid+31 of the slice as two result tiles
   float* S = A.state + (long)bh * CK_D * CK_D + col0 + r16;
   f32x4_t st[2];
@@ -380,10 +390,9 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
     *reinterpret_cast<float4*>(&sST[r16][row]) = make_float4(st[t][0], st[t][1], st[t][2], st[t][3]);
   }
 
-  for (int ci = 0; ci < A.n_chunks; ++ci) {
-    // the next chunk's operands fly during this one (the last chunk reloads its own)
-    ScanOps nxt;
-    load_scan_ops(recs + (long)min(ci + 1, A.n_chunks - 1) * CK_REC, wid, g4, r16, col0, nxt);
+  auto chunk = [&](int ci, const ScanOps& cur, ScanOps& ahead) {
+    // chunk ci + 2's operands fly during this one (clamped at the last chunk)
+    load_scan_ops(recs + (long)min(ci + 2, A.n_chunks - 1) * CK_REC, wid, g4, r16, col0, ahead);
     __syncthreads();
     // rows 16wid.. of w S and q_dec S
     f32x4_t aw = {0.f, 0.f, 0.f, 0.f}, ao = {0.f, 0.f, 0.f, 0.f};
@@ -420,7 +429,12 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
       st[t] = acc;
       *reinterpret_cast<float4*>(&sST[r16][row + 4 * g4]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     }
-    cur = nxt;
+  };
+
+  for (int ci = 0; ci < A.n_chunks; ci += 3) {
+    chunk(ci, o0, o2);
+    if (ci + 1 < A.n_chunks) chunk(ci + 1, o1, o0);
+    if (ci + 2 < A.n_chunks) chunk(ci + 2, o2, o1);
   }
 
 #pragma unroll

@@ -164,10 +164,12 @@ int qm_qsa_page_index(int page_size, int head_dim, int* k_index, int* v_index);
  *   qg [B, S, Hq, 2*d]; k_new, v_new [B, S, Hkv, d]; iq [B, S, idx_heads*idx_dim];
  *   ik [B, S, idx_dim] (act); *_norm f32 weights; cos/sin [n_pos, rope_dim] f32;
  *   positions [B] int32 = position of the first row; page_table [B, max_pages].
- *   Outputs: q_out [B, S, 2, Hq, d] bf16: the normed, roped query as hi and lo
- *   parts (hi = bf16(q), lo = bf16(q - hi)), the operand form of the attention
- *   MFMA; iq_out [B, S, idx_heads,
- *   idx_dim] f32; pools, raw keys and block cache updated in place.
+ *   Outputs: q_out, B*S*2*Hq*d bf16: the normed, roped query as hi and lo
+ *   parts (hi = bf16(q), lo = bf16(q - hi)), in the operand order of the
+ *   attention MFMA: element (row, part, head h, channel c) at
+ *   ((((((row*Hkv + h/8)*2 + part)*8 + c/32)*4 + (c%32)/8)*8 + h%8)*8 + c%8;
+ *   iq_out [B, S, idx_heads, idx_dim] f32; pools, raw keys and block cache
+ *   updated in place.
  *   qg may be NULL (no attention query: q_norm, q_out unused) and k_new/v_new
  *   may both be NULL (no K/V append), which leaves the indexer part alone. */
 int qm_qsa_prep(const qm_qsa_geom* g, int seq, const void* qg, const void* k_new, const void* v_new,
@@ -253,7 +255,7 @@ int qm_qsa_attend_splits(const qm_qsa_geom* g, int first_position, int last_posi
  * (reference/model.py:365-382 with the mask of :306-326): fp32 softmax of
  * q.k/sqrt(d) over the visible keys, times v, cast to act, times
  * sigmoid(gate). K/V of every row must already be in the pages (qm_qsa_prep).
- *   q [B, S, 2, Hq, d] bf16 hi/lo (from qm_qsa_prep); qg [B, S, Hq, 2*d] act (the gate is
+ *   q: qm_qsa_prep's q_out (hi/lo, operand order); qg [B, S, Hq, 2*d] act (the gate is
  *   the second half of each head); items from qm_qsa_select;
  *   out [B, S, Hq*d] act. */
 int qm_qsa_attend(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool,
@@ -270,7 +272,7 @@ size_t qm_qsa_attend_chunk_workspace(const qm_qsa_geom* g, int seq);
  * block's keys and values are read once and scored for every row that attends
  * it (a tail block only up to the row's own position), and a row's partials
  * are merged with the gate. Indexer ratio 32 or 64, at most 4096 blocks.
- *   q [B, S, 2, Hq, d] bf16 hi/lo and qg [B, S, Hq, 2*d] act as qm_qsa_attend;
+ *   q (qm_qsa_prep's q_out) and qg [B, S, Hq, 2*d] act as qm_qsa_attend;
  *   positions [B] = position of row 0; ids [B, S, budget/ratio] and n_sel
  *   [B, S] from qm_qsa_select; out [B, S, Hq*d] act. */
 int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool,

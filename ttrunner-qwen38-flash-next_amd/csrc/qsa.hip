@@ -52,6 +52,16 @@ __host__ __device__ __forceinline__ int v_page_index(int row, int dim) {
   return ((((row >> 5) * 16 + (dim >> 4)) * 64 + (dim & 15) + 16 * (s >> 3)) << 3) + (s & 7);
 }
 
+// The bf16 query (hi and lo) as the attention MFMA's B operand reads it: per
+// (row, kv head g, hi/lo, 32-channel step sk) 512 contiguous bytes holding
+// [channel octet][head of the group][8 channels], so one wave-wide 16-byte load
+// of a row's 8 heads reads 512 contiguous bytes. 16 KB per row at Hkv = 2.
+__host__ __device__ __forceinline__ long q_index(long row, int hkv, int h2, int hq, int d) {
+  const int g = hq >> 3, hh = hq & 7, sk = d >> 5, oct = (d >> 3) & 3, e = d & 7;
+  return ((((((row * hkv + g) * 2 + h2) * 8 + sk) * 4 + oct) * 8 + hh) << 3) + e;
+}
+constexpr int Q_SK_STRIDE = 4 * 8 * 8;   // elements between 32-channel steps
+
 // y = rope(round_T(rms_norm(x) * w)) for one row of `n` channels held in LDS
 // by threads 0..n-1 (n <= blockDim). Rotates the first `rope` channels with the
 // cos/sin row given. Returns the value of channel tid (0 for tid >= n).
@@ -151,8 +161,8 @@ __device__ void prep_head(const PrepArgs<T>& A, int b, int s, int role) {
     // the attention MFMA takes q as bf16: keep it as hi + lo so the product
     // carries ~16 mantissa bits (rows [2 * row] hold hi, [2 * row + 1] lo)
     const uint16_t hi = f32_to_bf16(y);
-    A.q_out[((long)(2 * row) * A.hq + role) * QSA_D + tid] = hi;
-    A.q_out[((long)(2 * row + 1) * A.hq + role) * QSA_D + tid] = f32_to_bf16(y - bf16_to_f32(hi));
+    A.q_out[q_index(row, A.hkv, 0, role, tid)] = hi;
+    A.q_out[q_index(row, A.hkv, 1, role, tid)] = f32_to_bf16(y - bf16_to_f32(hi));
     return;
   }
   if (!A.k_new) return;
@@ -597,13 +607,13 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void qsa_attend_kernel(AttnArgs A) 
   bf16x8_t qhi[8], qlo[8];
   {
     const int hq = g * GQA + (col < GQA ? col : 0);
-    const uint16_t* qh = A.q + ((long)(2 * row) * A.hq + hq) * QSA_D + 8 * quad;
-    const uint16_t* ql = A.q + ((long)(2 * row + 1) * A.hq + hq) * QSA_D + 8 * quad;
+    const uint16_t* qh = A.q + q_index(row, A.hkv, 0, hq, 8 * quad);
+    const uint16_t* ql = A.q + q_index(row, A.hkv, 1, hq, 8 * quad);
     const bf16x8_t zero = {};
 #pragma unroll
     for (int sk = 0; sk < 8; ++sk) {
-      qhi[sk] = col < GQA ? load_bf16x8(qh + 32 * sk) : zero;
-      qlo[sk] = col < GQA ? load_bf16x8(ql + 32 * sk) : zero;
+      qhi[sk] = col < GQA ? load_bf16x8(qh + Q_SK_STRIDE * sk) : zero;
+      qlo[sk] = col < GQA ? load_bf16x8(ql + Q_SK_STRIDE * sk) : zero;
     }
   }
 
@@ -941,12 +951,12 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
     bf16x8_t qhi[8], qlo[8];
     {
       const int hqi = g * GQA + hh;
-      const uint16_t* qh = A.q + ((2 * row) * A.hq + hqi) * QSA_D + 8 * quad;
-      const uint16_t* ql = A.q + ((2 * row + 1) * A.hq + hqi) * QSA_D + 8 * quad;
+      const uint16_t* qh = A.q + q_index(row, A.hkv, 0, hqi, 8 * quad);
+      const uint16_t* ql = A.q + q_index(row, A.hkv, 1, hqi, 8 * quad);
 #pragma unroll
       for (int sk = 0; sk < 8; ++sk) {
-        qhi[sk] = load_bf16x8(qh + 32 * sk);
-        qlo[sk] = load_bf16x8(ql + 32 * sk);
+        qhi[sk] = load_bf16x8(qh + Q_SK_STRIDE * sk);
+        qlo[sk] = load_bf16x8(ql + Q_SK_STRIDE * sk);
       }
     }
     // stage the block's groups: per group 16 KB of key and 16 KB of value pieces

@@ -182,7 +182,8 @@ class Qwen4MixModel:
         stream = native.stream_handle(self.device)
         self._sync_blocks(lc, g, cos_t, sin_t, query_offset, layer)
         pos = self._positions(batch, query_offset)
-        q_out = torch.empty(batch, seq, 2, c.num_attention_heads, c.head_dim, dtype=torch.bfloat16,
+        # the query in the attention MFMA's operand order (hi and lo bf16 parts), per row
+        q_out = torch.empty(batch, seq, 2 * c.num_attention_heads * c.head_dim, dtype=torch.bfloat16,
                             device=self.device) if qg is not None else None
         iq_out = torch.empty(batch, seq, c.indexer_heads, c.indexer_head_dim, dtype=torch.float32, device=self.device)
         lib = native.load()

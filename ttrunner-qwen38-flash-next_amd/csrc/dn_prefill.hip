@@ -68,6 +68,10 @@ __global__ __launch_bounds__(CONV_CH) void dn_conv_chunk_kernel(ConvChunkArgs<T>
       const float val = Act<T>::load(x, (long)tc * A.conv_dim);
       win[i] = (i < K - 1 && t < 0) ? hist[i < K - 1 ? i : 0] : val;
     }
+    // the chunk's last K-1 inputs, for the ring (used by the first token block)
+    T last[K - 1];
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i) last[i] = x[(long)max(A.seq - (K - 1) + i, 0) * A.conv_dim];
 #pragma unroll
     for (int i = 0; i < CONV_TOK; ++i) {
       if (i < nt) {
@@ -80,8 +84,11 @@ __global__ __launch_bounds__(CONV_CH) void dn_conv_chunk_kernel(ConvChunkArgs<T>
     }
     if (tb == 0) {
       // the last K-1 inputs of the chunk (or all of them, when S < K-1) go to their slots
-      for (int t = max(0, A.seq - (K - 1)); t < A.seq; ++t)
-        Act<T>::store(ring, (pos0 + t) % K, Act<T>::load(x, (long)t * A.conv_dim));
+#pragma unroll
+      for (int i = 0; i < K - 1; ++i) {
+        const int t = A.seq - (K - 1) + i;
+        if (t >= 0) ring[(pos0 + t) % K] = last[i];
+      }
     }
     return;
   }

@@ -10,7 +10,9 @@ resident in HBM, and rotated over enough independent layer instances that the
 data touched per rotation exceeds twice the 256 MB Infinity Cache.
 
 Prints one JSON line (see the driver contract); ``--sweep`` adds per-position
-lines (192, 1984, 4032, 8128) and the 128-token prefill chunk to stderr.
+lines (192, 1984, 4032, 8128), the 128-token prefill chunk and the layer
+projections around the core at one token (qm_gemv, weights streamed from HBM)
+to stderr and to the line's "sweep" object.
 """
 
 from __future__ import annotations
@@ -73,7 +75,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--position", type=int, default=8128)
     ap.add_argument("--instances", type=int, default=0, help="rotated layer instances (0: auto, > 512 MB)")
-    ap.add_argument("--sweep", action="store_true", help="also time positions 192/1984/4032 and a prefill chunk")
+    ap.add_argument("--sweep", action="store_true",
+                    help="also time positions 192/1984/4032, a prefill chunk and the layer projections")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-mb", type=int, default=0,
@@ -358,6 +361,53 @@ def run_prefill(qm, dev, reps=20, n_inst=4):
             "qsa_mfma_util": round(flops / (out["qsa"] * 1e-3) / MFMA_BF16_PEAK, 5)}
 
 
+PROJECTION_GROUPS = (   # (name, rows per projection, k): the layer GEMVs around the core at one token
+    ("dn_in", (8192, 4096, 32, 32), 2048),           # attn_qkv | attn_gate | ssm_beta | ssm_alpha
+    ("qsa_in", (8192, 512, 512, 512, 128), 2048),    # attn_q | attn_k | attn_v | indexer q | indexer k
+    ("dn_out", (2048,), 4096),                       # ssm_out
+    ("qsa_out", (2048,), 4096),                      # attn_output
+)
+
+
+def run_projections(qm, dev, reps=200, rotate_mb=600):
+    """qm_gemv at M = 1 for each projection group, bf16 weights rotated over
+    `rotate_mb` of copies so that they stream from HBM. Event time per call."""
+    import torch
+    out = {}
+    s = qm.native.stream_handle(dev)
+    for name, rows, k in PROJECTION_GROUPS:
+        n = sum(rows)
+        nbytes = n * k * 2
+        copies = max(2, (rotate_mb << 20) // nbytes)
+        g = torch.Generator(device=dev).manual_seed(n)
+        ws = [torch.randn(n, k, generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+        x = torch.randn(1, k, generator=g, device=dev).to(torch.bfloat16)
+        outs = [torch.empty(1, r, dtype=torch.bfloat16, device=dev) for r in rows]
+        seg_rows = (ctypes.c_int * len(rows))(*rows)
+        seg_out = (ctypes.c_void_p * len(rows))(*[o.data_ptr() for o in outs])
+
+        def call(w):
+            qm.native.call("qm_gemv", qm.native.QM_ACT_BF16, 1, n, k, w.data_ptr(), x.data_ptr(), len(rows),
+                           seg_rows, seg_out, s)
+        for i in range(20):
+            call(ws[i % copies])
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        stream = torch.cuda.current_stream(dev)
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(evs):
+            a.record(stream)
+            call(ws[i % copies])
+            b.record(stream)
+        torch.cuda.synchronize()
+        us = statistics.median(a.elapsed_time(b) for a, b in evs) * 1000
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"weights_mb": round(nbytes / 1e6, 1), "us": round(us, 2), "gbs": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del ws
+    torch.cuda.synchronize()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -407,6 +457,8 @@ def main():
             print(f"[sweep] {json.dumps(line)}", file=sys.stderr)
         sweep["prefill_chunk"] = run_prefill(qm, dev)
         print(f"[sweep] prefill {json.dumps(sweep['prefill_chunk'])}", file=sys.stderr)
+        sweep["projections"] = run_projections(qm, dev)
+        print(f"[sweep] projections {json.dumps(sweep['projections'])}", file=sys.stderr)
 
     cpu = None
     if not args.no_cpu:

@@ -49,6 +49,8 @@ extern "C" {
 #define QM_ACT_F32 0
 #define QM_ACT_BF16 1
 
+#define QM_GEMV_MAX_SEG 8
+
 /* Last error message of the calling thread ("" after success). */
 const char* qm_last_error(void);
 /* ABI version of this library. */
@@ -278,6 +280,17 @@ size_t qm_qsa_attend_chunk_workspace(const qm_qsa_geom* g, int seq);
 int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool,
                         const void* v_pool, const int* positions, const int* page_table, const int* ids,
                         const int* n_sel, void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* The layer projections at small M (the F.linear calls of
+ * reference/model.py:184-187, 244, 270, 274, 345-352, 383 for decode):
+ * y[m][n] = sum_k w[n][k] x[m][k] for m < M <= 4, one stream over w.
+ *   w [n, k] and x [m, k] in act_dtype (row-major); k = 2048 or 4096 (bf16),
+ *   1024, 2048 or 4096 (f32). The n rows split into n_seg <= 8 consecutive
+ *   segments of seg_rows[s] rows: segment s is written to seg_out[s] as
+ *   [m, seg_rows[s]] (act_dtype). seg_rows and seg_out are host arrays.
+ *   Products accumulate in f32 and are rounded once to act_dtype. */
+int qm_gemv(int act_dtype, int m, int n, int k, const void* w, const void* x, int n_seg, const int* seg_rows,
+            void* const* seg_out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

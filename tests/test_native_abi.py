@@ -101,6 +101,22 @@ def test_bad_geometry_is_rejected_without_a_launch(qm):
         n.call("qm_qsa_select", ctypes.byref(q), 1, *([None] * 8), None)
 
 
+def test_gemv_rejects_unsupported_shapes_before_a_launch(qm):
+    """qm_gemv checks its sizes on the host: m above 4, k outside the tiled
+    widths, segments that do not add up, and null outputs are errors."""
+    lib = qm.native.load()
+    rows = (ctypes.c_int * 2)(3, 5)
+    outs = (ctypes.c_void_p * 2)(16, 32)
+    dummy = ctypes.c_void_p(64)
+    bf16 = qm.native.QM_ACT_BF16
+    assert lib.qm_gemv(bf16, 5, 8, 2048, dummy, dummy, 2, rows, outs, None) < 0      # m > 4
+    assert lib.qm_gemv(bf16, 1, 8, 1024, dummy, dummy, 2, rows, outs, None) < 0      # k not 2048/4096 for bf16
+    assert lib.qm_gemv(bf16, 1, 9, 2048, dummy, dummy, 2, rows, outs, None) < 0      # 3 + 5 != 9
+    bad = (ctypes.c_void_p * 2)(16, None)
+    assert lib.qm_gemv(bf16, 1, 8, 2048, dummy, dummy, 2, rows, bad, None) < 0       # null output
+    assert b"qm_gemv" in lib.qm_last_error()
+
+
 def test_workspace_sizes_are_sane(qm):
     n = qm.native
     lib = n.load()

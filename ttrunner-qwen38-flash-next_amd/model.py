@@ -62,6 +62,60 @@ class Qwen4MixModel:
             self._dev[key] = t
         return t
 
+    # projections that read the same input, concatenated row-wise so that the
+    # small-M GEMV streams a layer's weights for them in one launch
+    PROJ_GROUPS = {
+        "dn_in": ("attn_qkv.weight", "attn_gate.weight", "ssm_beta.weight", "ssm_alpha.weight"),
+        "dn_out": ("ssm_out.weight",),
+        "qsa_in": ("attn_q.weight", "attn_k.weight", "attn_v.weight", "indexer.q_proj.weight",
+                   "indexer.k_proj.weight"),
+        "qsa_out": ("attn_output.weight",),
+    }
+
+    def _wcat(self, layer: int, group: str, dtype):
+        """(weights [N, K], rows per projection) of a projection group; the
+        layer's single matrices become row views of it."""
+        key = (layer, "group:" + group, dtype)
+        hit = self._dev.get(key)
+        if hit is None:
+            names = self.PROJ_GROUPS[group]
+            parts = [self.bw(layer, n).to(self.device, dtype) for n in names]
+            w = torch.cat(parts, 0).contiguous()
+            rows = [int(t.shape[0]) for t in parts]
+            start = 0
+            for n, r in zip(names, rows):
+                self._dev[(layer, n, dtype)] = w[start:start + r]
+                start += r
+            hit = (w, rows)
+            self._dev[key] = hit
+        return hit
+
+    @staticmethod
+    def _gemv_fits(dtype, m: int, k: int) -> bool:
+        ks = (2048, 4096) if dtype == torch.bfloat16 else (1024, 2048, 4096)
+        return m <= 4 and k in ks and dtype in (torch.bfloat16, torch.float32)
+
+    def project(self, x: torch.Tensor, layer: int, group: str) -> list:
+        """The group's projections of x [B, S, K] (F.linear with each weight), as
+        a list of [B, S, rows] tensors. Up to 4 rows of x: one qm_gemv launch over
+        the concatenated weights; more: a library GEMM per projection."""
+        dt = x.dtype
+        w, rows = self._wcat(layer, group, dt)
+        batch, seq, k = x.shape
+        if self._gemv_fits(dt, batch * seq, k):
+            xc = x.contiguous()
+            outs = [torch.empty(batch, seq, r, dtype=dt, device=self.device) for r in rows]
+            seg_rows = (ctypes.c_int * len(rows))(*rows)
+            seg_out = (ctypes.c_void_p * len(rows))(*[o.data_ptr() for o in outs])
+            native.call("qm_gemv", native.act_code(dt), batch * seq, int(w.shape[0]), k, native.ptr(w),
+                        native.ptr(xc), len(rows), seg_rows, seg_out, native.stream_handle(self.device))
+            return outs
+        outs, start = [], 0
+        for r in rows:
+            outs.append(F.linear(x, w[start:start + r]))
+            start += r
+        return outs
+
     def _workspace(self, name: str, nbytes: int) -> torch.Tensor:
         buf = self._ws.get(name)
         if buf is None or buf.numel() < nbytes:
@@ -128,12 +182,9 @@ class Qwen4MixModel:
         if cache is None:
             cache = MixHybridCache(layer + 1, self.config, batch, max(seq, 64), self.device, dt)
         lc = cache[layer]
-        qkv = F.linear(hidden, self._dw(layer, "attn_qkv.weight", dt))
-        z = F.linear(hidden, self._dw(layer, "attn_gate.weight", dt))
-        b = F.linear(hidden, self._dw(layer, "ssm_beta.weight", dt))
-        a = F.linear(hidden, self._dw(layer, "ssm_alpha.weight", dt))
+        qkv, z, b, a = self.project(hidden, layer, "dn_in")
         out = self.dn_core(qkv.contiguous(), z.contiguous(), a.contiguous(), b.contiguous(), layer, lc)
-        return F.linear(out, self._dw(layer, "ssm_out.weight", dt))
+        return self.project(out, layer, "dn_out")[0]
 
     # -- QSA -------------------------------------------------------------------
 
@@ -268,13 +319,9 @@ class Qwen4MixModel:
         dt = hidden.dtype
         if cache is None:
             cache = MixHybridCache(layer + 1, self.config, batch, max(query_offset + seq, 64), self.device, dt)
-        qg = F.linear(hidden, self._dw(layer, "attn_q.weight", dt)).contiguous()
-        k = F.linear(hidden, self._dw(layer, "attn_k.weight", dt)).contiguous()
-        v = F.linear(hidden, self._dw(layer, "attn_v.weight", dt)).contiguous()
-        iq = F.linear(hidden, self._dw(layer, "indexer.q_proj.weight", dt)).contiguous()
-        ik = F.linear(hidden, self._dw(layer, "indexer.k_proj.weight", dt)).contiguous()
+        qg, k, v, iq, ik = (t.contiguous() for t in self.project(hidden, layer, "qsa_in"))
         out = self.qsa_core(qg, k, v, iq, ik, layer, cache, query_offset, cos, sin)
-        return F.linear(out, self._dw(layer, "attn_output.weight", dt))
+        return self.project(out, layer, "qsa_out")[0]
 
     def selection_mask(self, lc, kv_len: int, query_offset: int) -> torch.Tensor:
         """Boolean (B, 1, S, kv_len) mask of the layer's last selection plus tails."""

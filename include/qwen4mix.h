@@ -292,6 +292,47 @@ int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void
 int qm_gemv(int act_dtype, int m, int n, int k, const void* w, const void* x, int n_seg, const int* seg_rows,
             void* const* seg_out, hipStream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Hyper-connections around each branch                                     */
+/* ------------------------------------------------------------------------ */
+
+typedef struct qm_hc_geom {
+  int rows;         /* M: token rows (batch * seq)                         */
+  int streams;      /* hc_count (4): copies of the hidden vector            */
+  int hidden;       /* hidden_size: width of one stream                     */
+  int rank;         /* hc_lowrank (320): width of the down/up products      */
+  int act_dtype;    /* QM_ACT_F32 or QM_ACT_BF16                            */
+  float eps;        /* rms_norm_eps of the stream norm                      */
+} qm_hc_geom;
+
+/* Bytes of workspace qm_hc_mix needs (normalised rows and the down product);
+ * 0 if the geometry is unsupported. */
+size_t qm_hc_mix_workspace(const qm_hc_geom* g);
+
+/* The hyper-connection read gate, Qwen4ExpModel._gated_residual
+ * (reference/model.py:53-77): per-stream rms_norm of hyper, the down and
+ * inject products, silu / 2 sigmoid of their outputs over `streams`, the up
+ * product, sigmoid, and the mean over streams of gate * normed.
+ *   hyper [M, streams * hidden] act; norm_w [streams * hidden] f32;
+ *   down_inject_w [rank + (with_inject ? streams : 0), streams * hidden] act:
+ *   the down rows, then the inject rows; up_w [streams * hidden, rank] act.
+ *   mixed [M, hidden] act (the branch input); inject [M, streams] act when
+ *   with_inject (the layer mixers), unused otherwise (the final mixer).
+ *   streams * hidden must be 1, 2, 4, 5, 8 or 10 times 2048 (bf16) or 1024
+ *   (f32); hidden a multiple of 8; rank a multiple of 8 (4 for f32), <= 512.
+ * Two launches; every pointer except inject and mixed 16-byte aligned. */
+int qm_hc_mix(const qm_hc_geom* g, const void* hyper, const float* norm_w, const void* down_inject_w,
+              int with_inject, const void* up_w, void* mixed, void* inject, void* workspace,
+              size_t workspace_bytes, hipStream_t stream);
+
+/* Qwen4ExpModel._reinject (reference/model.py:79-81):
+ * out[m][s * hidden + h] = hyper[m][s * hidden + h] + branch[m][h] * inject[m][s],
+ * each product and sum rounded to act. hyper/out [M, streams * hidden],
+ * branch [M, hidden], inject [M, streams]; out may be hyper. Reads rows,
+ * streams, hidden and act_dtype of g (hidden a multiple of 8). */
+int qm_hc_reinject(const qm_hc_geom* g, const void* hyper, const void* branch, const void* inject, void* out,
+                   hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -2,8 +2,8 @@
 
 Follows the fields and derivations of reference/config.py:80-104 and :136-158
 (``linear_key_dim``, ``linear_value_dim``, ``conv_dim``, ``is_full_attention``).
-Only the fields the token-mixing layers read are kept; the MoE, PLE and
-hyper-connection fields are outside this path.
+Only the fields the token-mixing layers and the hyper-connections around them
+read are kept; the MoE and PLE fields are outside this path.
 
 Pinned by: the derived quantities are closed forms checked in
 tests/test_oracle_layers.py (conv_dim = 2*Hk*d + Hv*d, the full-attention
@@ -38,6 +38,13 @@ class OracleConfig:
     linear_head_dim: int = 128
     conv_kernel: int = 4
     output_gate_type: str = "sigmoid"
+    # hyper-connections (reference/config.py:51-52, 80-81)
+    hc_count: int = 4
+    hc_lowrank: int = 320
+
+    @property
+    def hc_hidden_size(self) -> int:
+        return self.hc_count * self.hidden_size
 
     @property
     def linear_key_dim(self) -> int:

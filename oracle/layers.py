@@ -25,15 +25,22 @@ import torch
 import torch.nn.functional as F
 
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """reference/layers.py:31-43 (the group_size=None branch).
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, group_size: int | None = None) -> torch.Tensor:
+    """reference/layers.py:31-43.
 
-    Normalises the last axis in float32 and returns the input dtype.
+    Normalises the last axis in float32 -- or, with ``group_size``, each run of
+    ``group_size`` consecutive elements of it on its own (one residual stream
+    each) -- scales by the weight and returns the input dtype.
     """
     in_dtype = x.dtype
     xf = x.float()
-    scale = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return (xf * scale * weight.float()).to(in_dtype)
+    if group_size is not None:
+        groups = xf.unflatten(-1, (-1, group_size))
+        scale = torch.rsqrt(groups.pow(2).mean(-1, keepdim=True) + eps)
+        xf = (groups * scale).flatten(-2)
+    else:
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (xf * weight.float()).to(in_dtype)
 
 
 def rms_norm_gated(x, gate, weight, eps: float, activation: str = "sigmoid"):

@@ -63,6 +63,39 @@ class OracleMixer:
         return self.store.get(f"blk.{layer}.{suffix}")
 
     # ------------------------------------------------------------------
+    # Hyper-connections around each branch
+    # ------------------------------------------------------------------
+
+    def _gated_residual(self, hyper, layer, kind: str):
+        """reference/model.py:53-77: (mixed, hyper, inject or None).
+
+        ``hyper`` holds ``hc_count`` residual streams of ``hidden_size`` side by
+        side. Each stream is rms-normalised on its own; a low-rank
+        down/silu/up/sigmoid product gates every element, and the gated streams
+        are averaged into the branch input. The layer mixers also return the
+        per-stream injection weights 2 sigmoid(normed . inject_w^T / hc_count);
+        the final mixer (``layer is None``) returns None there.
+        """
+        cfg = self.config
+        hc, width = cfg.hc_count, cfg.hidden_size
+        prefix = "output_hc" if layer is None else f"blk.{layer}.hc_{kind}"
+        normed = rms_norm(hyper, self.w(f"{prefix}_norm.weight"), cfg.rms_norm_eps, group_size=width)
+        low = F.silu(F.linear(normed, self.w(f"{prefix}_down.weight")) / hc)
+        gate = torch.sigmoid(F.linear(low, self.w(f"{prefix}_up.weight")))
+        gated = gate.unflatten(-1, (hc, width)) * normed.unflatten(-1, (hc, width))
+        mixed = gated.mean(dim=-2)
+        if layer is None:
+            return mixed, hyper, None
+        inject = 2 * torch.sigmoid(F.linear(normed, self.w(f"{prefix}_inject.weight")) / hc)
+        return mixed, hyper, inject
+
+    @staticmethod
+    def _reinject(hyper, branch_out, inject):
+        """reference/model.py:79-81: stream s gains branch_out * inject[..., s]."""
+        scaled = inject.unsqueeze(-1) * branch_out.unsqueeze(-2)
+        return hyper + scaled.flatten(-2)
+
+    # ------------------------------------------------------------------
     # Gated DeltaNet
     # ------------------------------------------------------------------
 

@@ -96,6 +96,22 @@ def qsa_weights(layer: int, seed: int, dtype=torch.float32, hidden: int = HIDDEN
     }
 
 
+def hc_weights(prefix: str, seed: int, dtype=torch.float32, hidden: int = HIDDEN, streams: int = 4,
+               rank: int = 320, with_inject: bool = True) -> dict:
+    """One hyper-connection mixer (``blk.{l}.hc_{kind}`` or ``output_hc``):
+    norm weight 1 + N(0, 0.1), projections N(0, fan_in^-1/2)."""
+    r = rng(seed)
+    k = streams * hidden
+    w = {
+        prefix + "_norm.weight": 1.0 + normal(r, (k,), 0.1),
+        prefix + "_down.weight": normal(r, (rank, k), k ** -0.5, dtype),
+        prefix + "_up.weight": normal(r, (k, rank), rank ** -0.5, dtype),
+    }
+    if with_inject:
+        w[prefix + "_inject.weight"] = normal(r, (streams, k), k ** -0.5, dtype)
+    return w
+
+
 def qsa_past(seed: int, past: int, dtype=torch.float32):
     """Past K (bf16-valued, float32 as the reference's roped keys are), V and raw
     indexer keys for ``past`` tokens, batch 1."""

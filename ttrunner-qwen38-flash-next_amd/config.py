@@ -1,8 +1,9 @@
 """Dimensions of the token-mixing layers.
 
 Same field names and derivations as the reference config
-(reference/config.py:80-104, 136-158), restricted to what QSA and Gated DeltaNet
-read, plus the paging parameters this implementation adds (``page_size``).
+(reference/config.py:51-52, 80-104, 136-158), restricted to what QSA, Gated
+DeltaNet and the hyper-connections around them read, plus the paging
+parameters this implementation adds (``page_size``).
 ``from_reference`` accepts any object carrying the reference's field names
 (a ``Qwen4ExpConfig`` or a test double), so the layers drop into the reference
 engine with its own config object.
@@ -33,7 +34,13 @@ class MixConfig:
     linear_head_dim: int = 128
     conv_kernel: int = 4
     output_gate_type: str = "sigmoid"
+    hc_count: int = 4
+    hc_lowrank: int = 320
     page_size: int = 64
+
+    @property
+    def hc_hidden_size(self) -> int:
+        return self.hc_count * self.hidden_size
 
     @property
     def linear_key_dim(self) -> int:

@@ -116,6 +116,69 @@ class Qwen4MixModel:
             start += r
         return outs
 
+    # -- hyper-connections around each branch (reference/model.py:53-81) --------
+
+    def hc_weights(self, layer, kind: str, dtype):
+        """(norm_w f32, down|inject [rank + hc or rank, K], up [K, rank], with_inject)
+        of one mixer on the device; ``layer is None`` is the final mixer."""
+        prefix = "output_hc" if layer is None else f"blk.{layer}.hc_{kind}"
+        key = (prefix, "hc", dtype)
+        hit = self._dev.get(key)
+        if hit is None:
+            norm_w = self.w(f"{prefix}_norm.weight").to(self.device, torch.float32).contiguous()
+            rows = [self.w(f"{prefix}_down.weight")]
+            if layer is not None:
+                rows.append(self.w(f"{prefix}_inject.weight"))
+            di = torch.cat([r.to(self.device, dtype) for r in rows], 0).contiguous()
+            up = self.w(f"{prefix}_up.weight").to(self.device, dtype).contiguous()
+            hit = (norm_w, di, up, layer is not None)
+            self._dev[key] = hit
+        return hit
+
+    def hc_geom(self, rows: int, dtype) -> native.HcGeom:
+        c = self.config
+        return native.HcGeom(rows, c.hc_count, c.hidden_size, c.hc_lowrank, native.act_code(dtype), c.rms_norm_eps)
+
+    def _gated_residual(self, hyper: torch.Tensor, layer, kind: str, mixed=None, inject=None):
+        """reference/model.py:53-77: (mixed [.., hidden], hyper, inject [.., hc_count] or None).
+
+        One qm_hc_mix call (two launches): the per-stream norm, the down and
+        inject products and their gates, the up product and the gated mean.
+        ``mixed``/``inject`` may be preallocated outputs."""
+        c = self.config
+        dt = hyper.dtype
+        lead = hyper.shape[:-1]
+        rows = hyper.numel() // hyper.shape[-1]
+        norm_w, di, up, with_inject = self.hc_weights(layer, kind, dt)
+        g = self.hc_geom(rows, dt)
+        ws = self._workspace("hc", native.load().qm_hc_mix_workspace(ctypes.byref(g)))
+        hyper_c = hyper.contiguous()
+        if mixed is None:
+            mixed = torch.empty(*lead, c.hidden_size, dtype=dt, device=self.device)
+        if with_inject and inject is None:
+            inject = torch.empty(*lead, c.hc_count, dtype=dt, device=self.device)
+        native.call("qm_hc_mix", ctypes.byref(g), native.ptr(hyper_c), native.ptr(norm_w), native.ptr(di),
+                    int(with_inject), native.ptr(up), native.ptr(mixed), native.ptr(inject) if with_inject else None,
+                    native.ptr(ws), ws.numel(), native.stream_handle(self.device))
+        return mixed, hyper, (inject if with_inject else None)
+
+    @staticmethod
+    def _reinject(hyper: torch.Tensor, branch_out: torch.Tensor, inject: torch.Tensor, out=None) -> torch.Tensor:
+        """reference/model.py:79-81: hyper + branch_out scaled into every stream
+        (one qm_hc_reinject launch; ``out`` may be ``hyper`` itself)."""
+        streams, hidden = inject.shape[-1], branch_out.shape[-1]
+        rows = branch_out.numel() // hidden
+        if hyper.shape[-1] != streams * hidden or hyper.numel() != rows * streams * hidden:
+            raise ValueError(f"_reinject: hyper {tuple(hyper.shape)} does not hold {streams} streams of "
+                             f"{tuple(branch_out.shape)}")
+        hyper_c = hyper.contiguous()
+        if out is None:
+            out = torch.empty_like(hyper_c)
+        g = native.HcGeom(rows, streams, hidden, 0, native.act_code(hyper.dtype), 0.0)
+        native.call("qm_hc_reinject", ctypes.byref(g), native.ptr(hyper_c), native.ptr(branch_out.contiguous()),
+                    native.ptr(inject.contiguous()), native.ptr(out), native.stream_handle(hyper.device))
+        return out
+
     def _workspace(self, name: str, nbytes: int) -> torch.Tensor:
         buf = self._ws.get(name)
         if buf is None or buf.numel() < nbytes:

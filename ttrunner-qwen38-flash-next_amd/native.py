@@ -37,6 +37,10 @@ class QsaGeom(ctypes.Structure):
                 ("max_pages", _i), ("max_ctx", _i), ("max_blocks", _i), ("act_dtype", _i), ("eps", _f)]
 
 
+class HcGeom(ctypes.Structure):
+    _fields_ = [("rows", _i), ("streams", _i), ("hidden", _i), ("rank", _i), ("act_dtype", _i), ("eps", _f)]
+
+
 # name -> (restype, argtypes); every symbol include/qwen4mix.h declares
 SIGNATURES = {
     "qm_last_error": (ctypes.c_char_p, []),
@@ -66,6 +70,9 @@ SIGNATURES = {
     "qm_dn_prefill_workspace": (_sz, [ctypes.POINTER(DnGeom), _i]),
     "qm_dn_prefill": (_i, [ctypes.POINTER(DnGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _vp, _sz, _vp]),
+    "qm_hc_mix_workspace": (_sz, [ctypes.POINTER(HcGeom)]),
+    "qm_hc_mix": (_i, [ctypes.POINTER(HcGeom), _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "qm_hc_reinject": (_i, [ctypes.POINTER(HcGeom), _vp, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None

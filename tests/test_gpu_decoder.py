@@ -1,0 +1,212 @@
+"""The token-mixing halves of a layer stack as one step (MixDecoder): graph
+replay against eager launches, the step against the reference-interface layer
+methods, and the k-token verify step against k single steps.
+
+Stack: layers 0-2 Gated DeltaNet, layer 3 QSA (full_attention_interval 4),
+each wrapped in its hyper-connection mix and reinjection, bf16, batch 1, a
+seeded random history of ~1000 tokens in a randomly paged cache.
+
+Bars:
+* graph replay == eager launches bit for bit, every replay (with eager work
+  and host synchronisations between replays), across a bucket switch (position
+  1023 -> 1024) and a block completion, and the caches after the steps
+  bit-identical;
+* decoder step vs the layer methods (_gated_residual, _linear_attention,
+  _full_attention, _reinject): within 2e-2 (the QSA split-K grid is sized for
+  the bucket in one and for the position in the other, so partial sums meet
+  in another order);
+* step_n over k tokens vs k single steps: within 2e-2 (chunk paths vs decode
+  paths); the first layer's fp32 state within 1e-3 (both paths see the same
+  inputs there), every other cache tensor within 2e-2 (a later layer's inputs
+  are the earlier layers' bf16 outputs, which differ by up to that between the
+  paths); the conv ring compared as the reference's conv_state (its last K-1
+  inputs).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import sys
+
+import pytest
+import torch
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+import inputs as gi  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+N_LAYERS = 4
+START = 1020
+
+
+def rel_err(got, want):
+    got, want = got.float().cpu(), want.float().cpu()
+    return ((got - want).abs().max() / want.abs().max().clamp_min(1e-30)).item()
+
+
+@pytest.fixture(scope="module")
+def stack(gpu):
+    qm = gpu
+    w = {}
+    for l in range(N_LAYERS):
+        w.update(gi.qsa_weights(l, 100 + l, BF) if (l + 1) % 4 == 0 else gi.dn_weights(l, 100 + l, BF))
+        w.update(gi.hc_weights(f"blk.{l}.hc_attn", 200 + l, BF))
+    cfg = qm.config.MixConfig()
+    model = qm.model.Qwen4MixModel(cfg, gi.FakeStore(w), device=DEV)
+    cache = qm.cache.MixHybridCache(N_LAYERS, cfg, batch=1, max_ctx=4096, device=DEV, dtype=BF,
+                                    page_table="random", seed=3)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    for l in range(N_LAYERS):
+        lc = cache[l]
+        if cfg.is_full_attention(l):
+            lc.ensure_qsa(1, BF)
+            for t in (lc.k_pool, lc.v_pool, lc.raw_keys):
+                t.copy_(torch.randn(t.shape, generator=g, device=DEV).to(t.dtype))
+            geom = model.qsa_geom(cache, BF)
+            cos, sin = model.rope.get(cache.max_ctx)
+            n_blocks = START // cfg.indexer_compress_ratio
+            qm.native.call("qm_qsa_pool_blocks", ctypes.byref(geom), lc.raw_keys.data_ptr(),
+                           model._dw(l, "indexer.k_norm.weight", torch.float32).data_ptr(), cos.data_ptr(),
+                           sin.data_ptr(), 0, n_blocks, lc.block_keys.data_ptr(), qm.native.stream_handle())
+            lc.blocks_valid = n_blocks
+        else:
+            lc.ensure_dn(1, BF)
+            lc.recurrent_state.copy_(torch.randn(lc.recurrent_state.shape, generator=g, device=DEV) * 0.02)
+            lc.conv_ring.copy_(torch.randn(lc.conv_ring.shape, generator=g, device=DEV).to(BF))
+        lc.n_tokens = START
+    torch.cuda.synchronize()
+    return qm, model, cache
+
+
+FIELDS = ("conv_ring", "recurrent_state", "k_pool", "v_pool", "raw_keys", "block_keys")
+
+
+def snapshot(cache):
+    snap = []
+    for lc in cache.layers:
+        t = {f: getattr(lc, f).clone() for f in FIELDS if getattr(lc, f) is not None}
+        if lc.conv_ring is not None:
+            # the reference's conv_state: the last K-1 inputs (the ring's K-th slot is dead state)
+            t["conv_state"] = lc.conv_state.clone()
+        snap.append((t, lc.n_tokens, lc.blocks_valid))
+    return snap
+
+
+def restore(cache, snap):
+    for lc, (tensors, n, b) in zip(cache.layers, snap):
+        for f, t in tensors.items():
+            if f in FIELDS:
+                getattr(lc, f).copy_(t)
+        lc.n_tokens, lc.blocks_valid = n, b
+    torch.cuda.synchronize()
+
+
+def inputs(n, k=1, seed=11):
+    r = gi.rng(seed)
+    return [gi.normal(r, (1, k, 4 * 2048)).to(BF).to(DEV) for _ in range(n)]
+
+
+def test_graph_replay_matches_eager_launches(stack):
+    qm, model, cache = stack
+    snap = snapshot(cache)
+    xs = inputs(8)
+    print(f"decoder eager, positions {START}..{START + len(xs) - 1}", flush=True)
+    dec = qm.decoder.MixDecoder(model, cache)
+    eager = [dec.step_eager(x).clone() for x in xs]
+    torch.cuda.synchronize()
+    after_eager = snapshot(cache)
+    assert dec.position == START + len(xs)
+
+    restore(cache, snap)
+    print("decoder graph replay", flush=True)
+    dec = qm.decoder.MixDecoder(model, cache)
+    junk = torch.randn(512, 512, device=DEV)
+    for i, x in enumerate(xs):
+        out = dec.step(x)
+        torch.cuda.synchronize()
+        # eager work of the program's own between replays
+        junk = torch.tanh(junk @ junk.t() * 1e-3)
+        assert torch.equal(out, eager[i]), f"replay {i} (position {START + i}) differs from the eager step"
+    assert len(dec._graphs) == 2, "positions 1020..1027 span two buckets"
+    torch.cuda.synchronize()
+    for l, ((a, na, ba), (b, nb, bb)) in enumerate(zip(after_eager, snapshot(cache))):
+        assert (na, ba) == (nb, bb)
+        for f in a:
+            assert torch.equal(a[f], b[f]), f"layer {l} {f} differs after graph steps"
+    restore(cache, snap)
+
+
+def test_decoder_step_matches_layer_methods(stack):
+    qm, model, cache = stack
+    snap = snapshot(cache)
+    xs = inputs(3, seed=12)
+    dec = qm.decoder.MixDecoder(model, cache)
+    got = [dec.step(x).clone() for x in xs]
+    torch.cuda.synchronize()
+    restore(cache, snap)
+    print("layer methods, eager", flush=True)
+    for i, x in enumerate(xs):
+        h = x
+        for l in range(N_LAYERS):
+            mixed, _, inject = model._gated_residual(h, l, "attn")
+            if model.config.is_full_attention(l):
+                branch = model._full_attention(mixed, l, None, None, cache, START + i)
+            else:
+                branch = model._linear_attention(mixed, l, cache)
+            h = model._reinject(h, branch, inject)
+        torch.cuda.synchronize()
+        assert rel_err(got[i], h) < 2e-2, f"step {i}"
+    restore(cache, snap)
+
+
+@pytest.mark.parametrize("k", [3, 6])
+def test_step_n_matches_single_steps(stack, k):
+    qm, model, cache = stack
+    snap = snapshot(cache)
+    x = inputs(1, k=k, seed=13)[0]
+    print(f"step_n k={k}", flush=True)
+    dec = qm.decoder.MixDecoder(model, cache)
+    rows = dec.step_n(x).clone()
+    torch.cuda.synchronize()
+    after_n = snapshot(cache)
+    assert dec.position == START + k and int(dec.positions[0]) == START + k
+    restore(cache, snap)
+    dec = qm.decoder.MixDecoder(model, cache)
+    singles = [dec.step_eager(x[:, i:i + 1]).clone() for i in range(k)]
+    torch.cuda.synchronize()
+    for i in range(k):
+        assert rel_err(rows[:, i:i + 1], singles[i]) < 2e-2, f"row {i}"
+    for l, ((a, na, _), (b, nb, _)) in enumerate(zip(after_n, snapshot(cache))):
+        assert na == nb == START + k
+        for f in a:
+            if f == "conv_ring":
+                continue   # compared as conv_state: the chunk path does not write the dead slot
+            if f == "recurrent_state" and l == 0:
+                # same inputs on both paths: the fp32 state bar
+                assert (a[f] - b[f]).abs().max().item() < 1e-3, f"layer {l}"
+            else:
+                assert rel_err(a[f], b[f]) < 2e-2, f"layer {l} {f}"
+    restore(cache, snap)
+
+
+def test_reset_rewinds_in_place(stack):
+    qm, model, cache = stack
+    snap = snapshot(cache)
+    dec = qm.decoder.MixDecoder(model, cache)
+    ptrs = [lc.k_pool.data_ptr() if lc.k_pool is not None else lc.conv_ring.data_ptr() for lc in cache.layers]
+    dec.reset()
+    assert dec.position == 0 and int(dec.positions[0]) == 0
+    for lc, p in zip(cache.layers, ptrs):
+        assert lc.n_tokens == 0
+        assert (lc.k_pool.data_ptr() if lc.k_pool is not None else lc.conv_ring.data_ptr()) == p
+        for f in FIELDS:
+            t = getattr(lc, f)
+            if t is not None:
+                assert not t.any()
+    out = dec.step(inputs(1, seed=14)[0])
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all() and dec.position == 1
+    restore(cache, snap)

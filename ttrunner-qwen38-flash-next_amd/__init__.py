@@ -10,6 +10,7 @@ native library must be built (``build.build()``) before any layer is used.
 from . import native
 from .cache import MixHybridCache, MixLayerCache
 from .config import MixConfig
+from .decoder import MixDecoder
 from .model import Qwen4MixModel
 
-__all__ = ["native", "MixHybridCache", "MixLayerCache", "MixConfig", "Qwen4MixModel"]
+__all__ = ["native", "MixHybridCache", "MixLayerCache", "MixConfig", "MixDecoder", "Qwen4MixModel"]

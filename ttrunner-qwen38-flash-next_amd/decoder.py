@@ -1,0 +1,260 @@
+"""The token-mixing half of a decode step over a stack of layers, replayable
+from one HIP graph.
+
+For one token per sequence, ``MixDecoder`` runs the attention half of every
+decoder layer of the reference's forward pass (reference/model.py:443-452):
+
+    mixed, hyper, inject = _gated_residual(hyper, layer, "attn")
+    branch = _full_attention(mixed, ...)  or  _linear_attention(mixed, ...)
+    hyper = _reinject(hyper, branch, inject)
+
+Every buffer is bound at construction, so a step is a fixed sequence of kernel
+launches -- per layer: the hyper-connection mix (two launches), the input
+projections (one GEMV launch over the layer's concatenated weights), the
+mixer core, the output projection and the reinjection in place -- and it is
+captured once into a graph and replayed, the MI355X analogue of the
+reference's traced decoder (tt/traced.py:156-314). The three things that make
+that capture valid there hold here by construction:
+
+* positions are device data: one int32 [B] tensor that every layer's kernels
+  read, advanced by one inside the graph (tt/model.py:402-432 binds them as
+  inputs for the same reason);
+* the DeltaNet conv ring is phase-invariant: the kernels pick slot p % K from
+  the device position, so a replay never sees a frozen ring phase (the
+  reference needed ``trace_safe_rings``, tt/model.py:739-826);
+* eligible-prefix bucketing (tt/model.py:117-129): the QSA decode sizes its
+  split-K grid for a maximum position, so one graph is captured per
+  power-of-two bucket of positions, on first use, and a step replays the
+  graph of its position's bucket.
+
+The host keeps only bookkeeping (each layer cache's token count and pooled
+block count), advanced after each replay, so eager calls of the layer methods
+can follow graph steps on the same cache. ``step_n`` runs k tokens of one
+sequence through the same layers at once (the multi-row verify step of
+tt/model.py:2135-2165), every per-token stage over k rows and the cores on
+their chunk paths.
+
+The FFN half of each layer (the MoE) and the PLE injection are not part of
+this path; callers run them between the layers' token-mixing halves when they
+build a whole model.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import native
+from .plan import DnDecodePlan, QsaDecodePlan
+
+
+class _LayerStep:
+    """One layer's token-mixing half for B rows, every buffer bound."""
+
+    def __init__(self, model, cache, layer: int, max_position: int, positions: torch.Tensor, dtype):
+        c = model.config
+        B = cache.batch
+        dev = model.device
+        lib = native.load()
+        self.model, self.layer, self.dtype = model, layer, dtype
+        self.is_qsa = c.is_full_attention(layer)
+        self.act = native.act_code(dtype)
+        self.rows = B
+        # hyper-connection read gate
+        self.norm_w, self.w_di, self.w_up, _ = model.hc_weights(layer, "attn", dtype)
+        self.hc_geom = model.hc_geom(B, dtype)
+        self.hc_ws = torch.zeros(lib.qm_hc_mix_workspace(ctypes.byref(self.hc_geom)), dtype=torch.uint8,
+                                 device=dev)
+        self.mixed = torch.empty(B, 1, c.hidden_size, dtype=dtype, device=dev)
+        self.inject = torch.empty(B, 1, c.hc_count, dtype=dtype, device=dev)
+        self.ri_geom = native.HcGeom(B, c.hc_count, c.hidden_size, 0, self.act, 0.0)
+        # projections
+        g_in, g_out = ("qsa_in", "qsa_out") if self.is_qsa else ("dn_in", "dn_out")
+        self.w_in, rows_in = model._wcat(layer, g_in, dtype)
+        self.w_out, rows_out = model._wcat(layer, g_out, dtype)
+        self.ins = [torch.empty(B, 1, r, dtype=dtype, device=dev) for r in rows_in]
+        self.branch = torch.empty(B, 1, rows_out[0], dtype=dtype, device=dev)
+        self.rows_in, self.rows_out = rows_in, rows_out
+        self.gemv_in = model._gemv_fits(dtype, B, c.hidden_size)
+        self.gemv_out = model._gemv_fits(dtype, B, int(self.w_out.shape[1]))
+        self._seg_in = (ctypes.c_int * len(rows_in))(*rows_in)
+        self._out_in = (ctypes.c_void_p * len(rows_in))(*[t.data_ptr() for t in self.ins])
+        self._seg_out = (ctypes.c_int * 1)(rows_out[0])
+        self._out_out = (ctypes.c_void_p * 1)(self.branch.data_ptr())
+        # mixer core, reading the shared device positions
+        if self.is_qsa:
+            self.core = QsaDecodePlan(model, cache, layer, max_position, dtype)
+        else:
+            self.core = DnDecodePlan(model, cache, layer, dtype)
+        self.core.positions = positions
+
+    def _project(self, x, w, rows, outs, seg_rows, seg_out, use_gemv, stream):
+        if use_gemv:
+            native.call("qm_gemv", self.act, self.rows, int(w.shape[0]), int(w.shape[1]), w.data_ptr(),
+                        x.data_ptr(), len(rows), seg_rows, seg_out, stream)
+            return
+        x2 = x.view(self.rows, -1)
+        start = 0
+        for r, o in zip(rows, outs):
+            torch.matmul(x2, w[start:start + r].t(), out=o.view(self.rows, r))
+            start += r
+
+    def launch(self, hyper: torch.Tensor, stream: int):
+        native.call("qm_hc_mix", ctypes.byref(self.hc_geom), hyper.data_ptr(), self.norm_w.data_ptr(),
+                    self.w_di.data_ptr(), 1, self.w_up.data_ptr(), self.mixed.data_ptr(), self.inject.data_ptr(),
+                    self.hc_ws.data_ptr(), self.hc_ws.numel(), stream)
+        self._project(self.mixed, self.w_in, self.rows_in, self.ins, self._seg_in, self._out_in, self.gemv_in, stream)
+        if self.is_qsa:
+            qg, k, v, iq, ik = self.ins
+            out = self.core.run(qg, k, v, iq, ik, stream)
+        else:
+            qkv, z, b, a = self.ins
+            out = self.core.run(qkv, z, a, b, stream)
+        self._project(out, self.w_out, self.rows_out, [self.branch], self._seg_out, self._out_out, self.gemv_out,
+                      stream)
+        native.call("qm_hc_reinject", ctypes.byref(self.ri_geom), hyper.data_ptr(), self.branch.data_ptr(),
+                    self.inject.data_ptr(), hyper.data_ptr(), stream)
+
+
+class MixDecoder:
+    """The token-mixing halves of ``layers`` (default: every layer of the cache)
+    for one token per sequence, eager (``step_eager``) or from a captured graph
+    (``step``). ``hyper`` is the bound residual [B, 1, hc_count * hidden]: a
+    step reads it and leaves the new residual in it."""
+
+    def __init__(self, model, cache, layers=None, dtype=torch.bfloat16, min_bucket: int = 1024):
+        c = model.config
+        self.model, self.cache, self.dtype = model, cache, dtype
+        self.layers = list(range(len(cache.layers))) if layers is None else list(layers)
+        if not self.layers:
+            raise ValueError("MixDecoder needs at least one layer")
+        starts = {cache[l].n_tokens for l in self.layers}
+        if len(starts) != 1:
+            raise ValueError(f"layers of the cache are at different positions: {sorted(starts)}")
+        self.position = starts.pop()
+        self.min_bucket = min_bucket
+        dev = model.device
+        self.hyper = torch.zeros(cache.batch, 1, c.hc_count * c.hidden_size, dtype=dtype, device=dev)
+        self.positions = torch.full((cache.batch,), self.position, dtype=torch.int32, device=dev)
+        self._steps = {}
+        self._graphs = {}
+
+    # -- buckets of positions (tt/model.py:117-129) ---------------------------
+
+    def bucket(self, position: int) -> int:
+        """Largest position the step plans of ``position``'s bucket cover."""
+        size = self.min_bucket
+        while size <= position:
+            size *= 2
+        top = min(size, self.cache.max_ctx) - 1
+        if position > top:
+            raise ValueError(f"position {position} is beyond the cache ({self.cache.max_ctx} tokens)")
+        return top
+
+    def _layer_steps(self, bucket: int):
+        steps = self._steps.get(bucket)
+        if steps is None:
+            steps = [_LayerStep(self.model, self.cache, l, bucket, self.positions, self.dtype) for l in self.layers]
+            self._steps[bucket] = steps
+        return steps
+
+    # -- one step ----------------------------------------------------------------
+
+    def _launch(self, steps, stream: int):
+        for st in steps:
+            st.launch(self.hyper, stream)
+        self.positions.add_(1)
+
+    def _advance(self, n: int, host_only: bool):
+        ratio = self.model.config.indexer_compress_ratio
+        self.position += n
+        if host_only:
+            return
+        for l in self.layers:
+            lc = self.cache[l]
+            lc.n_tokens += n
+            if self.model.config.is_full_attention(l):
+                lc.blocks_valid = max(lc.blocks_valid, self.position // ratio)
+
+    def _fill(self, hyper_in):
+        if hyper_in is not None:
+            self.hyper.copy_(hyper_in.reshape(self.hyper.shape))
+
+    def step_eager(self, hyper_in=None) -> torch.Tensor:
+        """One step by direct launches on the current stream."""
+        self._fill(hyper_in)
+        steps = self._layer_steps(self.bucket(self.position))
+        self._launch(steps, torch.cuda.current_stream(self.model.device).cuda_stream)
+        self._advance(1, host_only=False)
+        return self.hyper
+
+    def graph(self, bucket: int) -> torch.cuda.CUDAGraph:
+        """The captured step of ``bucket`` (captured on first use; capturing
+        launches nothing, so the cache is untouched)."""
+        g = self._graphs.get(bucket)
+        if g is None:
+            steps = self._layer_steps(bucket)
+            if not all(st.gemv_in and st.gemv_out for st in steps):
+                # the library GEMMs initialise their handles on first use: not inside a capture
+                for st in steps:
+                    st._project(st.mixed, st.w_in, st.rows_in, [torch.empty_like(t) for t in st.ins], None, None,
+                                False, 0)
+                torch.cuda.synchronize(self.model.device)
+            g = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream(self.model.device)
+            side.wait_stream(torch.cuda.current_stream(self.model.device))
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(g, stream=side):
+                    self._launch(steps, side.cuda_stream)
+            torch.cuda.current_stream(self.model.device).wait_stream(side)
+            self._graphs[bucket] = g
+        return g
+
+    def step(self, hyper_in=None) -> torch.Tensor:
+        """One step replayed from the graph of the current position's bucket."""
+        self._fill(hyper_in)
+        self.graph(self.bucket(self.position)).replay()
+        self._advance(1, host_only=False)
+        return self.hyper
+
+    # -- k tokens of one sequence (tt/model.py:2135-2165) ----------------------
+
+    def step_n(self, hyper_rows: torch.Tensor) -> torch.Tensor:
+        """k consecutive tokens of each sequence in one pass: hyper_rows
+        [B, k, hc_count * hidden] -> the residual after the layers at all k
+        positions. The per-token stages run over B*k rows; the cores run their
+        chunk paths. The cache consumes all k tokens, and the bound residual
+        is left holding the last row's."""
+        m = self.model
+        h = hyper_rows.to(self.dtype).contiguous()
+        k = h.shape[1]
+        if self.position + k > self.cache.max_ctx:
+            raise ValueError(f"{k} tokens from position {self.position} overrun the cache")
+        for l in self.layers:
+            mixed, _, inject = m._gated_residual(h, l, "attn")
+            if m.config.is_full_attention(l):
+                branch = m._full_attention(mixed, l, None, None, self.cache, self.position)
+            else:
+                branch = m._linear_attention(mixed, l, self.cache)
+            h = m._reinject(h, branch, inject)
+        self.hyper.copy_(h[:, -1:])
+        self.positions.add_(k)
+        self._advance(k, host_only=True)   # the layer methods advanced the caches
+        return h
+
+    # -- rewind ------------------------------------------------------------------
+
+    def reset(self) -> None:
+        """Back to position 0 with every buffer at its bound address (the graphs
+        stay valid): state, rings, pools and keys cleared in place."""
+        for l in self.layers:
+            lc = self.cache[l]
+            for t in (lc.conv_ring, lc.recurrent_state, lc.k_pool, lc.v_pool, lc.raw_keys, lc.block_keys):
+                if t is not None:
+                    t.zero_()
+            lc.n_tokens = 0
+            lc.blocks_valid = 0
+        self.hyper.zero_()
+        self.positions.zero_()
+        self.position = 0

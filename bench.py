@@ -10,9 +10,13 @@ resident in HBM, and rotated over enough independent layer instances that the
 data touched per rotation exceeds twice the 256 MB Infinity Cache.
 
 Prints one JSON line (see the driver contract); ``--sweep`` adds per-position
-lines (192, 1984, 4032, 8128), the 128-token prefill chunk and the layer
-projections around the core at one token (qm_gemv, weights streamed from HBM)
-to stderr and to the line's "sweep" object.
+lines (192, 1984, 4032, 8128), the 128-token prefill chunk, the layer
+projections around the core at one token (qm_gemv, weights streamed from HBM),
+the hyper-connection mix and reinjection at one token, and one token through
+the token-mixing halves of a 48-layer stack (36 DeltaNet + 12 QSA layers, each
+with its mix, projections and reinjection) launched eagerly and replayed from
+a HIP graph, to stderr and to the line's "sweep" object. ``--part stack`` or
+``--part hc`` times only that part.
 """
 
 from __future__ import annotations
@@ -79,6 +83,9 @@ def parse():
                     help="also time positions 192/1984/4032, a prefill chunk and the layer projections")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--part", choices=("stack", "hc"), default=None,
+                    help="time only this part (the token-mixing layer stack, or the hyper-connection mix) and "
+                         "print its result as one JSON line")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="after timing, copy a buffer of this many MiB device to device three times (a kernel of "
                          "known traffic that scales hardware byte counters)")
@@ -408,6 +415,184 @@ def run_projections(qm, dev, reps=200, rotate_mb=600):
     return out
 
 
+HC_STREAMS, HC_RANK, HIDDEN = 4, 320, 2048
+HC_BYTES = ((HC_RANK + HC_STREAMS) * HC_STREAMS * HIDDEN * 2      # down | inject weights
+            + HC_STREAMS * HIDDEN * HC_RANK * 2                    # up weights
+            + HC_STREAMS * HIDDEN * 4                               # norm weight (float32)
+            + HC_STREAMS * HIDDEN * 2 + HIDDEN * 2 + HC_STREAMS * 2)   # hyper in, mixed and inject out
+REINJECT_BYTES = 2 * HC_STREAMS * HIDDEN * 2 + HIDDEN * 2 + HC_STREAMS * 2
+
+
+def run_hc(qm, dev, reps=200, rotate_mb=600):
+    """qm_hc_mix at one token (a layer mixer: norm, down|inject, up, gated mean)
+    with its weights rotated over `rotate_mb` of copies, and qm_hc_reinject.
+    Event time per call."""
+    import torch
+    s = qm.native.stream_handle(dev)
+    stream = torch.cuda.current_stream(dev)
+    K = HC_STREAMS * HIDDEN
+    g = torch.Generator(device=dev).manual_seed(5)
+    bf = torch.bfloat16
+    per = (HC_RANK + HC_STREAMS) * K * 2 + K * HC_RANK * 2
+    copies = max(2, (rotate_mb << 20) // per)
+    ws = [((torch.randn(HC_RANK + HC_STREAMS, K, generator=g, device=dev) * K ** -0.5).to(bf),
+           (torch.randn(K, HC_RANK, generator=g, device=dev) * HC_RANK ** -0.5).to(bf)) for _ in range(copies)]
+    norm_w = torch.ones(K, device=dev)
+    hyper = torch.randn(1, K, generator=g, device=dev).to(bf)
+    mixed = torch.empty(1, HIDDEN, dtype=bf, device=dev)
+    inject = torch.empty(1, HC_STREAMS, dtype=bf, device=dev)
+    geom = qm.native.HcGeom(1, HC_STREAMS, HIDDEN, HC_RANK, qm.native.QM_ACT_BF16, 1e-6)
+    wsb = torch.zeros(qm.native.load().qm_hc_mix_workspace(ctypes.byref(geom)), dtype=torch.uint8, device=dev)
+    branch = torch.randn(1, HIDDEN, generator=g, device=dev).to(bf)
+
+    def mix(i):
+        di, up = ws[i % copies]
+        qm.native.call("qm_hc_mix", ctypes.byref(geom), hyper.data_ptr(), norm_w.data_ptr(), di.data_ptr(), 1,
+                       up.data_ptr(), mixed.data_ptr(), inject.data_ptr(), wsb.data_ptr(), wsb.numel(), s)
+
+    def reinject(i):
+        qm.native.call("qm_hc_reinject", ctypes.byref(geom), hyper.data_ptr(), branch.data_ptr(),
+                       inject.data_ptr(), hyper.data_ptr(), s)
+    out = {}
+    for name, fn, nbytes in (("mix", mix, HC_BYTES), ("reinject", reinject, REINJECT_BYTES)):
+        for i in range(20):
+            fn(i)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(evs):
+            a.record(stream)
+            fn(i)
+            b.record(stream)
+        torch.cuda.synchronize()
+        us = statistics.median(a.elapsed_time(b) for a, b in evs) * 1000
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"mb": round(nbytes / 1e6, 2), "us": round(us, 2), "gbs": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    del ws
+    torch.cuda.synchronize()
+    return out
+
+
+STACK_LAYERS = 48            # 36 Gated DeltaNet + 12 QSA (full attention every 4th layer)
+
+
+def stack_bytes(pos: int, n_layers: int = STACK_LAYERS) -> int:
+    """HBM bytes of one token through the token-mixing halves of the stack:
+    every weight once, plus each core's algorithmic bytes."""
+    total = 0
+    for l in range(n_layers):
+        qsa = (l + 1) % 4 == 0
+        proj_in = sum(PROJECTION_GROUPS[1 if qsa else 0][1]) * 2048 * 2
+        proj_out = 2048 * 4096 * 2
+        core = qsa_bytes(pos) if qsa else DN_BYTES
+        total += HC_BYTES + proj_in + proj_out + core + REINJECT_BYTES
+    return total
+
+
+def stack_store(dev, n_layers: int):
+    """Random-init weights of every token-mixing half (device tensors)."""
+    import torch
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(77)
+    w = {}
+
+    def rnd(*shape, scale=None, dtype=bf):
+        t = torch.randn(*shape, generator=g, device=dev)
+        return (t * (scale if scale is not None else shape[-1] ** -0.5)).to(dtype)
+    K = HC_STREAMS * HIDDEN
+    for l in range(n_layers):
+        p = f"blk.{l}."
+        w[p + "hc_attn_norm.weight"] = torch.ones(K, device=dev)
+        w[p + "hc_attn_down.weight"] = rnd(HC_RANK, K)
+        w[p + "hc_attn_up.weight"] = rnd(K, HC_RANK)
+        w[p + "hc_attn_inject.weight"] = rnd(HC_STREAMS, K)
+        if (l + 1) % 4 == 0:
+            w[p + "attn_q.weight"] = rnd(16 * 512, HIDDEN)
+            w[p + "attn_k.weight"] = rnd(512, HIDDEN)
+            w[p + "attn_v.weight"] = rnd(512, HIDDEN)
+            w[p + "indexer.q_proj.weight"] = rnd(512, HIDDEN)
+            w[p + "indexer.k_proj.weight"] = rnd(128, HIDDEN)
+            w[p + "attn_output.weight"] = rnd(HIDDEN, 4096)
+            for s in ("attn_q_norm.weight", "attn_k_norm.weight"):
+                w[p + s] = torch.ones(256, device=dev)
+            for s in ("indexer.q_norm.weight", "indexer.k_norm.weight"):
+                w[p + s] = torch.ones(128, device=dev)
+        else:
+            w[p + "attn_qkv.weight"] = rnd(8192, HIDDEN)
+            w[p + "attn_gate.weight"] = rnd(4096, HIDDEN)
+            w[p + "ssm_beta.weight"] = rnd(32, HIDDEN)
+            w[p + "ssm_alpha.weight"] = rnd(32, HIDDEN)
+            w[p + "ssm_out.weight"] = rnd(HIDDEN, 4096)
+            w[p + "ssm_conv1d.weight"] = rnd(8192, 4, scale=0.5)
+            w[p + "ssm_a"] = -torch.rand(32, generator=g, device=dev) * 2 - 0.1
+            w[p + "ssm_dt.bias"] = torch.randn(32, generator=g, device=dev) * 0.1
+            w[p + "ssm_norm.weight"] = torch.ones(128, device=dev)
+
+    class Store:
+        def get(self, name):
+            return w[name]
+    return Store()
+
+
+def run_stack(qm, dev, pos=8128, n_layers=STACK_LAYERS, steps=30, warmup=5):
+    """One token through the token-mixing halves of an n_layers stack (HC mix,
+    projections, core, output projection, reinjection per layer) at `pos`:
+    eager launches and graph replay (MixDecoder), seeded random history."""
+    import torch
+    bf = torch.bfloat16
+    max_ctx = max(((pos + 1 + 63) // 64) * 64, 8192)
+    cfg = qm.MixConfig()
+    model = qm.Qwen4MixModel(cfg, stack_store(dev, n_layers), device=dev, max_ctx=max_ctx)
+    cache = qm.MixHybridCache(n_layers, cfg, 1, max_ctx, dev, bf, page_table="random", seed=9)
+    g = torch.Generator(device=dev).manual_seed(10)
+    cos, sin = model.rope.get(max_ctx)
+    geom = model.qsa_geom(cache, bf)
+    for l in range(n_layers):
+        lc = cache[l]
+        if cfg.is_full_attention(l):
+            lc.ensure_qsa(1, bf)
+            for t in (lc.k_pool, lc.v_pool, lc.raw_keys):
+                t.copy_(torch.randn(t.shape, generator=g, device=dev).to(t.dtype))
+            qm.native.call("qm_qsa_pool_blocks", ctypes.byref(geom), lc.raw_keys.data_ptr(),
+                           model._dw(l, "indexer.k_norm.weight", torch.float32).data_ptr(), cos.data_ptr(),
+                           sin.data_ptr(), 0, pos // cfg.indexer_compress_ratio, lc.block_keys.data_ptr(),
+                           qm.native.stream_handle(dev))
+            lc.blocks_valid = pos // cfg.indexer_compress_ratio
+        else:
+            lc.ensure_dn(1, bf)
+            lc.recurrent_state.copy_(torch.randn(lc.recurrent_state.shape, generator=g, device=dev) * 0.02)
+            lc.conv_ring.copy_(torch.randn(lc.conv_ring.shape, generator=g, device=dev).to(bf))
+        lc.n_tokens = pos
+    dec = qm.MixDecoder(model, cache)
+    x = torch.randn(1, 1, HC_STREAMS * HIDDEN, generator=g, device=dev).to(bf)
+    out = {}
+    for mode in ("eager", "graph"):
+        run = dec.step_eager if mode == "eager" else dec.step
+        for _ in range(warmup):
+            # every step at one position, as the headline's rotation: the history does not grow
+            dec.position = pos
+            dec.positions.fill_(pos)
+            run(x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            dec.position = pos
+            dec.positions.fill_(pos)
+            run(x)
+        torch.cuda.synchronize()
+        out[mode] = (time.perf_counter() - t0) / steps * 1e6
+        for l in range(n_layers):
+            cache[l].n_tokens = pos
+    nbytes = stack_bytes(pos, n_layers)
+    res = {"layers": n_layers, "pos": pos, "mb_per_token": round(nbytes / 1e6, 1),
+           "eager_us": round(out["eager"], 1), "graph_us": round(out["graph"], 1),
+           "graph_gbs": round(nbytes / (out["graph"] * 1e-6) / 1e9, 1),
+           "graph_hbm_frac": round(nbytes / (out["graph"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del dec, cache, model
+    torch.cuda.synchronize()
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -421,6 +606,10 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     pos = args.position
+    if args.part is not None:
+        res = run_stack(qm, dev, pos) if args.part == "stack" else run_hc(qm, dev)
+        print(json.dumps({"part": args.part, **res}))
+        return
     head = run_decode(qm, dev, pos, args.steps, args.warmup, args.instances)
     max_ctx, n_inst, touched = head["max_ctx"], head["instances"], head["touched"]
     print(f"[bench] {n_inst} instances, {n_inst * touched / 1e6:.0f} MB touched per rotation", file=sys.stderr)
@@ -459,6 +648,10 @@ def main():
         print(f"[sweep] prefill {json.dumps(sweep['prefill_chunk'])}", file=sys.stderr)
         sweep["projections"] = run_projections(qm, dev)
         print(f"[sweep] projections {json.dumps(sweep['projections'])}", file=sys.stderr)
+        sweep["hyper_connections"] = run_hc(qm, dev)
+        print(f"[sweep] hyper_connections {json.dumps(sweep['hyper_connections'])}", file=sys.stderr)
+        sweep["layer_stack"] = run_stack(qm, dev, pos)
+        print(f"[sweep] layer_stack {json.dumps(sweep['layer_stack'])}", file=sys.stderr)
 
     cpu = None
     if not args.no_cpu:

@@ -292,6 +292,16 @@ int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void
 int qm_gemv(int act_dtype, int m, int n, int k, const void* w, const void* x, int n_seg, const int* seg_rows,
             void* const* seg_out, hipStream_t stream);
 
+/* A branch's output projection with the hyper-connection reinjection as its
+ * epilogue: the output projection of reference/model.py:244 (ssm_out) or :383
+ * (attn_output) followed by Qwen4ExpModel._reinject (reference/model.py:79-81).
+ * y = w x as qm_gemv computes it (one segment of n rows, rounded to act), then
+ * hyper[m][s * n + j] = round(hyper[m][s * n + j] + round(y[m][j] * inject[m][s]))
+ * for every stream s < streams, in place. hyper [m, streams * n],
+ * inject [m, streams] act; m, k as qm_gemv. */
+int qm_gemv_reinject(int act_dtype, int m, int n, int k, const void* w, const void* x, int streams,
+                     const void* inject, void* hyper, hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Hyper-connections around each branch                                     */
 /* ------------------------------------------------------------------------ */

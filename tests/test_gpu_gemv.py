@@ -73,3 +73,28 @@ def test_layer_projections_take_the_gemv(gpu):
         for t, name in zip(got, model.PROJ_GROUPS["dn_in"]):
             want = F.linear(hidden.float(), store.get(f"blk.0.{name}").to(DEV).float())
             assert rel_err(t, want) < 1e-2, (seq, name)
+
+
+@pytest.mark.parametrize("dtype,k", [(torch.bfloat16, 4096), (torch.float32, 2048)])
+@pytest.mark.parametrize("m", [1, 3])
+def test_gemv_reinject_equals_gemv_then_reinject(gpu, dtype, k, m):
+    """qm_gemv_reinject == qm_gemv + qm_hc_reinject, bit for bit (the same two
+    roundings of each product and sum)."""
+    qm = gpu
+    n, streams = 2048, 4
+    g = torch.Generator(device=DEV).manual_seed(31 * m + k)
+    print(f"gemv_reinject {dtype} m={m} k={k}", flush=True)
+    w = (torch.randn(n, k, generator=g, device=DEV) * k ** -0.5).to(dtype)
+    x = torch.randn(m, k, generator=g, device=DEV).to(dtype)
+    hyper = torch.randn(m, streams * n, generator=g, device=DEV).to(dtype)
+    inject = (2 * torch.sigmoid(torch.randn(m, streams, generator=g, device=DEV))).to(dtype)
+    branch = run_gemv(qm, w, x, [n])[0]
+    want = torch.empty_like(hyper)
+    geom = qm.native.HcGeom(m, streams, n, 0, qm.native.act_code(dtype), 0.0)
+    qm.native.call("qm_hc_reinject", ctypes.byref(geom), hyper.data_ptr(), branch.data_ptr(), inject.data_ptr(),
+                   want.data_ptr(), qm.native.stream_handle())
+    got = hyper.clone()
+    qm.native.call("qm_gemv_reinject", qm.native.act_code(dtype), m, n, k, w.data_ptr(), x.data_ptr(), streams,
+                   inject.data_ptr(), got.data_ptr(), qm.native.stream_handle())
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)

@@ -8,6 +8,12 @@
 // launch streams them all, and a segment table sends each row range to its own
 // output tensor.
 //
+// qm_gemv_reinject is the output projection of a branch with the
+// hyper-connection reinjection (reference/model.py:79-81) as its epilogue:
+// each output y[m][j], rounded as F.linear rounds it, is added into every
+// stream s of the residual, hyper[m][s * n + j] += round(y * inject[m][s]), so
+// the branch output never goes through memory.
+//
 // Work split: a 256-thread workgroup of four waves; wave w takes R consecutive
 // weight rows. A lane owns fixed 16-byte column chunks (8 bf16 or 4 fp32 per
 // chunk, chunk c = lane + 64 j), so every wave-wide weight load reads 1 KB of
@@ -32,6 +38,9 @@ struct GemvArgs {
   int n_seg;
   int seg_end[QM_GEMV_MAX_SEG];
   T* seg_out[QM_GEMV_MAX_SEG];   // rows [seg_end[s-1], seg_end[s]) -> seg_out[s] as [M, rows of s]
+  T* hyper;                      // reinjection: [M, streams * N], updated in place
+  const T* inject;               //              [M, streams]
+  int streams;
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -52,7 +61,7 @@ __device__ __forceinline__ float chunk_dot(const uint4& w, const uint4& x, float
   return fmaf(__uint_as_float(w.w), __uint_as_float(x.w), acc);
 }
 
-template <typename T, int MM, int R, int KC>
+template <typename T, int MM, int R, int KC, bool RJ>
 __global__ __launch_bounds__(GV_NT) void gemv_kernel(GemvArgs<T> A) {
   constexpr int VE = 16 / sizeof(T);          // elements per 16-byte chunk
   constexpr int CPR = KC * 64;                // 16-byte chunks per row
@@ -111,15 +120,24 @@ __global__ __launch_bounds__(GV_NT) void gemv_kernel(GemvArgs<T> A) {
 #pragma unroll
       for (int rr = 0; rr < R; ++rr) v = (mm == m && rr == r) ? acc[mm][rr] : v;
     if (row < A.N && m < A.M) {
-      int s = 0, start = 0;
-      while (s + 1 < A.n_seg && row >= A.seg_end[s]) { start = A.seg_end[s]; ++s; }
-      const int n_s = A.seg_end[s] - start;
-      Act<T>::store(A.seg_out[s], (long)m * n_s + (row - start), v);
+      if constexpr (RJ) {
+        const float y = Act<T>::round(v);
+        for (int s = 0; s < A.streams; ++s) {
+          const long i = ((long)m * A.streams + s) * A.N + row;
+          const float inj = Act<T>::load(A.inject, (long)m * A.streams + s);
+          Act<T>::store(A.hyper, i, add_rn(Act<T>::load(A.hyper, i), Act<T>::round(mul_rn(y, inj))));
+        }
+      } else {
+        int s = 0, start = 0;
+        while (s + 1 < A.n_seg && row >= A.seg_end[s]) { start = A.seg_end[s]; ++s; }
+        const int n_s = A.seg_end[s] - start;
+        Act<T>::store(A.seg_out[s], (long)m * n_s + (row - start), v);
+      }
     }
   }
 }
 
-template <typename T, int MM>
+template <typename T, int MM, bool RJ>
 int launch_mm(const GemvArgs<T>& A, hipStream_t stream) {
   constexpr int VE = 16 / sizeof(T);
   const int kc = A.K / (64 * VE);
@@ -127,13 +145,13 @@ int launch_mm(const GemvArgs<T>& A, hipStream_t stream) {
   // 16 KB of weights in flight per wave: R rows x KC chunks of 1 KB
   if (kc == 4) {
     const int rows = (GV_NT / 64) * 4;
-    hipLaunchKernelGGL((gemv_kernel<T, MM, 4, 4>), dim3((A.N + rows - 1) / rows), dim3(GV_NT), lds, stream, A);
+    hipLaunchKernelGGL((gemv_kernel<T, MM, 4, 4, RJ>), dim3((A.N + rows - 1) / rows), dim3(GV_NT), lds, stream, A);
   } else if (kc == 8) {
     const int rows = (GV_NT / 64) * 2;
-    hipLaunchKernelGGL((gemv_kernel<T, MM, 2, 8>), dim3((A.N + rows - 1) / rows), dim3(GV_NT), lds, stream, A);
+    hipLaunchKernelGGL((gemv_kernel<T, MM, 2, 8, RJ>), dim3((A.N + rows - 1) / rows), dim3(GV_NT), lds, stream, A);
   } else if (kc == 16) {
     const int rows = (GV_NT / 64) * 1;
-    hipLaunchKernelGGL((gemv_kernel<T, MM, 1, 16>), dim3((A.N + rows - 1) / rows), dim3(GV_NT), lds, stream, A);
+    hipLaunchKernelGGL((gemv_kernel<T, MM, 1, 16, RJ>), dim3((A.N + rows - 1) / rows), dim3(GV_NT), lds, stream, A);
   } else {
     return qm_fail(QM_ERR_UNSUPPORTED, "qm_gemv: k must be 2048 or 4096 (bf16), 1024, 2048 or 4096 (f32)");
   }
@@ -141,10 +159,19 @@ int launch_mm(const GemvArgs<T>& A, hipStream_t stream) {
   return QM_OK;
 }
 
+template <typename T, bool RJ>
+int launch_m(const GemvArgs<T>& A, hipStream_t stream) {
+  switch (A.M) {
+    case 1: return launch_mm<T, 1, RJ>(A, stream);
+    case 2: return launch_mm<T, 2, RJ>(A, stream);
+    default: return launch_mm<T, 4, RJ>(A, stream);
+  }
+}
+
 template <typename T>
 int launch_gemv(int m, int n, int k, const void* w, const void* x, int n_seg, const int* seg_rows,
                 void* const* seg_out, hipStream_t stream) {
-  GemvArgs<T> A;
+  GemvArgs<T> A = {};
   A.w = static_cast<const T*>(w); A.x = static_cast<const T*>(x);
   A.M = m; A.N = n; A.K = k; A.n_seg = n_seg;
   int end = 0;
@@ -154,11 +181,17 @@ int launch_gemv(int m, int n, int k, const void* w, const void* x, int n_seg, co
     A.seg_out[s] = static_cast<T*>(seg_out[s]);
   }
   if (end != n) return qm_fail(QM_ERR_ARG, "qm_gemv: segment rows must add up to n");
-  switch (m) {
-    case 1: return launch_mm<T, 1>(A, stream);
-    case 2: return launch_mm<T, 2>(A, stream);
-    default: return launch_mm<T, 4>(A, stream);
-  }
+  return launch_m<T, false>(A, stream);
+}
+
+template <typename T>
+int launch_reinject(int m, int n, int k, const void* w, const void* x, int streams, const void* inject, void* hyper,
+                    hipStream_t stream) {
+  GemvArgs<T> A = {};
+  A.w = static_cast<const T*>(w); A.x = static_cast<const T*>(x);
+  A.M = m; A.N = n; A.K = k; A.n_seg = 1; A.seg_end[0] = n;
+  A.hyper = static_cast<T*>(hyper); A.inject = static_cast<const T*>(inject); A.streams = streams;
+  return launch_m<T, true>(A, stream);
 }
 
 }  // namespace
@@ -176,4 +209,17 @@ extern "C" int qm_gemv(int act_dtype, int m, int n, int k, const void* w, const 
   if (act_dtype == QM_ACT_BF16) return launch_gemv<bf16_t>(m, n, k, w, x, n_seg, seg_rows, seg_out, stream);
   if (act_dtype == QM_ACT_F32) return launch_gemv<float>(m, n, k, w, x, n_seg, seg_rows, seg_out, stream);
   return qm_fail(QM_ERR_DTYPE, "qm_gemv: act_dtype must be QM_ACT_F32 or QM_ACT_BF16");
+}
+
+extern "C" int qm_gemv_reinject(int act_dtype, int m, int n, int k, const void* w, const void* x, int streams,
+                                const void* inject, void* hyper, hipStream_t stream) {
+  if (m <= 0 || m > GV_MAX_M) return qm_fail(QM_ERR_UNSUPPORTED, "qm_gemv_reinject: m must be 1..4");
+  if (n <= 0 || k <= 0 || streams <= 0) return qm_fail(QM_ERR_ARG, "qm_gemv_reinject: bad sizes");
+  if (!w || !x || !inject || !hyper) return qm_fail(QM_ERR_ARG, "qm_gemv_reinject: null pointer");
+  const bool k_ok = act_dtype == QM_ACT_BF16 ? (k == 2048 || k == 4096) : (k == 1024 || k == 2048 || k == 4096);
+  if (!k_ok)
+    return qm_fail(QM_ERR_UNSUPPORTED, "qm_gemv_reinject: k must be 2048 or 4096 (bf16), 1024, 2048 or 4096 (f32)");
+  if (act_dtype == QM_ACT_BF16) return launch_reinject<bf16_t>(m, n, k, w, x, streams, inject, hyper, stream);
+  if (act_dtype == QM_ACT_F32) return launch_reinject<float>(m, n, k, w, x, streams, inject, hyper, stream);
+  return qm_fail(QM_ERR_DTYPE, "qm_gemv_reinject: act_dtype must be QM_ACT_F32 or QM_ACT_BF16");
 }

@@ -122,6 +122,14 @@ __global__ __launch_bounds__(HC_NT) void hc_norm_down_kernel(HcArgs<T> A) {
     for (int j = 0; j < KQ; ++j) wv[r][j] = *reinterpret_cast<const uint4*>(wr + j * 64 * VE);
   }
 
+  // the norm weights of this thread's chunks (used after the reductions)
+  float4 nwv[KQ][VE / 4];
+#pragma unroll
+  for (int i = 0; i < KQ; ++i)
+#pragma unroll
+    for (int v = 0; v < VE / 4; ++v)
+      nwv[i][v] = reinterpret_cast<const float4*>(A.norm_w + (long)(tid + HC_NT * i) * VE)[v];
+
   // hyper rows of this group into LDS as stored (rows >= M read row M-1 and are
   // never written out)
 #pragma unroll
@@ -160,10 +168,9 @@ __global__ __launch_bounds__(HC_NT) void hc_norm_down_kernel(HcArgs<T> A) {
     const int c = tid + HC_NT * i;
     const int s = (c * VE) / A.hidden;
     float nw[VE];
-    const float4* wp = reinterpret_cast<const float4*>(A.norm_w + (long)c * VE);
 #pragma unroll
     for (int v = 0; v < VE / 4; ++v) {
-      const float4 f = wp[v];
+      const float4 f = nwv[i][v];
       nw[4 * v] = f.x; nw[4 * v + 1] = f.y; nw[4 * v + 2] = f.z; nw[4 * v + 3] = f.w;
     }
 #pragma unroll
@@ -248,6 +255,10 @@ __global__ __launch_bounds__(HC_NT) void hc_up_mean_kernel(HcArgs<T> A) {
     const int m = c / CK, kc = c - m * CK;
     s_mix[c] = *reinterpret_cast<const uint4*>(A.mix + (long)min(m0 + m, A.M - 1) * A.rank + kc * VE);
   }
+  // the normalised value this thread gates later: thread p owns (row m, stream
+  // s, position hr), p < MG * streams * HB <= 256
+  const int gm = tid / (A.streams * HB), gs = (tid / HB) % A.streams, ghr = tid % HB;
+  const float nv = Act<T>::load(A.normed, (long)min(m0 + gm, A.M - 1) * A.K + min(gs * A.hidden + h0 + ghr, A.K - 1));
   __syncthreads();
 
 #pragma unroll
@@ -264,16 +275,12 @@ __global__ __launch_bounds__(HC_NT) void hc_up_mean_kernel(HcArgs<T> A) {
   }
   __syncthreads();
 
-  for (int p = tid; p < MG * A.streams * HB; p += HC_NT) {
-    const int m = p / (A.streams * HB), sr = p - m * A.streams * HB;
-    const int s = sr / HB, hr = sr - s * HB;
-    const float* pr = s_part + (long)p * stride;
+  if (tid < MG * A.streams * HB) {
+    const float* pr = s_part + (long)tid * stride;
     float lin = 0.f;
     for (int kc = 0; kc < CK; ++kc) lin += pr[kc];
-    const int mm = min(m0 + m, A.M - 1);
     const float g = Act<T>::round(sigmoid_f(Act<T>::round(lin)));
-    const float nv = Act<T>::load(A.normed, (long)mm * A.K + s * A.hidden + h0 + hr);
-    s_gate[m][s][hr] = Act<T>::round(g * nv);
+    s_gate[gm][gs][ghr] = Act<T>::round(g * nv);
   }
   __syncthreads();
 
@@ -331,7 +338,7 @@ HcLayout hc_layout(const qm_hc_geom& g) {
 // positions a workgroup (HB x streams up rows: 5 KB at bf16, rank 320, 4 streams).
 // hc_norm_down stages as many rows (MG, at most 4) as fit HC_LDS.
 template <typename T> struct HcTile;
-template <> struct HcTile<bf16_t> { static constexpr int R = 4, MG_UP = 4, HB = 8; };
+template <> struct HcTile<bf16_t> { static constexpr int R = 2, MG_UP = 4, HB = 8; };
 template <> struct HcTile<float> { static constexpr int R = 2, MG_UP = 2, HB = 4; };
 
 int hc_up_chunks(const qm_hc_geom& g) {   // 16-byte up chunks of one hc_up_mean workgroup
@@ -339,10 +346,17 @@ int hc_up_chunks(const qm_hc_geom& g) {   // 16-byte up chunks of one hc_up_mean
                                     : g.streams * HcTile<float>::HB * (g.rank / 4);
 }
 
-int hc_down_rows(long K, int es) {
-  for (int mg = 4; mg > 1; mg /= 2)
-    if ((long)mg * K * es <= HC_LDS) return mg;
-  return 1;
+// rows of a workgroup's group: the fewest of 1, 2, 4 that cover M (at most
+// `cap`, and for hc_norm_down at most what fits HC_LDS)
+int hc_group_rows(int M, int cap) {
+  const int need = M >= 3 ? 4 : M;
+  return need < cap ? need : cap;
+}
+
+int hc_down_rows(long K, int es, int M) {
+  int mg = 4;
+  while (mg > 1 && (long)mg * K * es > HC_LDS) mg /= 2;
+  return hc_group_rows(M, mg);
 }
 
 bool hc_kq_ok(long kq) { return kq == 1 || kq == 2 || kq == 4 || kq == 5 || kq == 8 || kq == 10; }
@@ -365,12 +379,20 @@ const char* hc_check(const qm_hc_geom* g) {
   return nullptr;
 }
 
-template <typename T, int NQ>
-void launch_up(const HcArgs<T>& A, hipStream_t stream) {
-  constexpr int MG = HcTile<T>::MG_UP, HB = HcTile<T>::HB;
+template <typename T, int MG, int NQ>
+void launch_up_mg(const HcArgs<T>& A, hipStream_t stream) {
+  constexpr int HB = HcTile<T>::HB;
   const size_t lds = (size_t)MG * A.streams * HB * (A.rank / Chunk<T>::VE + 1) * sizeof(float);
   hipLaunchKernelGGL((hc_up_mean_kernel<T, MG, HB, NQ>), dim3(A.hidden / HB, (A.M + MG - 1) / MG), dim3(HC_NT), lds,
                      stream, A);
+}
+
+template <typename T, int NQ>
+void launch_up(const HcArgs<T>& A, hipStream_t stream) {
+  const int mg = hc_group_rows(A.M, HcTile<T>::MG_UP);
+  if (mg >= 4) launch_up_mg<T, HcTile<T>::MG_UP, NQ>(A, stream);
+  else if (mg == 2) launch_up_mg<T, 2, NQ>(A, stream);
+  else launch_up_mg<T, 1, NQ>(A, stream);
 }
 
 template <typename T, int MG, int KQ>
@@ -383,7 +405,7 @@ void launch_down_mg(const HcArgs<T>& A, hipStream_t stream) {
 
 template <typename T, int KQ>
 void launch_down(const HcArgs<T>& A, hipStream_t stream) {
-  const int mg = hc_down_rows(A.K, sizeof(T));
+  const int mg = hc_down_rows(A.K, sizeof(T), A.M);
   if (mg == 4) launch_down_mg<T, 4, KQ>(A, stream);
   else if (mg == 2) launch_down_mg<T, 2, KQ>(A, stream);
   else launch_down_mg<T, 1, KQ>(A, stream);

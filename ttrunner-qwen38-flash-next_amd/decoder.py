@@ -10,10 +10,10 @@ decoder layer of the reference's forward pass (reference/model.py:443-452):
 
 Every buffer is bound at construction, so a step is a fixed sequence of kernel
 launches -- per layer: the hyper-connection mix (two launches), the input
-projections (one GEMV launch over the layer's concatenated weights), the
-mixer core, the output projection and the reinjection in place -- and it is
-captured once into a graph and replayed, the MI355X analogue of the
-reference's traced decoder (tt/traced.py:156-314). The three things that make
+projections (one GEMV launch over the layer's concatenated weights), the mixer
+core, and the output projection with the reinjection into the residual as its
+epilogue (one launch) -- and it is captured once into a graph and replayed,
+the MI355X analogue of the reference's traced decoder (tt/traced.py:156-314). The three things that make
 that capture valid there hold here by construction:
 
 * positions are device data: one int32 [B] tensor that every layer's kernels
@@ -69,6 +69,7 @@ class _LayerStep:
         self.mixed = torch.empty(B, 1, c.hidden_size, dtype=dtype, device=dev)
         self.inject = torch.empty(B, 1, c.hc_count, dtype=dtype, device=dev)
         self.ri_geom = native.HcGeom(B, c.hc_count, c.hidden_size, 0, self.act, 0.0)
+        self.hc = c.hc_count
         # projections
         g_in, g_out = ("qsa_in", "qsa_out") if self.is_qsa else ("dn_in", "dn_out")
         self.w_in, rows_in = model._wcat(layer, g_in, dtype)
@@ -111,8 +112,13 @@ class _LayerStep:
         else:
             qkv, z, b, a = self.ins
             out = self.core.run(qkv, z, a, b, stream)
-        self._project(out, self.w_out, self.rows_out, [self.branch], self._seg_out, self._out_out, self.gemv_out,
-                      stream)
+        if self.gemv_out:
+            # the output projection with the reinjection as its epilogue
+            native.call("qm_gemv_reinject", self.act, self.rows, self.rows_out[0], int(self.w_out.shape[1]),
+                        self.w_out.data_ptr(), out.data_ptr(), self.hc, self.inject.data_ptr(), hyper.data_ptr(),
+                        stream)
+            return
+        self._project(out, self.w_out, self.rows_out, [self.branch], self._seg_out, self._out_out, False, stream)
         native.call("qm_hc_reinject", ctypes.byref(self.ri_geom), hyper.data_ptr(), self.branch.data_ptr(),
                     self.inject.data_ptr(), hyper.data_ptr(), stream)
 

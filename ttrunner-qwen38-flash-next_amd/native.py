@@ -67,6 +67,7 @@ SIGNATURES = {
     "qm_qsa_attend_chunk": (_i, [ctypes.POINTER(QsaGeom), _i] + [_vp] * 9 + [_vp, _sz, _vp]),
     "qm_qsa_pool_blocks": (_i, [ctypes.POINTER(QsaGeom), _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "qm_gemv": (_i, [_i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp]),
+    "qm_gemv_reinject": (_i, [_i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp]),
     "qm_dn_prefill_workspace": (_sz, [ctypes.POINTER(DnGeom), _i]),
     "qm_dn_prefill": (_i, [ctypes.POINTER(DnGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _vp, _sz, _vp]),

@@ -220,13 +220,16 @@ int qm_qsa_decode_front(const qm_qsa_geom* g, const void* qg, const void* k_new,
                         const int* page_table, void* k_pool, void* v_pool, void* raw_keys, float* block_keys,
                         void* q_out, float* iq_out, int* ids, int* n_sel, void* items, hipStream_t stream);
 
-/* Workgroups per kv head of qm_qsa_decode for queries up to max_position: a
- * power of two, about twice the 4-item batches of attention work there are
- * (the workgroups that start first take the batches; the rest leave at once). */
+/* Workgroups per kv head of qm_qsa_decode for queries up to max_position: the
+ * largest number of 32-token attention items of any position in the last
+ * `ratio` positions up to it (at most 1024). */
 int qm_qsa_decode_splits(const qm_qsa_geom* g, int max_position);
 /* Bytes of workspace qm_qsa_decode needs; zero it once before first use and
- * keep it for that geometry (it holds the kernel's ticket and completion
- * counters between calls). Calls that overlap on one workspace race. */
+ * keep it for that geometry: it holds, per (sequence, kv head), a generation
+ * word, a give-up counter (its second word; nonzero only if a wait for the
+ * other workgroups' partials ever gave up, which a correct launch never does),
+ * the workgroups' flags and their partials. Calls that overlap on one
+ * workspace race. */
 size_t qm_qsa_decode_workspace(const qm_qsa_geom* g, int splits);
 
 /* One QSA decode step (one token per sequence) in a single launch: everything
@@ -234,9 +237,10 @@ size_t qm_qsa_decode_workspace(const qm_qsa_geom* g, int splits);
  * raw indexer key append and block pooling, indexer query, block scores and
  * top-k, paged GQA attention over the selected blocks and the tail, sigmoid
  * gate (reference/model.py:248-382). Every working workgroup recomputes the
- * selection it needs; the last one of each kv head merges the partials.
+ * selection it needs and attends one 32-token item; the partials cross to the
+ * workgroups that merge them inside the same launch.
  * Requires max_blocks, max_pages <= 2048, budget/ratio <= 256, ratio <= 64 and
- * splits a power of two <= 128 (qm_qsa_decode_splits).
+ * 1 <= splits <= 1024 (qm_qsa_decode_splits).
  *   out [B, Hq*d] act; ids [B, budget/ratio], n_sel [B], items, iq_out
  *   [B, idx_heads, idx_dim] are optional inspection outputs (may be NULL). */
 int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k_new, const void* v_new, const void* iq,

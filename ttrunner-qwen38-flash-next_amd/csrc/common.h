@@ -74,6 +74,74 @@ __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
+// ---------------------------------------------------------------------------
+// Hand-off between the workgroups of one launch, on any die. The data crosses
+// through device-scope (sc1) accesses: stores write through to the device's
+// point of coherence and loads read from it, so publishing needs no L2
+// writeback (a release fence walks the die's whole L2) and reading no L2
+// invalidate. A workgroup waits until its own stores have completed before it
+// raises its flag; a reader polls the flags, then loads.
+//
+// Flags carry a generation number: every workgroup of a group reads the
+// group's generation word at its start, raises its flag to generation + 1,
+// and one workgroup advances the word once every flag has been seen, by which
+// time every workgroup of the group has read it. Flags and words start at
+// zero (a zeroed workspace); a later launch over fewer workgroups leaves the
+// rest of the flags behind, which the wrapping comparison tolerates.
+// ---------------------------------------------------------------------------
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+constexpr int CPOL_DEVICE = 16;             // sc1: device-scope coherence
+constexpr int BUF_DWORD3 = 0x00020000;      // raw 32-bit buffer resource, gfx9 encoding
+constexpr int FLAG_SPIN_MAX = 1 << 20;      // polls before a wait gives up (about a second)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base, long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, BUF_DWORD3);
+}
+__device__ __forceinline__ float ld_dev(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, CPOL_DEVICE));
+}
+__device__ __forceinline__ float2 ld_dev2(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, CPOL_DEVICE));
+}
+__device__ __forceinline__ void st_dev(__amdgpu_buffer_rsrc_t r, int byte_off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, byte_off, 0, CPOL_DEVICE);
+}
+__device__ __forceinline__ void st_dev2(__amdgpu_buffer_rsrc_t r, int byte_off, float2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, byte_off, 0, CPOL_DEVICE);
+}
+__device__ __forceinline__ void st_dev4(__amdgpu_buffer_rsrc_t r, int byte_off, float4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, byte_off, 0, CPOL_DEVICE);
+}
+__device__ __forceinline__ unsigned ld_flag(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_flag(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// every outstanding memory operation of this wave complete (stores acknowledged)
+__device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+// One wave polls flags[0..n), n <= MAXN, until each has reached `target` (a
+// wrapping comparison); false if it gave up after FLAG_SPIN_MAX polls. A poll
+// issues all of a lane's loads before it tests any, so it costs one round trip.
+template <int MAXN>
+__device__ __forceinline__ bool wait_flags(const unsigned* flags, int n, unsigned target) {
+  constexpr int K = (MAXN + 63) / 64;
+  const int lane = threadIdx.x & 63;
+  for (int it = 0; it < FLAG_SPIN_MAX; ++it) {
+    unsigned f[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (64 * k < n) f[k] = ld_flag(flags + min(lane + 64 * k, n - 1));
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (64 * k < n) ok = ok & ((int)(f[k] - target) >= 0);
+    if (__builtin_amdgcn_ballot_w64(!ok) == 0ull) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
 // Workgroups are dealt round-robin to the 8 XCDs; this gives each XCD a
 // contiguous range of logical work items so that neighbours share an L2.
 __device__ __forceinline__ int xcd_remap(int bid, int n) {

@@ -10,13 +10,16 @@
 //   norm   : out = rms_norm(o) * w * sigmoid(z)
 // with v-head h reading q/k head h % Hk (the tiled layout of the checkpoint).
 //
-// Work split: one 1024-thread workgroup per (sequence, value head) holds the
-// head's 64 KB float32 state in registers and computes everything for it: the
-// conv of its 384 channels, the norms, the update, and the gated RMS norm of
-// its 128 outputs, with no cross-workgroup step (a split across workgroups
-// would need an agent-scope release per workgroup, which writes dirty L2 lines
-// back, plus a dependent read of the parked outputs). All loads that depend on
-// nothing (state, gate inputs, z, norm weight) are issued before the conv.
+// Work split: 8 workgroups of 256 threads per (sequence, value head), each
+// holding 16 of the head's 128 state columns (8 KB of float32): the delta rule
+// is independent per column, so a workgroup updates its columns alone and a
+// compute unit moves 16 KB instead of the head's 128 KB. Each workgroup
+// recomputes the conv of the head's q/k channels (L2-resident) and convolves
+// its own 16 v channels. The gated RMS norm needs the head's sum of squares of
+// o: each workgroup publishes its 16 columns' share in one 64-bit write-through
+// store that carries the launch's generation number, writes its state columns
+// back, then polls the head's 8 shares (one cache line) and normalises its
+// columns. All loads are issued at the start, the conv's first.
 //
 // The conv window is a ring of K slots per channel: the input of the token at
 // position p lives in slot p % K, so the K-1 history slots read by this step are
@@ -29,8 +32,12 @@ namespace {
 
 constexpr int DN_D = 128;      // head dim (k and v)
 constexpr int DN_TILE = 16;    // state columns per workgroup
-constexpr int DN_NT = 256;     // threads per workgroup of the multi-token kernel
-constexpr int DN_HEAD_NT = 1024;  // threads per workgroup of the decode kernel (one head)
+constexpr int DN_NT = 256;     // threads per workgroup
+constexpr int DN_SLICES = DN_D / DN_TILE;   // decode workgroups per head
+// per (sequence, head) a 128-byte line of the decode workspace: the generation
+// word, a give-up counter, then the slices' (generation, sum of squares) words
+constexpr int DN_SYNC_WORDS = 32;
+constexpr int DN_SHARE0 = 4;   // first share, in 64-bit words
 
 template <typename T>
 struct DnDecodeArgs {
@@ -39,6 +46,7 @@ struct DnDecodeArgs {
   const T* conv_w; const float* norm_w;
   const int* positions;
   T* ring; float* state; T* out;
+  unsigned* sync;                  // DN_SYNC_WORDS per (sequence, head)
   int batch, hv, hk, conv_dim, K;
   float eps;
 };
@@ -54,24 +62,35 @@ __device__ __forceinline__ float vget(const uint2& v, int i) {
   return bf16_to_f32(static_cast<uint16_t>((i & 1) ? (w >> 16) : (w & 0xffffu)));
 }
 
+// A channel's conv inputs (K = 4): its ring row and weight row (one 8-byte or
+// 16-byte load each) and the token's input, loaded before any is used.
 template <typename T>
-__device__ __forceinline__ float conv_channel4(const DnDecodeArgs<T>& A, int b, int ch, int pos, bool write_ring) {
+struct ConvIn {
+  typename Vec4<T>::type r, w;
+  float x;
+};
+template <typename T>
+__device__ __forceinline__ ConvIn<T> conv_load4(const DnDecodeArgs<T>& A, int b, int ch) {
   typedef typename Vec4<T>::type V;
-  T* ring = A.ring + ((long)b * A.conv_dim + ch) * 4;
-  const V r = *reinterpret_cast<const V*>(ring);
-  const V w = *reinterpret_cast<const V*>(A.conv_w + (long)ch * 4);
-  const float x = Act<T>::load(A.qkv, (long)b * A.conv_dim + ch);
+  ConvIn<T> c;
+  c.r = *reinterpret_cast<const V*>(A.ring + ((long)b * A.conv_dim + ch) * 4);
+  c.w = *reinterpret_cast<const V*>(A.conv_w + (long)ch * 4);
+  c.x = Act<T>::load(A.qkv, (long)b * A.conv_dim + ch);
+  return c;
+}
+template <typename T>
+__device__ __forceinline__ float conv_finish4(const DnDecodeArgs<T>& A, const ConvIn<T>& c, int b, int ch, int pos,
+                                              bool write_ring) {
   float acc = 0.f;
 #pragma unroll
-  for (int j = 0; j < 3; ++j) acc = fmaf(vget(w, j), vget(r, (pos + 1 + j) & 3), acc);
-  acc = fmaf(vget(w, 3), x, acc);
-  if (write_ring) Act<T>::store(ring, pos & 3, x);
+  for (int j = 0; j < 3; ++j) acc = fmaf(vget(c.w, j), vget(c.r, (pos + 1 + j) & 3), acc);
+  acc = fmaf(vget(c.w, 3), c.x, acc);
+  if (write_ring) Act<T>::store(A.ring + ((long)b * A.conv_dim + ch) * 4, pos & 3, c.x);
   return Act<T>::round(silu_f(Act<T>::round(acc)));
 }
 
 template <typename T>
 __device__ __forceinline__ float conv_channel(const DnDecodeArgs<T>& A, int b, int ch, int pos, bool write_ring) {
-  if (A.K == 4) return conv_channel4(A, b, ch, pos, write_ring);
   const int K = A.K;
   const T* w = A.conv_w + (long)ch * K;
   T* ring = A.ring + ((long)b * A.conv_dim + ch) * K;
@@ -88,65 +107,63 @@ __device__ __forceinline__ float conv_channel(const DnDecodeArgs<T>& A, int b, i
   return Act<T>::round(silu_f(y));
 }
 
-// One workgroup of 1024 threads per (sequence, value head): the head's whole
-// 128 x 128 float32 state (64 KB) in registers, 16 floats per thread, so the
-// gated RMS norm over the head's 128 outputs needs no other workgroup. Thread t
-// owns columns 4*(t%32)..+3 of rows t/32 + 32*i (i = 0..3).
+// grid: batch * hv * DN_SLICES workgroups of DN_NT threads; workgroup (b, h, s)
+// owns columns 16s..16s+15. Thread t holds rows t/4 and t/4 + 64 of columns
+// 16s + 4(t%4)..+3.
 template <typename T>
-__global__ __launch_bounds__(DN_HEAD_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
-  const int b = blockIdx.x / A.hv, h = blockIdx.x % A.hv;
+__global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
+  const int s = blockIdx.x % DN_SLICES;
+  const int h = (blockIdx.x / DN_SLICES) % A.hv;
+  const int b = blockIdx.x / (DN_SLICES * A.hv);
   const int hk = h % A.hk;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wid = tid >> 6;
-  const int c4 = tid & 31, r0 = tid >> 5;
-  constexpr int NW = DN_HEAD_NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c4 = tid & 3, r = tid >> 2;
+  const int col0 = s * DN_TILE;
+  constexpr int NW = DN_NT / 64;
 
-  __shared__ float s_q[DN_D], s_k[DN_D], s_v[DN_D], s_o[DN_D];
-  __shared__ __attribute__((aligned(16))) float s_delta[DN_D];
-  __shared__ __attribute__((aligned(16))) float s_red[NW][2 * DN_D];
+  __shared__ float s_q[DN_D], s_k[DN_D], s_v[DN_TILE];
+  __shared__ float s_red[NW][2 * DN_TILE];
+  __shared__ float s_delta[DN_TILE];
   __shared__ float s_w3[2][3];
-  __shared__ float s_scal[4];
+  __shared__ float s_scal[2];
 
-  // everything that depends on nothing is requested first: the state, this
-  // head's gate inputs, z and the norm weight
-  float4* S = reinterpret_cast<float4*>(A.state + ((long)(b * A.hv + h) * DN_D) * DN_D);
-  float4 st[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) st[i] = S[(r0 + 32 * i) * (DN_D / 4) + c4];
-  // wave 0 finishes the head: z and the norm weight of channels lane, lane + 64
-  float zv0 = 0.f, zv1 = 0.f, nw0 = 0.f, nw1 = 0.f;
-  if (wid == 0) {
-    zv0 = Act<T>::load(A.z, (long)b * A.hv * DN_D + h * DN_D + lane);
-    zv1 = Act<T>::load(A.z, (long)b * A.hv * DN_D + h * DN_D + lane + 64);
-    nw0 = A.norm_w[lane];
-    nw1 = A.norm_w[lane + 64];
-  }
-  float gate_b = 0.f, gate_a = 0.f, a_neg = 0.f, dtb = 0.f;
-  if (tid == 0) {
-    gate_b = Act<T>::load(A.b, (long)b * A.hv + h);
-    gate_a = Act<T>::load(A.a, (long)b * A.hv + h);
-    a_neg = A.a_neg[h];
-    dtb = A.dt_bias[h];
-  }
-
-  // short conv on the head's 128 q, 128 k and 128 v channels; meanwhile thread
-  // 0 turns this head's gate inputs into beta and the decay
-  const int pos = A.positions[b];
+  // ---- loads, all issued before any is used: the conv inputs of q/k channel
+  // t (and of v column t < 16), the position, the gates, z, the norm weight,
+  // the state columns and last the generation word (needed last)
+  unsigned* line = A.sync + (long)(b * A.hv + h) * DN_SYNC_WORDS;
+  unsigned long long* shares = reinterpret_cast<unsigned long long*>(line) + DN_SHARE0;
   const int key_dim = A.hk * DN_D;
-  if (tid < 3 * DN_D) {
-    const int part = tid / DN_D, i = tid % DN_D;
-    const int ch = part == 0 ? hk * DN_D + i : part == 1 ? key_dim + hk * DN_D + i : 2 * key_dim + h * DN_D + i;
-    const bool writer = part == 2 || h == hk;      // one writer per q/k channel
-    const float y = conv_channel(A, b, ch, pos, writer);
-    (part == 0 ? s_q : part == 1 ? s_k : s_v)[i] = y;
+  const int ch_qk = tid < DN_D ? hk * DN_D + tid : key_dim + hk * DN_D + (tid - DN_D);
+  const int ch_v = 2 * key_dim + h * DN_D + col0 + (tid & (DN_TILE - 1));
+  const bool k4 = A.K == 4;
+  ConvIn<T> cin_qk, cin_v;
+  if (k4) {
+    cin_qk = conv_load4(A, b, ch_qk);
+    cin_v = conv_load4(A, b, ch_v);
   }
+  const int pos = A.positions[b];
+  const float gate_b = Act<T>::load(A.b, (long)b * A.hv + h), gate_a = Act<T>::load(A.a, (long)b * A.hv + h);
+  const float a_neg = A.a_neg[h], dtb = A.dt_bias[h];
+  const int jt = tid & (DN_TILE - 1);
+  const float zv = Act<T>::load(A.z, (long)b * A.hv * DN_D + h * DN_D + col0 + jt);
+  const float nw = A.norm_w[col0 + jt];
+  float4* S = reinterpret_cast<float4*>(A.state + ((long)(b * A.hv + h) * DN_D) * DN_D) + col0 / 4 + c4;
+  float4 s0 = S[r * (DN_D / 4)], s1 = S[(r + 64) * (DN_D / 4)];
+  const unsigned gen = ld_flag(line);
+
+  // ---- conv: q/k channel t (one writer of each q/k channel's ring slot: the
+  // first slice of the head with h == hk), v column t < 16; then the gates
+  const bool qk_writer = h == hk && s == 0;
+  const float y_qk = k4 ? conv_finish4(A, cin_qk, b, ch_qk, pos, qk_writer) : conv_channel(A, b, ch_qk, pos, qk_writer);
+  (tid < DN_D ? s_q[tid] : s_k[tid - DN_D]) = y_qk;
+  if (tid < DN_TILE) s_v[tid] = k4 ? conv_finish4(A, cin_v, b, ch_v, pos, true) : conv_channel(A, b, ch_v, pos, true);
   if (tid == 0) {
     s_scal[0] = Act<T>::round(sigmoid_f(gate_b));
     s_scal[1] = expf(a_neg * softplus_f(gate_a + dtb));
   }
   __syncthreads();
 
-  // l2 norms of q and k and their dot product: waves 0-1 hold the 128 channels
+  // ---- l2 norms of q and k and their dot product: waves 0-1 hold the 128 channels
   if (tid < DN_D) {
     const float qv = s_q[tid], kv = s_k[tid];
     const float a0 = wave_sum(qv * qv), a1 = wave_sum(kv * kv), a2 = wave_sum(qv * kv);
@@ -158,61 +175,95 @@ __global__ __launch_bounds__(DN_HEAD_NT) void dn_decode_kernel(DnDecodeArgs<T> A
   const float sqrt_d = 11.313708498984761f;
   const float qk = div_rn(sqk * rq * rk, sqrt_d);       // q^ . k^
 
-  // decay, then per column pred = S^T k^ and qd = S^T q^
+  // ---- decay, then per column pred = S^T k^ and qd = S^T q^ over the rows
   const float decay = s_scal[1];
-  float pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
-  float kr[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = r0 + 32 * i;
-    kr[i] = mul_rn(s_k[row], rk);
-    const float qr = div_rn(mul_rn(s_q[row], rq), sqrt_d);
-    st[i].x *= decay; st[i].y *= decay; st[i].z *= decay; st[i].w *= decay;
-    pk[0] = fmaf(st[i].x, kr[i], pk[0]); pk[1] = fmaf(st[i].y, kr[i], pk[1]);
-    pk[2] = fmaf(st[i].z, kr[i], pk[2]); pk[3] = fmaf(st[i].w, kr[i], pk[3]);
-    pq[0] = fmaf(st[i].x, qr, pq[0]); pq[1] = fmaf(st[i].y, qr, pq[1]);
-    pq[2] = fmaf(st[i].z, qr, pq[2]); pq[3] = fmaf(st[i].w, qr, pq[3]);
-  }
+  const float kr0 = mul_rn(s_k[r], rk), kr1 = mul_rn(s_k[r + 64], rk);
+  const float qr0 = div_rn(mul_rn(s_q[r], rq), sqrt_d), qr1 = div_rn(mul_rn(s_q[r + 64], rq), sqrt_d);
+  float st0[4] = {s0.x * decay, s0.y * decay, s0.z * decay, s0.w * decay};
+  float st1[4] = {s1.x * decay, s1.y * decay, s1.z * decay, s1.w * decay};
+  float pk[4], pq[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    pk[c] = xor32_sum(pk[c]);
-    pq[c] = xor32_sum(pq[c]);
+    pk[c] = fmaf(st1[c], kr1, st0[c] * kr0);
+    pq[c] = fmaf(st1[c], qr1, st0[c] * qr0);
   }
-  if (lane < 32) {
-    *reinterpret_cast<float4*>(&s_red[wid][4 * c4]) = make_float4(pk[0], pk[1], pk[2], pk[3]);
-    *reinterpret_cast<float4*>(&s_red[wid][DN_D + 4 * c4]) = make_float4(pq[0], pq[1], pq[2], pq[3]);
-  }
-  __syncthreads();
-  if (tid < DN_D) {
-    float pred = 0.f, qd = 0.f;
+  // lanes of one c4 within a 16-lane row (rotations by 4 and 8), then across rows
 #pragma unroll
-    for (int w = 0; w < NW; ++w) { pred += s_red[w][tid]; qd += s_red[w][DN_D + tid]; }
-    const float delta = (s_v[tid] - pred) * s_scal[0];
-    s_delta[tid] = delta;
-    s_o[tid] = Act<T>::round(fmaf(qk, delta, qd));
+  for (int c = 0; c < 4; ++c) {
+    pk[c] += dpp_f<0x124>(pk[c]);
+    pk[c] += dpp_f<0x128>(pk[c]);
+    pk[c] = xor32_sum(xor16_sum(pk[c]));
+    pq[c] += dpp_f<0x124>(pq[c]);
+    pq[c] += dpp_f<0x128>(pq[c]);
+    pq[c] = xor32_sum(xor16_sum(pq[c]));
   }
-  __syncthreads();
-
-  // rank-1 update and write-back
-  {
-    const float4 dl = *reinterpret_cast<const float4*>(s_delta + 4 * c4);
+  if (lane < 4) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float4 n;
-      n.x = fmaf(kr[i], dl.x, st[i].x); n.y = fmaf(kr[i], dl.y, st[i].y);
-      n.z = fmaf(kr[i], dl.z, st[i].z); n.w = fmaf(kr[i], dl.w, st[i].w);
-      S[(r0 + 32 * i) * (DN_D / 4) + c4] = n;
+    for (int c = 0; c < 4; ++c) {
+      s_red[wid][4 * lane + c] = pk[c];
+      s_red[wid][DN_TILE + 4 * lane + c] = pq[c];
     }
   }
+  __syncthreads();
 
-  // gated RMS norm over the head's 128 outputs, by wave 0 (two channels a lane)
+  // ---- delta and o of the 16 columns (wave 0, lanes 0-15); their share of the
+  // head's sum of squares leaves at once
+  float o = 0.f;
+  if (tid < DN_TILE) {
+    float pred = 0.f, qd = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) { pred += s_red[w][tid]; qd += s_red[w][DN_TILE + tid]; }
+    const float delta = (s_v[tid] - pred) * s_scal[0];
+    s_delta[tid] = delta;
+    o = Act<T>::round(fmaf(qk, delta, qd));
+  }
   if (wid == 0) {
-    const float o0 = s_o[lane], o1 = s_o[lane + 64];
-    const float ss = wave_sum(o0 * o0 + o1 * o1);
-    const float rn = rsqrt_rn(ss / (float)DN_D + A.eps);
-    const long ob = (long)b * A.hv * DN_D + h * DN_D;
-    Act<T>::store(A.out, ob + lane, (nw0 * (o0 * rn)) * sigmoid_f(zv0));
-    Act<T>::store(A.out, ob + lane + 64, (nw1 * (o1 * rn)) * sigmoid_f(zv1));
+    const float ss = row16_sum(tid < DN_TILE ? o * o : 0.f);
+    if (lane == 0) {
+      const unsigned long long word = ((unsigned long long)(gen + 1) << 32) | __float_as_uint(ss);
+      __hip_atomic_store(shares + s, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+
+  // ---- rank-1 update and write-back of the columns
+  {
+    float4 dl = *reinterpret_cast<const float4*>(s_delta + 4 * c4);
+    const float d4[4] = {dl.x, dl.y, dl.z, dl.w};
+    float n0[4], n1[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      n0[c] = fmaf(kr0, d4[c], st0[c]);
+      n1[c] = fmaf(kr1, d4[c], st1[c]);
+    }
+    S[r * (DN_D / 4)] = make_float4(n0[0], n0[1], n0[2], n0[3]);
+    S[(r + 64) * (DN_D / 4)] = make_float4(n1[0], n1[1], n1[2], n1[3]);
+  }
+
+  // ---- the head's sum of squares from its 8 shares (one line, polled by wave
+  // 0), then the gated RMS norm of the 16 columns
+  if (wid == 0) {
+    float ss_all = 0.f;
+    bool done = false;
+    for (int it = 0; it < FLAG_SPIN_MAX && !done; ++it) {
+      const unsigned long long w =
+          __hip_atomic_load(shares + (lane & (DN_SLICES - 1)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool ok = (int)((unsigned)(w >> 32) - (gen + 1)) >= 0;
+      if (__builtin_amdgcn_ballot_w64(!ok) == 0ull) {
+        const float v = __uint_as_float((unsigned)w);
+#pragma unroll
+        for (int k = 0; k < DN_SLICES; ++k) ss_all += readlane_f(v, k);
+        done = true;
+      } else {
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    if (!done && lane == 0) __hip_atomic_fetch_add(line + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (s == 0 && lane == 0) st_flag(line, gen + 1);
+    if (tid < DN_TILE) {
+      const float rn = rsqrt_rn(ss_all / (float)DN_D + A.eps);
+      Act<T>::store(A.out, (long)b * A.hv * DN_D + h * DN_D + col0 + tid, (nw * (o * rn)) * sigmoid_f(zv));
+    }
   }
 }
 
@@ -344,8 +395,9 @@ int launch_dn_decode(const qm_dn_geom* g, const void* qkv, const void* z, const 
   A.batch = g->batch; A.hv = g->n_v_heads; A.hk = g->n_k_heads;
   A.conv_dim = 2 * g->n_k_heads * DN_D + g->n_v_heads * DN_D;
   A.K = g->conv_kernel; A.eps = g->eps;
-  const int nwg = g->batch * g->n_v_heads;
-  hipLaunchKernelGGL(dn_decode_kernel<T>, dim3(nwg), dim3(DN_HEAD_NT), 0, stream, A);
+  A.sync = static_cast<unsigned*>(ws);
+  const int nwg = g->batch * g->n_v_heads * DN_SLICES;
+  hipLaunchKernelGGL(dn_decode_kernel<T>, dim3(nwg), dim3(DN_NT), 0, stream, A);
   QM_CHECK_LAUNCH();
   return QM_OK;
 }
@@ -367,9 +419,10 @@ int launch_dn_recurrent(int batch, int seq, int heads, int hk, long q_stride, lo
 }  // namespace
 
 extern "C" size_t qm_dn_decode_workspace(int batch, int n_v_heads, int head_dim) {
-  // the one-workgroup-per-head kernel needs no scratch; kept for ABI stability
+  // one 128-byte line per (sequence, head): generation word and the shares of
+  // the gated norm's sum of squares
   if (batch <= 0 || n_v_heads <= 0 || head_dim <= 0) return 0;
-  return 256;
+  return qm_align256((size_t)batch * n_v_heads * DN_SYNC_WORDS * sizeof(unsigned));
 }
 
 extern "C" int qm_dn_decode(const qm_dn_geom* g, const void* qkv, const void* z, const void* a, const void* b,

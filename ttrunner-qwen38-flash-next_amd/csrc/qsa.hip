@@ -1059,23 +1059,19 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
 }
 
 // ---------------------------------------------------------------------------
-// decode step: two launches per token
+// decode step: one launch per token
 // ---------------------------------------------------------------------------
 // qsa_decode_kernel, grid (G, kv head g, sequence b) of 256-thread workgroups,
-// G at least the position's number of 32-token attention items. One workgroup
-// attends one item: spreading the key/value reads over one item per compute
+// G at least the position's number of 32-token attention items. Workgroup x
+// attends item x: spreading the key/value reads over one item per compute
 // unit is what lets them run near the memory system's speed (a unit reading
 // four items' 128 KB takes twice as long as four units reading 32 KB each).
-// Items are not tied to blockIdx: each workgroup takes a ticket from a
-// per-(b, g) counter as it starts and does item `ticket`, so the workgroups
-// that start first (the dies start a launch's workgroups microseconds apart)
-// take the work and spare ones leave; qsa_decode_combine resets the counter.
 // A workgroup:
-//   0. takes its ticket and issues its loads: those that do not depend on the
-//      position first (its 8 query heads, the token's key and value, the
-//      indexer query and key, the norm weights), then the rope row, the
-//      page-table row, the first 128 block keys and, when this token completes
-//      a block, that block's raw keys;
+//   0. issues its loads, every one of them unconditional and, but for the
+//      rope row and a completed block's raw keys, independent of the position:
+//      its 8 query heads, the token's key and value, the indexer query and
+//      key, the norm weights, the page-table row, the first 128 block keys and
+//      the group's generation word, so they share one round trip;
 //   1. RMS-norms and ropes the indexer query and the pooled block key (sums of
 //      squares in torch's order);
 //   2. scores the eligible blocks and ranks them (redundantly in every
@@ -1087,12 +1083,16 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
 //   4. scores the item on bf16 MFMA (waves 0-1), shares the scores through LDS,
 //      and every wave forms the softmax weights and its 64 output channels;
 //      the current token's key/value come from LDS, not the pages;
-//   5. writes the item's (max, sum, unnormalised output) partial. The workgroup
-//      of item 0 also appends the token's key/value to its page slot, and for
-//      kv head 0 writes the per-sequence outputs (raw indexer key, pooled key).
-// qsa_decode_combine, grid (64-channel quarter, query head, sequence), merges
-// the items' partials of its head, applies the sigmoid gate and resets the
-// ticket counter.
+//   5. writes the item's (max, sum, unnormalised output) partial through to
+//      the device's point of coherence. The workgroup of item 0 also appends
+//      the token's key/value to its page slot, and for kv head 0 writes the
+//      per-sequence outputs (raw indexer key, pooled key);
+//   6. raises its flag, and, when it holds one of the 64 (query head, 32
+//      channels) slices of the group's output, waits for the flags of every
+//      item of the group, merges that slice's partials and applies the gate.
+// Every workgroup of a group is resident at once: workgroups are dispatched in
+// order, so at most one group is ever partly dispatched, and a group (at most
+// DEC_MAX_ITEMS small workgroups) fits the device.
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_NT = 64 * DEC_WAVES;
 constexpr int DEC_MAX_BLOCKS = 2048;
@@ -1100,7 +1100,8 @@ constexpr int DEC_MAX_PAGES = 2048;
 constexpr int DEC_MAX_TOPK = 256;
 constexpr int DEC_MAX_ITEMS = 1024;   // workgroups per (sequence, kv head)
 constexpr int DEC_MAX_RATIO = 64;     // raw keys of a completed block are held in registers
-constexpr int DEC_CTR_STRIDE = 32;    // counters 128 bytes apart, one cache line each
+constexpr int DEC_GEN_STRIDE = 32;    // generation words 128 bytes apart, one cache line each
+constexpr int DEC_SLICES = GQA * QSA_D / 32;   // output slices of a group: (query head, 32 channels)
 
 // rows of the two norm passes, at these LDS offsets: the 4 indexer-query rows
 // and the pooled block key (128 wide) first, then the 8 query heads and the
@@ -1116,7 +1117,10 @@ __device__ __forceinline__ int norm_row_offset(int r) {
 template <typename T>
 struct DecArgs {
   PrepArgs<T> P;
-  float* part_o; float* part_ml; unsigned* tickets;
+  float* part_o; float* part_ml;        // per group: [G][8][256] outputs, [G][8] (max, sum)
+  unsigned* gen;                        // per group: generation word, then a give-up counter
+  unsigned* flags;                      // per group: G flags
+  T* out;
   int* ids; int* n_sel; int2* items; float* iq_out;   // optional inspection outputs
   int splits, topk, max_items;
 };
@@ -1136,7 +1140,6 @@ struct DecShared {
   int sel[DEC_MAX_TOPK];
   int rscr[rank_scratch(DEC_MAX_TOPK)];
   alignas(16) float s[GQA][32];                   // the item's scores, head-major
-  int ticket;
 };
 
 // item -> (first token t0, visible rows [lo, hi)) of a query at position p
@@ -1197,25 +1200,88 @@ __device__ __forceinline__ void norm_rinv(DecShared& sh, int r0, int r1, float e
   }
 }
 
+// Output slice sl = (query head h = sl / 8, channels 32 (sl % 8) ..+31) of
+// group (b, g): out[d] = round(sum_i w_i o_i[d] / sum_i w_i l_i) *
+// round(sigmoid(gate[d])), w_i = exp(m_i - max m), over the n items. Thread
+// (ch = tid % 32, il = tid / 32) takes items il, il + 8, ...; every load of a
+// 128-item chunk is issued before any is used, indices clamped to the last
+// item and weighted by zero past it.
+template <typename T>
+__device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, int g, int sl, int n,
+                                     __amdgpu_buffer_rsrc_t ro, __amdgpu_buffer_rsrc_t rml) {
+  constexpr int CHUNK = 16;                     // items per thread per round trip (128 per workgroup)
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int ch = tid & 31, il = tid >> 5;
+  const int h = sl / 8, d = 32 * (sl % 8) + ch;
+  const int hq = D.P.hq, qh = g * GQA + h;
+  float* s_w = reinterpret_cast<float*>(sh.key);           // DEC_MAX_ITEMS + 128 weights
+  float* red = sh.part;                                   // 8 x 32 partial sums, then 2 x 4 wave values
+  const float gate = Act<T>::load(D.P.qg, ((long)b * hq + qh) * (2 * QSA_D) + QSA_D + d);
+  float ov[CHUNK];
+#pragma unroll
+  for (int k = 0; k < CHUNK; ++k) ov[k] = ld_dev(ro, ((min(il + 8 * k, n - 1) * GQA + h) * QSA_D + d) * 4);
+  float2 ml[DEC_MAX_ITEMS / DEC_NT];
+#pragma unroll
+  for (int k = 0; k < DEC_MAX_ITEMS / DEC_NT; ++k) ml[k] = ld_dev2(rml, ((min(tid + DEC_NT * k, n - 1) * GQA + h) * 2) * 4);
+  float M = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < DEC_MAX_ITEMS / DEC_NT; ++k)
+    if (tid + DEC_NT * k < n) M = fmaxf(M, ml[k].x);
+  M = wave_max(M);
+  if (lane == 0) red[256 + wv] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[256], red[257]), fmaxf(red[258], red[259]));
+  float L = 0.f;
+  const int n_pad = (n + 127) & ~127;
+#pragma unroll
+  for (int k = 0; k < DEC_MAX_ITEMS / DEC_NT; ++k) {
+    const int i = tid + DEC_NT * k;
+    const float w = i < n ? __expf(ml[k].x - M) : 0.f;
+    if (i < n_pad) s_w[i] = w;
+    L += ml[k].y * w;
+  }
+  L = wave_sum(L);
+  if (lane == 0) red[260 + wv] = L;
+  __syncthreads();
+  L = (red[260] + red[261]) + (red[262] + red[263]);
+  float acc = 0.f;
+  for (int i0 = 0;; i0 += 8 * CHUNK) {
+#pragma unroll
+    for (int k = 0; k < CHUNK; ++k) acc += ov[k] * s_w[i0 + il + 8 * k];
+    if (i0 + 8 * CHUNK >= n) break;
+#pragma unroll
+    for (int k = 0; k < CHUNK; ++k)
+      ov[k] = ld_dev(ro, ((min(i0 + 8 * CHUNK + il + 8 * k, n - 1) * GQA + h) * QSA_D + d) * 4);
+  }
+  red[il * 32 + ch] = acc;
+  __syncthreads();
+  if (tid < 32) {
+    float o = red[ch];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) o += red[k * 32 + ch];
+    Act<T>::store(D.out, ((long)b * hq + qh) * QSA_D + d, Act<T>::round(o / L) * Act<T>::round(sigmoid_f(gate)));
+  }
+  __syncthreads();
+}
+
 template <typename T>
 __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   const PrepArgs<T>& A = D.P;
-  const int g = blockIdx.y, b = blockIdx.z;
+  const int item = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int col = lane & 15, quad = lane >> 4;
   const int e128 = tid & 127, hh = tid >> 7;
   const int bg = b * A.hkv + g;
   __shared__ DecShared sh;
 
-  // ---- 0. a ticket, then the loads
-  unsigned ticket = 0;
-  if (tid == 0)
-    ticket = __hip_atomic_fetch_add(D.tickets + bg * DEC_CTR_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // ---- 0. the loads
+  const unsigned gen = ld_flag(D.gen + (long)bg * DEC_GEN_STRIDE);
   float iqv[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
-    const int i = tid + DEC_NT * k;
-    iqv[k] = i < A.idx_heads * IDX_D ? Act<T>::load(A.iq, (long)b * A.idx_heads * IDX_D + i) : 0.f;
+    const int i = tid + DEC_NT * k, n_iq = A.idx_heads * IDX_D;
+    const float v = Act<T>::load(A.iq, (long)b * n_iq + min(i, n_iq - 1));
+    iqv[k] = i < n_iq ? v : 0.f;
   }
   const float ikv = Act<T>::load(A.ik, (long)b * IDX_D + e128);
   float qx[GQA];
@@ -1243,17 +1309,18 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   const float cs = A.cos[(long)p * rope + ec], sn = A.sin[(long)p * rope + ec];
   const long t0r = (long)max(j_new, 0) * ratio * rope + ec;
   const float cs0 = A.cos[t0r], sn0 = A.sin[t0r];
-  const int n_lpages = min(A.max_pages, (p + A.page_size) / A.page_size);
+  // the whole page-table row and the first 128 block keys, whatever the position
   int pg[DEC_MAX_PAGES / DEC_NT];
 #pragma unroll
   for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k)
-    pg[k] = A.page_table[(long)b * A.max_pages + min(tid + DEC_NT * k, n_lpages - 1)];
+    pg[k] = A.page_table[(long)b * A.max_pages + min(tid + DEC_NT * k, A.max_pages - 1)];
   const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
   const bool scoring = n_elig > topk;
   float4 kp[SCORE_PRE][4];
-  prefetch_block_keys<DEC_NT>(kp, bk, n_elig, j_new, scoring);
+  prefetch_block_keys<DEC_NT>(kp, bk, A.max_blocks, -1, true);
   // raw keys of the block this token completes: thread (e128, hh) takes the
   // 16-row chunks hh and hh + 2; the token's own row is ik (not yet stored)
+  // (loads unconditional, rows clamped, so that none waits alone)
   float rk[2][16];
   if (j_new >= 0) {
     const T* raw = A.raw_keys + ((long)b * A.max_ctx + (long)j_new * ratio) * IDX_D + e128;
@@ -1262,12 +1329,12 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = 16 * (hh + 2 * c) + i;
-        rk[c][i] = r >= ratio ? 0.f : j_new * ratio + r == p ? ikv : Act<T>::load(raw, (long)r * IDX_D);
+        const float v = Act<T>::load(raw, (long)min(r, ratio - 1) * IDX_D);
+        rk[c][i] = r >= ratio ? 0.f : j_new * ratio + r == p ? ikv : v;
       }
   }
 
-  // ---- 1. the indexer query and the pooled block key; the ticket decides
-  // whether this workgroup has an item at all
+  // ---- 1. the indexer query and the pooled block key
   if (j_new >= 0) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -1288,12 +1355,12 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   sh.x[X_K + tid] = kx;
   sh.vnb[tid] = f32_to_bf16(vx);
 #pragma unroll
-  for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k)
-    if (tid + DEC_NT * k < n_lpages) sh.pages[tid + DEC_NT * k] = pg[k];
-  if (tid == 0) sh.ticket = (int)ticket;
+  for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k) sh.pages[tid + DEC_NT * k] = pg[k];
+  // a workgroup past the position's items has nothing to do: the waits of
+  // this launch cover only the first n_att flags
+  const int n_att = min(n_items, D.splits);
+  if (item >= n_att) return;
   __syncthreads();
-  const int item = sh.ticket;
-  if (item >= min(n_items, D.splits)) return;
   const bool blk_item = item < ic.n_blk_items;
   float pmean = 0.f;
   if (j_new >= 0) {
@@ -1465,16 +1532,18 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
       vf[i] = __builtin_bit_cast(bf16x8_t, u);
     }
   }
-  // O^T[d][head] = V^T[d][tok] P^T[tok][head] for this wave's 64 channels
+  // O^T[d][head] = V^T[d][tok] P^T[tok][head] for this wave's 64 channels,
+  // written through to the point of coherence (read by other workgroups)
   const long gbase = (long)bg * D.splits;
-  float* po = D.part_o + ((gbase + item) * GQA + hcol) * QSA_D;
+  const __amdgpu_buffer_rsrc_t ro = dev_rsrc(D.part_o + gbase * GQA * QSA_D, (long)D.splits * GQA * QSA_D * 4);
+  const __amdgpu_buffer_rsrc_t rml = dev_rsrc(D.part_ml + gbase * GQA * 2, (long)D.splits * GQA * 2 * 4);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const f32x4_t o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[i], pf, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    if (col < GQA) *reinterpret_cast<float4*>(po + 16 * (4 * wv + i) + 4 * quad) = make_float4(o[0], o[1], o[2], o[3]);
+    if (col < GQA)
+      st_dev4(ro, ((item * GQA + hcol) * QSA_D + 16 * (4 * wv + i) + 4 * quad) * 4, make_float4(o[0], o[1], o[2], o[3]));
   }
-  if (wv == 0 && quad == 0 && col < GQA)
-    *reinterpret_cast<float2*>(D.part_ml + ((gbase + item) * GQA + col) * 2) = make_float2(mx, lsum);
+  if (wv == 0 && quad == 0 && col < GQA) st_dev2(rml, ((item * GQA + col) * 2) * 4, make_float2(mx, lsum));
 
   // ---- 5. the stores that outlive this step: the token's key/value into its
   // page slot (item 0 of each kv head), and per sequence (item 0 of kv head 0)
@@ -1507,83 +1576,19 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
       }
     }
   }
-}
 
-template <typename T>
-struct DecCombineArgs {
-  const float* part_o; const float* part_ml; unsigned* tickets;
-  const int* positions; const T* qg; T* out;
-  int hq, hkv, splits, ratio, topk, max_blocks;
-};
-
-constexpr int DC_NT = 64;          // one wave per (64-channel quarter, query head, sequence)
-constexpr int DC_CHUNK = 96;       // partial outputs in flight per lane
-
-// out[d] = round(sum_i w_i o_i[d] / sum_i w_i l_i) * round(sigmoid(gate[d])),
-// w_i = exp(m_i - max m) over the position's items; lane = channel, and every
-// item's value of that channel is loaded before any is used (one round trip
-// for up to DC_CHUNK items). Loads are unconditional and do not wait for the
-// position: indices are clamped to the workspace's `splits` items (every one
-// holds finite values: the workspace starts zeroed and only ever receives
-// partials) and values past the position's item count are weighted by zero.
-template <typename T>
-__global__ __launch_bounds__(DC_NT) void qsa_decode_combine_kernel(DecCombineArgs<T> C) {
-  const int quarter = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
-  const int lane = threadIdx.x, d = 64 * quarter + lane;
-  const int g = hq / GQA, h = hq % GQA;
-  const int bg = b * C.hkv + g;
-  __shared__ __attribute__((aligned(16))) float s_w[DEC_MAX_ITEMS + DC_CHUNK];
-  const float gate = Act<T>::load(C.qg, ((long)b * C.hq + hq) * (2 * QSA_D) + QSA_D + d);
-  const int p = C.positions[b];
-  const int n = min(ItemCount(p, C.ratio, C.topk, C.max_blocks).n_items, C.splits);
-  const int n_round = (n + DC_CHUNK - 1) / DC_CHUNK * DC_CHUNK;
-  const long base = (long)bg * C.splits;
-  const float* pml = C.part_ml + (base * GQA + h) * 2;
-  const float* po = C.part_o + (base * GQA + h) * QSA_D + d;
-  constexpr long ISTRIDE = (long)GQA * QSA_D;     // floats between two items' outputs of a head
-  const int last = C.splits - 1;
-  float ov[DC_CHUNK];
-#pragma unroll
-  for (int u = 0; u < DC_CHUNK; ++u) ov[u] = po[min(u, last) * ISTRIDE];
-  float2 ml[DEC_MAX_ITEMS / DC_NT];
-  const int n_ml = (C.splits + DC_NT - 1) / DC_NT;
-#pragma unroll
-  for (int k = 0; k < DEC_MAX_ITEMS / DC_NT; ++k)
-    if (k < n_ml) ml[k] = *reinterpret_cast<const float2*>(pml + (long)min(lane + DC_NT * k, last) * GQA * 2);
-  float M = -INFINITY;
-#pragma unroll
-  for (int k = 0; k < DEC_MAX_ITEMS / DC_NT; ++k)
-    if (k < n_ml && lane + DC_NT * k < n) M = fmaxf(M, ml[k].x);
-  M = wave_max(M);
-  float L = 0.f;
-#pragma unroll
-  for (int k = 0; k < DEC_MAX_ITEMS / DC_NT; ++k) {
-    const int i = lane + DC_NT * k;
-    if (k < n_ml && i < n) {
-      const float w = __expf(ml[k].x - M);
-      s_w[i] = w;
-      L += ml[k].y * w;
-    }
-  }
-  L = wave_sum(L);
-  for (int i = n + lane; i < n_round; i += DC_NT) s_w[i] = 0.f;    // weights past the items: zero
+  // ---- 6. arrive; the workgroups holding output slices wait for every item
+  // of the group, then merge their slices
+  wait_all_memory();
   __syncthreads();
-  float o = 0.f;
-  for (int i0 = 0;; i0 += DC_CHUNK) {
-#pragma unroll
-    for (int u = 0; u < DC_CHUNK; u += 4) {
-      const float4 w = *reinterpret_cast<const float4*>(&s_w[i0 + u]);
-      o += ov[u] * w.x;
-      o += ov[u + 1] * w.y;
-      o += ov[u + 2] * w.z;
-      o += ov[u + 3] * w.w;
-    }
-    if (i0 + DC_CHUNK >= n) break;
-#pragma unroll
-    for (int u = 0; u < DC_CHUNK; ++u) ov[u] = po[min(i0 + DC_CHUNK + u, last) * ISTRIDE];
-  }
-  Act<T>::store(C.out, ((long)b * C.hq + hq) * QSA_D + d, Act<T>::round(o / L) * Act<T>::round(sigmoid_f(gate)));
-  if (h == 0 && quarter == 0 && lane == 0) C.tickets[bg * DEC_CTR_STRIDE] = 0u;
+  unsigned* flags = D.flags + gbase;
+  if (tid == 0) st_flag(flags + item, gen + 1);
+  if (item >= DEC_SLICES) return;
+  if (wv == 0 && !wait_flags<DEC_MAX_ITEMS>(flags, n_att, gen + 1) && lane == 0)
+    __hip_atomic_fetch_add(D.gen + (long)bg * DEC_GEN_STRIDE + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (item == 0 && tid == 0) st_flag(D.gen + (long)bg * DEC_GEN_STRIDE, gen + 1);
+  for (int sl = item; sl < DEC_SLICES; sl += n_att) decode_combine_slice(D, sh, b, g, sl, n_att, ro, rml);
 }
 
 int check_geom(const qm_qsa_geom* g, const char* who) {
@@ -1941,10 +1946,14 @@ extern "C" int qm_qsa_decode_splits(const qm_qsa_geom* g, int max_position) {
 }
 
 namespace {
-// workspace of qm_qsa_decode: ticket counters (one cache line each), then the
-// items' (max, sum) and their unnormalised outputs
-size_t dec_ticket_bytes(const qm_qsa_geom* g) {
-  return qm_align256((size_t)g->batch * g->n_kv_heads * DEC_CTR_STRIDE * sizeof(unsigned));
+// workspace of qm_qsa_decode, per (sequence, kv head) group: a generation word
+// and a give-up counter (one cache line), the items' flags, their (max, sum)
+// and their unnormalised outputs
+size_t dec_gen_bytes(const qm_qsa_geom* g) {
+  return qm_align256((size_t)g->batch * g->n_kv_heads * DEC_GEN_STRIDE * sizeof(unsigned));
+}
+size_t dec_flag_bytes(const qm_qsa_geom* g, int splits) {
+  return qm_align256((size_t)g->batch * g->n_kv_heads * splits * sizeof(unsigned));
 }
 size_t dec_ml_bytes(const qm_qsa_geom* g, int splits) {
   return qm_align256((size_t)g->batch * g->n_kv_heads * splits * GQA * 2 * sizeof(float));
@@ -1953,7 +1962,7 @@ size_t dec_ml_bytes(const qm_qsa_geom* g, int splits) {
 
 extern "C" size_t qm_qsa_decode_workspace(const qm_qsa_geom* g, int splits) {
   if (!g || splits <= 0) return 0;
-  return dec_ticket_bytes(g) + dec_ml_bytes(g, splits) + part_o_bytes(g, g->batch, splits);
+  return dec_gen_bytes(g) + dec_flag_bytes(g, splits) + dec_ml_bytes(g, splits) + part_o_bytes(g, g->batch, splits);
 }
 
 extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k_new, const void* v_new, const void* iq,
@@ -1978,23 +1987,20 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
   if (!workspace || workspace_bytes < qm_qsa_decode_workspace(g, splits))
     return qm_fail(QM_ERR_WORKSPACE, "qm_qsa_decode: workspace too small");
   char* ws = static_cast<char*>(workspace);
-  unsigned* tickets = reinterpret_cast<unsigned*>(ws);
-  float* part_ml = reinterpret_cast<float*>(ws + dec_ticket_bytes(g));
-  float* part_o = reinterpret_cast<float*>(ws + dec_ticket_bytes(g) + dec_ml_bytes(g, splits));
-  const dim3 grid(splits, g->n_kv_heads, g->batch), cgrid(QSA_D / DC_NT, g->n_heads, g->batch);
+  unsigned* gen = reinterpret_cast<unsigned*>(ws);
+  unsigned* flags = reinterpret_cast<unsigned*>(ws + dec_gen_bytes(g));
+  float* part_ml = reinterpret_cast<float*>(ws + dec_gen_bytes(g) + dec_flag_bytes(g, splits));
+  float* part_o = reinterpret_cast<float*>(ws + dec_gen_bytes(g) + dec_flag_bytes(g, splits) + dec_ml_bytes(g, splits));
+  const dim3 grid(splits, g->n_kv_heads, g->batch);
   auto run = [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
     DecArgs<T> D;
     D.P = prep_args<T>(g, 1, qg, k_new, v_new, iq, ik, q_norm, k_norm, iq_norm, ik_norm, cos, sin, positions,
                        page_table, k_pool, v_pool, raw_keys, block_keys, nullptr, nullptr);
-    D.part_o = part_o; D.part_ml = part_ml; D.tickets = tickets;
+    D.part_o = part_o; D.part_ml = part_ml; D.gen = gen; D.flags = flags; D.out = static_cast<T*>(out);
     D.ids = ids; D.n_sel = n_sel; D.items = static_cast<int2*>(items); D.iq_out = iq_out;
     D.splits = splits; D.topk = g->budget / g->ratio; D.max_items = item_stride(g);
     hipLaunchKernelGGL(qsa_decode_kernel<T>, grid, dim3(DEC_NT), 0, stream, D);
-    QM_CHECK_LAUNCH();
-    DecCombineArgs<T> C{part_o, part_ml, tickets, positions, static_cast<const T*>(qg), static_cast<T*>(out),
-                        g->n_heads, g->n_kv_heads, splits, g->ratio, g->budget / g->ratio, g->max_blocks};
-    hipLaunchKernelGGL(qsa_decode_combine_kernel<T>, cgrid, dim3(DC_NT), 0, stream, C);
     QM_CHECK_LAUNCH();
     return QM_OK;
   };

@@ -309,9 +309,11 @@ class Qwen4MixModel:
         norms = [native.ptr(self._dw(layer, n, torch.float32)) for n in
                  ("attn_q_norm.weight", "attn_k_norm.weight", "indexer.q_norm.weight", "indexer.k_norm.weight")]
         if seq == 1 and qg is not None and k is not None and attend and self.fused_decode_fits(cache):
-            # decode: the whole QSA step in qm_qsa_decode (attend + combine launches)
+            # decode: the whole QSA step in one qm_qsa_decode launch; its workspace
+            # (generation words, flags, partials) is kept per layer and batch
             splits = lib.qm_qsa_decode_splits(ctypes.byref(g), query_offset)
-            ws = self._workspace(f"qsa_decode_{layer}", lib.qm_qsa_decode_workspace(ctypes.byref(g), splits))
+            ws = self._workspace(f"qsa_decode_{layer}_{batch}",
+                                 lib.qm_qsa_decode_workspace(ctypes.byref(g), splits))
             if out is None:
                 out = torch.empty(batch, seq, c.num_attention_heads * c.head_dim, dtype=dt, device=self.device)
             native.call("qm_qsa_decode", ctypes.byref(g), native.ptr(qg), native.ptr(k), native.ptr(v),

@@ -132,6 +132,12 @@ def test_64_compounding_decode_steps_stay_within_tolerance(gpu):
     print(f"64 steps: worst out rel {worst_out:.2e}, worst state abs {worst_state:.2e}", flush=True)
     assert worst_out < OUT_TOL and worst_state < STATE_TOL
     assert torch.equal(cache[0].conv_state.cpu(), ocache[0].conv_state)
+    # the in-launch hand-off of the gated norm's shares: one 128-byte line per
+    # head, whose generation word counts the launches and whose second word
+    # counts waits that gave up (never)
+    lines = model._ws["dn_decode"].view(torch.int32).cpu()[: 32 * 32].reshape(32, 32)
+    assert lines[:, 0].tolist() == [64] * 32
+    assert lines[:, 1].tolist() == [0] * 32
 
 
 @pytest.mark.parametrize("seq", [2, 7, 64, 128])

@@ -305,6 +305,11 @@ def test_consecutive_decode_steps_cross_a_block_boundary(gpu):
         want = om._full_attention(hidden, 3, cos, sin, ocache, pos)
         got = model._full_attention(hidden.to(DEV), 3, cos.to(DEV), sin.to(DEV), cache, pos)
         assert rel_err(got, want) < OUT_TOL, pos
+    # the in-launch hand-off of the partials: per (sequence, kv head) a
+    # generation word counting the launches, then a count of waits that gave up
+    gen = model._ws["qsa_decode_3_1"].view(torch.int32).cpu()[: 2 * 32].reshape(2, 32)
+    assert gen[:, 0].tolist() == [6, 6]
+    assert gen[:, 1].tolist() == [0, 0]
 
 
 @pytest.mark.parametrize("pos", [63, 127, 2047, 4095, 8127, 8128, 300, 9000, 20031])

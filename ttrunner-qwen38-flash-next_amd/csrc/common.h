@@ -100,6 +100,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base, lon
 __device__ __forceinline__ float ld_dev(__amdgpu_buffer_rsrc_t r, int byte_off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, CPOL_DEVICE));
 }
+__device__ __forceinline__ float ld_dev_bf16(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, byte_off, 0, CPOL_DEVICE));
+}
+__device__ __forceinline__ void st_dev_u32x2(__amdgpu_buffer_rsrc_t r, int byte_off, unsigned lo, unsigned hi) {
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{lo, hi}, r, byte_off, 0, CPOL_DEVICE);
+}
 __device__ __forceinline__ float2 ld_dev2(__amdgpu_buffer_rsrc_t r, int byte_off) {
   return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, CPOL_DEVICE));
 }
@@ -117,6 +123,19 @@ __device__ __forceinline__ unsigned ld_flag(const unsigned* p) {
 }
 __device__ __forceinline__ void st_flag(unsigned* p, unsigned v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Raise a flag (or publish a 64-bit word) by an atomic exchange and wait for
+// its return: once it returns the value sits at the point of coherence, so a
+// poller's next load sees it (a plain write-through store gets there about
+// 300 ns later). The empty asm consumes the old value, which keeps the
+// returning form of the atomic.
+__device__ __forceinline__ void raise_flag(unsigned* p, unsigned v) {
+  const unsigned old = __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("" ::"v"(old));
+}
+__device__ __forceinline__ void raise_word(unsigned long long* p, unsigned long long v) {
+  const unsigned long long old = __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("" ::"v"(old));
 }
 // every outstanding memory operation of this wave complete (stores acknowledged)
 __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }

@@ -10,16 +10,17 @@
 //   norm   : out = rms_norm(o) * w * sigmoid(z)
 // with v-head h reading q/k head h % Hk (the tiled layout of the checkpoint).
 //
-// Work split: 8 workgroups of 256 threads per (sequence, value head), each
-// holding 16 of the head's 128 state columns (8 KB of float32): the delta rule
-// is independent per column, so a workgroup updates its columns alone and a
-// compute unit moves 16 KB instead of the head's 128 KB. Each workgroup
-// recomputes the conv of the head's q/k channels (L2-resident) and convolves
-// its own 16 v channels. The gated RMS norm needs the head's sum of squares of
-// o: each workgroup publishes its 16 columns' share in one 64-bit write-through
-// store that carries the launch's generation number, writes its state columns
-// back, then polls the head's 8 shares (one cache line) and normalises its
-// columns. All loads are issued at the start, the conv's first.
+// Work split: 4 workgroups of 256 threads per (sequence, value head), each
+// holding 32 of the head's 128 state columns (16 KB of float32, whole 128-byte
+// lines of every row): the delta rule is independent per column, so a
+// workgroup updates its columns alone and a compute unit moves 32 KB instead
+// of the head's 128 KB. Each workgroup recomputes the conv of the head's q/k
+// channels (L2-resident) and convolves its own 32 v channels. The gated RMS
+// norm needs the head's sum of squares of o: each workgroup publishes its 32
+// columns' share in one 64-bit atomic exchange that carries the launch's
+// generation number, writes its state columns back, then polls the head's 4
+// shares (one cache line) and normalises its columns. All loads are issued at
+// the start, the conv's first.
 //
 // The conv window is a ring of K slots per channel: the input of the token at
 // position p lives in slot p % K, so the K-1 history slots read by this step are
@@ -33,7 +34,8 @@ namespace {
 constexpr int DN_D = 128;      // head dim (k and v)
 constexpr int DN_TILE = 16;    // state columns per workgroup
 constexpr int DN_NT = 256;     // threads per workgroup
-constexpr int DN_SLICES = DN_D / DN_TILE;   // decode workgroups per head
+constexpr int DN_DCOLS = 32;   // state columns per decode workgroup (whole 128-byte lines)
+constexpr int DN_SLICES = DN_D / DN_DCOLS;  // decode workgroups per head
 // per (sequence, head) a 128-byte line of the decode workspace: the generation
 // word, a give-up counter, then the slices' (generation, sum of squares) words
 constexpr int DN_SYNC_WORDS = 32;
@@ -108,8 +110,8 @@ __device__ __forceinline__ float conv_channel(const DnDecodeArgs<T>& A, int b, i
 }
 
 // grid: batch * hv * DN_SLICES workgroups of DN_NT threads; workgroup (b, h, s)
-// owns columns 16s..16s+15. Thread t holds rows t/4 and t/4 + 64 of columns
-// 16s + 4(t%4)..+3.
+// owns columns 32s..32s+31. Thread t holds rows t/8 + 32k (k = 0..3) of
+// columns 32s + 4(t%8)..+3: a wave reads 8 whole rows' lines per load.
 template <typename T>
 __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
   const int s = blockIdx.x % DN_SLICES;
@@ -117,24 +119,25 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
   const int b = blockIdx.x / (DN_SLICES * A.hv);
   const int hk = h % A.hk;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int c4 = tid & 3, r = tid >> 2;
-  const int col0 = s * DN_TILE;
+  const int c8 = tid & 7, r = tid >> 3;
+  const int col0 = s * DN_DCOLS;
   constexpr int NW = DN_NT / 64;
 
-  __shared__ float s_q[DN_D], s_k[DN_D], s_v[DN_TILE];
-  __shared__ float s_red[NW][2 * DN_TILE];
-  __shared__ float s_delta[DN_TILE];
+  __shared__ float s_q[DN_D], s_k[DN_D], s_v[DN_DCOLS];
+  __shared__ float s_red[NW][2 * DN_DCOLS];
+  __shared__ __attribute__((aligned(16))) float s_delta[DN_DCOLS];
   __shared__ float s_w3[2][3];
   __shared__ float s_scal[2];
 
   // ---- loads, all issued before any is used: the conv inputs of q/k channel
-  // t (and of v column t < 16), the position, the gates, z, the norm weight,
+  // t (and of v column t < 32), the position, the gates, z, the norm weight,
   // the state columns and last the generation word (needed last)
   unsigned* line = A.sync + (long)(b * A.hv + h) * DN_SYNC_WORDS;
   unsigned long long* shares = reinterpret_cast<unsigned long long*>(line) + DN_SHARE0;
   const int key_dim = A.hk * DN_D;
   const int ch_qk = tid < DN_D ? hk * DN_D + tid : key_dim + hk * DN_D + (tid - DN_D);
-  const int ch_v = 2 * key_dim + h * DN_D + col0 + (tid & (DN_TILE - 1));
+  const int jt = tid & (DN_DCOLS - 1);
+  const int ch_v = 2 * key_dim + h * DN_D + col0 + jt;
   const bool k4 = A.K == 4;
   ConvIn<T> cin_qk, cin_v;
   if (k4) {
@@ -144,19 +147,20 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
   const int pos = A.positions[b];
   const float gate_b = Act<T>::load(A.b, (long)b * A.hv + h), gate_a = Act<T>::load(A.a, (long)b * A.hv + h);
   const float a_neg = A.a_neg[h], dtb = A.dt_bias[h];
-  const int jt = tid & (DN_TILE - 1);
   const float zv = Act<T>::load(A.z, (long)b * A.hv * DN_D + h * DN_D + col0 + jt);
   const float nw = A.norm_w[col0 + jt];
-  float4* S = reinterpret_cast<float4*>(A.state + ((long)(b * A.hv + h) * DN_D) * DN_D) + col0 / 4 + c4;
-  float4 s0 = S[r * (DN_D / 4)], s1 = S[(r + 64) * (DN_D / 4)];
+  float4* S = reinterpret_cast<float4*>(A.state + ((long)(b * A.hv + h) * DN_D) * DN_D) + col0 / 4 + c8;
+  float4 st4[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) st4[k] = S[(r + 32 * k) * (DN_D / 4)];
   const unsigned gen = ld_flag(line);
 
   // ---- conv: q/k channel t (one writer of each q/k channel's ring slot: the
-  // first slice of the head with h == hk), v column t < 16; then the gates
+  // first slice of the head with h == hk), v column t < 32; then the gates
   const bool qk_writer = h == hk && s == 0;
   const float y_qk = k4 ? conv_finish4(A, cin_qk, b, ch_qk, pos, qk_writer) : conv_channel(A, b, ch_qk, pos, qk_writer);
   (tid < DN_D ? s_q[tid] : s_k[tid - DN_D]) = y_qk;
-  if (tid < DN_TILE) s_v[tid] = k4 ? conv_finish4(A, cin_v, b, ch_v, pos, true) : conv_channel(A, b, ch_v, pos, true);
+  if (tid < DN_DCOLS) s_v[tid] = k4 ? conv_finish4(A, cin_v, b, ch_v, pos, true) : conv_channel(A, b, ch_v, pos, true);
   if (tid == 0) {
     s_scal[0] = Act<T>::round(sigmoid_f(gate_b));
     s_scal[1] = expf(a_neg * softplus_f(gate_a + dtb));
@@ -177,71 +181,69 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
 
   // ---- decay, then per column pred = S^T k^ and qd = S^T q^ over the rows
   const float decay = s_scal[1];
-  const float kr0 = mul_rn(s_k[r], rk), kr1 = mul_rn(s_k[r + 64], rk);
-  const float qr0 = div_rn(mul_rn(s_q[r], rq), sqrt_d), qr1 = div_rn(mul_rn(s_q[r + 64], rq), sqrt_d);
-  float st0[4] = {s0.x * decay, s0.y * decay, s0.z * decay, s0.w * decay};
-  float st1[4] = {s1.x * decay, s1.y * decay, s1.z * decay, s1.w * decay};
-  float pk[4], pq[4];
+  float st[4][4], kr[4], pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    pk[c] = fmaf(st1[c], kr1, st0[c] * kr0);
-    pq[c] = fmaf(st1[c], qr1, st0[c] * qr0);
+  for (int k = 0; k < 4; ++k) {
+    const int row = r + 32 * k;
+    kr[k] = mul_rn(s_k[row], rk);
+    const float qr = div_rn(mul_rn(s_q[row], rq), sqrt_d);
+    st[k][0] = st4[k].x * decay; st[k][1] = st4[k].y * decay;
+    st[k][2] = st4[k].z * decay; st[k][3] = st4[k].w * decay;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      pk[c] = fmaf(st[k][c], kr[k], pk[c]);
+      pq[c] = fmaf(st[k][c], qr, pq[c]);
+    }
   }
-  // lanes of one c4 within a 16-lane row (rotations by 4 and 8), then across rows
+  // the 8 lanes of one c8 in a wave: lane ^ 8 within a 16-lane row (rotation
+  // by 8), then across the rows
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    pk[c] += dpp_f<0x124>(pk[c]);
     pk[c] += dpp_f<0x128>(pk[c]);
     pk[c] = xor32_sum(xor16_sum(pk[c]));
-    pq[c] += dpp_f<0x124>(pq[c]);
     pq[c] += dpp_f<0x128>(pq[c]);
     pq[c] = xor32_sum(xor16_sum(pq[c]));
   }
-  if (lane < 4) {
+  if (lane < 8) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       s_red[wid][4 * lane + c] = pk[c];
-      s_red[wid][DN_TILE + 4 * lane + c] = pq[c];
+      s_red[wid][DN_DCOLS + 4 * lane + c] = pq[c];
     }
   }
   __syncthreads();
 
-  // ---- delta and o of the 16 columns (wave 0, lanes 0-15); their share of the
+  // ---- delta and o of the 32 columns (wave 0, lanes 0-31); their share of the
   // head's sum of squares leaves at once
   float o = 0.f;
-  if (tid < DN_TILE) {
+  if (tid < DN_DCOLS) {
     float pred = 0.f, qd = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) { pred += s_red[w][tid]; qd += s_red[w][DN_TILE + tid]; }
+    for (int w = 0; w < NW; ++w) { pred += s_red[w][tid]; qd += s_red[w][DN_DCOLS + tid]; }
     const float delta = (s_v[tid] - pred) * s_scal[0];
     s_delta[tid] = delta;
     o = Act<T>::round(fmaf(qk, delta, qd));
   }
   if (wid == 0) {
-    const float ss = row16_sum(tid < DN_TILE ? o * o : 0.f);
+    const float ss = xor16_sum(row16_sum(tid < DN_DCOLS ? o * o : 0.f));
     if (lane == 0) {
       const unsigned long long word = ((unsigned long long)(gen + 1) << 32) | __float_as_uint(ss);
-      __hip_atomic_store(shares + s, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      raise_word(shares + s, word);
     }
   }
   __syncthreads();
 
   // ---- rank-1 update and write-back of the columns
   {
-    float4 dl = *reinterpret_cast<const float4*>(s_delta + 4 * c4);
-    const float d4[4] = {dl.x, dl.y, dl.z, dl.w};
-    float n0[4], n1[4];
+    const float4 dl = *reinterpret_cast<const float4*>(s_delta + 4 * c8);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      n0[c] = fmaf(kr0, d4[c], st0[c]);
-      n1[c] = fmaf(kr1, d4[c], st1[c]);
-    }
-    S[r * (DN_D / 4)] = make_float4(n0[0], n0[1], n0[2], n0[3]);
-    S[(r + 64) * (DN_D / 4)] = make_float4(n1[0], n1[1], n1[2], n1[3]);
+    for (int k = 0; k < 4; ++k)
+      S[(r + 32 * k) * (DN_D / 4)] = make_float4(fmaf(kr[k], dl.x, st[k][0]), fmaf(kr[k], dl.y, st[k][1]),
+                                                 fmaf(kr[k], dl.z, st[k][2]), fmaf(kr[k], dl.w, st[k][3]));
   }
 
-  // ---- the head's sum of squares from its 8 shares (one line, polled by wave
-  // 0), then the gated RMS norm of the 16 columns
+  // ---- the head's sum of squares from its shares (one line, polled by wave
+  // 0), then the gated RMS norm of the 32 columns
   if (wid == 0) {
     float ss_all = 0.f;
     bool done = false;
@@ -260,7 +262,7 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
     }
     if (!done && lane == 0) __hip_atomic_fetch_add(line + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (s == 0 && lane == 0) st_flag(line, gen + 1);
-    if (tid < DN_TILE) {
+    if (tid < DN_DCOLS) {
       const float rn = rsqrt_rn(ss_all / (float)DN_D + A.eps);
       Act<T>::store(A.out, (long)b * A.hv * DN_D + h * DN_D + col0 + tid, (nw * (o * rn)) * sigmoid_f(zv));
     }

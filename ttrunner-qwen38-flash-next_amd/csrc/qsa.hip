@@ -1083,8 +1083,8 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
 //   4. scores the item on bf16 MFMA (waves 0-1), shares the scores through LDS,
 //      and every wave forms the softmax weights and its 64 output channels;
 //      the current token's key/value come from LDS, not the pages;
-//   5. writes the item's (max, sum, unnormalised output) partial through to
-//      the device's point of coherence. The workgroup of item 0 also appends
+//   5. writes the item's partial through to the device's point of coherence:
+//      (max, sum) in float32, the output divided by the sum in bf16. The workgroup of item 0 also appends
 //      the token's key/value to its page slot, and for kv head 0 writes the
 //      per-sequence outputs (raw indexer key, pooled key);
 //   6. raises its flag, and, when it holds one of the 64 (query head, 32
@@ -1117,7 +1117,7 @@ __device__ __forceinline__ int norm_row_offset(int r) {
 template <typename T>
 struct DecArgs {
   PrepArgs<T> P;
-  float* part_o; float* part_ml;        // per group: [G][8][256] outputs, [G][8] (max, sum)
+  uint16_t* part_o; float* part_ml;     // per group: [G][8][256] bf16 outputs / sum, [G][8] (max, sum)
   unsigned* gen;                        // per group: generation word, then a give-up counter
   unsigned* flags;                      // per group: G flags
   T* out;
@@ -1201,8 +1201,9 @@ __device__ __forceinline__ void norm_rinv(DecShared& sh, int r0, int r1, float e
 }
 
 // Output slice sl = (query head h = sl / 8, channels 32 (sl % 8) ..+31) of
-// group (b, g): out[d] = round(sum_i w_i o_i[d] / sum_i w_i l_i) *
-// round(sigmoid(gate[d])), w_i = exp(m_i - max m), over the n items. Thread
+// group (b, g): out[d] = round(sum_i w_i o_i[d] / sum_i w_i) *
+// round(sigmoid(gate[d])), w_i = exp(m_i - max m) l_i, over the n items (o_i
+// is the item's output divided by its sum l_i). Thread
 // (ch = tid % 32, il = tid / 32) takes items il, il + 8, ...; every load of a
 // 128-item chunk is issued before any is used, indices clamped to the last
 // item and weighted by zero past it.
@@ -1219,7 +1220,7 @@ __device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, 
   const float gate = Act<T>::load(D.P.qg, ((long)b * hq + qh) * (2 * QSA_D) + QSA_D + d);
   float ov[CHUNK];
 #pragma unroll
-  for (int k = 0; k < CHUNK; ++k) ov[k] = ld_dev(ro, ((min(il + 8 * k, n - 1) * GQA + h) * QSA_D + d) * 4);
+  for (int k = 0; k < CHUNK; ++k) ov[k] = ld_dev_bf16(ro, ((min(il + 8 * k, n - 1) * GQA + h) * QSA_D + d) * 2);
   float2 ml[DEC_MAX_ITEMS / DEC_NT];
 #pragma unroll
   for (int k = 0; k < DEC_MAX_ITEMS / DEC_NT; ++k) ml[k] = ld_dev2(rml, ((min(tid + DEC_NT * k, n - 1) * GQA + h) * 2) * 4);
@@ -1236,9 +1237,9 @@ __device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, 
 #pragma unroll
   for (int k = 0; k < DEC_MAX_ITEMS / DEC_NT; ++k) {
     const int i = tid + DEC_NT * k;
-    const float w = i < n ? __expf(ml[k].x - M) : 0.f;
+    const float w = i < n ? __expf(ml[k].x - M) * ml[k].y : 0.f;
     if (i < n_pad) s_w[i] = w;
-    L += ml[k].y * w;
+    L += w;
   }
   L = wave_sum(L);
   if (lane == 0) red[260 + wv] = L;
@@ -1251,7 +1252,7 @@ __device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, 
     if (i0 + 8 * CHUNK >= n) break;
 #pragma unroll
     for (int k = 0; k < CHUNK; ++k)
-      ov[k] = ld_dev(ro, ((min(i0 + 8 * CHUNK + il + 8 * k, n - 1) * GQA + h) * QSA_D + d) * 4);
+      ov[k] = ld_dev_bf16(ro, ((min(i0 + 8 * CHUNK + il + 8 * k, n - 1) * GQA + h) * QSA_D + d) * 2);
   }
   red[il * 32 + ch] = acc;
   __syncthreads();
@@ -1535,13 +1536,17 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   // O^T[d][head] = V^T[d][tok] P^T[tok][head] for this wave's 64 channels,
   // written through to the point of coherence (read by other workgroups)
   const long gbase = (long)bg * D.splits;
-  const __amdgpu_buffer_rsrc_t ro = dev_rsrc(D.part_o + gbase * GQA * QSA_D, (long)D.splits * GQA * QSA_D * 4);
+  const __amdgpu_buffer_rsrc_t ro = dev_rsrc(D.part_o + gbase * GQA * QSA_D, (long)D.splits * GQA * QSA_D * 2);
   const __amdgpu_buffer_rsrc_t rml = dev_rsrc(D.part_ml + gbase * GQA * 2, (long)D.splits * GQA * 2 * 4);
+  const float linv = 1.0f / lsum;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const f32x4_t o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[i], pf, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    if (col < GQA)
-      st_dev4(ro, ((item * GQA + hcol) * QSA_D + 16 * (4 * wv + i) + 4 * quad) * 4, make_float4(o[0], o[1], o[2], o[3]));
+    if (col < GQA) {
+      const unsigned lo = f32_to_bf16(o[0] * linv) | ((unsigned)f32_to_bf16(o[1] * linv) << 16);
+      const unsigned hi = f32_to_bf16(o[2] * linv) | ((unsigned)f32_to_bf16(o[3] * linv) << 16);
+      st_dev_u32x2(ro, ((item * GQA + hcol) * QSA_D + 16 * (4 * wv + i) + 4 * quad) * 2, lo, hi);
+    }
   }
   if (wv == 0 && quad == 0 && col < GQA) st_dev2(rml, ((item * GQA + col) * 2) * 4, make_float2(mx, lsum));
 
@@ -1582,7 +1587,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   wait_all_memory();
   __syncthreads();
   unsigned* flags = D.flags + gbase;
-  if (tid == 0) st_flag(flags + item, gen + 1);
+  if (tid == 0) raise_flag(flags + item, gen + 1);
   if (item >= DEC_SLICES) return;
   if (wv == 0 && !wait_flags<DEC_MAX_ITEMS>(flags, n_att, gen + 1) && lane == 0)
     __hip_atomic_fetch_add(D.gen + (long)bg * DEC_GEN_STRIDE + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1958,11 +1963,14 @@ size_t dec_flag_bytes(const qm_qsa_geom* g, int splits) {
 size_t dec_ml_bytes(const qm_qsa_geom* g, int splits) {
   return qm_align256((size_t)g->batch * g->n_kv_heads * splits * GQA * 2 * sizeof(float));
 }
+size_t dec_o_bytes(const qm_qsa_geom* g, int splits) {
+  return qm_align256((size_t)g->batch * g->n_kv_heads * splits * GQA * QSA_D * sizeof(uint16_t));
+}
 }  // namespace
 
 extern "C" size_t qm_qsa_decode_workspace(const qm_qsa_geom* g, int splits) {
   if (!g || splits <= 0) return 0;
-  return dec_gen_bytes(g) + dec_flag_bytes(g, splits) + dec_ml_bytes(g, splits) + part_o_bytes(g, g->batch, splits);
+  return dec_gen_bytes(g) + dec_flag_bytes(g, splits) + dec_ml_bytes(g, splits) + dec_o_bytes(g, splits);
 }
 
 extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k_new, const void* v_new, const void* iq,
@@ -1990,7 +1998,7 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
   unsigned* gen = reinterpret_cast<unsigned*>(ws);
   unsigned* flags = reinterpret_cast<unsigned*>(ws + dec_gen_bytes(g));
   float* part_ml = reinterpret_cast<float*>(ws + dec_gen_bytes(g) + dec_flag_bytes(g, splits));
-  float* part_o = reinterpret_cast<float*>(ws + dec_gen_bytes(g) + dec_flag_bytes(g, splits) + dec_ml_bytes(g, splits));
+  uint16_t* part_o = reinterpret_cast<uint16_t*>(ws + dec_gen_bytes(g) + dec_flag_bytes(g, splits) + dec_ml_bytes(g, splits));
   const dim3 grid(splits, g->n_kv_heads, g->batch);
   auto run = [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;

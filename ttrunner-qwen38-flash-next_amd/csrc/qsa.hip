@@ -1090,6 +1090,14 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
 //   6. raises its flag, and, when it holds one of the 64 (query head, 32
 //      channels) slices of the group's output, waits for the flags of every
 //      item of the group, merges that slice's partials and applies the gate.
+// When the plan has fewer than 64 items (short contexts), the grid is widened
+// to 64 workgroups per group so that every slice has its own merger (a
+// workgroup merging several slices pays a round trip per slice): those past
+// the position's items only merge, and raise their flag as soon as they have
+// read the generation word; workgroup 0 then advances the word only after it
+// has seen the flags of all 64, so that no workgroup reads the advanced word in
+// the launch that advances it. Otherwise the attending workgroups merge the
+// slices among themselves and only their flags are waited for.
 // Every workgroup of a group is resident at once: workgroups are dispatched in
 // order, so at most one group is ever partly dispatched, and a group (at most
 // DEC_MAX_ITEMS small workgroups) fits the device.
@@ -1265,15 +1273,40 @@ __device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, 
   __syncthreads();
 }
 
-template <typename T>
+// flags of a group: one per workgroup that attends an item or holds a slice
+__host__ __device__ inline int dec_flag_stride(int splits) { return splits > DEC_SLICES ? splits : DEC_SLICES; }
+
+// Workgroup `item` < DEC_SLICES of group (b, g): wait (wave 0 polling) until
+// the flags of the n_att attending workgroups (workgroup 0 of a widened grid:
+// of all 64 slice holders) have reached gen + 1, advance the generation word
+// (workgroup 0), then merge output slices item, item + step, ...
+template <bool WIDE, typename T>
+__device__ __forceinline__ void decode_merge(const DecArgs<T>& D, DecShared& sh, int b, int g, int item, int n_att,
+                                             unsigned gen) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int bg = b * D.P.hkv + g;
+  const long gbase = (long)bg * D.splits;
+  const __amdgpu_buffer_rsrc_t ro = dev_rsrc(D.part_o + gbase * GQA * QSA_D, (long)D.splits * GQA * QSA_D * 2);
+  const __amdgpu_buffer_rsrc_t rml = dev_rsrc(D.part_ml + gbase * GQA * 2, (long)D.splits * GQA * 2 * 4);
+  const int n_wait = WIDE && item == 0 ? DEC_SLICES : n_att;
+  if (wv == 0 && !wait_flags<DEC_MAX_ITEMS>(D.flags + (long)bg * dec_flag_stride(D.splits), n_wait, gen + 1) &&
+      lane == 0)
+    __hip_atomic_fetch_add(D.gen + (long)bg * DEC_GEN_STRIDE + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (item == 0 && tid == 0) st_flag(D.gen + (long)bg * DEC_GEN_STRIDE, gen + 1);
+  const int step = WIDE ? DEC_SLICES : n_att;
+  for (int sl = item; sl < DEC_SLICES; sl += step) decode_combine_slice(D, sh, b, g, sl, n_att, ro, rml);
+}
+
+template <typename T, bool WIDE>
 __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
+  __shared__ DecShared sh;
   const PrepArgs<T>& A = D.P;
   const int item = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int col = lane & 15, quad = lane >> 4;
   const int e128 = tid & 127, hh = tid >> 7;
   const int bg = b * A.hkv + g;
-  __shared__ DecShared sh;
 
   // ---- 0. the loads
   const unsigned gen = ld_flag(D.gen + (long)bg * DEC_GEN_STRIDE);
@@ -1310,7 +1343,9 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   const float cs = A.cos[(long)p * rope + ec], sn = A.sin[(long)p * rope + ec];
   const long t0r = (long)max(j_new, 0) * ratio * rope + ec;
   const float cs0 = A.cos[t0r], sn0 = A.sin[t0r];
-  // the whole page-table row and the first 128 block keys, whatever the position
+  // the whole page-table row and, when this launch's positions may need
+  // scoring (more items than the top-k blocks hold), the first 128 block keys,
+  // whatever the position
   int pg[DEC_MAX_PAGES / DEC_NT];
 #pragma unroll
   for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k)
@@ -1318,7 +1353,8 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
   const bool scoring = n_elig > topk;
   float4 kp[SCORE_PRE][4];
-  prefetch_block_keys<DEC_NT>(kp, bk, A.max_blocks, -1, true);
+  const bool may_score = D.splits > topk * (ratio >= 32 ? ratio / 32 : 1);
+  prefetch_block_keys<DEC_NT>(kp, bk, A.max_blocks, -1, may_score);
   // raw keys of the block this token completes: thread (e128, hh) takes the
   // 16-row chunks hh and hh + 2; the token's own row is ik (not yet stored)
   // (loads unconditional, rows clamped, so that none waits alone)
@@ -1357,10 +1393,19 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   sh.vnb[tid] = f32_to_bf16(vx);
 #pragma unroll
   for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k) sh.pages[tid + DEC_NT * k] = pg[k];
-  // a workgroup past the position's items has nothing to do: the waits of
-  // this launch cover only the first n_att flags
+  // a workgroup past the position's items only merges: the waits of this
+  // launch cover only the first n_att flags
   const int n_att = min(n_items, D.splits);
-  if (item >= n_att) return;
+  if (item >= n_att) {
+    if constexpr (WIDE) {
+      // a slice holder past the items: flag raised once the word is read
+      if (item < DEC_SLICES) {
+        if (tid == 0) raise_flag(D.flags + (long)bg * dec_flag_stride(D.splits) + item, gen + 1);
+        decode_merge<WIDE>(D, sh, b, g, item, n_att, gen);
+      }
+    }
+    return;
+  }
   __syncthreads();
   const bool blk_item = item < ic.n_blk_items;
   float pmean = 0.f;
@@ -1586,14 +1631,8 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   // of the group, then merge their slices
   wait_all_memory();
   __syncthreads();
-  unsigned* flags = D.flags + gbase;
-  if (tid == 0) raise_flag(flags + item, gen + 1);
-  if (item >= DEC_SLICES) return;
-  if (wv == 0 && !wait_flags<DEC_MAX_ITEMS>(flags, n_att, gen + 1) && lane == 0)
-    __hip_atomic_fetch_add(D.gen + (long)bg * DEC_GEN_STRIDE + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (item == 0 && tid == 0) st_flag(D.gen + (long)bg * DEC_GEN_STRIDE, gen + 1);
-  for (int sl = item; sl < DEC_SLICES; sl += n_att) decode_combine_slice(D, sh, b, g, sl, n_att, ro, rml);
+  if (tid == 0) raise_flag(D.flags + (long)bg * dec_flag_stride(D.splits) + item, gen + 1);
+  if (item < DEC_SLICES) decode_merge<WIDE>(D, sh, b, g, item, n_att, gen);
 }
 
 int check_geom(const qm_qsa_geom* g, const char* who) {
@@ -1958,7 +1997,7 @@ size_t dec_gen_bytes(const qm_qsa_geom* g) {
   return qm_align256((size_t)g->batch * g->n_kv_heads * DEC_GEN_STRIDE * sizeof(unsigned));
 }
 size_t dec_flag_bytes(const qm_qsa_geom* g, int splits) {
-  return qm_align256((size_t)g->batch * g->n_kv_heads * splits * sizeof(unsigned));
+  return qm_align256((size_t)g->batch * g->n_kv_heads * dec_flag_stride(splits) * sizeof(unsigned));
 }
 size_t dec_ml_bytes(const qm_qsa_geom* g, int splits) {
   return qm_align256((size_t)g->batch * g->n_kv_heads * splits * GQA * 2 * sizeof(float));
@@ -1999,7 +2038,8 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
   unsigned* flags = reinterpret_cast<unsigned*>(ws + dec_gen_bytes(g));
   float* part_ml = reinterpret_cast<float*>(ws + dec_gen_bytes(g) + dec_flag_bytes(g, splits));
   uint16_t* part_o = reinterpret_cast<uint16_t*>(ws + dec_gen_bytes(g) + dec_flag_bytes(g, splits) + dec_ml_bytes(g, splits));
-  const dim3 grid(splits, g->n_kv_heads, g->batch);
+  const bool wide = splits < DEC_SLICES;
+  const dim3 grid(wide ? DEC_SLICES : splits, g->n_kv_heads, g->batch);
   auto run = [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
     DecArgs<T> D;
@@ -2008,7 +2048,8 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
     D.part_o = part_o; D.part_ml = part_ml; D.gen = gen; D.flags = flags; D.out = static_cast<T*>(out);
     D.ids = ids; D.n_sel = n_sel; D.items = static_cast<int2*>(items); D.iq_out = iq_out;
     D.splits = splits; D.topk = g->budget / g->ratio; D.max_items = item_stride(g);
-    hipLaunchKernelGGL(qsa_decode_kernel<T>, grid, dim3(DEC_NT), 0, stream, D);
+    if (wide) hipLaunchKernelGGL((qsa_decode_kernel<T, true>), grid, dim3(DEC_NT), 0, stream, D);
+    else hipLaunchKernelGGL((qsa_decode_kernel<T, false>), grid, dim3(DEC_NT), 0, stream, D);
     QM_CHECK_LAUNCH();
     return QM_OK;
   };

@@ -12,5 +12,7 @@ from .cache import MixHybridCache, MixLayerCache
 from .config import MixConfig
 from .decoder import MixDecoder
 from .model import Qwen4MixModel
+from .pages import PagePool, PoolExhausted
 
-__all__ = ["native", "MixHybridCache", "MixLayerCache", "MixConfig", "MixDecoder", "Qwen4MixModel"]
+__all__ = ["native", "MixHybridCache", "MixLayerCache", "MixConfig", "MixDecoder", "Qwen4MixModel", "PagePool",
+           "PoolExhausted"]

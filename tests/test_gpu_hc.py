@@ -47,7 +47,7 @@ def _pair(qm, hidden, layer, dtype, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("hidden,rows", [(2048, 1), (2048, 3), (2048, 4), (2048, 6), (2560, 1), (2560, 3)])
+@pytest.mark.parametrize("hidden,rows", [(2048, 1), (2048, 2), (2048, 3), (2048, 4), (2048, 6), (2560, 1), (2560, 3)])
 def test_gated_residual_matches_oracle(gpu, dtype, hidden, rows):
     qm = gpu
     for layer in (5, None):

@@ -253,7 +253,9 @@ __device__ __forceinline__ int2 make_item(int phys_row, int lo, int hi) { return
 // exchanges (all 8 lanes end with the same sum: float addition commutes). Each
 // lane keeps the matching chunks of the 4 query heads in registers.
 constexpr int SCORE_LANES = 8;                  // NT / 8 blocks per pass of NT threads
-constexpr int SCORE_PRE = 4;                    // passes of keys held in registers ahead of use
+// passes of keys held in registers ahead of use: four at 256 threads; two at
+// 1024, where a thread has 128 VGPRs and four (64 VGPRs) would spill
+template <int NT> constexpr int score_pre() { return NT >= 1024 ? 2 : 4; }
 
 // (an invalid j loads row 0, always allocated, and zeroes the result: the
 // loads stay unconditional so later waits on them stay exact)
@@ -295,12 +297,12 @@ __device__ __forceinline__ float oct_block_score(const float4 (&q)[4][4], const 
 
 // keys[j] = sel_key(score_j, j) for every eligible block j (and scores_out[j]
 // when given), then zeros up to a multiple of 32. kp[u] comes in holding pass
-// u's keys (load_block_part); later passes load SCORE_PRE passes ahead of use.
+// u's keys (load_block_part); later passes load PRE passes ahead of use.
 // Block new_j's key is new_key (LDS), not the cache's. s_iq: 4 rows of 128.
-template <int NT>
+template <int NT, int PRE>
 __device__ void score_blocks(const float* s_iq, const float* new_key, const float* bk, int n_elig, int new_j,
                              int idx_heads, unsigned long long* keys, float* scores_out,
-                             float4 (&kp)[SCORE_PRE][4]) {
+                             float4 (&kp)[PRE][4]) {
   constexpr int SCORE_PASS = NT / SCORE_LANES;
   const int tid = threadIdx.x, jl = tid >> 3, part = tid & 7;
   float4 q[4][4];
@@ -309,9 +311,9 @@ __device__ void score_blocks(const float* s_iq, const float* new_key, const floa
 #pragma unroll
     for (int i = 0; i < 4; ++i) q[h][i] = reinterpret_cast<const float4*>(s_iq + h * IDX_D)[8 * i + part];
   const int n_pass = (n_elig + SCORE_PASS - 1) / SCORE_PASS;
-  for (int ps0 = 0; ps0 < n_pass; ps0 += SCORE_PRE) {
+  for (int ps0 = 0; ps0 < n_pass; ps0 += PRE) {
 #pragma unroll
-    for (int u = 0; u < SCORE_PRE; ++u) {
+    for (int u = 0; u < PRE; ++u) {
       const int ps = ps0 + u;
       if (ps < n_pass) {
         const int j = ps * SCORE_PASS + jl;
@@ -325,8 +327,8 @@ __device__ void score_blocks(const float* s_iq, const float* new_key, const floa
           keys[j] = sel_key(sc, j);
           if (scores_out) scores_out[j] = sc;
         }
-        const int jn = j + SCORE_PRE * SCORE_PASS;
-        if (ps + SCORE_PRE < n_pass) load_block_part(kp[u], bk, jn, jn < n_elig && jn != new_j);
+        const int jn = j + PRE * SCORE_PASS;
+        if (ps + PRE < n_pass) load_block_part(kp[u], bk, jn, jn < n_elig && jn != new_j);
       }
     }
   }
@@ -334,14 +336,14 @@ __device__ void score_blocks(const float* s_iq, const float* new_key, const floa
   for (int j = n_elig + tid; j < npad; j += NT) keys[j] = 0ull;
 }
 
-// prefetch of the first SCORE_PRE passes (issued before the scores are needed)
-template <int NT>
-__device__ __forceinline__ void prefetch_block_keys(float4 (&kp)[SCORE_PRE][4], const float* bk, int n_elig,
+// prefetch of the first PRE passes (issued before the scores are needed)
+template <int NT, int PRE>
+__device__ __forceinline__ void prefetch_block_keys(float4 (&kp)[PRE][4], const float* bk, int n_elig,
                                                     int new_j, bool on) {
   constexpr int SCORE_PASS = NT / SCORE_LANES;
   const int jl = threadIdx.x >> 3;
 #pragma unroll
-  for (int u = 0; u < SCORE_PRE; ++u) {
+  for (int u = 0; u < PRE; ++u) {
     const int j = u * SCORE_PASS + jl;
     load_block_part(kp[u], bk, j, on && j < n_elig && j != new_j);
   }
@@ -472,7 +474,7 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
   if (n_elig > A.topk || A.scores_out) {
     // the first two passes of block keys are in flight across the barrier
     const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
-    float4 kp[SCORE_PRE][4];
+    float4 kp[score_pre<NT>()][4];
     prefetch_block_keys<NT>(kp, bk, n_elig, new_j, true);
     __syncthreads();    // S.q and S.newkey visible
     score_blocks<NT>(S.q, S.newkey, bk, n_elig, new_j, A.idx_heads, S.key,
@@ -1352,7 +1354,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
     pg[k] = A.page_table[(long)b * A.max_pages + min(tid + DEC_NT * k, A.max_pages - 1)];
   const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
   const bool scoring = n_elig > topk;
-  float4 kp[SCORE_PRE][4];
+  float4 kp[score_pre<DEC_NT>()][4];
   const bool may_score = D.splits > topk * (ratio >= 32 ? ratio / 32 : 1);
   prefetch_block_keys<DEC_NT>(kp, bk, A.max_blocks, -1, may_score);
   // raw keys of the block this token completes: thread (e128, hh) takes the

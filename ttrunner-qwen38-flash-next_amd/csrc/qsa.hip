@@ -353,11 +353,104 @@ __device__ __forceinline__ void prefetch_block_keys(float4 (&kp)[PRE][4], const 
 // number of larger keys). `keys` is padded with zeros (below every real key) to
 // a multiple of 32. Up to 128 keys (n <= NT/2), by counting: two adjacent lanes
 // split the comparisons of one key and add their counts by DPP. Beyond, by
-// radix select: eight passes of an 8-bit histogram (LDS atomics, then a suffix
-// scan over the 256 digits) pin the topk-th largest key T exactly, the keys
-// >= T are gathered, and only they are ranked among themselves. `scr` holds
-// rank_scratch(MAXK) ints of LDS; topk <= MAXK.
+// a threshold from one histogram over the keys' own range: the upper 32 bits
+// (the score) of every key go into 256 equal buckets between their minimum and
+// maximum (integer arithmetic, so the bucket is monotone in the key), a suffix
+// scan finds the bucket that holds the topk-th largest key, and the keys in it
+// and above (typically topk plus a few) are gathered and ranked among
+// themselves by counting (1024-thread workgroups; the 256-thread decode
+// kernels keep their code small and go straight to radix select). When more
+// than RANK_CAND keys share that bucket
+// (many equal or clustered scores), radix select instead: eight passes of an
+// 8-bit histogram (LDS atomics, then a suffix scan over the 256 digits) pin the
+// topk-th largest key T exactly, the keys >= T are gathered, and only they are
+// ranked among themselves. `scr` holds rank_scratch(MAXK) ints of LDS;
+// topk <= MAXK.
 constexpr int rank_scratch(int maxk) { return 256 + 40 + maxk; }
+constexpr int RANK_CAND = 128;          // candidates the bucket threshold may leave
+
+// The bucket threshold (above). Returns false, having written nothing to sel,
+// when more than RANK_CAND keys are at or above the threshold bucket. The
+// bucket of a key is ((score bits - min) * floor(2^40 / width)) >> 32, width =
+// max - min + 1: monotone in the key and below 256.
+template <int NT>
+__device__ bool bucket_topk(const unsigned long long* keys, int n, int topk, int* sel, int* hist, int* wtot,
+                            int* state, int* cand) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  constexpr int NW = NT / 64;
+  unsigned lo = 0xffffffffu, hi = 0u;
+  for (int j = tid; j < n; j += NT) {
+    const unsigned v = static_cast<unsigned>(keys[j] >> 32);
+    lo = min(lo, v);
+    hi = max(hi, v);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    lo = min(lo, static_cast<unsigned>(__shfl_xor(static_cast<int>(lo), o, 64)));
+    hi = max(hi, static_cast<unsigned>(__shfl_xor(static_cast<int>(hi), o, 64)));
+  }
+  if (tid < 256) hist[tid] = 0;
+  if (tid < 8) state[tid] = 0;
+  if (lane == 0) {
+    wtot[wv] = static_cast<int>(lo);        // wtot[0..15] lows, [16..31] highs
+    wtot[16 + wv] = static_cast<int>(hi);
+  }
+  __syncthreads();
+  unsigned glo = 0xffffffffu, ghi = 0u;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    glo = min(glo, static_cast<unsigned>(wtot[w]));
+    ghi = max(ghi, static_cast<unsigned>(wtot[16 + w]));
+  }
+  const unsigned long long mul = (1ull << 40) / (static_cast<unsigned long long>(ghi - glo) + 1ull);
+  auto bucket = [&](unsigned long long k) {
+    return static_cast<int>((static_cast<unsigned long long>(static_cast<unsigned>(k >> 32) - glo) * mul) >> 32);
+  };
+  for (int j = tid; j < n; j += NT) atomicAdd(&hist[bucket(keys[j])], 1);
+  __syncthreads();                        // every thread has read the range: wtot is free
+  // suffix sums over the buckets: thread t takes bucket 255 - t
+  int h = 0, incl = 0;
+  if (tid < 256) {
+    h = hist[255 - tid];
+    incl = h;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int x = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += x;
+    }
+    if (lane == 63) wtot[wv] = incl;
+  }
+  __syncthreads();
+  if (tid < 256) {
+    for (int w = 0; w < wv; ++w) incl += wtot[w];
+    if (incl - h < topk && incl >= topk) {   // the bucket of the topk-th largest key
+      state[0] = 255 - tid;
+      state[1] = incl;                       // keys in it and above
+    }
+  }
+  __syncthreads();
+  const int bstar = state[0], n_cand = state[1];
+  if (n_cand > RANK_CAND) return false;
+  // gather, in any order (the ranks below do not depend on it); the keys go
+  // where the histogram was
+  unsigned long long* ckey = reinterpret_cast<unsigned long long*>(hist);
+  for (int j = tid; j < n; j += NT) {
+    const unsigned long long k = keys[j];
+    if (bucket(k) >= bstar) {
+      const int at = atomicAdd(&state[2], 1);
+      ckey[at] = k;
+      cand[at] = j;
+    }
+  }
+  __syncthreads();
+  for (int c = tid; c < n_cand; c += NT) {
+    const unsigned long long kc = ckey[c];
+    int rank = 0;
+    for (int i = 0; i < n_cand; ++i) rank += ckey[i] > kc ? 1 : 0;
+    if (rank < topk) sel[rank] = cand[c];
+  }
+  return true;
+}
 
 template <int NT, int MAXK>
 __device__ void rank_topk(const unsigned long long* keys, int n, int topk, int* sel, int* scr) {
@@ -384,6 +477,8 @@ __device__ void rank_topk(const unsigned long long* keys, int n, int topk, int* 
   int* state = scr + 256 + 32;            // prefix lo, prefix hi, remaining, count
   int* cand = scr + 256 + 40;             // [topk]
   const int lane = tid & 63, wv = tid >> 6;
+  if constexpr (NT >= 1024)
+    if (topk <= RANK_CAND && bucket_topk<NT>(keys, n, topk, sel, hist, wtot, state, cand)) return;
   unsigned long long prefix = 0ull;
   int r = topk;
   for (int shift = 56; shift >= 0; shift -= 8) {
@@ -449,7 +544,7 @@ struct SelShared {
   unsigned long long key[SEL_MAX_BLOCKS];
   int pages[SEL_MAX_BLOCKS];
   int sel[SEL_MAX_BLOCKS / 2];
-  int rscr[rank_scratch(SEL_MAX_BLOCKS / 2)];
+  alignas(16) int rscr[rank_scratch(SEL_MAX_BLOCKS / 2)];
 };
 
 // Selection for one query row at position p, by a whole SEL_NT-thread block.
@@ -1148,7 +1243,7 @@ struct DecShared {
   float chunk[DEC_MAX_RATIO / 16][IDX_D];
   int pages[DEC_MAX_PAGES];
   int sel[DEC_MAX_TOPK];
-  int rscr[rank_scratch(DEC_MAX_TOPK)];
+  alignas(16) int rscr[rank_scratch(DEC_MAX_TOPK)];
   alignas(16) float s[GQA][32];                   // the item's scores, head-major
 };
 

@@ -196,8 +196,11 @@ def time_graph_steps(instances, steps, warmup):
     return sec
 
 
-def time_kernels(instances, reps, stream_obj):
-    """Average duration of each entry point's launches, HIP events on the launch stream."""
+def time_kernels(instances, reps, stream_obj, batches=5):
+    """Average duration of each entry point's launches: HIP events on the launch
+    stream around `reps` back-to-back launches (rotating over the instances),
+    divided by `reps`; the median over `batches` batches. A pair of events
+    around every single launch would add the events' own cost to each."""
     import torch
     n = len(instances)
     s = stream_obj.cuda_stream
@@ -205,15 +208,16 @@ def time_kernels(instances, reps, stream_obj):
              "dn_decode": lambda x: x.dn.run(x.qkv, x.z, x.a, x.b, s)}
     out = {}
     for name, fn in parts.items():
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for i in range(reps):
-            x = instances[i % n]
-            evs[i][0].record(stream_obj)
-            fn(x)
-            evs[i][1].record(stream_obj)
-        torch.cuda.synchronize()
-        ms = sorted(a.elapsed_time(b) for a, b in evs)
-        out[name] = statistics.median(ms) * 1000.0   # microseconds
+        per = []
+        for _ in range(batches):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream_obj)
+            for i in range(reps):
+                fn(instances[i % n])
+            end.record(stream_obj)
+            torch.cuda.synchronize()
+            per.append(start.elapsed_time(end) * 1000.0 / reps)     # microseconds per launch
+        out[name] = statistics.median(per)
     return out
 
 

@@ -900,28 +900,35 @@ struct ChunkIndexArgs {
   int seq, hkv, ratio, topk, max_work;
 };
 
-// every entry's block, eight per thread at a time with all loads issued first;
-// j[k] = -1 for an unused slot, -2 past the end
+// every entry's block, eight per thread at a time: entry_loads issues the
+// loads (which do not depend on the position), entry_blocks turns them into
+// blocks; j[k] = -1 for an unused slot, -2 past the end
+struct EntryLoads { int nsel[8], idv[8], s[8], i[8]; };
+
 template <int NT>
-__device__ __forceinline__ void entry_blocks(const ChunkIndexArgs& A, int b, int pos0, int base, int (&j)[8],
-                                             int (&s)[8], int (&i)[8]) {
+__device__ __forceinline__ void entry_loads(const ChunkIndexArgs& A, int b, int base, EntryLoads& L) {
   const int nslot = A.topk + 1, n_ent = A.seq * nslot;
-  int nsel[8], idv[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const int e = min(base + k * NT + (int)threadIdx.x, n_ent - 1);
-    s[k] = e / nslot;
-    i[k] = e - s[k] * nslot;
-    const long row = (long)b * A.seq + s[k];
-    nsel[k] = A.n_sel[row];
-    idv[k] = A.ids[row * A.topk + min(i[k], A.topk - 1)];
+    L.s[k] = e / nslot;
+    L.i[k] = e - L.s[k] * nslot;
+    const long row = (long)b * A.seq + L.s[k];
+    L.nsel[k] = A.n_sel[row];
+    L.idv[k] = A.ids[row * A.topk + min(L.i[k], A.topk - 1)];
   }
+}
+
+template <int NT>
+__device__ __forceinline__ void entry_blocks(const ChunkIndexArgs& A, int pos0, int base, const EntryLoads& L,
+                                             int (&j)[8]) {
+  const int n_ent = A.seq * (A.topk + 1);
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    const int p = pos0 + s[k];
+    const int p = pos0 + L.s[k];
     const int ts = ((p + 1) / A.ratio) * A.ratio;
     const int tail = ts <= p ? ts / A.ratio : -1;
-    const int jj = i[k] < A.topk ? (i[k] < nsel[k] ? idv[k] : -1) : tail;
+    const int jj = L.i[k] < A.topk ? (L.i[k] < L.nsel[k] ? L.idv[k] : -1) : tail;
     j[k] = base + k * NT + (int)threadIdx.x < n_ent ? jj : -2;
   }
 }
@@ -930,6 +937,11 @@ __global__ __launch_bounds__(CI_NT) void qsa_chunk_index_kernel(ChunkIndexArgs A
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nslot = A.topk + 1;
   const int n_ent = A.seq * nslot;
+  // when every entry fits one pass (8 per thread), its loads are issued before
+  // the position is waited for and serve both passes below
+  const bool one_pass = n_ent <= 8 * CI_NT;
+  EntryLoads L0;
+  if (one_pass) entry_loads<CI_NT>(A, b, 0, L0);
   const int pos0 = A.positions[b];
   // blocks any entry can name: selected blocks are complete ones before the
   // row, a tail block holds the row itself
@@ -939,16 +951,19 @@ __global__ __launch_bounds__(CI_NT) void qsa_chunk_index_kernel(ChunkIndexArgs A
   for (int j = tid; j < NB; j += CI_NT) cnt[j] = 0;
   __syncthreads();
   for (int base = 0; base < n_ent; base += 8 * CI_NT) {
-    int j[8], s[8], i[8];
-    entry_blocks<CI_NT>(A, b, pos0, base, j, s, i);
+    EntryLoads L;
+    if (one_pass) L = L0;
+    else entry_loads<CI_NT>(A, b, base, L);
+    int j[8];
+    entry_blocks<CI_NT>(A, pos0, base, L, j);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       if (j[k] >= 0) {
         atomicAdd(&cnt[j[k]], 1);
       } else if (j[k] == -1) {
-        const long row = (long)b * A.seq + s[k];
+        const long row = (long)b * A.seq + L.s[k];
         for (int gh = 0; gh < A.hkv * GQA; ++gh) {
-          const long pb = ((row * A.hkv + gh / GQA) * nslot + i[k]) * GQA + gh % GQA;
+          const long pb = ((row * A.hkv + gh / GQA) * nslot + L.i[k]) * GQA + gh % GQA;
           A.part_ml[pb * 2 + 0] = -INFINITY;
           A.part_ml[pb * 2 + 1] = 0.f;
         }
@@ -997,14 +1012,17 @@ __global__ __launch_bounds__(CI_NT) void qsa_chunk_index_kernel(ChunkIndexArgs A
   for (int j = tid; j < NB; j += CI_NT) cnt[j] = 0;
   __syncthreads();
   for (int base = 0; base < n_ent; base += 8 * CI_NT) {
-    int j[8], s[8], i[8];
-    entry_blocks<CI_NT>(A, b, pos0, base, j, s, i);
+    EntryLoads L;
+    if (one_pass) L = L0;
+    else entry_loads<CI_NT>(A, b, base, L);
+    int j[8];
+    entry_blocks<CI_NT>(A, pos0, base, L, j);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       if (j[k] >= 0) {
         const int c = atomicAdd(&cnt[j[k]], 1);
-        A.ent[(long)b * n_ent + off[j[k]] + c] = (static_cast<unsigned>(s[k]) << 16) |
-                                                  (i[k] == A.topk ? 1u << 9 : 0u) | static_cast<unsigned>(i[k]);
+        A.ent[(long)b * n_ent + off[j[k]] + c] = (static_cast<unsigned>(L.s[k]) << 16) |
+                                                  (L.i[k] == A.topk ? 1u << 9 : 0u) | static_cast<unsigned>(L.i[k]);
       }
     }
   }

@@ -76,23 +76,28 @@ def test_layer_projections_take_the_gemv(gpu):
 
 
 @pytest.mark.parametrize("dtype,k", [(torch.bfloat16, 4096), (torch.float32, 2048)])
-@pytest.mark.parametrize("m", [1, 3])
-def test_gemv_reinject_equals_gemv_then_reinject(gpu, dtype, k, m):
+@pytest.mark.parametrize("m,streams", [(1, 4), (3, 4), (2, 1), (1, 10)])
+def test_gemv_reinject_equals_gemv_then_reinject(gpu, dtype, k, m, streams):
     """qm_gemv_reinject == qm_gemv + qm_hc_reinject, bit for bit (the same two
-    roundings of each product and sum)."""
+    roundings of each product and sum); past qm_hc_reinject's 8 streams, the
+    same two roundings in torch."""
     qm = gpu
-    n, streams = 2048, 4
-    g = torch.Generator(device=DEV).manual_seed(31 * m + k)
-    print(f"gemv_reinject {dtype} m={m} k={k}", flush=True)
+    n = 2048
+    g = torch.Generator(device=DEV).manual_seed(31 * m + k + streams)
+    print(f"gemv_reinject {dtype} m={m} k={k} streams={streams}", flush=True)
     w = (torch.randn(n, k, generator=g, device=DEV) * k ** -0.5).to(dtype)
     x = torch.randn(m, k, generator=g, device=DEV).to(dtype)
     hyper = torch.randn(m, streams * n, generator=g, device=DEV).to(dtype)
     inject = (2 * torch.sigmoid(torch.randn(m, streams, generator=g, device=DEV))).to(dtype)
     branch = run_gemv(qm, w, x, [n])[0]
-    want = torch.empty_like(hyper)
-    geom = qm.native.HcGeom(m, streams, n, 0, qm.native.act_code(dtype), 0.0)
-    qm.native.call("qm_hc_reinject", ctypes.byref(geom), hyper.data_ptr(), branch.data_ptr(), inject.data_ptr(),
-                   want.data_ptr(), qm.native.stream_handle())
+    if streams <= 8:
+        want = torch.empty_like(hyper)
+        geom = qm.native.HcGeom(m, streams, n, 0, qm.native.act_code(dtype), 0.0)
+        qm.native.call("qm_hc_reinject", ctypes.byref(geom), hyper.data_ptr(), branch.data_ptr(), inject.data_ptr(),
+                       want.data_ptr(), qm.native.stream_handle())
+    else:
+        scaled = (branch.float()[:, None, :] * inject.float()[:, :, None]).to(dtype).float()
+        want = (hyper.float().view(m, streams, n) + scaled).to(dtype).view(m, streams * n)
     got = hyper.clone()
     qm.native.call("qm_gemv_reinject", qm.native.act_code(dtype), m, n, k, w.data_ptr(), x.data_ptr(), streams,
                    inject.data_ptr(), got.data_ptr(), qm.native.stream_handle())

@@ -29,6 +29,7 @@ namespace {
 
 constexpr int GV_NT = 256;
 constexpr int GV_MAX_M = 4;
+constexpr int GV_RJ_PRE = 8;       // reinjection streams whose residual values load with the weights
 
 template <typename T>
 struct GemvArgs {
@@ -77,6 +78,21 @@ __global__ __launch_bounds__(GV_NT) void gemv_kernel(GemvArgs<T> A) {
 #pragma unroll
     for (int j = 0; j < KC; ++j) wv[r][j] = *reinterpret_cast<const uint4*>(wr + j * 64 * VE);
   }
+  // reinjection: the residual values and inject weights this lane will update
+  // (lane = (row r, activation row m) of the epilogue), in the same round trip
+  // as the weights rather than after the reduction; indices clamped
+  float hv[GV_RJ_PRE], iv[GV_RJ_PRE];
+  if constexpr (RJ) {
+    if (lane < R * MM) {
+      const int row = min(row0 + lane % R, A.N - 1), mc = min(lane / R, A.M - 1);
+#pragma unroll
+      for (int s = 0; s < GV_RJ_PRE; ++s) {
+        const int sc = min(s, A.streams - 1);
+        hv[s] = Act<T>::load(A.hyper, ((long)mc * A.streams + sc) * A.N + row);
+        iv[s] = Act<T>::load(A.inject, (long)mc * A.streams + sc);
+      }
+    }
+  }
   // the activation rows, all of a thread's 16-byte loads at once; rows >= M are zero
   constexpr int XC = (MM * CPR + GV_NT - 1) / GV_NT;
   uint4 xr[XC];
@@ -122,7 +138,11 @@ __global__ __launch_bounds__(GV_NT) void gemv_kernel(GemvArgs<T> A) {
     if (row < A.N && m < A.M) {
       if constexpr (RJ) {
         const float y = Act<T>::round(v);
-        for (int s = 0; s < A.streams; ++s) {
+#pragma unroll
+        for (int s = 0; s < GV_RJ_PRE; ++s)
+          if (s < A.streams)
+            Act<T>::store(A.hyper, ((long)m * A.streams + s) * A.N + row, add_rn(hv[s], Act<T>::round(mul_rn(y, iv[s]))));
+        for (int s = GV_RJ_PRE; s < A.streams; ++s) {
           const long i = ((long)m * A.streams + s) * A.N + row;
           const float inj = Act<T>::load(A.inject, (long)m * A.streams + s);
           Act<T>::store(A.hyper, i, add_rn(Act<T>::load(A.hyper, i), Act<T>::round(mul_rn(y, inj))));

@@ -63,11 +63,12 @@ __host__ __device__ __forceinline__ long q_index(long row, int hkv, int h2, int 
 constexpr int Q_SK_STRIDE = 4 * 8 * 8;   // elements between 32-channel steps
 
 // y = rope(round_T(rms_norm(x) * w)) for one row of `n` channels held in LDS
-// by threads 0..n-1 (n <= blockDim). Rotates the first `rope` channels with the
-// cos/sin row given. Returns the value of channel tid (0 for tid >= n).
+// by threads 0..n-1 (n <= blockDim). Rotates the first `rope` channels; c and
+// s are this thread's cos and sin (rope_cs), loaded by the caller with its
+// first loads. Returns the value of channel tid (0 for tid >= n).
 template <typename T>
 __device__ float norm_rope_row(float* s_x, float* s_y, float* s_scr, int n, const float* w, float eps,
-                               int rope, const float* cs, const float* sn) {
+                               int rope, float c, float s) {
   const int tid = threadIdx.x;
   const float ss = torch_row_sumsq(s_x, n, s_scr);
   const float rinv = rsqrt_rn(add_rn(div_rn(ss, (float)n), eps));
@@ -80,9 +81,15 @@ __device__ float norm_rope_row(float* s_x, float* s_y, float* s_scr, int n, cons
   if (tid < rope) {
     const int half = rope / 2;
     const float rot = tid < half ? -s_y[tid + half] : s_y[tid - half];
-    y = add_rn(mul_rn(y, cs[tid]), mul_rn(rot, sn[tid]));
+    y = add_rn(mul_rn(y, c), mul_rn(rot, s));
   }
   return y;
+}
+
+// this thread's cos and sin of a table row (channel clamped into the rope range)
+__device__ __forceinline__ float2 rope_cs(const float* cos, const float* sin, long row, int rope) {
+  const long i = row * rope + min((int)threadIdx.x, rope - 1);
+  return make_float2(cos[i], sin[i]);
 }
 
 // The indexer key of block j (reference/model.py:289-294): the float32 mean
@@ -97,6 +104,7 @@ __device__ float pool_block(int j, int ratio, int rope, float eps, const float* 
                            float* s_y, float* s_scr) {
   const int tid = threadIdx.x;
   const int t0 = j * ratio;
+  const float2 csv = rope_cs(cos, sin, t0, rope);
   if (tid < IDX_D) {
     // 64 rows' loads are issued together: each row's source is chosen by
     // address, and rows past the block are clamped and not added
@@ -122,8 +130,7 @@ __device__ float pool_block(int j, int ratio, int rope, float eps, const float* 
     }
     s_x[tid] = Act<T>::round(div_rn(total, (float)ratio));
   }
-  const float y = norm_rope_row<T>(s_x, s_y, s_scr, IDX_D, k_norm, eps, rope, cos + (long)t0 * rope,
-                                   sin + (long)t0 * rope);
+  const float y = norm_rope_row<T>(s_x, s_y, s_scr, IDX_D, k_norm, eps, rope, csv.x, csv.y);
   if (tid < IDX_D) blocks[(long)j * IDX_D + tid] = y;
   return y;
 }
@@ -151,13 +158,13 @@ __device__ void prep_head(const PrepArgs<T>& A, int b, int s, int role) {
   const int row = b * A.seq + s;
   const int tid = threadIdx.x;
   const int pos = A.positions[b] + s;
-  const float* cs = A.cos + (long)pos * A.rope;
-  const float* sn = A.sin + (long)pos * A.rope;
   if (role < A.hq) {
     if (!A.qg) return;
     const T* src = A.qg + ((long)row * A.hq + role) * (2 * QSA_D);
-    s_x[tid] = Act<T>::load(src, tid);
-    const float y = norm_rope_row<T>(s_x, s_y, s_scr, QSA_D, A.q_norm, A.eps, A.rope, cs, sn);
+    const float xv = Act<T>::load(src, tid);
+    const float2 csv = rope_cs(A.cos, A.sin, pos, A.rope);
+    s_x[tid] = xv;
+    const float y = norm_rope_row<T>(s_x, s_y, s_scr, QSA_D, A.q_norm, A.eps, A.rope, csv.x, csv.y);
     // the attention MFMA takes q as bf16: keep it as hi + lo so the product
     // carries ~16 mantissa bits (rows [2 * row] hold hi, [2 * row + 1] lo)
     const uint16_t hi = f32_to_bf16(y);
@@ -168,13 +175,17 @@ __device__ void prep_head(const PrepArgs<T>& A, int b, int s, int role) {
   if (!A.k_new) return;
   const int g = role - A.hq;
   const long src = ((long)row * A.hkv + g) * QSA_D;
-  s_x[tid] = Act<T>::load(A.k_new, src + tid);
-  const float y = norm_rope_row<T>(s_x, s_y, s_scr, QSA_D, A.k_norm, A.eps, A.rope, cs, sn);
+  // the key, the value, the rope row and the page share one round trip
+  const float xv = Act<T>::load(A.k_new, src + tid);
+  const float vv = Act<T>::load(A.v_new, src + tid);
+  const float2 csv = rope_cs(A.cos, A.sin, pos, A.rope);
   const int page = A.page_table[(long)b * A.max_pages + pos / A.page_size];
+  s_x[tid] = xv;
+  const float y = norm_rope_row<T>(s_x, s_y, s_scr, QSA_D, A.k_norm, A.eps, A.rope, csv.x, csv.y);
   const int prow = pos % A.page_size;
   const long pbase = ((long)page * A.hkv + g) * A.page_size * QSA_D;
   A.k_pool[pbase + k_page_index(prow, tid)] = f32_to_bf16(y);
-  A.v_pool[pbase + v_page_index(prow, tid)] = f32_to_bf16(Act<T>::load(A.v_new, src + tid));
+  A.v_pool[pbase + v_page_index(prow, tid)] = f32_to_bf16(vv);
 }
 
 template <typename T>
@@ -187,8 +198,6 @@ __global__ __launch_bounds__(PREP_NT) void qsa_prep_kernel(PrepArgs<T> A) {
   const int tid = threadIdx.x;
   const int pos0 = A.positions[b];
   const int pos = pos0 + s;
-  const float* cs = A.cos + (long)pos * A.rope;
-  const float* sn = A.sin + (long)pos * A.rope;
 
   __shared__ float s_x[QSA_D], s_y[QSA_D], s_scr[32];
 
@@ -199,8 +208,10 @@ __global__ __launch_bounds__(PREP_NT) void qsa_prep_kernel(PrepArgs<T> A) {
   if (role < A.hq + A.hkv + A.idx_heads) {
     // -------- one indexer query head
     const int h = role - A.hq - A.hkv;
-    if (tid < IDX_D) s_x[tid] = Act<T>::load(A.iq, ((long)row * A.idx_heads + h) * IDX_D + tid);
-    const float y = norm_rope_row<T>(s_x, s_y, s_scr, IDX_D, A.iq_norm, A.eps, A.rope, cs, sn);
+    const float xv = Act<T>::load(A.iq, ((long)row * A.idx_heads + h) * IDX_D + min(tid, IDX_D - 1));
+    const float2 csv = rope_cs(A.cos, A.sin, pos, A.rope);
+    if (tid < IDX_D) s_x[tid] = xv;
+    const float y = norm_rope_row<T>(s_x, s_y, s_scr, IDX_D, A.iq_norm, A.eps, A.rope, csv.x, csv.y);
     if (tid < IDX_D) A.iq_out[((long)row * A.idx_heads + h) * IDX_D + tid] = y;
     return;
   }
@@ -639,8 +650,7 @@ __global__ __launch_bounds__(SEL_NT) void qsa_front_kernel(PrepArgs<T> A, SelArg
   __shared__ SelShared S;
   __shared__ float s_x[QSA_D], s_y[QSA_D], s_scr[32];
   if (tid < IDX_D) A.raw_keys[((long)b * A.max_ctx + p) * IDX_D + tid] = A.ik[(long)b * IDX_D + tid];
-  const float* cs = A.cos + (long)p * A.rope;
-  const float* sn = A.sin + (long)p * A.rope;
+  const float2 csv = rope_cs(A.cos, A.sin, p, A.rope);
   for (int h = 0; h < 4; ++h) {
     __syncthreads();
     if (h >= A.idx_heads) {
@@ -648,7 +658,7 @@ __global__ __launch_bounds__(SEL_NT) void qsa_front_kernel(PrepArgs<T> A, SelArg
       continue;
     }
     if (tid < IDX_D) s_x[tid] = Act<T>::load(A.iq, ((long)b * A.idx_heads + h) * IDX_D + tid);
-    const float y = norm_rope_row<T>(s_x, s_y, s_scr, IDX_D, A.iq_norm, A.eps, A.rope, cs, sn);
+    const float y = norm_rope_row<T>(s_x, s_y, s_scr, IDX_D, A.iq_norm, A.eps, A.rope, csv.x, csv.y);
     if (tid < IDX_D) {
       S.q[h * IDX_D + tid] = y;
       A.iq_out[((long)b * A.idx_heads + h) * IDX_D + tid] = y;

@@ -1062,13 +1062,26 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
   const int4* work = A.work + (long)b * A.max_work;
   __shared__ uint16_t kv[2][32][64 * 8];  // per 32-token group: 16 key then 16 value 1 KB pieces
 
-  for (int w = blockIdx.x; w < n_work; w += gridDim.x) {
-    const int4 item = work[w];
-    const int j = item.x, start = item.y, n = item.z;
-    // this lane's entry (column group il of the wave) and its query
-    const int e = 2 * wv + il;
+  // An item's descriptors are its work record, this lane's entry (column group
+  // il of the wave) and the pages of the block's groups. They are requested
+  // two items ahead: each item issues its own q and K/V loads first, then the
+  // next item's entry and pages (from the record that came in during the
+  // previous item) and the record of the item after that, so no item waits on
+  // a chain of dependent loads before its own.
+  const long ent0 = (long)b * A.seq * nslot;
+  const int e = 2 * wv + il;
+  const int pg1_off = gpb > 1 ? 32 : 0;
+  int w = blockIdx.x;
+  if (w >= n_work) return;
+  int4 item = work[w];
+  int4 item_n = work[min(w + (int)gridDim.x, n_work - 1)];
+  unsigned pk = A.ent[ent0 + item.y + min(e, item.z - 1)];
+  int pg0 = ptab[(item.x * A.ratio) / A.page_size];
+  int pg1 = ptab[(item.x * A.ratio + pg1_off) / A.page_size];
+  for (;;) {
+    const int wn = w + gridDim.x;
+    const int j = item.x, n = item.z;
     const bool ok = e < n;
-    const unsigned pk = A.ent[(long)b * A.seq * nslot + start + min(e, n - 1)];
     const int s = pk >> 16, slot = pk & 511;
     const bool tail = (pk >> 9) & 1u;
     const long row = (long)b * A.seq + s;
@@ -1084,28 +1097,34 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
         qlo[sk] = load_bf16x8(ql + Q_SK_STRIDE * sk);
       }
     }
-    // stage the block's groups: per group 16 KB of key and 16 KB of value pieces
+    // stage the block's groups: per group 16 KB of key and 16 KB of value
+    // pieces, both groups' loads issued before either is stored (a block of
+    // one group loads and stores it twice; the second copy is not read)
+    const int row0a = (j * A.ratio) % A.page_size, row0b = (j * A.ratio + pg1_off) % A.page_size;
+    const long pba = ((long)pg0 * A.hkv + g) * head_stride, pbb = ((long)(gpb > 1 ? pg1 : pg0) * A.hkv + g) * head_stride;
+    const uint16_t* ksa = A.k_pool + pba + (row0a >> 4) * 8 * 512;
+    const uint16_t* vsa = A.v_pool + pba + (row0a >> 5) * 16 * 512;
+    const uint16_t* ksb = A.k_pool + pbb + (row0b >> 4) * 8 * 512;
+    const uint16_t* vsb = A.v_pool + pbb + (row0b >> 5) * 16 * 512;
+    uint4 kra[4], vra[4], krb[4], vrb[4];
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      if (gi < gpb) {
-        const int t0 = j * A.ratio + gi * 32;
-        const long pb = ((long)ptab[t0 / A.page_size] * A.hkv + g) * head_stride;
-        const int row0 = t0 % A.page_size;
-        const uint16_t* ks = A.k_pool + pb + (row0 >> 4) * 8 * 512;
-        const uint16_t* vs = A.v_pool + pb + (row0 >> 5) * 16 * 512;
-        uint4 kr[4], vr[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          kr[k] = *reinterpret_cast<const uint4*>(ks + (k * CA_NT + tid) * 8);
-          vr[k] = *reinterpret_cast<const uint4*>(vs + (k * CA_NT + tid) * 8);
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          *reinterpret_cast<uint4*>(&kv[gi][0][0] + (k * CA_NT + tid) * 8) = kr[k];
-          *reinterpret_cast<uint4*>(&kv[gi][16][0] + (k * CA_NT + tid) * 8) = vr[k];
-        }
-      }
+    for (int k = 0; k < 4; ++k) {
+      kra[k] = *reinterpret_cast<const uint4*>(ksa + (k * CA_NT + tid) * 8);
+      vra[k] = *reinterpret_cast<const uint4*>(vsa + (k * CA_NT + tid) * 8);
+      krb[k] = *reinterpret_cast<const uint4*>(ksb + (k * CA_NT + tid) * 8);
+      vrb[k] = *reinterpret_cast<const uint4*>(vsb + (k * CA_NT + tid) * 8);
     }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      *reinterpret_cast<uint4*>(&kv[0][0][0] + (k * CA_NT + tid) * 8) = kra[k];
+      *reinterpret_cast<uint4*>(&kv[0][16][0] + (k * CA_NT + tid) * 8) = vra[k];
+      *reinterpret_cast<uint4*>(&kv[1][0][0] + (k * CA_NT + tid) * 8) = krb[k];
+      *reinterpret_cast<uint4*>(&kv[1][16][0] + (k * CA_NT + tid) * 8) = vrb[k];
+    }
+    const unsigned pk_n = A.ent[ent0 + item_n.y + min(e, item_n.z - 1)];
+    const int pg0_n = ptab[(item_n.x * A.ratio) / A.page_size];
+    const int pg1_n = ptab[(item_n.x * A.ratio + pg1_off) / A.page_size];
+    const int4 item_nn = work[min(wn + (int)gridDim.x, n_work - 1)];
     __syncthreads();
 
     if (2 * wv < n) {
@@ -1180,6 +1199,13 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
       }
     }
     __syncthreads();
+    if (wn >= n_work) break;
+    w = wn;
+    item = item_n;
+    item_n = item_nn;
+    pk = pk_n;
+    pg0 = pg0_n;
+    pg1 = pg1_n;
   }
 }
 

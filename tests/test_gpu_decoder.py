@@ -210,3 +210,64 @@ def test_reset_rewinds_in_place(stack):
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all() and dec.position == 1
     restore(cache, snap)
+
+
+ROWS = (1100, 317)      # row positions: buckets 2047 and 1023 when alone
+
+
+def _two_row_cache(qm, model, seed):
+    """Two sequences with seeded random histories of ROWS tokens, randomly paged."""
+    cfg = model.config
+    cache = qm.cache.MixHybridCache(N_LAYERS, cfg, batch=2, max_ctx=4096, device=DEV, dtype=BF,
+                                    page_table="random", seed=5)
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    for l in range(N_LAYERS):
+        lc = cache[l]
+        if cfg.is_full_attention(l):
+            lc.ensure_qsa(2, BF)
+            for t in (lc.k_pool, lc.v_pool, lc.raw_keys):
+                t.copy_(torch.randn(t.shape, generator=g, device=DEV).to(t.dtype))
+            geom = model.qsa_geom(cache, BF)
+            cos, sin = model.rope.get(cache.max_ctx)
+            # blocks past a row's position are pooled too and never read by it
+            n_blocks = max(ROWS) // cfg.indexer_compress_ratio
+            qm.native.call("qm_qsa_pool_blocks", ctypes.byref(geom), lc.raw_keys.data_ptr(),
+                           model._dw(l, "indexer.k_norm.weight", torch.float32).data_ptr(), cos.data_ptr(),
+                           sin.data_ptr(), 0, n_blocks, lc.block_keys.data_ptr(), qm.native.stream_handle())
+            lc.blocks_valid = n_blocks
+        else:
+            lc.ensure_dn(2, BF)
+            lc.recurrent_state.copy_(torch.randn(lc.recurrent_state.shape, generator=g, device=DEV) * 0.02)
+            lc.conv_ring.copy_(torch.randn(lc.conv_ring.shape, generator=g, device=DEV).to(BF))
+        lc.n_tokens = max(ROWS)
+    cache.slot_tokens[:] = list(ROWS)
+    torch.cuda.synchronize()
+    return cache
+
+
+def test_rows_at_different_positions_match_single_rows(stack):
+    """A two-row decoder with its rows at positions 1100 and 317 (continuous
+    batching: one graph, the larger row's bucket) against one single-row
+    decoder per row over a slot view of an identical cache (each row's own
+    bucket): the residual of every row bit for bit over three steps, the last
+    of which completes row 1's block 4 (position 319); positions advance per
+    row, and the k-token step refuses rows at different positions."""
+    qm, model, _ = stack
+    c = model.config
+    batch_cache = _two_row_cache(qm, model, 17)
+    single_cache = _two_row_cache(qm, model, 17)
+    dec = qm.decoder.MixDecoder(model, batch_cache, positions=ROWS)
+    singles = [qm.decoder.MixDecoder(model, single_cache.slot_view(r)) for r in range(2)]
+    assert [s.position for s in singles] == list(ROWS)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    for step in range(3):
+        print(f"rows at {dec.row_positions}: step {step}", flush=True)
+        h = torch.randn(2, 1, c.hc_count * c.hidden_size, generator=g, device=DEV).to(BF)
+        got = dec.step(h).clone()
+        for r in range(2):
+            want = singles[r].step(h[r:r + 1]).clone()
+            assert torch.equal(got[r], want[0]), (step, r, rel_err(got[r], want[0]))
+    assert dec.row_positions == [p + 3 for p in ROWS]
+    assert batch_cache.slot_tokens == [p + 3 for p in ROWS]
+    with pytest.raises(ValueError):
+        dec.step_n(torch.zeros(2, 2, c.hc_count * c.hidden_size, device=DEV))

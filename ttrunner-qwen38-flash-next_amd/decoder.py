@@ -127,22 +127,35 @@ class MixDecoder:
     """The token-mixing halves of ``layers`` (default: every layer of the cache)
     for one token per sequence, eager (``step_eager``) or from a captured graph
     (``step``). ``hyper`` is the bound residual [B, 1, hc_count * hidden]: a
-    step reads it and leaves the new residual in it."""
+    step reads it and leaves the new residual in it.
 
-    def __init__(self, model, cache, layers=None, dtype=torch.bfloat16, min_bucket: int = 1024):
+    Rows may sit at different positions (continuous batching: ``positions``,
+    one per row, default every row at the layers' common position). The
+    kernels read each row's position from device memory; a step replays the
+    graph of the largest position's bucket, and maps each row's next page
+    first when the cache draws its pages from a pool."""
+
+    def __init__(self, model, cache, layers=None, dtype=torch.bfloat16, min_bucket: int = 1024, positions=None):
         c = model.config
         self.model, self.cache, self.dtype = model, cache, dtype
         self.layers = list(range(len(cache.layers))) if layers is None else list(layers)
         if not self.layers:
             raise ValueError("MixDecoder needs at least one layer")
-        starts = {cache[l].n_tokens for l in self.layers}
-        if len(starts) != 1:
-            raise ValueError(f"layers of the cache are at different positions: {sorted(starts)}")
-        self.position = starts.pop()
+        if positions is None:
+            starts = {cache[l].n_tokens for l in self.layers}
+            if len(starts) != 1:
+                raise ValueError(f"layers of the cache are at different positions: {sorted(starts)}")
+            rows = [starts.pop()] * cache.batch
+        else:
+            rows = [int(p) for p in positions]
+            if len(rows) != cache.batch or min(rows) < 0:
+                raise ValueError(f"need {cache.batch} non-negative row positions, got {rows}")
+        self.row_positions = rows
+        self.position = max(rows)
         self.min_bucket = min_bucket
         dev = model.device
         self.hyper = torch.zeros(cache.batch, 1, c.hc_count * c.hidden_size, dtype=dtype, device=dev)
-        self.positions = torch.full((cache.batch,), self.position, dtype=torch.int32, device=dev)
+        self.positions = torch.tensor(rows, dtype=torch.int32, device=dev)
         self._steps = {}
         self._graphs = {}
 
@@ -172,16 +185,25 @@ class MixDecoder:
             st.launch(self.hyper, stream)
         self.positions.add_(1)
 
+    def _map_pages(self, n: int):
+        """Pages for every row's next n tokens (a no-op for static tables)."""
+        for slot, p in enumerate(self.row_positions):
+            self.cache.ensure_capacity(slot, p + n)
+
     def _advance(self, n: int, host_only: bool):
         ratio = self.model.config.indexer_compress_ratio
-        self.position += n
+        self.row_positions = [p + n for p in self.row_positions]
+        self.position = max(self.row_positions)
         if host_only:
             return
         for l in self.layers:
             lc = self.cache[l]
-            lc.n_tokens += n
+            lc.n_tokens = self.position
             if self.model.config.is_full_attention(l):
                 lc.blocks_valid = max(lc.blocks_valid, self.position // ratio)
+        if len(self.cache.slot_tokens) == len(self.row_positions):
+            for slot, p in enumerate(self.row_positions):
+                self.cache.slot_tokens[slot] = p
 
     def _fill(self, hyper_in):
         if hyper_in is not None:
@@ -190,6 +212,7 @@ class MixDecoder:
     def step_eager(self, hyper_in=None) -> torch.Tensor:
         """One step by direct launches on the current stream."""
         self._fill(hyper_in)
+        self._map_pages(1)
         steps = self._layer_steps(self.bucket(self.position))
         self._launch(steps, torch.cuda.current_stream(self.model.device).cuda_stream)
         self._advance(1, host_only=False)
@@ -218,8 +241,9 @@ class MixDecoder:
         return g
 
     def step(self, hyper_in=None) -> torch.Tensor:
-        """One step replayed from the graph of the current position's bucket."""
+        """One step replayed from the graph of the largest row position's bucket."""
         self._fill(hyper_in)
+        self._map_pages(1)
         self.graph(self.bucket(self.position)).replay()
         self._advance(1, host_only=False)
         return self.hyper
@@ -231,12 +255,16 @@ class MixDecoder:
         [B, k, hc_count * hidden] -> the residual after the layers at all k
         positions. The per-token stages run over B*k rows; the cores run their
         chunk paths. The cache consumes all k tokens, and the bound residual
-        is left holding the last row's."""
+        is left holding the last row's. Every row must be at the same
+        position (the layer methods take one)."""
         m = self.model
         h = hyper_rows.to(self.dtype).contiguous()
         k = h.shape[1]
+        if len(set(self.row_positions)) != 1:
+            raise ValueError(f"step_n needs every row at one position, not {self.row_positions}")
         if self.position + k > self.cache.max_ctx:
             raise ValueError(f"{k} tokens from position {self.position} overrun the cache")
+        self._map_pages(k)
         for l in self.layers:
             mixed, _, inject = m._gated_residual(h, l, "attn")
             if m.config.is_full_attention(l):
@@ -263,4 +291,7 @@ class MixDecoder:
             lc.blocks_valid = 0
         self.hyper.zero_()
         self.positions.zero_()
+        self.row_positions = [0] * len(self.row_positions)
         self.position = 0
+        if len(self.cache.slot_tokens) == len(self.row_positions):
+            self.cache.slot_tokens[:] = self.row_positions

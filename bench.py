@@ -574,14 +574,12 @@ def run_stack(qm, dev, pos=8128, n_layers=STACK_LAYERS, steps=30, warmup=5):
         run = dec.step_eager if mode == "eager" else dec.step
         for _ in range(warmup):
             # every step at one position, as the headline's rotation: the history does not grow
-            dec.position = pos
-            dec.positions.fill_(pos)
+            dec.seek(pos)
             run(x)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(steps):
-            dec.position = pos
-            dec.positions.fill_(pos)
+            dec.seek(pos)
             run(x)
         torch.cuda.synchronize()
         out[mode] = (time.perf_counter() - t0) / steps * 1e6

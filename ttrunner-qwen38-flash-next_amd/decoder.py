@@ -185,6 +185,21 @@ class MixDecoder:
             st.launch(self.hyper, stream)
         self.positions.add_(1)
 
+    def seek(self, positions) -> None:
+        """Set every row's position (an int, or one per row) on the host and in
+        the device tensor the graphs read, without touching the caches: a
+        replay then runs at those positions (the bench repeats one position
+        this way; a server rewinds a row it refilled)."""
+        rows = [int(positions)] * len(self.row_positions) if isinstance(positions, int) else [int(p) for p in positions]
+        if len(rows) != len(self.row_positions) or min(rows) < 0:
+            raise ValueError(f"need {len(self.row_positions)} non-negative row positions, got {rows}")
+        self.row_positions = rows
+        self.position = max(rows)
+        if isinstance(positions, int):
+            self.positions.fill_(rows[0])          # a device fill, no host copy on the stream
+        else:
+            self.positions.copy_(torch.tensor(rows, dtype=torch.int32))
+
     def _map_pages(self, n: int):
         """Pages for every row's next n tokens (a no-op for static tables)."""
         for slot, p in enumerate(self.row_positions):

@@ -269,5 +269,10 @@ def test_rows_at_different_positions_match_single_rows(stack):
             assert torch.equal(got[r], want[0]), (step, r, rel_err(got[r], want[0]))
     assert dec.row_positions == [p + 3 for p in ROWS]
     assert batch_cache.slot_tokens == [p + 3 for p in ROWS]
+    assert dec.positions.cpu().tolist() == [p + 3 for p in ROWS]
     with pytest.raises(ValueError):
         dec.step_n(torch.zeros(2, 2, c.hc_count * c.hidden_size, device=DEV))
+    dec.seek(list(ROWS))
+    assert dec.positions.cpu().tolist() == list(ROWS) and dec.position == max(ROWS)
+    dec.seek(500)
+    assert dec.positions.cpu().tolist() == [500, 500] and dec.row_positions == [500, 500]

@@ -162,14 +162,15 @@ int launch_mm(const GemvArgs<T>& A, hipStream_t stream) {
   constexpr int VE = 16 / sizeof(T);
   const int kc = A.K / (64 * VE);
   const size_t lds = (size_t)MM * A.K * sizeof(T);
-  // R rows x KC chunks of 1 KB in flight per wave: two rows (8 KB) at k = 2048
-  // and one (8 KB) at k = 4096 (bf16). More workgroups with fewer rows each
-  // measured faster than 16 KB per wave: a 48-layer step 1707 -> 1696 us (one
-  // row at k = 4096, 512 workgroups for an output projection), then -> 1666 us
-  // (two rows at k = 2048, 1544 workgroups for the DeltaNet input projection)
+  // one row of KC chunks of 1 KB in flight per wave (4 KB at k = 2048, 8 KB at
+  // k = 4096, bf16): more workgroups with fewer rows each measured faster than
+  // 16 KB per wave. A 48-layer step went 1707 -> 1696 us (one row at k = 4096:
+  // 512 workgroups for an output projection), -> 1666 us (two rows at k =
+  // 2048), -> 1653 us (one row: 3088 workgroups for the DeltaNet input
+  // projection)
   if (kc == 4) {
-    const int rows = (GV_NT / 64) * 2;
-    hipLaunchKernelGGL((gemv_kernel<T, MM, 2, 4, RJ>), dim3((A.N + rows - 1) / rows), dim3(GV_NT), lds, stream, A);
+    const int rows = (GV_NT / 64) * 1;
+    hipLaunchKernelGGL((gemv_kernel<T, MM, 1, 4, RJ>), dim3((A.N + rows - 1) / rows), dim3(GV_NT), lds, stream, A);
   } else if (kc == 8) {
     const int rows = (GV_NT / 64) * 1;
     hipLaunchKernelGGL((gemv_kernel<T, MM, 1, 8, RJ>), dim3((A.N + rows - 1) / rows), dim3(GV_NT), lds, stream, A);

@@ -89,6 +89,25 @@ int qm_dn_decode(const qm_dn_geom* g, const void* qkv, const void* z, const void
                  const int* positions, void* conv_ring, float* state, void* out, void* workspace,
                  size_t workspace_bytes, hipStream_t stream);
 
+/* Hand-off health of qm_dn_decode's workspace: *giveups = the number of
+ * waits for the other workgroups of a head that gave up since the last reset
+ * (a correct launch never gives up; the output of such a head is NaN). Waits
+ * for the stream. reset != 0 then zeroes the workspace, the state of a fresh
+ * one. No counterpart in the reference: its device ops return no such state. */
+int qm_dn_decode_check(int batch, int n_v_heads, int head_dim, void* workspace, size_t workspace_bytes, int reset,
+                       unsigned* giveups, hipStream_t stream);
+
+/* Depthwise causal conv1d over (B, C, T), the free functions causal_conv1d
+ * (reference/layers.py:133-138, state == NULL: zero history) and
+ * causal_conv1d_step (reference/layers.py:141-147, with the rolling state):
+ *   full = [state | x] (K-1 + T columns), out[b,c,t] = silu?(sum_j w[c,j]
+ *   full[b,c,t+j]) with tap 0 the oldest; new_state = full[:, :, T:].
+ *   x, out [B, C, T]; state, new_state [B, C, K-1] (either may be NULL;
+ *   new_state may be state itself); weight [C, K]; all act_dtype, contiguous;
+ *   out must not alias x or state. 1 <= K <= 8. */
+int qm_causal_conv1d(int act_dtype, int batch, int channels, int seq, int taps, const void* x, const void* state,
+                     const void* weight, int activation, void* out, void* new_state, hipStream_t stream);
+
 /* The gated delta rule over T tokens on split, expanded inputs:
  * recurrent_gated_delta_rule (reference/layers.py:155-192).
  *   q, k [B, T, H, d], v [B, T, H, d] act; g, beta [B, T, H] f32;
@@ -232,6 +251,29 @@ int qm_qsa_decode_splits(const qm_qsa_geom* g, int max_position);
  * workspace race. */
 size_t qm_qsa_decode_workspace(const qm_qsa_geom* g, int splits);
 
+/* Workgroups of one (sequence, kv head) group of qm_qsa_decode for `splits`:
+ * max(splits, 64) (short contexts widen the grid so every output slice has its
+ * own merging workgroup). */
+int qm_qsa_decode_group(int splits);
+/* Resident capacity of the qm_qsa_decode kernel that `splits` selects on the
+ * current device: workgroups that fit at once (occupancy per compute unit x
+ * compute units), or a negative QM_ERR_* code (no device). */
+int qm_qsa_decode_resident(int act_dtype, int splits);
+/* QM_OK if a group of qm_qsa_decode_group(splits) workgroups fits `resident`
+ * resident workgroups (every workgroup of a group waits for the others, so the
+ * whole group must be on the device at once), else QM_ERR_UNSUPPORTED or
+ * QM_ERR_ARG. qm_qsa_decode applies it with qm_qsa_decode_resident. */
+int qm_qsa_decode_fits(int splits, int resident);
+/* Hand-off health of qm_qsa_decode's workspace since the last reset:
+ * counts[0] = waits for a group's partials that gave up, counts[1] = launches
+ * whose position had more attention items than `splits` (a plan sized for
+ * smaller positions). Either leaves NaN in the affected output; a correct
+ * plan keeps both zero. Waits for the stream. reset != 0 then zeroes the
+ * generation words and flags, the state of a fresh workspace. No counterpart in
+ * the reference: its device ops return no such state. */
+int qm_qsa_decode_check(const qm_qsa_geom* g, int splits, void* workspace, size_t workspace_bytes, int reset,
+                        unsigned* counts, hipStream_t stream);
+
 /* One QSA decode step (one token per sequence) in a single launch: everything
  * qm_qsa_decode_front + qm_qsa_attend compute -- token prep and K/V append,
  * raw indexer key append and block pooling, indexer query, block scores and
@@ -239,8 +281,10 @@ size_t qm_qsa_decode_workspace(const qm_qsa_geom* g, int splits);
  * gate (reference/model.py:248-382). Every working workgroup recomputes the
  * selection it needs and attends one 32-token item; the partials cross to the
  * workgroups that merge them inside the same launch.
- * Requires max_blocks, max_pages <= 2048, budget/ratio <= 256, ratio <= 64 and
- * 1 <= splits <= 1024 (qm_qsa_decode_splits).
+ * Requires max_blocks, max_pages <= 2048, budget/ratio <= 256, ratio <= 64,
+ * 1 <= splits <= 1024 (qm_qsa_decode_splits) and a group that fits the device
+ * (qm_qsa_decode_fits); positions whose items exceed `splits` are counted and
+ * poisoned (qm_qsa_decode_check).
  *   out [B, Hq*d] act; ids [B, budget/ratio], n_sel [B], items, iq_out
  *   [B, idx_heads, idx_dim] are optional inspection outputs (may be NULL). */
 int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k_new, const void* v_new, const void* iq,

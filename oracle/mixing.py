@@ -36,6 +36,7 @@ import math
 import torch
 import torch.nn.functional as F
 
+from .cnative import block_scores
 from .layers import (
     apply_rotary,
     causal_conv1d,
@@ -190,7 +191,19 @@ class OracleMixer:
         return pooled.squeeze(2)
 
     def indexer_scores(self, q, pooled):
-        """reference/model.py:297-298: sum over heads of relu(q_h . block) / sqrt(d)."""
+        """reference/model.py:297-298: sum over heads of relu(q_h . block) / sqrt(d).
+
+        The reference computes this with torch's einsum; its float32 result
+        depends on the summation order the host's BLAS takes. The oracle
+        restates the order that produced the golden score vectors (scores.c),
+        so its scores do not change with the machine it runs on;
+        ``indexer_scores_torch`` is the reference's own expression."""
+        if self.config.indexer_head_dim != 128:
+            return self.indexer_scores_torch(q, pooled)
+        return block_scores(q, pooled).to(q.device)
+
+    def indexer_scores_torch(self, q, pooled):
+        """reference/model.py:297-298 as the reference writes it (torch einsum)."""
         dim = self.config.indexer_head_dim
         s = torch.einsum("bqhd,bkd->bqhk", q.float(), pooled.float())
         return torch.relu(s).sum(dim=2) / math.sqrt(dim)

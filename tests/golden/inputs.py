@@ -142,3 +142,21 @@ def delta_rule_inputs(seed: int, seq: int, heads: int = DN_HV, d: int = DN_D):
     g = -torch.nn.functional.softplus(normal(r, (1, seq, heads)))
     beta = torch.sigmoid(normal(r, (1, seq, heads)))
     return q, k, v, g, beta
+
+
+def golden_rope(rot, n: int):
+    """(cos, sin) [1, n, 64] for positions 0..n-1 from the oracle's rotary
+    tables, with the rows tests/golden/rope.npz holds (the golden generator's
+    own, at the positions the score fixtures use) patched in: the last bit of a
+    few entries depends on the host CPU's math library."""
+    import os
+    p = torch.arange(n)[None]
+    cos, sin = rot(p[None].expand(3, -1, -1))
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "rope.npz"))
+    pos = z["positions"]
+    keep = pos < n
+    idx = torch.from_numpy(pos[keep].astype(np.int64))
+    cos, sin = cos.clone(), sin.clone()
+    cos[0, idx] = torch.from_numpy(z["cos"][keep])
+    sin[0, idx] = torch.from_numpy(z["sin"][keep])
+    return cos, sin

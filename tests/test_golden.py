@@ -11,6 +11,7 @@ digest check is skipped and the stored samples are compared to tolerance.
 from __future__ import annotations
 
 import json
+import math
 import os
 import sys
 
@@ -104,7 +105,10 @@ def test_decode_layers_match_reference(tag, rot):
     pooled = mixer.indexer_pooled(raw, 3, cos, sin, n_blocks)
     scores = mixer.indexer_scores(q, pooled)[0, 0]
     if SAME_BUILD:
+        # the restated summation order (oracle/scores.c) and torch's own einsum
+        # both give the reference's score vector bit for bit
         assert np.array_equal(scores.numpy(), z["scores"])
+        assert np.array_equal(mixer.indexer_scores_torch(q, pooled)[0, 0].numpy(), z["scores"])
     ids = sel.select_blocks(z["scores"], pos, gi.RATIO, gi.BUDGET, n_blocks)
     assert np.array_equal(np.sort(ids), z["selected"])
 
@@ -152,3 +156,33 @@ def test_prefill_chunk_matches_reference(rot):
     _check(y, "cfg5", "dn_out", z["dn_out"])
     _check(cache[0].recurrent_state, "cfg5", "dn_state", z["dn_state"])
     _check(cache[0].conv_state, "cfg5", "dn_conv")
+
+
+@pytest.mark.parametrize("seq", [1, 2, 3, 8, 128])
+def test_restated_score_orders_equal_torch_einsum(seq):
+    """oracle/scores.c reproduces torch's CPU einsum of reference/model.py:297
+    bit for bit on the golden generator's build, for one query row (its
+    16-partial order) and several (one chain per dot product), over block
+    counts from 15 to 2048: random float32 inputs, so a wrong order would
+    differ in most entries."""
+    if not SAME_BUILD:
+        pytest.skip("torch's einsum order belongs to the golden generator's build")
+    from oracle.cnative import block_scores
+    rng = np.random.default_rng(seq)
+    for n in (15, 127, 512, 2048):
+        q = torch.from_numpy(rng.standard_normal((1, seq, 4, 128)).astype(np.float32))
+        k = torch.from_numpy(rng.standard_normal((1, n, 128)).astype(np.float32))
+        want = torch.relu(torch.einsum("bqhd,bkd->bqhk", q, k)).sum(dim=2) / math.sqrt(128)
+        assert torch.equal(block_scores(q, k), want), (seq, n)
+
+
+def test_rope_rows_fixture_is_the_golden_builds(rot):
+    """tests/golden/rope.npz holds the golden generator's table rows (the
+    digests of the full tables pin them on that build)."""
+    if not SAME_BUILD:
+        pytest.skip("different torch build than the golden generator")
+    cos, sin = _tables(rot, 32768)
+    z = np.load(os.path.join(HERE, "rope.npz"))
+    pos = torch.from_numpy(z["positions"].astype(np.int64))
+    assert torch.equal(cos[0, pos], torch.from_numpy(z["cos"]))
+    assert torch.equal(sin[0, pos], torch.from_numpy(z["sin"]))

@@ -192,6 +192,106 @@ def test_step_n_matches_single_steps(stack, k):
     restore(cache, snap)
 
 
+def _export(cache):
+    """The device caches as the reference's layer caches (reference/cache.py:19-29), on the CPU."""
+    from oracle.cache import OracleHybridCache
+    oc = OracleHybridCache(N_LAYERS)
+    for l, lc in enumerate(cache.layers):
+        if lc.conv_ring is not None:
+            oc[l].conv_state = lc.conv_state.cpu()
+            oc[l].recurrent_state = lc.recurrent_state.cpu().clone()
+        if lc.k_pool is not None:
+            oc[l].keys, oc[l].values = lc.keys.cpu(), lc.values.cpu()
+            oc[l].indexer_keys = lc.indexer_keys.cpu()
+    return oc
+
+
+def _oracle_chain(model, oc, h, position):
+    """reference/model.py:443-452 for the token-mixing halves, every piece the
+    oracle's: _gated_residual, the branch, _reinject, for the rows of h at
+    position, position + 1, ... (the cores take their chunk paths for k > 1)."""
+    from oracle.config import OracleConfig
+    from oracle.layers import RotaryEmbedding
+    from oracle.mixing import OracleMixer
+    om = OracleMixer(OracleConfig(), model.store)
+    k = h.shape[1]
+    rot = RotaryEmbedding(64, 1e7, [11, 11, 10])
+    p = torch.arange(position + k)[None]
+    cos, sin = rot(p[None].expand(3, -1, -1))
+    for l in range(N_LAYERS):
+        mixed, _, inject = om._gated_residual(h, l, "attn")
+        if model.config.is_full_attention(l):
+            branch = om._full_attention(mixed, l, cos, sin, oc, position)
+        else:
+            branch = om._linear_attention(mixed, l, oc)
+        h = om._reinject(h, branch, inject)
+    return h
+
+
+@pytest.mark.parametrize("k", [1, 3])
+def test_decoder_matches_oracle_chain(stack, k):
+    """MixDecoder.step (k = 1, from the graph) and step_n (k = 3) against the
+    all-oracle chain on the CPU over the same exported history: the residual
+    within 2e-2; the first layer's fp32 state within 1e-3 (its inputs differ
+    from the oracle's only by the rounding of the mix and the projections), the
+    other states, the appended keys/values and the conv windows (which hold the
+    bf16 projections each side computed) within 2e-2."""
+    qm, model, cache = stack
+    snap = snapshot(cache)
+    x = inputs(1, k=k, seed=21)[0]
+    oc = _export(cache)
+    print(f"decoder vs oracle chain k={k}", flush=True)
+    want = _oracle_chain(model, oc, x.cpu(), START)
+    dec = qm.decoder.MixDecoder(model, cache)
+    got = dec.step(x).clone() if k == 1 else dec.step_n(x).clone()
+    torch.cuda.synchronize()
+    assert rel_err(got, want) < 2e-2, rel_err(got, want)
+    got_oc = _export(cache)
+    for l in range(N_LAYERS):
+        if model.config.is_full_attention(l):
+            assert rel_err(got_oc[l].keys[:, :, -k:], oc[l].keys[:, :, -k:]) < 2e-2, l
+            assert rel_err(got_oc[l].values[:, :, -k:], oc[l].values[:, :, -k:]) < 2e-2, l
+            assert got_oc[l].indexer_keys.shape == oc[l].indexer_keys.shape
+        else:
+            bar = 1e-3 if l == 0 else None
+            diff = (got_oc[l].recurrent_state - oc[l].recurrent_state).abs().max().item()
+            if bar is not None:
+                assert diff < bar, (l, diff)
+            else:
+                assert rel_err(got_oc[l].recurrent_state, oc[l].recurrent_state) < 2e-2, l
+            assert rel_err(got_oc[l].conv_state, oc[l].conv_state) < 2e-2, l
+    dec.check_handoffs()
+    restore(cache, snap)
+
+
+def test_seek_then_step_n_matches_a_run_at_that_position(stack):
+    """After seek(p) the k-token step runs every layer at p: the same residual
+    and caches, bit for bit, as a decoder whose layers were already at p."""
+    qm, model, cache = stack
+    snap = snapshot(cache)
+    x = inputs(1, k=3, seed=22)[0]
+    target = START + 2
+    print("seek then step_n", flush=True)
+    dec = qm.decoder.MixDecoder(model, cache)
+    dec.seek(target)
+    assert all(cache[l].n_tokens == target for l in range(N_LAYERS))
+    got = dec.step_n(x).clone()
+    torch.cuda.synchronize()
+    after_seek = snapshot(cache)
+    restore(cache, snap)
+    for l in range(N_LAYERS):
+        cache[l].n_tokens = target
+    dec = qm.decoder.MixDecoder(model, cache)
+    want = dec.step_n(x).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    for l, ((a, na, _), (b, nb, _)) in enumerate(zip(after_seek, snapshot(cache))):
+        assert na == nb == target + 3
+        for f in a:
+            assert torch.equal(a[f], b[f]), f"layer {l} {f}"
+    restore(cache, snap)
+
+
 def test_reset_rewinds_in_place(stack):
     qm, model, cache = stack
     snap = snapshot(cache)

@@ -135,9 +135,11 @@ def test_64_compounding_decode_steps_stay_within_tolerance(gpu):
     # the in-launch hand-off of the gated norm's shares: one 128-byte line per
     # head, whose generation word counts the launches and whose second word
     # counts waits that gave up (never)
-    lines = model._ws["dn_decode"].view(torch.int32).cpu()[: 32 * 32].reshape(32, 32)
+    lines = model._ws["dn_decode_1"].view(torch.int32).cpu()[: 32 * 32].reshape(32, 32)
     assert lines[:, 0].tolist() == [64] * 32
     assert lines[:, 1].tolist() == [0] * 32
+    model.check_handoffs()          # the same counters through qm_dn_decode_check, then reset
+    assert model._ws["dn_decode_1"].view(torch.int32).cpu()[: 32 * 32].abs().sum().item() == 0
 
 
 @pytest.mark.parametrize("seq", [2, 7, 64, 128])

@@ -106,7 +106,7 @@ def test_indexer_stages_and_selection_match_reference(gpu, tag):
     else:
         iq = torch.from_numpy(z["idx_q_raw"]).reshape(1, 1, -1)
         ik = torch.from_numpy(z["idx_k_raw"]).reshape(1, 1, -1)
-    cos, sin = tables(pos + 1)
+    cos, sin = gi.golden_rope(ROT, pos + 1)
     model, cache = _model_and_cache(gpu, store, dtype, pos + 64)
     cache[3].indexer_keys = idx_keys.to(DEV)
     print(f"indexer {tag} pos={pos}", flush=True)
@@ -176,7 +176,7 @@ def test_decode_layer_matches_golden_reference(gpu, tag):
     store = gi.FakeStore(gi.qsa_weights(3, m["qsa_seeds"][0], dtype))
     keys, values, idx_keys = gi.qsa_past(m["qsa_seeds"][1], pos, dtype)
     hidden = gi.hidden_states(m["hidden_seed"], 1, dtype)
-    cos, sin = tables(pos + 1)
+    cos, sin = gi.golden_rope(ROT, pos + 1)
     model, cache = _model_and_cache(gpu, store, dtype, pos + 64)
     cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
     print(f"golden layer {tag}", flush=True)
@@ -196,7 +196,7 @@ def test_prefill_chunk_matches_golden_reference(gpu):
     store = gi.FakeStore(gi.qsa_weights(3, m["qsa_seeds"][0], dtype))
     keys, values, idx_keys = gi.qsa_past(m["qsa_seeds"][1], past, dtype)
     hidden = gi.hidden_states(m["hidden_seed"], seq, dtype)
-    cos, sin = tables(past + seq)
+    cos, sin = gi.golden_rope(ROT, past + seq)
     model, cache = _model_and_cache(gpu, store, dtype, past + seq)
     cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
     qg, k, v, _, _ = _projections(store, hidden)
@@ -310,6 +310,8 @@ def test_consecutive_decode_steps_cross_a_block_boundary(gpu):
     gen = model._ws["qsa_decode_3_1"].view(torch.int32).cpu()[: 2 * 32].reshape(2, 32)
     assert gen[:, 0].tolist() == [6, 6]
     assert gen[:, 1].tolist() == [0, 0]
+    assert gen[:, 2].tolist() == [0, 0]      # no position outran the launch's splits
+    model.check_handoffs()
 
 
 @pytest.mark.parametrize("pos", [63, 127, 2047, 4095, 8127, 8128, 300, 9000, 20031])

@@ -1,7 +1,8 @@
 """Top-k of the block selection (qm_qsa_select, reference/model.py:297-326):
 the ids the kernel selects must be the reference's top-k of the kernel's own
 block scores, ties to the lower block index. The scores themselves are pinned
-bit for bit elsewhere; here the inputs are shaped to drive each ranking path:
+bit for bit against the reference's score vectors in test_gpu_pins.py; here
+the inputs are shaped to drive each ranking path:
 counting (up to 128 blocks), the bucket threshold over the scores' range
 (typically topk plus a few candidates), and radix select where more than 128
 keys crowd the threshold bucket (equal, clustered or mostly-zero scores, one

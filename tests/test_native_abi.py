@@ -139,3 +139,28 @@ def test_rope_tables_bit_identical_to_reference(qm):
     cos, sin = rope.rope_tables_cpu(32768, 64, 1e7, [11, 11, 10])
     assert gi.digest(cos) == meta["digests"]["rope"]["cos_sha"]
     assert gi.digest(sin) == meta["digests"]["rope"]["sin_sha"]
+
+
+def test_decode_group_guard(qm):
+    """qm_qsa_decode's workgroups of one (sequence, kv head) group wait for one
+    another, so a group must fit the device's resident capacity: the guard is
+    pure host arithmetic (no launch), checked here at the sizes that matter --
+    66 items at pos 8128, 514 at top-k 256 of 64-token blocks against a device
+    of 256 compute units holding two workgroups each."""
+    lib = qm.native.load()
+    UNSUPPORTED, ARG = -5, -1
+    assert lib.qm_qsa_decode_group(7) == 64 and lib.qm_qsa_decode_group(66) == 66
+    assert lib.qm_qsa_decode_fits(66, 512) == 0
+    assert lib.qm_qsa_decode_fits(512, 512) == 0
+    assert lib.qm_qsa_decode_fits(514, 512) == UNSUPPORTED
+    assert b"resident" in lib.qm_last_error()
+    assert lib.qm_qsa_decode_fits(7, 63) == UNSUPPORTED      # widened to 64 slice holders
+    assert lib.qm_qsa_decode_fits(0, 512) == ARG
+    assert lib.qm_qsa_decode_fits(1025, 4096) == ARG
+
+
+def test_causal_conv1d_rejects_bad_arguments_before_launch(qm):
+    lib = qm.native.load()
+    assert lib.qm_causal_conv1d(1, 1, 8, 4, 9, None, None, None, 1, None, None, None) == -1   # taps > 8
+    assert lib.qm_causal_conv1d(1, 1, 8, 4, 4, None, None, None, 1, None, None, None) == -1   # null x
+    assert lib.qm_causal_conv1d(7, 1, 8, 0, 4, None, None, 1, 1, None, None, None) == -2      # dtype

@@ -264,11 +264,14 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
         __builtin_amdgcn_s_sleep(1);
       }
     }
+    // a wait that gave up counts itself (qm_dn_decode_check) and leaves NaN,
+    // never an output normalised by a partial sum
     if (!done && lane == 0) __hip_atomic_fetch_add(line + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (s == 0 && lane == 0) st_flag(line, gen + 1);
     if (tid < DN_DCOLS) {
       const float rn = rsqrt_rn(ss_all / (float)DN_D + A.eps);
-      Act<T>::store(A.out, (long)b * A.hv * DN_D + h * DN_D + col0 + tid, (nw * (o * rn)) * sigmoid_f(zv));
+      const float y = (nw * (o * rn)) * sigmoid_f(zv);
+      Act<T>::store(A.out, (long)b * A.hv * DN_D + h * DN_D + col0 + tid, done ? y : __builtin_nanf(""));
     }
   }
 }
@@ -429,6 +432,26 @@ extern "C" size_t qm_dn_decode_workspace(int batch, int n_v_heads, int head_dim)
   // the gated norm's sum of squares
   if (batch <= 0 || n_v_heads <= 0 || head_dim <= 0) return 0;
   return qm_align256((size_t)batch * n_v_heads * DN_SYNC_WORDS * sizeof(unsigned));
+}
+
+extern "C" int qm_dn_decode_check(int batch, int n_v_heads, int head_dim, void* workspace, size_t workspace_bytes,
+                                  int reset, unsigned* giveups, hipStream_t stream) {
+  if (!workspace || !giveups) return qm_fail(QM_ERR_ARG, "qm_dn_decode_check: null pointer");
+  const size_t need = qm_dn_decode_workspace(batch, n_v_heads, head_dim);
+  if (need == 0 || workspace_bytes < need) return qm_fail(QM_ERR_WORKSPACE, "qm_dn_decode_check: workspace too small");
+  const long n_lines = (long)batch * n_v_heads;
+  unsigned* host = new unsigned[n_lines * DN_SYNC_WORDS];
+  hipError_t e = hipMemcpyAsync(host, workspace, n_lines * DN_SYNC_WORDS * sizeof(unsigned), hipMemcpyDeviceToHost,
+                                stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) {
+    delete[] host;
+    return qm_fail(QM_ERR_LAUNCH, hipGetErrorString(e));
+  }
+  *giveups = 0;
+  for (long i = 0; i < n_lines; ++i) *giveups += host[i * DN_SYNC_WORDS + 1];
+  delete[] host;
+  return reset ? qm_zero_words(workspace, n_lines * DN_SYNC_WORDS, stream) : QM_OK;
 }
 
 extern "C" int qm_dn_decode(const qm_dn_geom* g, const void* qkv, const void* z, const void* a, const void* b,

@@ -257,70 +257,80 @@ __device__ __forceinline__ unsigned long long sel_key(float s, int j) {
 // .y = lo | hi << 8. items[row][0].x holds the item count.
 __device__ __forceinline__ int2 make_item(int phys_row, int lo, int hi) { return make_int2(phys_row, lo | (hi << 8)); }
 
-// Block scores, 32 blocks per pass of a 256-thread block: the 8 lanes of
-// block j = 32 * pass + t / 8 hold its 16-byte channel chunks part, part + 8,
-// part + 16, part + 24 (part = t % 8), so every load instruction reads whole
-// 128-byte lines, and the lanes add their partial dot products with three DPP
-// exchanges (all 8 lanes end with the same sum: float addition commutes). Each
-// lane keeps the matching chunks of the 4 query heads in registers.
-constexpr int SCORE_LANES = 8;                  // NT / 8 blocks per pass of NT threads
-// passes of keys held in registers ahead of use: four at 256 threads; two at
-// 1024, where a thread has 128 VGPRs and four (64 VGPRs) would spill
-template <int NT> constexpr int score_pre() { return NT >= 1024 ? 2 : 4; }
+// Block scores s_j = sum_h relu(q_h . k_j) / sqrt(128) in the summation orders
+// of the reference's CPU path (torch's einsum, reference/model.py:297-298),
+// which the golden score vectors pin bit for bit:
+//  * one query row (a decode step): each dot product is 16 partial sums,
+//    partial m accumulating elements m, m + 16, ..., m + 112 by fused
+//    multiply-add in that order; partials m, m + 4, m + 8, m + 12 are added in
+//    that order into c_(m mod 4); the dot product is (c0 + c1) + (c2 + c3);
+//  * several query rows (a prefill chunk): one fused multiply-add chain over
+//    elements 0 .. 127;
+// then ((relu(D_0) + relu(D_1)) + relu(D_2)) + relu(D_3), divided by sqrt(128)
+// rounded to float.
+//
+// One-row order: 16 lanes per block (a DPP row), lane m holding partial m: its
+// key elements m + 16 i are 8 loads, and a row of lanes reads whole 64-byte
+// runs. The lanes add the partials by row shifts (lane i reads lane i + n).
+constexpr int SCORE_LANES = 16;                 // NT / 16 blocks per pass of NT threads
+// passes of keys held in registers ahead of use: eight at 256 threads (the
+// first 128 blocks); two at 1024, where a thread has 128 VGPRs
+template <int NT> constexpr int score_pre() { return NT >= 1024 ? 2 : 8; }
 
 // (an invalid j loads row 0, always allocated, and zeroes the result: the
 // loads stay unconditional so later waits on them stay exact)
-__device__ __forceinline__ void load_block_part(float4 (&k)[4], const float* bk, int j, bool valid) {
-  const float4* src = reinterpret_cast<const float4*>(bk + (long)(valid ? j : 0) * IDX_D) + (threadIdx.x & 7);
-  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+__device__ __forceinline__ void load_block_part(float (&k)[8], const float* bk, int j, bool valid) {
+  const float* src = bk + (long)(valid ? j : 0) * IDX_D + (threadIdx.x & 15);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float4 v = src[8 * i];
-    k[i] = valid ? v : zero;
+  for (int i = 0; i < 8; ++i) {
+    const float v = src[16 * i];
+    k[i] = valid ? v : 0.f;
   }
 }
 
-// sum over the first idx_heads heads of relu(q_h . k), divided by sqrt(128);
-// q holds this lane's chunks of the 4 query rows (rows past idx_heads unused)
-__device__ __forceinline__ float oct_block_score(const float4 (&q)[4][4], const float4 (&k)[4], int idx_heads) {
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+template <int N>
+__device__ __forceinline__ float row_shl(float v) { return dpp_f<0x100 + N>(v); }
+
+// the one-row score of the block whose 16 lanes call this (valid in lane 0 of
+// the 16); q holds this lane's elements of the 4 query rows
+__device__ __forceinline__ float row16_block_score(const float (&q)[4][8], const float (&k)[8], int idx_heads) {
+  float p[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int h = 0; h < 4; ++h) {
+    p[h] = 0.f;
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      acc[h] = fmaf(q[h][i].x, k[i].x, acc[h]);
-      acc[h] = fmaf(q[h][i].y, k[i].y, acc[h]);
-      acc[h] = fmaf(q[h][i].z, k[i].z, acc[h]);
-      acc[h] = fmaf(q[h][i].w, k[i].w, acc[h]);
-    }
+    for (int i = 0; i < 8; ++i) p[h] = fmaf(q[h][i], k[i], p[h]);
+  }
 #pragma unroll
-  for (int h = 0; h < 4; ++h) acc[h] = acc[h] + dpp_f<0xB1>(acc[h]);      // lane ^ 1
-#pragma unroll
-  for (int h = 0; h < 4; ++h) acc[h] = acc[h] + dpp_f<0x4E>(acc[h]);      // lane ^ 2
-#pragma unroll
-  for (int h = 0; h < 4; ++h) acc[h] = acc[h] + dpp_f<0x141>(acc[h]);     // 7 - lane within 8
+  for (int h = 0; h < 4; ++h) {
+    float c = add_rn(p[h], row_shl<4>(p[h]));
+    c = add_rn(c, row_shl<8>(p[h]));
+    c = add_rn(c, row_shl<12>(p[h]));           // lanes 0..3: c_0 .. c_3
+    const float u = add_rn(c, row_shl<1>(c));     // lane 0: c0 + c1, lane 2: c2 + c3
+    p[h] = add_rn(u, row_shl<2>(u));              // lane 0: the dot product
+  }
   float sc = 0.f;
 #pragma unroll
   for (int h = 0; h < 4; ++h)
-    if (h < idx_heads) sc = add_rn(sc, fmaxf(acc[h], 0.f));
-  return div_rn(sc, 11.313708498984761f);     // sqrt(128)
+    if (h < idx_heads) sc = add_rn(sc, fmaxf(p[h], 0.f));
+  return div_rn(sc, 11.313708498984761f);     // sqrt(128) as a float
 }
 
 // keys[j] = sel_key(score_j, j) for every eligible block j (and scores_out[j]
-// when given), then zeros up to a multiple of 32. kp[u] comes in holding pass
-// u's keys (load_block_part); later passes load PRE passes ahead of use.
-// Block new_j's key is new_key (LDS), not the cache's. s_iq: 4 rows of 128.
+// when given) in the one-row order, then zeros up to a multiple of 32. kp[u]
+// comes in holding pass u's keys (load_block_part); later passes load PRE
+// passes ahead of use. Block new_j's key is new_key (LDS), not the cache's.
+// s_iq: 4 rows of 128.
 template <int NT, int PRE>
 __device__ void score_blocks(const float* s_iq, const float* new_key, const float* bk, int n_elig, int new_j,
-                             int idx_heads, unsigned long long* keys, float* scores_out,
-                             float4 (&kp)[PRE][4]) {
+                             int idx_heads, unsigned long long* keys, float* scores_out, float (&kp)[PRE][8]) {
   constexpr int SCORE_PASS = NT / SCORE_LANES;
-  const int tid = threadIdx.x, jl = tid >> 3, part = tid & 7;
-  float4 q[4][4];
+  const int tid = threadIdx.x, jl = tid >> 4, m = tid & 15;
+  float q[4][8];
 #pragma unroll
   for (int h = 0; h < 4; ++h)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) q[h][i] = reinterpret_cast<const float4*>(s_iq + h * IDX_D)[8 * i + part];
+    for (int i = 0; i < 8; ++i) q[h][i] = s_iq[h * IDX_D + 16 * i + m];
   const int n_pass = (n_elig + SCORE_PASS - 1) / SCORE_PASS;
   for (int ps0 = 0; ps0 < n_pass; ps0 += PRE) {
 #pragma unroll
@@ -329,12 +339,11 @@ __device__ void score_blocks(const float* s_iq, const float* new_key, const floa
       if (ps < n_pass) {
         const int j = ps * SCORE_PASS + jl;
         if (j == new_j) {
-          const float4* src = reinterpret_cast<const float4*>(new_key) + part;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) kp[u][i] = src[8 * i];
+          for (int i = 0; i < 8; ++i) kp[u][i] = new_key[16 * i + m];
         }
-        const float sc = oct_block_score(q, kp[u], idx_heads);
-        if (part == 0 && j < n_elig) {
+        const float sc = row16_block_score(q, kp[u], idx_heads);
+        if (m == 0 && j < n_elig) {
           keys[j] = sel_key(sc, j);
           if (scores_out) scores_out[j] = sc;
         }
@@ -349,15 +358,63 @@ __device__ void score_blocks(const float* s_iq, const float* new_key, const floa
 
 // prefetch of the first PRE passes (issued before the scores are needed)
 template <int NT, int PRE>
-__device__ __forceinline__ void prefetch_block_keys(float4 (&kp)[PRE][4], const float* bk, int n_elig,
-                                                    int new_j, bool on) {
+__device__ __forceinline__ void prefetch_block_keys(float (&kp)[PRE][8], const float* bk, int n_elig, int new_j,
+                                                    bool on) {
   constexpr int SCORE_PASS = NT / SCORE_LANES;
-  const int jl = threadIdx.x >> 3;
+  const int jl = threadIdx.x >> 4;
 #pragma unroll
   for (int u = 0; u < PRE; ++u) {
     const int j = u * SCORE_PASS + jl;
     load_block_part(kp[u], bk, j, on && j < n_elig && j != new_j);
   }
+}
+
+// The several-rows order: one lane per block walks the block's 128 elements in
+// order, 32 at a time, the next 32 in flight; the query rows come from LDS
+// (every lane reads the same address: a broadcast).
+template <int NT>
+__device__ void score_blocks_seq(const float* s_iq, const float* bk, int n_elig, int idx_heads,
+                                 unsigned long long* keys, float* scores_out) {
+  const int tid = threadIdx.x;
+  for (int j0 = 0; j0 < n_elig; j0 += NT) {
+    const int j = j0 + tid;
+    const bool valid = j < n_elig;
+    const float4* row = reinterpret_cast<const float4*>(bk + (long)(valid ? j : 0) * IDX_D);
+    float4 kc[2][8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kc[0][e] = row[e];
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c < 3) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kc[(c + 1) & 1][e] = row[8 * (c + 1) + e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float4 kv = kc[c & 1][e];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const float4 qv = reinterpret_cast<const float4*>(s_iq + h * IDX_D)[8 * c + e];
+          acc[h] = fmaf(qv.x, kv.x, acc[h]);
+          acc[h] = fmaf(qv.y, kv.y, acc[h]);
+          acc[h] = fmaf(qv.z, kv.z, acc[h]);
+          acc[h] = fmaf(qv.w, kv.w, acc[h]);
+        }
+      }
+    }
+    float sc = 0.f;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      if (h < idx_heads) sc = add_rn(sc, fmaxf(acc[h], 0.f));
+    sc = div_rn(sc, 11.313708498984761f);
+    if (valid) {
+      keys[j] = sel_key(sc, j);
+      if (scores_out) scores_out[j] = sc;
+    }
+  }
+  const int npad = (n_elig + 31) & ~31;
+  for (int j = n_elig + tid; j < npad; j += NT) keys[j] = 0ull;
 }
 
 // Top-k of distinct 64-bit keys; sel[rank] = j for rank < topk (rank = the
@@ -578,13 +635,19 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
       if (j >= n_elig) A.scores_out[(long)row * A.max_blocks + j] = -INFINITY;
 
   if (n_elig > A.topk || A.scores_out) {
-    // the first two passes of block keys are in flight across the barrier
     const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
-    float4 kp[score_pre<NT>()][4];
-    prefetch_block_keys<NT>(kp, bk, n_elig, new_j, true);
-    __syncthreads();    // S.q and S.newkey visible
-    score_blocks<NT>(S.q, S.newkey, bk, n_elig, new_j, A.idx_heads, S.key,
-                         A.scores_out ? A.scores_out + (long)row * A.max_blocks : nullptr, kp);
+    float* sc_out = A.scores_out ? A.scores_out + (long)row * A.max_blocks : nullptr;
+    if (A.seq == 1) {
+      // one query row: the first passes of block keys are in flight across the barrier
+      float kp[score_pre<NT>()][8];
+      prefetch_block_keys<NT>(kp, bk, n_elig, new_j, true);
+      __syncthreads();    // S.q and S.newkey visible
+      score_blocks<NT>(S.q, S.newkey, bk, n_elig, new_j, A.idx_heads, S.key, sc_out, kp);
+    } else {
+      // several rows (a block completed in this call is already in the cache)
+      __syncthreads();
+      score_blocks_seq<NT>(S.q, bk, n_elig, A.idx_heads, S.key, sc_out);
+    }
   }
   __syncthreads();
   if (n_elig <= A.topk) {
@@ -1289,6 +1352,7 @@ struct DecShared {
   unsigned long long key[DEC_MAX_BLOCKS];         // selection keys
   float part[SLOTS_ALL];
   float rinv[16];
+  int fault;                                      // the merge saw a wait give up
   float iq[4 * IDX_D];
   float newkey[IDX_D];
   alignas(16) uint16_t knb[QSA_D];                // the token's roped key and its value, bf16
@@ -1367,7 +1431,7 @@ __device__ __forceinline__ void norm_rinv(DecShared& sh, int r0, int r1, float e
 // 128-item chunk is issued before any is used, indices clamped to the last
 // item and weighted by zero past it.
 template <typename T>
-__device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, int g, int sl, int n,
+__device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, int g, int sl, int n, bool poison,
                                      __amdgpu_buffer_rsrc_t ro, __amdgpu_buffer_rsrc_t rml) {
   constexpr int CHUNK = 16;                     // items per thread per round trip (128 per workgroup)
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -1419,7 +1483,8 @@ __device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, 
     float o = red[ch];
 #pragma unroll
     for (int k = 1; k < 8; ++k) o += red[k * 32 + ch];
-    Act<T>::store(D.out, ((long)b * hq + qh) * QSA_D + d, Act<T>::round(o / L) * Act<T>::round(sigmoid_f(gate)));
+    const float y = Act<T>::round(o / L) * Act<T>::round(sigmoid_f(gate));
+    Act<T>::store(D.out, ((long)b * hq + qh) * QSA_D + d, poison ? __builtin_nanf("") : y);
   }
   __syncthreads();
 }
@@ -1430,23 +1495,33 @@ __host__ __device__ inline int dec_flag_stride(int splits) { return splits > DEC
 // Workgroup `item` < DEC_SLICES of group (b, g): wait (wave 0 polling) until
 // the flags of the n_att attending workgroups (workgroup 0 of a widened grid:
 // of all 64 slice holders) have reached gen + 1, advance the generation word
-// (workgroup 0), then merge output slices item, item + step, ...
+// (workgroup 0), then merge output slices item, item + step, ... A wait that
+// gives up counts itself in the group's give-up word and the slices this
+// workgroup merges become NaN (never a merge of missing partials); so do all
+// slices when the position has more items than the launch has workgroups
+// (`overflow`). qm_qsa_decode_check reads and resets both counters.
 template <bool WIDE, typename T>
 __device__ __forceinline__ void decode_merge(const DecArgs<T>& D, DecShared& sh, int b, int g, int item, int n_att,
-                                             unsigned gen) {
+                                             unsigned gen, bool overflow) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int bg = b * D.P.hkv + g;
   const long gbase = (long)bg * D.splits;
   const __amdgpu_buffer_rsrc_t ro = dev_rsrc(D.part_o + gbase * GQA * QSA_D, (long)D.splits * GQA * QSA_D * 2);
   const __amdgpu_buffer_rsrc_t rml = dev_rsrc(D.part_ml + gbase * GQA * 2, (long)D.splits * GQA * 2 * 4);
   const int n_wait = WIDE && item == 0 ? DEC_SLICES : n_att;
-  if (wv == 0 && !wait_flags<DEC_MAX_ITEMS>(D.flags + (long)bg * dec_flag_stride(D.splits), n_wait, gen + 1) &&
-      lane == 0)
-    __hip_atomic_fetch_add(D.gen + (long)bg * DEC_GEN_STRIDE + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (wv == 0) {
+    const bool ok = wait_flags<DEC_MAX_ITEMS>(D.flags + (long)bg * dec_flag_stride(D.splits), n_wait, gen + 1);
+    if (lane == 0) {
+      if (!ok) __hip_atomic_fetch_add(D.gen + (long)bg * DEC_GEN_STRIDE + 1, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+      sh.fault = ok ? 0 : 1;
+    }
+  }
   __syncthreads();
+  const bool poison = overflow || sh.fault != 0;
   if (item == 0 && tid == 0) st_flag(D.gen + (long)bg * DEC_GEN_STRIDE, gen + 1);
   const int step = WIDE ? DEC_SLICES : n_att;
-  for (int sl = item; sl < DEC_SLICES; sl += step) decode_combine_slice(D, sh, b, g, sl, n_att, ro, rml);
+  for (int sl = item; sl < DEC_SLICES; sl += step) decode_combine_slice(D, sh, b, g, sl, n_att, poison, ro, rml);
 }
 
 template <typename T, bool WIDE>
@@ -1503,7 +1578,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
     pg[k] = A.page_table[(long)b * A.max_pages + min(tid + DEC_NT * k, A.max_pages - 1)];
   const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
   const bool scoring = n_elig > topk;
-  float4 kp[score_pre<DEC_NT>()][4];
+  float kp[score_pre<DEC_NT>()][8];
   const bool may_score = D.splits > topk * (ratio >= 32 ? ratio / 32 : 1);
   prefetch_block_keys<DEC_NT>(kp, bk, A.max_blocks, -1, may_score);
   // raw keys of the block this token completes: thread (e128, hh) takes the
@@ -1546,13 +1621,19 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k) sh.pages[tid + DEC_NT * k] = pg[k];
   // a workgroup past the position's items only merges: the waits of this
   // launch cover only the first n_att flags
+  // A position with more items than the launch has workgroups (a plan sized
+  // for smaller positions) cannot be attended: its output is poisoned and
+  // workgroup 0 counts it in the group's word 2.
+  const bool overflow = n_items > D.splits;
   const int n_att = min(n_items, D.splits);
+  if (overflow && item == 0 && tid == 0)
+    __hip_atomic_fetch_add(D.gen + (long)bg * DEC_GEN_STRIDE + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (item >= n_att) {
     if constexpr (WIDE) {
       // a slice holder past the items: flag raised once the word is read
       if (item < DEC_SLICES) {
         if (tid == 0) raise_flag(D.flags + (long)bg * dec_flag_stride(D.splits) + item, gen + 1);
-        decode_merge<WIDE>(D, sh, b, g, item, n_att, gen);
+        decode_merge<WIDE>(D, sh, b, g, item, n_att, gen, overflow);
       }
     }
     return;
@@ -1783,7 +1864,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   wait_all_memory();
   __syncthreads();
   if (tid == 0) raise_flag(D.flags + (long)bg * dec_flag_stride(D.splits) + item, gen + 1);
-  if (item < DEC_SLICES) decode_merge<WIDE>(D, sh, b, g, item, n_att, gen);
+  if (item < DEC_SLICES) decode_merge<WIDE>(D, sh, b, g, item, n_att, gen, overflow);
 }
 
 int check_geom(const qm_qsa_geom* g, const char* who) {
@@ -2158,6 +2239,65 @@ size_t dec_o_bytes(const qm_qsa_geom* g, int splits) {
 }
 }  // namespace
 
+namespace {
+const void* dec_kernel(int act_dtype, bool wide) {
+  if (act_dtype == QM_ACT_F32)
+    return wide ? reinterpret_cast<const void*>(&qsa_decode_kernel<float, true>)
+                : reinterpret_cast<const void*>(&qsa_decode_kernel<float, false>);
+  return wide ? reinterpret_cast<const void*>(&qsa_decode_kernel<bf16_t, true>)
+              : reinterpret_cast<const void*>(&qsa_decode_kernel<bf16_t, false>);
+}
+}  // namespace
+
+extern "C" int qm_qsa_decode_group(int splits) { return splits < DEC_SLICES ? DEC_SLICES : splits; }
+
+extern "C" int qm_qsa_decode_fits(int splits, int resident) {
+  if (splits <= 0 || splits > DEC_MAX_ITEMS)
+    return qm_fail(QM_ERR_ARG, "qm_qsa_decode: splits must be 1..1024 (qm_qsa_decode_splits)");
+  if (qm_qsa_decode_group(splits) > resident)
+    return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_decode: a (sequence, kv head) group of this many workgroups cannot "
+                                       "be resident on the device at once (use qm_qsa_decode_front + "
+                                       "qm_qsa_attend)");
+  return QM_OK;
+}
+
+extern "C" int qm_qsa_decode_resident(int act_dtype, int splits) {
+  if (act_dtype != QM_ACT_F32 && act_dtype != QM_ACT_BF16)
+    return qm_fail(QM_ERR_DTYPE, "qm_qsa_decode_resident: act_dtype must be QM_ACT_F32 or QM_ACT_BF16");
+  int v = 0;
+  const int rc = qm_resident_workgroups(dec_kernel(act_dtype, splits < DEC_SLICES), DEC_NT, 0, &v);
+  return rc ? rc : v;
+}
+
+extern "C" int qm_qsa_decode_check(const qm_qsa_geom* g, int splits, void* workspace, size_t workspace_bytes,
+                                   int reset, unsigned* counts, hipStream_t stream) {
+  int rc = check_geom(g, "qm_qsa_decode_check: null geometry");
+  if (rc) return rc;
+  if (!workspace || !counts) return qm_fail(QM_ERR_ARG, "qm_qsa_decode_check: null pointer");
+  if (splits <= 0 || workspace_bytes < qm_qsa_decode_workspace(g, splits))
+    return qm_fail(QM_ERR_WORKSPACE, "qm_qsa_decode_check: workspace too small for these splits");
+  const long n_groups = (long)g->batch * g->n_kv_heads;
+  unsigned* lines = static_cast<unsigned*>(workspace);
+  unsigned* host = new unsigned[n_groups * DEC_GEN_STRIDE];
+  hipError_t e = hipMemcpyAsync(host, lines, n_groups * DEC_GEN_STRIDE * sizeof(unsigned), hipMemcpyDeviceToHost,
+                                stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) {
+    delete[] host;
+    return qm_fail(QM_ERR_LAUNCH, hipGetErrorString(e));
+  }
+  counts[0] = counts[1] = 0;
+  for (long i = 0; i < n_groups; ++i) {
+    counts[0] += host[i * DEC_GEN_STRIDE + 1];
+    counts[1] += host[i * DEC_GEN_STRIDE + 2];
+  }
+  delete[] host;
+  if (!reset) return QM_OK;
+  // generation words, counters and flags back to zero: the state of a fresh workspace
+  const size_t words = (dec_gen_bytes(g) + dec_flag_bytes(g, splits)) / sizeof(unsigned);
+  return qm_zero_words(workspace, (long)words, stream);
+}
+
 extern "C" size_t qm_qsa_decode_workspace(const qm_qsa_geom* g, int splits) {
   if (!g || splits <= 0) return 0;
   return dec_gen_bytes(g) + dec_flag_bytes(g, splits) + dec_ml_bytes(g, splits) + dec_o_bytes(g, splits);
@@ -2184,6 +2324,13 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
   if (g->batch > 65535) return qm_fail(QM_ERR_ARG, "qm_qsa_decode: batch above 65535");
   if (!workspace || workspace_bytes < qm_qsa_decode_workspace(g, splits))
     return qm_fail(QM_ERR_WORKSPACE, "qm_qsa_decode: workspace too small");
+  // every workgroup of a (sequence, kv head) group waits for the others: the
+  // group must fit on the device at once (groups are dispatched in order, so
+  // one group at a time is enough)
+  const int resident = qm_qsa_decode_resident(g->act_dtype, splits);
+  if (resident < 0) return resident;
+  rc = qm_qsa_decode_fits(splits, resident);
+  if (rc) return rc;
   char* ws = static_cast<char*>(workspace);
   unsigned* gen = reinterpret_cast<unsigned*>(ws);
   unsigned* flags = reinterpret_cast<unsigned*>(ws + dec_gen_bytes(g));

@@ -23,3 +23,11 @@ size_t qm_dn_rule_chunk_workspace(int batch, int seq, int heads);
 int qm_dn_rule_chunk(int act_dtype, int batch, int seq, int heads, int hk, long q_stride, long v_stride,
                      const void* q, const void* k, const void* v, const float* g, const float* beta, float* state,
                      void* out, void* ws, size_t ws_bytes, hipStream_t stream);
+
+// Workgroups of `kernel` (launched with block_threads threads and dyn_lds bytes
+// of dynamic LDS) that can be resident on the current device at once: the
+// occupancy per compute unit times the compute units. Cached per device.
+int qm_resident_workgroups(const void* kernel, int block_threads, size_t dyn_lds, int* out);
+
+// Zero n_words 32-bit words at p with a fill kernel on `stream`.
+int qm_zero_words(void* p, long n_words, hipStream_t stream);

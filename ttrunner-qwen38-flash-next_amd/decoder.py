@@ -135,7 +135,8 @@ class MixDecoder:
     graph of the largest position's bucket, and maps each row's next page
     first when the cache draws its pages from a pool."""
 
-    def __init__(self, model, cache, layers=None, dtype=torch.bfloat16, min_bucket: int = 1024, positions=None):
+    def __init__(self, model, cache, layers=None, dtype=torch.bfloat16, min_bucket: int = 1024, positions=None,
+                 check_every: int = 64):
         c = model.config
         self.model, self.cache, self.dtype = model, cache, dtype
         self.layers = list(range(len(cache.layers))) if layers is None else list(layers)
@@ -158,6 +159,10 @@ class MixDecoder:
         self.positions = torch.tensor(rows, dtype=torch.int32, device=dev)
         self._steps = {}
         self._graphs = {}
+        # every check_every steps (0: never by itself) the decode kernels'
+        # hand-off counters are read back (a sync) and a fault raises QmError
+        self.check_every = check_every
+        self._since_check = 0
 
     # -- buckets of positions (tt/model.py:117-129) ---------------------------
 
@@ -177,6 +182,24 @@ class MixDecoder:
             steps = [_LayerStep(self.model, self.cache, l, bucket, self.positions, self.dtype) for l in self.layers]
             self._steps[bucket] = steps
         return steps
+
+    # -- hand-off health ----------------------------------------------------------
+
+    def check_handoffs(self, reset: bool = True) -> None:
+        """Read every plan's hand-off counters (a sync) and raise QmError if a
+        wait gave up or a position outran its plan since the last check."""
+        faults = []
+        for steps in self._steps.values():
+            for st in steps:
+                faults += st.core.check(reset)
+        self._since_check = 0
+        if faults:
+            raise native.QmError("decode hand-off failed: " + "; ".join(faults))
+
+    def _count_step(self):
+        self._since_check += 1
+        if self.check_every and self._since_check >= self.check_every:
+            self.check_handoffs()
 
     # -- one step ----------------------------------------------------------------
 
@@ -199,6 +222,16 @@ class MixDecoder:
             self.positions.fill_(rows[0])          # a device fill, no host copy on the stream
         else:
             self.positions.copy_(torch.tensor(rows, dtype=torch.int32))
+        # the layer caches' bookkeeping follows, so that the layer methods
+        # (step_n) run every layer at the new position: the DeltaNet cores take
+        # theirs from n_tokens, and no block past the position counts as pooled
+        ratio = self.model.config.indexer_compress_ratio
+        for l in self.layers:
+            lc = self.cache[l]
+            lc.n_tokens = self.position
+            lc.blocks_valid = min(lc.blocks_valid, self.position // ratio)
+        if len(self.cache.slot_tokens) == len(rows):
+            self.cache.slot_tokens[:] = rows
 
     def _map_pages(self, n: int):
         """Pages for every row's next n tokens (a no-op for static tables)."""
@@ -231,6 +264,7 @@ class MixDecoder:
         steps = self._layer_steps(self.bucket(self.position))
         self._launch(steps, torch.cuda.current_stream(self.model.device).cuda_stream)
         self._advance(1, host_only=False)
+        self._count_step()
         return self.hyper
 
     def graph(self, bucket: int) -> torch.cuda.CUDAGraph:
@@ -261,6 +295,7 @@ class MixDecoder:
         self._map_pages(1)
         self.graph(self.bucket(self.position)).replay()
         self._advance(1, host_only=False)
+        self._count_step()
         return self.hyper
 
     # -- k tokens of one sequence (tt/model.py:2135-2165) ----------------------

@@ -43,6 +43,7 @@ class Qwen4MixModel:
         self.rope = RopeTable(self.config.rope_dim, self.config.rope_theta, self.config.mrope_section, self.device)
         self._dev = {}
         self._ws = {}
+        self._handoff = {}      # decode workspaces whose hand-off counters check_handoffs() reads
         native.load()
 
     # -- weights (reference/model.py:45-49) -----------------------------------
@@ -229,7 +230,8 @@ class Qwen4MixModel:
                 native.ptr(lc.recurrent_state), native.ptr(out))
         if seq == 1:
             nbytes = native.load().qm_dn_decode_workspace(batch, c.linear_num_v_heads, c.linear_head_dim)
-            ws = self._workspace("dn_decode", nbytes)
+            ws = self._workspace(f"dn_decode_{batch}", nbytes)
+            self._handoff[f"dn_decode_{batch}"] = ("dn", batch)
             native.call("qm_dn_decode", ctypes.byref(g), *args, native.ptr(ws), ws.numel(), stream)
         else:
             nbytes = native.load().qm_dn_prefill_workspace(ctypes.byref(g), seq)
@@ -308,12 +310,14 @@ class Qwen4MixModel:
                             device=self.device) if attend and not chunked else None
         norms = [native.ptr(self._dw(layer, n, torch.float32)) for n in
                  ("attn_q_norm.weight", "attn_k_norm.weight", "indexer.q_norm.weight", "indexer.k_norm.weight")]
-        if seq == 1 and qg is not None and k is not None and attend and self.fused_decode_fits(cache):
+        splits = lib.qm_qsa_decode_splits(ctypes.byref(g), query_offset) if seq == 1 else 0
+        if (seq == 1 and qg is not None and k is not None and attend and self.fused_decode_fits(cache)
+                and self.decode_group_fits(splits, dt)):
             # decode: the whole QSA step in one qm_qsa_decode launch; its workspace
             # (generation words, flags, partials) is kept per layer and batch
-            splits = lib.qm_qsa_decode_splits(ctypes.byref(g), query_offset)
-            ws = self._workspace(f"qsa_decode_{layer}_{batch}",
-                                 lib.qm_qsa_decode_workspace(ctypes.byref(g), splits))
+            name = f"qsa_decode_{layer}_{batch}"
+            ws = self._workspace(name, lib.qm_qsa_decode_workspace(ctypes.byref(g), splits))
+            self._handoff[name] = ("qsa", g, splits)
             if out is None:
                 out = torch.empty(batch, seq, c.num_attention_heads * c.head_dim, dtype=dt, device=self.device)
             native.call("qm_qsa_decode", ctypes.byref(g), native.ptr(qg), native.ptr(k), native.ptr(v),
@@ -378,6 +382,34 @@ class Qwen4MixModel:
         return (cache.max_blocks <= 2048 and cache.max_pages <= 2048 and c.block_topk <= 256
                 and c.indexer_compress_ratio <= 64)
 
+    def decode_group_fits(self, splits: int, dtype) -> bool:
+        """Whether a qm_qsa_decode group of ``splits`` workgroups can be resident
+        on the device at once (its workgroups wait for one another); larger
+        plans go through qm_qsa_decode_front + qm_qsa_attend."""
+        lib = native.load()
+        resident = lib.qm_qsa_decode_resident(native.act_code(dtype), splits)
+        if resident < 0:
+            raise native.QmError(f"qm_qsa_decode_resident failed ({resident}): "
+                                 f"{lib.qm_last_error().decode(errors='replace')}")
+        return lib.qm_qsa_decode_fits(splits, resident) == 0
+
+    def check_handoffs(self, reset: bool = True) -> None:
+        """Read the hand-off counters of every decode workspace this model has
+        used (a sync); raise QmError if a wait gave up or a position outran its
+        plan since the last check (the affected outputs are NaN). ``reset``
+        clears the counters and the hand-off words either way."""
+        c = self.config
+        faults = []
+        for name, spec in self._handoff.items():
+            ws = self._ws[name]
+            if spec[0] == "dn":
+                faults += native.dn_decode_faults(spec[1], c.linear_num_v_heads, c.linear_head_dim, ws, reset,
+                                                  name, self.device)
+            else:
+                faults += native.qsa_decode_faults(spec[1], spec[2], ws, reset, name, self.device)
+        if faults:
+            raise native.QmError("decode hand-off failed: " + "; ".join(faults))
+
     def _full_attention(self, hidden, layer: int, cos, sin, cache, query_offset: int) -> torch.Tensor:
         """reference/model.py:331-383."""
         batch, seq, _ = hidden.shape
@@ -394,12 +426,15 @@ class Qwen4MixModel:
         ratio = c.indexer_compress_ratio
         ids, n_sel = lc.last_ids.long(), lc.last_n_sel.long()
         batch, seq, k = ids.shape
-        mask = torch.zeros(batch, seq, kv_len, dtype=torch.bool, device=self.device)
+        # one spare column takes the unused ranks' writes, so every write to a
+        # real column is True and duplicate indices cannot race
+        mask = torch.zeros(batch, seq, kv_len + 1, dtype=torch.bool, device=self.device)
         valid = torch.arange(k, device=self.device)[None, None] < n_sel[..., None]
         tok = (ids[..., None] * ratio + torch.arange(ratio, device=self.device)).flatten(2)
         keep = valid[..., None].expand(-1, -1, -1, ratio).flatten(2)
-        tok = torch.where(keep, tok, torch.zeros_like(tok))
-        mask.scatter_(2, tok, keep)
+        tok = torch.where(keep, tok, torch.full_like(tok, kv_len))
+        mask.scatter_(2, tok, torch.ones_like(keep))
+        mask = mask[..., :kv_len]
         qpos = torch.arange(seq, device=self.device) + query_offset
         tail_start = ((qpos + 1) // ratio) * ratio
         kpos = torch.arange(kv_len, device=self.device)

@@ -48,6 +48,8 @@ SIGNATURES = {
     "qm_dn_decode_workspace": (_sz, [_i, _i, _i]),
     "qm_dn_decode": (_i, [ctypes.POINTER(DnGeom), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                           _vp, _sz, _vp]),
+    "qm_dn_decode_check": (_i, [_i, _i, _i, _vp, _sz, _i, _vp, _vp]),
+    "qm_causal_conv1d": (_i, [_i, _i, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp]),
     "qm_dn_recurrent": (_i, [_i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "qm_dn_chunked_workspace": (_sz, [_i, _i, _i, _i]),
     "qm_dn_chunked": (_i, [_i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
@@ -57,6 +59,10 @@ SIGNATURES = {
     "qm_qsa_items_stride": (_i, [ctypes.POINTER(QsaGeom)]),
     "qm_qsa_decode_splits": (_i, [ctypes.POINTER(QsaGeom), _i]),
     "qm_qsa_decode_workspace": (_sz, [ctypes.POINTER(QsaGeom), _i]),
+    "qm_qsa_decode_group": (_i, [_i]),
+    "qm_qsa_decode_resident": (_i, [_i, _i]),
+    "qm_qsa_decode_fits": (_i, [_i, _i]),
+    "qm_qsa_decode_check": (_i, [ctypes.POINTER(QsaGeom), _i, _vp, _sz, _i, _vp, _vp]),
     "qm_qsa_decode": (_i, [ctypes.POINTER(QsaGeom)] + [_vp] * 18 + [_i, _vp, _sz, _vp, _vp, _vp, _vp, _vp]),
     "qm_qsa_decode_front": (_i, [ctypes.POINTER(QsaGeom)] + [_vp] * 22 + [_vp]),
     "qm_qsa_select": (_i, [ctypes.POINTER(QsaGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -124,3 +130,24 @@ def act_code(dtype) -> int:
     if dtype == torch.bfloat16:
         return QM_ACT_BF16
     raise QmError(f"unsupported activation dtype {dtype}; use float32 or bfloat16")
+
+
+def dn_decode_faults(batch: int, n_v_heads: int, head_dim: int, ws, reset: bool, name: str, device=None) -> list:
+    """Messages for the give-ups qm_dn_decode_check finds in a decode workspace."""
+    n = ctypes.c_uint(0)
+    call("qm_dn_decode_check", batch, n_v_heads, head_dim, ws.data_ptr(), ws.numel(), int(reset), ctypes.byref(n),
+         stream_handle(device))
+    return [f"{name}: {n.value} DeltaNet decode waits gave up"] if n.value else []
+
+
+def qsa_decode_faults(geom, splits: int, ws, reset: bool, name: str, device=None) -> list:
+    """Messages for the give-ups and overflows qm_qsa_decode_check finds."""
+    counts = (ctypes.c_uint * 2)()
+    call("qm_qsa_decode_check", ctypes.byref(geom), splits, ws.data_ptr(), ws.numel(), int(reset), counts,
+         stream_handle(device))
+    out = []
+    if counts[0]:
+        out.append(f"{name}: {counts[0]} QSA decode waits gave up")
+    if counts[1]:
+        out.append(f"{name}: {counts[1]} QSA decode launches had more attention items than their {splits} splits")
+    return out

@@ -37,6 +37,12 @@ class DnDecodePlan:
                                                           ("ssm_conv1d.weight", dtype),
                                                           ("ssm_norm.weight", torch.float32))}
 
+    def check(self, reset: bool = True) -> list:
+        """Hand-off faults of this plan's launches since the last check (a sync)."""
+        c = self.model.config
+        return native.dn_decode_faults(self.geom.batch, c.linear_num_v_heads, c.linear_head_dim, self.ws, reset,
+                                       f"layer {self.layer}", self.model.device)
+
     def run(self, qkv, z, a, b, stream=None):
         w, lc = self.w, self.lc
         native.call("qm_dn_decode", ctypes.byref(self.geom), qkv.data_ptr(), z.data_ptr(), a.data_ptr(),
@@ -64,8 +70,10 @@ class QsaDecodePlan:
         self.splits = lib.qm_qsa_attend_splits(ctypes.byref(self.geom), max_position, max_position)
         self.ws = torch.zeros(lib.qm_qsa_attend_workspace(ctypes.byref(self.geom), 1, self.splits),
                               dtype=torch.uint8, device=dev)
-        self.fused = model.fused_decode_fits(cache)
         self.dec_splits = lib.qm_qsa_decode_splits(ctypes.byref(self.geom), max_position)
+        # one launch when the geometry allows it and a group of dec_splits
+        # workgroups fits the device at once; else the front + attend launches
+        self.fused = model.fused_decode_fits(cache) and model.decode_group_fits(self.dec_splits, dtype)
         self.dec_ws = torch.zeros(lib.qm_qsa_decode_workspace(ctypes.byref(self.geom), self.dec_splits),
                                   dtype=torch.uint8, device=dev)
         self.positions = torch.zeros(batch, dtype=torch.int32, device=dev)
@@ -114,7 +122,7 @@ class QsaDecodePlan:
                     self.splits, self.ws.data_ptr(), self.ws.numel(), stream)
 
     def decode(self, qg, k, v, iq, ik, stream):
-        """The whole step (qm_qsa_decode: an attention launch and a combine launch)."""
+        """The whole step in one qm_qsa_decode launch."""
         lc, w = self.lc, self.w
         native.call("qm_qsa_decode", ctypes.byref(self.geom), qg.data_ptr(), k.data_ptr(), v.data_ptr(),
                     iq.data_ptr(), ik.data_ptr(), w["attn_q_norm.weight"].data_ptr(),
@@ -123,6 +131,14 @@ class QsaDecodePlan:
                     self.positions.data_ptr(), lc.page_table.data_ptr(), lc.k_pool.data_ptr(),
                     lc.v_pool.data_ptr(), lc.raw_keys.data_ptr(), lc.block_keys.data_ptr(), self.out.data_ptr(),
                     self.dec_splits, self.dec_ws.data_ptr(), self.dec_ws.numel(), None, None, None, None, stream)
+
+    def check(self, reset: bool = True) -> list:
+        """Hand-off faults of this plan's fused launches since the last check
+        (a sync): waits that gave up, positions beyond the plan's splits."""
+        if not self.fused:
+            return []
+        return native.qsa_decode_faults(self.geom, self.dec_splits, self.dec_ws, reset, f"layer {self.layer}",
+                                        self.model.device)
 
     def run(self, qg, k, v, iq, ik, stream=None):
         s = stream if stream is not None else native.stream_handle(self.model.device)

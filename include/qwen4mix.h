@@ -143,6 +143,21 @@ int qm_dn_prefill(const qm_dn_geom* g, int seq, const void* qkv, const void* z, 
                   const int* positions, void* conv_ring, float* state, void* out, void* workspace,
                   size_t workspace_bytes, hipStream_t stream);
 
+/* qm_dn_prefill without a workspace argument: the same kernels, with the
+ * library's own scratch, one array of qm_dn_prefill_noalloc_max_bytes()
+ * (32 MiB) per device, held until the process ends. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, serving loops that forbid hipMalloc); it calls no hipMalloc/hipFree.
+ * A chunk whose qm_dn_prefill_workspace() exceeds the scratch (about 256
+ * tokens at batch 1 and 32 value heads) is refused with QM_ERR_UNSUPPORTED.
+ * Every call on one device shares that device's array: calls that overlap on
+ * one GPU (other streams, other threads) race. */
+int qm_dn_prefill_noalloc(const qm_dn_geom* g, int seq, const void* qkv, const void* z, const void* a, const void* b,
+                          const float* a_neg, const float* dt_bias, const void* conv_w, const float* norm_w,
+                          const int* positions, void* conv_ring, float* state, void* out, hipStream_t stream);
+/* Bytes of the built-in scratch of qm_dn_prefill_noalloc. */
+size_t qm_dn_prefill_noalloc_max_bytes(void);
+
 /* ------------------------------------------------------------------------ */
 /* QSA (Qwen Sparse Attention)                                              */
 /* ------------------------------------------------------------------------ */

@@ -164,3 +164,13 @@ def test_causal_conv1d_rejects_bad_arguments_before_launch(qm):
     assert lib.qm_causal_conv1d(1, 1, 8, 4, 9, None, None, None, 1, None, None, None) == -1   # taps > 8
     assert lib.qm_causal_conv1d(1, 1, 8, 4, 4, None, None, None, 1, None, None, None) == -1   # null x
     assert lib.qm_causal_conv1d(7, 1, 8, 0, 4, None, None, 1, 1, None, None, None) == -2      # dtype
+
+
+def test_noalloc_prefill_refuses_chunks_beyond_its_scratch(qm):
+    """qm_dn_prefill_noalloc's size guard is host arithmetic: nothing launches."""
+    lib = qm.native.load()
+    g = qm.native.DnGeom(1, 32, 16, 128, 4, qm.native.QM_ACT_BF16, 1e-6)
+    assert lib.qm_dn_prefill_noalloc_max_bytes() == 32 << 20
+    assert lib.qm_dn_prefill_workspace(ctypes.byref(g), 128) <= lib.qm_dn_prefill_noalloc_max_bytes()
+    rc = lib.qm_dn_prefill_noalloc(ctypes.byref(g), 4096, *([1] * 12), None)
+    assert rc == -5 and b"scratch" in lib.qm_last_error()

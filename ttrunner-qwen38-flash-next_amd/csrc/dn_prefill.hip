@@ -11,6 +11,8 @@
 //   delta rule      the WY/UT chunked kernels (dn_chunk.hip) for chunks of 16
 //                   tokens or more, the token loop for shorter ones
 //   dn_gated_norm   one wavefront per (token, head) row of 128
+#include <atomic>
+
 #include "common.h"
 #include "qwen4mix_internal.h"
 
@@ -180,6 +182,56 @@ int launch_prefill(const qm_dn_geom* g, int seq, const void* qkv, const void* z,
 }
 
 }  // namespace
+
+// The allocation-free variant's workspace: one array per device, for the
+// whole process. Its address on each device comes from hipGetSymbolAddress
+// (the array's name in host code is only a stand-in); calls on one device
+// share it, so they must not overlap.
+constexpr size_t NOALLOC_SCRATCH_BYTES = 32ull << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::atomic<void*> g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// the current device's address of `scratch`, looked up once per device
+int scratch_on_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+    return qm_fail(QM_ERR_LAUNCH, "qm_dn_prefill_noalloc: no current HIP device");
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return qm_fail(QM_ERR_LAUNCH, "qm_dn_prefill_noalloc: hipGetSymbolAddress failed");
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return QM_OK;
+}
+
+}  // namespace
+
+extern "C" size_t qm_dn_prefill_noalloc_max_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int qm_dn_prefill_noalloc(const qm_dn_geom* g, int seq, const void* qkv, const void* z, const void* a,
+                                     const void* b, const float* a_neg, const float* dt_bias, const void* conv_w,
+                                     const float* norm_w, const int* positions, void* conv_ring, float* state,
+                                     void* out, hipStream_t stream) {
+  if (!g) return qm_fail(QM_ERR_ARG, "qm_dn_prefill_noalloc: null geometry");
+  if (g->batch <= 0 || seq <= 0) return qm_fail(QM_ERR_ARG, "qm_dn_prefill_noalloc: bad sizes");
+  const size_t need = qm_dn_prefill_workspace(g, seq);
+  if (need > NOALLOC_SCRATCH_BYTES)
+    return qm_fail(QM_ERR_UNSUPPORTED, "qm_dn_prefill_noalloc: this batch * seq needs more than the 32 MiB of "
+                                       "built-in scratch (about 256 tokens at 32 heads; use qm_dn_prefill with a "
+                                       "workspace)");
+  void* ws = nullptr;
+  const int rc = scratch_on_device(&ws);
+  if (rc) return rc;
+  return qm_dn_prefill(g, seq, qkv, z, a, b, a_neg, dt_bias, conv_w, norm_w, positions, conv_ring, state, out, ws,
+                       NOALLOC_SCRATCH_BYTES, stream);
+}
 
 extern "C" size_t qm_dn_prefill_workspace(const qm_dn_geom* g, int seq) {
   if (!g || seq <= 0) return 0;

@@ -77,6 +77,8 @@ SIGNATURES = {
     "qm_dn_prefill_workspace": (_sz, [ctypes.POINTER(DnGeom), _i]),
     "qm_dn_prefill": (_i, [ctypes.POINTER(DnGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _vp, _sz, _vp]),
+    "qm_dn_prefill_noalloc": (_i, [ctypes.POINTER(DnGeom), _i] + [_vp] * 12 + [_vp]),
+    "qm_dn_prefill_noalloc_max_bytes": (_sz, []),
     "qm_hc_mix_workspace": (_sz, [ctypes.POINTER(HcGeom)]),
     "qm_hc_mix": (_i, [ctypes.POINTER(HcGeom), _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     "qm_hc_reinject": (_i, [ctypes.POINTER(HcGeom), _vp, _vp, _vp, _vp, _vp]),

@@ -9,14 +9,17 @@ one DeltaNet decode core (conv ring, gates, delta-rule update of the
 resident in HBM, and rotated over enough independent layer instances that the
 data touched per rotation exceeds twice the 256 MB Infinity Cache.
 
-Prints one JSON line (see the driver contract); ``--sweep`` adds per-position
-lines (192, 1984, 4032, 8128), the 128-token prefill chunk, the layer
-projections around the core at one token (qm_gemv, weights streamed from HBM),
-the hyper-connection mix and reinjection at one token, and one token through
-the token-mixing halves of a 48-layer stack (36 DeltaNet + 12 QSA layers, each
-with its mix, projections and reinjection) launched eagerly and replayed from
-a HIP graph, to stderr and to the line's "sweep" object. ``--part stack`` or
-``--part hc`` times only that part.
+Prints one JSON line (see the driver contract). Besides the headline, its
+"configs" list holds every workload of the benchmark's configuration set, each
+next to the CPU oracle timed on this host's cores: the decode step at
+positions 192, 1984 and 4032 (and 8128, the headline), the 128-token prefill
+chunk at 32640..32767 of a 32768-token context (QSA and DeltaNet, with MFMA
+utilisation), and the chunked delta rule over 4096 tokens. ``--head-only``
+skips them. ``--sweep`` adds the layer projections around the core at one
+token (qm_gemv, weights streamed from HBM), the hyper-connection mix and
+reinjection, and one token through the token-mixing halves of a 48-layer stack
+(36 DeltaNet + 12 QSA layers) launched eagerly and replayed from a HIP graph.
+``--part stack`` or ``--part hc`` times only that part.
 """
 
 from __future__ import annotations
@@ -34,6 +37,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK = 2.5e15          # dense bf16 FLOP/s
+MFMA_F32_PEAK = 157.3e12         # dense fp32 FLOP/s (the chunked delta rule's v_mfma_f32_16x16x4_f32)
 METRIC = "attention µs/token at batch 1, pos 8128 (QSA sel on + DeltaNet); % HBM roofline"
 
 # algorithmic bytes (bf16 KV and activations, float32 DeltaNet state)
@@ -80,9 +84,11 @@ def parse():
     ap.add_argument("--position", type=int, default=8128)
     ap.add_argument("--instances", type=int, default=0, help="rotated layer instances (0: auto, > 512 MB)")
     ap.add_argument("--sweep", action="store_true",
-                    help="also time positions 192/1984/4032, a prefill chunk and the layer projections")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+                    help="also time the layer projections, the hyper-connections and the 48-layer stack")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--cpu-seconds", type=float, default=5.0, help="CPU oracle time per decode config")
+    ap.add_argument("--head-only", action="store_true",
+                    help="time only the headline workload (no other configs), e.g. under a profiler")
     ap.add_argument("--part", choices=("stack", "hc"), default=None,
                     help="time only this part (the token-mixing layer stack, or the hyper-connection mix) and "
                          "print its result as one JSON line")
@@ -221,17 +227,49 @@ def time_kernels(instances, reps, stream_obj, batches=5):
     return out
 
 
-def cpu_baseline(position: int, seconds: float):
-    """The oracle (torch CPU restatement of the reference layers) on this host."""
+def host_cpu() -> dict:
+    """The host's CPU model and the threads the CPU baselines use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "threads": os.cpu_count() or 1}
+
+
+def _oracle_env():
     import torch
     sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    torch.set_num_threads(os.cpu_count() or 1)
+
+
+def _time_cpu(fn, seconds: float, min_runs: int = 3, warm: int = 1):
+    for _ in range(warm):
+        fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < min_runs:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(position: int, seconds: float):
+    """The oracle (torch CPU restatement of the reference layers) on this host:
+    one QSA decode core at `position` (indexer + the reference's dense masked
+    softmax) plus one DeltaNet decode core, bf16, median over ~`seconds`."""
+    import torch
+    _oracle_env()
     import inputs as gi
     from oracle.cache import OracleHybridCache
     from oracle.config import OracleConfig
     from oracle.layers import RotaryEmbedding
     from oracle.mixing import OracleMixer
-    threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
     dt = torch.bfloat16
     cfg = OracleConfig()
     qstore = gi.FakeStore(gi.qsa_weights(3, 90, dt))
@@ -262,22 +300,91 @@ def cpu_baseline(position: int, seconds: float):
         dm_.dn_core(*proj_d[:2], proj_d[2], proj_d[3], 0, dc)
         return out
 
-    for _ in range(3):
-        one()
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 5:
-        t0 = time.perf_counter()
-        one()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times) * 1e6
-    return {"value": round(med, 1), "unit": "µs/token", "cores": threads, "kind": "port",
-            "sample": f"{len(times)} steps of the oracle's QSA core at pos {position} (indexer + dense masked "
-                      f"softmax, as the reference computes it) + DeltaNet decode core, bf16, median"}
+    med, n = _time_cpu(one, seconds, min_runs=5, warm=3)
+    host = host_cpu()
+    return {"value": round(med * 1e6, 1), "unit": "µs/token", "cores": host["threads"], "kind": "port",
+            "cpu_model": host["cpu_model"],
+            "sample": f"{n} steps of the oracle's QSA core at pos {position} (indexer + dense masked softmax, as "
+                      f"the reference computes it) + DeltaNet decode core, bf16, median"}
+
+
+def cpu_prefill_chunk(seconds: float):
+    """The oracle's 128-token chunk at 32640..32767: the QSA core (per-query
+    indexer top-32 + the reference's dense masked softmax over 32768 keys) and
+    the DeltaNet core (chunked rule continuing a state), bf16."""
+    import torch
+    _oracle_env()
+    import inputs as gi
+    from oracle.cache import OracleHybridCache
+    from oracle.config import OracleConfig
+    from oracle.layers import RotaryEmbedding
+    from oracle.mixing import OracleMixer
+    dt = torch.bfloat16
+    cfg = OracleConfig()
+    past, S = PREFILL_START, PREFILL_LEN
+    qstore = gi.FakeStore(gi.qsa_weights(3, 95, dt))
+    dstore = gi.FakeStore(gi.dn_weights(0, 96, dt))
+    keys, values, idx = gi.qsa_past(97, past, dt)
+    conv, state = gi.dn_past(98, dt)
+    rot = RotaryEmbedding(64, 1e7, [11, 11, 10])
+    p = torch.arange(past + S)[None]
+    cos, sin = rot(p[None].expand(3, -1, -1))
+    qm_, dm_ = OracleMixer(cfg, qstore), OracleMixer(cfg, dstore)
+    F = torch.nn.functional
+    hidden = gi.hidden_states(99, S, dt)
+    proj_d = [F.linear(hidden, dstore.get(f"blk.0.{n}")) for n in
+              ("attn_qkv.weight", "attn_gate.weight", "ssm_beta.weight", "ssm_alpha.weight")]
+
+    def qsa():
+        oc = OracleHybridCache(4)
+        oc[3].keys, oc[3].values, oc[3].indexer_keys = keys, values, idx
+        q, k, v, gate = qm_.qkv_prep(hidden, 3, cos, sin)
+        K, V = torch.cat([keys, k], 2), torch.cat([values, v], 2)
+        mask = qm_._indexer_mask(hidden, 3, cos, sin, oc, past + S, past)
+        kpos = torch.arange(past + S)
+        allowed = (kpos[None, :] <= (torch.arange(S)[:, None] + past))[None, None] & mask
+        return qm_.attention_core(q, K, V, allowed, dt)
+
+    def dn():
+        dc = OracleHybridCache(1)
+        dc[0].conv_state, dc[0].recurrent_state = conv, state
+        return dm_.dn_core(*proj_d[:2], proj_d[2], proj_d[3], 0, dc)
+
+    tq, nq = _time_cpu(qsa, seconds, min_runs=2)
+    td, nd = _time_cpu(dn, seconds / 2, min_runs=3)
+    host = host_cpu()
+    return {"qsa_ms": round(tq * 1e3, 2), "dn_ms": round(td * 1e3, 2), "unit": "ms/chunk",
+            "cores": host["threads"], "kind": "port", "cpu_model": host["cpu_model"],
+            "sample": f"median of {nq} QSA and {nd} DeltaNet chunk cores of the oracle, bf16"}
+
+
+def cpu_dn_4096(seconds: float):
+    """The oracle's chunked delta rule (reference/layers.py:195-275) over the
+    4096-token, 32-head float32 inputs of the delta-rule configuration."""
+    import torch
+    _oracle_env()
+    import inputs as gi
+    from oracle.layers import chunk_gated_delta_rule
+    q, k, v, g, beta = gi.delta_rule_inputs(404, DN_LONG)
+    s0 = gi.dn_past(405)[1]
+    t, n = _time_cpu(lambda: chunk_gated_delta_rule(q, k, v, g, beta, initial_state=s0), seconds, min_runs=1,
+                     warm=0)
+    host = host_cpu()
+    return {"value": round(t * 1e3, 1), "unit": f"ms per {DN_LONG} tokens", "cores": host["threads"],
+            "kind": "port", "cpu_model": host["cpu_model"],
+            "sample": f"median of {n} runs of the oracle's chunk_gated_delta_rule, float32, 32 heads"}
 
 
 SWEEP_POSITIONS = (192, 1984, 4032, 8128)
 PREFILL_START, PREFILL_LEN, PREFILL_CTX = 32640, 128, 32768
+DN_LONG = 4096                 # tokens of the chunked delta-rule workload
+DN_CHUNK_FLOPS = 5 * 2 * 64 * 64 * 128 + 64 ** 3 + 3 * 2 * 64 * 128 * 128   # per (64-token chunk, head)
+
+
+def dn_rule_flops(seq: int, heads: int = 32) -> int:
+    """Algorithmic FLOPs of the chunked delta rule: per (64-token chunk, head)
+    five C x C x d products, the forward substitution and three C x d x d products."""
+    return ((seq + 63) // 64) * heads * DN_CHUNK_FLOPS
 
 
 def qsa_chunk_flops(start: int, n: int, ratio: int = 64, topk: int = 32) -> int:
@@ -366,10 +473,41 @@ def run_prefill(qm, dev, reps=20, n_inst=4):
     del insts
     torch.cuda.synchronize()
     flops = qsa_chunk_flops(PREFILL_START, PREFILL_LEN)
+    dflops = dn_rule_flops(PREFILL_LEN)
     return {"positions": f"{PREFILL_START}-{PREFILL_START + PREFILL_LEN - 1} of {PREFILL_CTX}",
             "qsa_ms": round(out["qsa"], 4), "dn_ms": round(out["dn"], 4),
             "qsa_attention_gflop": round(flops / 1e9, 3),
-            "qsa_mfma_util": round(flops / (out["qsa"] * 1e-3) / MFMA_BF16_PEAK, 5)}
+            "qsa_mfma_util": round(flops / (out["qsa"] * 1e-3) / MFMA_BF16_PEAK, 5),
+            "dn_rule_gflop": round(dflops / 1e9, 3),
+            "dn_mfma_util": round(dflops / (out["dn"] * 1e-3) / MFMA_F32_PEAK, 5)}
+
+
+def run_dn_long(qm, dev, reps=10):
+    """The chunked delta rule (chunk_gated_delta_rule on the device) over the
+    4096-token, 32-head float32 workload: event time per call, median."""
+    import torch
+    from importlib import import_module
+    layers = import_module(qm.__name__ + ".layers")
+    g = torch.Generator(device=dev).manual_seed(404)
+    shp = (1, DN_LONG, 32, 128)
+    q, k, v = (torch.randn(*shp, generator=g, device=dev) for _ in range(3))
+    gate = -torch.nn.functional.softplus(torch.randn(1, DN_LONG, 32, generator=g, device=dev))
+    beta = torch.sigmoid(torch.randn(1, DN_LONG, 32, generator=g, device=dev))
+    s0 = torch.randn(1, 32, 128, 128, generator=g, device=dev) * 0.02
+    layers.chunk_gated_delta_rule(q, k, v, gate, beta, initial_state=s0)
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    torch.cuda.synchronize()
+    for a, b in evs:
+        a.record(stream)
+        layers.chunk_gated_delta_rule(q, k, v, gate, beta, initial_state=s0)
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = statistics.median(a.elapsed_time(b) for a, b in evs)
+    flops = dn_rule_flops(DN_LONG)
+    return {"tokens": DN_LONG, "ms": round(ms, 4), "rule_gflop": round(flops / 1e9, 2),
+            "mfma_util": round(flops / (ms * 1e-3) / MFMA_F32_PEAK, 5),
+            "us_per_token": round(ms * 1e3 / DN_LONG, 4)}
 
 
 PROJECTION_GROUPS = (   # (name, rows per projection, k): the layer GEMVs around the core at one token
@@ -633,21 +771,39 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    configs = []
+    if not args.head_only:
+        # the decode step at the other positions of the benchmark's configurations
+        for p in SWEEP_POSITIONS:
+            r = head if p == pos else run_decode(qm, dev, p, min(args.steps, 100), args.warmup, graphs=False)
+            qb = qsa_bytes(p)
+            entry = {"workload": f"decode step at pos {p}" + (" (headline)" if p == pos else ""), "pos": p,
+                     "selection": "on" if (p + 1) // 64 > 32 else "off (below the budget)",
+                     "us_per_token": round(r["us_step"], 3),
+                     "qsa_us": round(r["kernel_us"]["qsa_decode"], 3), "dn_us": round(r["kernel_us"]["dn_decode"], 3),
+                     "qsa_gbs": round(qb / (r["kernel_us"]["qsa_decode"] * 1e-6) / 1e9, 1),
+                     "dn_gbs": round(DN_BYTES / (r["kernel_us"]["dn_decode"] * 1e-6) / 1e9, 1),
+                     "step_mb": round((qb + DN_BYTES) / 1e6, 3),
+                     "step_hbm_frac": round((qb + DN_BYTES) / (r["us_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+            if not args.no_cpu:
+                entry["cpu_baseline"] = cpu_baseline(p, args.cpu_seconds)
+            configs.append(entry)
+            print(f"[config] {json.dumps(entry)}", file=sys.stderr)
+        entry = {"workload": "prefill chunk of 128 tokens at 32640..32767 of 32768 (QSA per-query top-32 + "
+                             "attention, DeltaNet chunked rule)", **run_prefill(qm, dev)}
+        if not args.no_cpu:
+            entry["cpu_baseline"] = cpu_prefill_chunk(args.cpu_seconds)
+        configs.append(entry)
+        print(f"[config] {json.dumps(entry)}", file=sys.stderr)
+        entry = {"workload": f"chunked delta rule over {DN_LONG} tokens, 32 heads, float32", **run_dn_long(qm, dev)}
+        if not args.no_cpu:
+            entry["cpu_baseline"] = cpu_dn_4096(args.cpu_seconds)
+        configs.append(entry)
+        print(f"[config] {json.dumps(entry)}", file=sys.stderr)
+
     sweep = None
     if args.sweep:
-        sweep = {"decode": [], "prefill_chunk": None}
-        for p in SWEEP_POSITIONS:
-            r = head if p == pos else run_decode(qm, dev, p, args.steps, args.warmup)
-            qb = qsa_bytes(p)
-            line = {"pos": p, "us_step": round(r["us_step"], 3),
-                    "qsa_us": round(r["kernel_us"]["qsa_decode"], 3), "dn_us": round(r["kernel_us"]["dn_decode"], 3),
-                    "qsa_gbs": round(qb / (r["kernel_us"]["qsa_decode"] * 1e-6) / 1e9, 1),
-                    "dn_gbs": round(DN_BYTES / (r["kernel_us"]["dn_decode"] * 1e-6) / 1e9, 1),
-                    "step_hbm_frac": round((qb + DN_BYTES) / (r["us_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-            sweep["decode"].append(line)
-            print(f"[sweep] {json.dumps(line)}", file=sys.stderr)
-        sweep["prefill_chunk"] = run_prefill(qm, dev)
-        print(f"[sweep] prefill {json.dumps(sweep['prefill_chunk'])}", file=sys.stderr)
+        sweep = {}
         sweep["projections"] = run_projections(qm, dev)
         print(f"[sweep] projections {json.dumps(sweep['projections'])}", file=sys.stderr)
         sweep["hyper_connections"] = run_hc(qm, dev)
@@ -657,7 +813,8 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(pos, args.cpu_seconds)
+        cpu = next((c["cpu_baseline"] for c in configs if c.get("pos") == pos), None) or \
+            cpu_baseline(pos, args.cpu_seconds)
 
     line = {
         "metric": METRIC,
@@ -682,6 +839,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(pos, dominant)},
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     if sweep is not None:
         line["sweep"] = sweep

@@ -25,7 +25,8 @@
  *   page table                int32   [B, max_pages]  logical page -> physical
  *   indexer raw keys          act     [B, max_ctx, idx_dim]
  *   indexer block cache       float32 [B, max_blocks, idx_dim]  pooled, normed,
- *                              roped keys of complete blocks
+ *                              roped keys of complete blocks, each row permuted:
+ *                              element d at (d % 16) * 8 + d / 16
  *   rope tables               float32 [n_pos, rope_dim]  (cos, sin)
  */
 #ifndef QWEN4MIX_H

@@ -131,7 +131,7 @@ def test_block_scores_bit_exact_vs_reference(gpu, tag):
         n_blocks = want.shape[1]
         pooled = om.indexer_pooled(torch.cat([idx_keys, ik], 1), 3, cos, sin, n_blocks).float()
         q_rows = (lc.last_iq.cpu() != q_want).reshape(seq, -1).any(-1).nonzero().flatten().tolist()
-        k_rows = (lc.block_keys[:, :n_blocks].cpu() != pooled)[0].any(-1).nonzero().flatten().tolist()
+        k_rows = (lc.block_keys_ref[:, :n_blocks].cpu() != pooled)[0].any(-1).nonzero().flatten().tolist()
         raise AssertionError(f"{tag}: {len(bad)} scores differ (rows {sorted(set(bad[:, 0].tolist()))[:8]}); "
                              f"max {_ulps(got, want)} ulp; rank-32/33 gap of row {r}: {_gap_32_33(want[r]):.3e}; "
                              f"query rows off {q_rows[:8]}, pooled blocks off {k_rows[:8]}")

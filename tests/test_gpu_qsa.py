@@ -119,7 +119,7 @@ def test_indexer_stages_and_selection_match_reference(gpu, tag):
     assert torch.equal(lc.last_iq.cpu(), q_want.float()), "indexer query not bit-exact"
     n_blocks = (pos + 1) // 64
     pooled = om.indexer_pooled(torch.cat([idx_keys, ik], 1), 3, cos, sin, n_blocks)
-    got_pooled = lc.block_keys[:, :n_blocks].cpu()
+    got_pooled = lc.block_keys_ref[:, :n_blocks].cpu()
     assert torch.equal(got_pooled, pooled.float()), \
         f"pooled keys differ in {(got_pooled != pooled).sum().item()} entries"
     got = _got_sets(lc)[0][0]

@@ -13,7 +13,8 @@ keys / values       ``k_pool`` / ``v_pool`` [n_pages, Hkv, P * d] bf16 under
                     in the attention kernels' MFMA lane order
                     (``qm_qsa_page_index`` maps (row, channel) to an offset)
 indexer_keys        ``raw_keys`` [B, max_ctx, idx_dim] (act) plus ``block_keys``
-                    [B, max_blocks, idx_dim] float32 (pooled, normed, roped)
+                    [B, max_blocks, idx_dim] float32 (pooled, normed, roped;
+                    each row permuted, ``block_keys_ref`` un-permutes)
 ==================  ==============================================================
 
 The reference attribute names are kept as properties: reading one gathers a
@@ -168,6 +169,16 @@ class MixLayerCache:
         base = self.k_pool if pool == "k" else self.v_pool
         index = (o.k_index if pool == "k" else o.v_index).view(o.config.page_size, -1)[row]
         return base[page][:, index]
+
+    @property
+    def block_keys_ref(self):
+        """The pooled block keys in the reference's element order, [B, max_blocks,
+        idx_dim] (a gathered copy: the device rows keep element d at
+        (d % 16) * 8 + d // 16, the order the scoring lanes read)."""
+        if self.block_keys is None:
+            return None
+        d = torch.arange(self.block_keys.shape[-1], device=self.block_keys.device)
+        return self.block_keys[..., (d % 16) * 8 + d // 16]
 
     @property
     def indexer_keys(self):

@@ -249,6 +249,53 @@ __device__ __forceinline__ float torch_row_sumsq(const float* x, int n, float* s
   return tot;
 }
 
+// Phase markers (a build compiled with -DQM_PHASE_TRACE, for timing a
+// kernel's stages; in every other build all three are nothing):
+// QM_PHASE_DECL declares a workgroup's 16 LDS time slots; QM_PHASE(slot) has
+// thread 0 record the wall clock (100 MHz) in one of them (an LDS write: no
+// global store that a later barrier would wait for); QM_PHASE_FLUSH writes the
+// slots to the workgroup's row of the translation unit's qm_phase_buf, and
+// QM_PHASE_ENTRY(tag) defines qm_phase_read_<tag> / qm_phase_clear_<tag> for
+// the host. Slot 15 holds the workgroup's XCC id.
+#ifdef QM_PHASE_TRACE
+constexpr int QM_PHASE_ROWS = 8192;
+static __device__ unsigned long long qm_phase_buf[QM_PHASE_ROWS * 16];
+static __shared__ unsigned long long qm_ph_[16];
+#define QM_PHASE_DECL \
+  if (threadIdx.x < 16) qm_ph_[threadIdx.x] = 0ull;
+#define QM_PHASE(slot)                                           \
+  do {                                                           \
+    if (threadIdx.x == 0) qm_ph_[(slot)] = wall_clock64() | (1ull << 63); \
+  } while (0)
+#define QM_PHASE_FLUSH()                                                                                   \
+  do {                                                                                                     \
+    if (threadIdx.x == 0) {                                                                                \
+      const unsigned row_ = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);                \
+      qm_ph_[15] = (unsigned long long)__builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)) | (1ull << 63); \
+      if (row_ < QM_PHASE_ROWS)                                                                            \
+        for (int s_ = 0; s_ < 16; ++s_) qm_phase_buf[row_ * 16 + s_] = qm_ph_[s_];                         \
+    }                                                                                                      \
+  } while (0)
+#define QM_PHASE_ENTRY(tag)                                                                              \
+  extern "C" int qm_phase_read_##tag(unsigned long long* host, int n) {                                  \
+    if (n > QM_PHASE_ROWS * 16) n = QM_PHASE_ROWS * 16;                                                  \
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(qm_phase_buf), n * 8ul) == hipSuccess ? 0 : -1;          \
+  }                                                                                                      \
+  extern "C" int qm_phase_clear_##tag(void) {                                                            \
+    static unsigned long long zeros_[QM_PHASE_ROWS * 16];                                                \
+    return hipMemcpyToSymbol(HIP_SYMBOL(qm_phase_buf), zeros_, sizeof(zeros_)) == hipSuccess ? 0 : -1;   \
+  }
+#else
+#define QM_PHASE_DECL
+#define QM_PHASE(slot) \
+  do {               \
+  } while (0)
+#define QM_PHASE_FLUSH() \
+  do {                 \
+  } while (0)
+#define QM_PHASE_ENTRY(tag)
+#endif
+
 #define QM_CHECK_LAUNCH()                                              \
   do {                                                                 \
     hipError_t e_ = hipGetLastError();                                 \

@@ -123,6 +123,8 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
   const int col0 = s * DN_DCOLS;
   constexpr int NW = DN_NT / 64;
 
+  QM_PHASE_DECL
+  QM_PHASE(0);
   __shared__ float s_q[DN_D], s_k[DN_D], s_v[DN_DCOLS];
   __shared__ float s_red[NW][2 * DN_DCOLS];
   __shared__ __attribute__((aligned(16))) float s_delta[DN_DCOLS];
@@ -167,6 +169,7 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
   }
   __syncthreads();
 
+  QM_PHASE(1);
   // ---- l2 norms of q and k and their dot product: waves 0-1 hold the 128 channels
   if (tid < DN_D) {
     const float qv = s_q[tid], kv = s_k[tid];
@@ -179,6 +182,7 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
   const float sqrt_d = 11.313708498984761f;
   const float qk = div_rn(sqk * rq * rk, sqrt_d);       // q^ . k^
 
+  QM_PHASE(2);
   // ---- decay, then per column pred = S^T k^ and qd = S^T q^ over the rows
   const float decay = s_scal[1];
   float st[4][4], kr[4], pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
@@ -213,6 +217,7 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
   }
   __syncthreads();
 
+  QM_PHASE(3);
   // ---- delta and o of the 32 columns (wave 0, lanes 0-31); their share of the
   // head's sum of squares leaves at once
   float o = 0.f;
@@ -233,6 +238,7 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
   }
   __syncthreads();
 
+  QM_PHASE(4);
   // ---- rank-1 update and write-back of the columns, written through to the
   // point of coherence: no dirty state lines are left in L2 for the end of
   // the kernel to write back (0.35 µs less per launch)
@@ -246,6 +252,7 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
                           fmaf(kr[k], dl.w, st[k][3])));
   }
 
+  QM_PHASE(5);
   // ---- the head's sum of squares from its shares (one line, polled by wave
   // 0), then the gated RMS norm of the 32 columns
   if (wid == 0) {
@@ -266,6 +273,7 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
     }
     // a wait that gave up counts itself (qm_dn_decode_check) and leaves NaN,
     // never an output normalised by a partial sum
+    QM_PHASE(6);
     if (!done && lane == 0) __hip_atomic_fetch_add(line + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (s == 0 && lane == 0) st_flag(line, gen + 1);
     if (tid < DN_DCOLS) {
@@ -274,6 +282,8 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
       Act<T>::store(A.out, (long)b * A.hv * DN_D + h * DN_D + col0 + tid, done ? y : __builtin_nanf(""));
     }
   }
+  QM_PHASE(7);
+  QM_PHASE_FLUSH();
 }
 
 // ---------------------------------------------------------------------------
@@ -426,6 +436,8 @@ int launch_dn_recurrent(int batch, int seq, int heads, int hk, long q_stride, lo
 }
 
 }  // namespace
+
+QM_PHASE_ENTRY(dn)
 
 extern "C" size_t qm_dn_decode_workspace(int batch, int n_v_heads, int head_dim) {
   // one 128-byte line per (sequence, head): generation word and the shares of

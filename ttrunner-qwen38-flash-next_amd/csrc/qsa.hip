@@ -36,6 +36,12 @@ __host__ __device__ __forceinline__ int v_slot(int row) {
   return (row & ~31) + 8 * ((t & 15) >> 2) + 4 * (t >> 4) + (t & 3);
 }
 
+// Block-key rows (the pooled, normed, roped indexer key of each block, 128
+// floats) are kept permuted: element d at (d % 16) * 8 + d / 16, so that the
+// 16 lanes that score a block for one query row (lane m owns elements m,
+// m + 16, ..., m + 112) each read 32 contiguous bytes.
+__host__ __device__ __forceinline__ int bk_index(int d) { return (d & 15) * 8 + (d >> 4); }
+
 // Page layouts (one page of one kv head = P x 256 bf16): both pools keep their
 // MFMA operands in lane order, so every wave-wide 16-byte load reads 1 KB of
 // contiguous memory.
@@ -131,7 +137,7 @@ __device__ float pool_block(int j, int ratio, int rope, float eps, const float* 
     s_x[tid] = Act<T>::round(div_rn(total, (float)ratio));
   }
   const float y = norm_rope_row<T>(s_x, s_y, s_scr, IDX_D, k_norm, eps, rope, csv.x, csv.y);
-  if (tid < IDX_D) blocks[(long)j * IDX_D + tid] = y;
+  if (tid < IDX_D) blocks[(long)j * IDX_D + bk_index(tid)] = y;
   return y;
 }
 
@@ -280,12 +286,11 @@ template <int NT> constexpr int score_pre() { return NT >= 1024 ? 2 : 8; }
 // (an invalid j loads row 0, always allocated, and zeroes the result: the
 // loads stay unconditional so later waits on them stay exact)
 __device__ __forceinline__ void load_block_part(float (&k)[8], const float* bk, int j, bool valid) {
-  const float* src = bk + (long)(valid ? j : 0) * IDX_D + (threadIdx.x & 15);
+  const float4* src = reinterpret_cast<const float4*>(bk + (long)(valid ? j : 0) * IDX_D + 8 * (threadIdx.x & 15));
+  const float4 a = src[0], c = src[1];
+  const float v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float v = src[16 * i];
-    k[i] = valid ? v : 0.f;
-  }
+  for (int i = 0; i < 8; ++i) k[i] = valid ? v[i] : 0.f;
 }
 
 template <int N>
@@ -356,6 +361,90 @@ __device__ void score_blocks(const float* s_iq, const float* new_key, const floa
   for (int j = n_elig + tid; j < npad; j += NT) keys[j] = 0ull;
 }
 
+// The one-row dot products of the 4 query rows with the block of the calling
+// 16 lanes (the order of row16_block_score), valid in lane 0 of the 16.
+__device__ __forceinline__ float4 row16_dots(const float (&q)[4][8], const float (&k)[8]) {
+  float p[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    p[h] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[h] = fmaf(q[h][i], k[i], p[h]);
+  }
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    float c = add_rn(p[h], row_shl<4>(p[h]));
+    c = add_rn(c, row_shl<8>(p[h]));
+    c = add_rn(c, row_shl<12>(p[h]));
+    const float u = add_rn(c, row_shl<1>(c));
+    p[h] = add_rn(u, row_shl<2>(u));
+  }
+  return make_float4(p[0], p[1], p[2], p[3]);
+}
+
+// keys[j] = sel_key(score_j, j) for every eligible block j in the one-row
+// order, in rounds of PRE passes (PRE * NT / 16 blocks): the passes leave each
+// block's 4 dot products in dsc (LDS), then one thread per block forms its
+// score and key, so that the relu, sum and division run once per block rather
+// than in all 16 of its lanes. kp[u] comes in holding pass u's keys; later
+// rounds load one round ahead. Block new_j's key is new_key (LDS). Ends with
+// the keys padded with zeros to a multiple of 32 (after a barrier the caller
+// issues).
+template <int NT, int PRE>
+__device__ void score_block_rounds(const float* s_iq, const float* new_key, const float* bk, int n_elig, int new_j,
+                                   int idx_heads, unsigned long long* keys, float4* dsc, float (&kp)[PRE][8]) {
+  constexpr int PASS = NT / SCORE_LANES;
+  constexpr int ROUND = PASS * PRE;
+  const int tid = threadIdx.x, jl = tid >> 4, m = tid & 15;
+  float q[4][8];
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[h][i] = s_iq[h * IDX_D + 16 * i + m];
+  for (int r0 = 0; r0 < n_elig; r0 += ROUND) {
+    if (new_j >= r0 && new_j < r0 + ROUND) {
+      // the block this launch completes is not in the cache yet: its key from LDS
+#pragma unroll
+      for (int u = 0; u < PRE; ++u)
+        if (r0 + u * PASS + jl == new_j) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) kp[u][i] = new_key[16 * i + m];
+        }
+    }
+    // every pass of the round at once (blocks past n_elig hold zeros), so that
+    // their independent chains interleave
+    float4 d[PRE];
+#pragma unroll
+    for (int u = 0; u < PRE; ++u) d[u] = row16_dots(q, kp[u]);
+    QM_PHASE(11);
+    if (m == 0) {
+#pragma unroll
+      for (int u = 0; u < PRE; ++u) dsc[u * PASS + jl] = d[u];
+    }
+    if (r0 + ROUND < n_elig) {
+#pragma unroll
+      for (int u = 0; u < PRE; ++u) {
+        const int jn = r0 + ROUND + u * PASS + jl;
+        load_block_part(kp[u], bk, jn, jn < n_elig && jn != new_j);
+      }
+    }
+    QM_PHASE(13);
+    __syncthreads();
+    for (int t = tid; t < ROUND && r0 + t < n_elig; t += NT) {
+      const float4 dd = dsc[t];
+      const float dv[4] = {dd.x, dd.y, dd.z, dd.w};
+      float sc = 0.f;
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        if (h < idx_heads) sc = add_rn(sc, fmaxf(dv[h], 0.f));
+      keys[r0 + t] = sel_key(div_rn(sc, 11.313708498984761f), r0 + t);
+    }
+    __syncthreads();
+  }
+  const int npad = (n_elig + 31) & ~31;
+  for (int j = n_elig + tid; j < npad; j += NT) keys[j] = 0ull;
+}
+
 // prefetch of the first PRE passes (issued before the scores are needed)
 template <int NT, int PRE>
 __device__ __forceinline__ void prefetch_block_keys(float (&kp)[PRE][8], const float* bk, int n_elig, int new_j,
@@ -379,29 +468,24 @@ __device__ void score_blocks_seq(const float* s_iq, const float* bk, int n_elig,
   for (int j0 = 0; j0 < n_elig; j0 += NT) {
     const int j = j0 + tid;
     const bool valid = j < n_elig;
+    // float4 c of the (permuted) row holds elements c / 2 + 16 (4 (c % 2) + t),
+    // t < 4: the even ones elements 0..63, the odd ones 64..127
     const float4* row = reinterpret_cast<const float4*>(bk + (long)(valid ? j : 0) * IDX_D);
-    float4 kc[2][8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) kc[0][e] = row[e];
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (c < 3) {
+    for (int half = 0; half < 2; ++half) {
+      float4 kc[16];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) kc[(c + 1) & 1][e] = row[8 * (c + 1) + e];
-      }
+      for (int m = 0; m < 16; ++m) kc[m] = row[2 * m + half];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float4 kv = kc[c & 1][e];
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          const float4 qv = reinterpret_cast<const float4*>(s_iq + h * IDX_D)[8 * c + e];
-          acc[h] = fmaf(qv.x, kv.x, acc[h]);
-          acc[h] = fmaf(qv.y, kv.y, acc[h]);
-          acc[h] = fmaf(qv.z, kv.z, acc[h]);
-          acc[h] = fmaf(qv.w, kv.w, acc[h]);
+        for (int m = 0; m < 16; ++m) {
+          const int d = 64 * half + 16 * t + m;
+          const float kv = t == 0 ? kc[m].x : t == 1 ? kc[m].y : t == 2 ? kc[m].z : kc[m].w;
+#pragma unroll
+          for (int h = 0; h < 4; ++h) acc[h] = fmaf(s_iq[h * IDX_D + d], kv, acc[h]);
         }
-      }
     }
     float sc = 0.f;
 #pragma unroll
@@ -1325,17 +1409,6 @@ constexpr int DEC_MAX_RATIO = 64;     // raw keys of a completed block are held 
 constexpr int DEC_GEN_STRIDE = 32;    // generation words 128 bytes apart, one cache line each
 constexpr int DEC_SLICES = GQA * QSA_D / 32;   // output slices of a group: (query head, 32 channels)
 
-// rows of the two norm passes, at these LDS offsets: the 4 indexer-query rows
-// and the pooled block key (128 wide) first, then the 8 query heads and the
-// key (256 wide)
-constexpr int NR_POOL = 4, NR_Q = 5, NR_K = 13, NR_ROWS = 14;
-constexpr int X_POOL = 4 * IDX_D, X_Q = X_POOL + IDX_D, X_K = X_Q + GQA * QSA_D, X_SIZE = X_K + QSA_D;
-constexpr int SLOTS_FRONT = NR_Q * 32, SLOTS_ALL = NR_ROWS * 32;   // 32 partial sums per row
-
-__device__ __forceinline__ int norm_row_offset(int r) {
-  return r < NR_POOL ? r * IDX_D : r == NR_POOL ? X_POOL : r < NR_K ? X_Q + (r - NR_Q) * QSA_D : X_K;
-}
-
 template <typename T>
 struct DecArgs {
   PrepArgs<T> P;
@@ -1348,13 +1421,12 @@ struct DecArgs {
 };
 
 struct DecShared {
-  float x[X_SIZE];                                // rows to norm
   unsigned long long key[DEC_MAX_BLOCKS];         // selection keys
-  float part[SLOTS_ALL];
-  float rinv[16];
+  float4 dsc[128];                                // a round's per-block dot products (4 heads)
+  float red[264];                                 // merge: partial sums and wave values
   int fault;                                      // the merge saw a wait give up
-  float iq[4 * IDX_D];
-  float newkey[IDX_D];
+  float iq[4 * IDX_D];                            // the roped indexer query rows
+  float newkey[IDX_D];                            // the pooled key of the block this token completes
   alignas(16) uint16_t knb[QSA_D];                // the token's roped key and its value, bf16
   alignas(16) uint16_t vnb[QSA_D];
   alignas(16) uint16_t qb[16][QSA_D];             // MFMA B operand: rows 0..7 bf16 hi of the heads, 8..15 lo
@@ -1364,6 +1436,55 @@ struct DecShared {
   alignas(16) int rscr[rank_scratch(DEC_MAX_TOPK)];
   alignas(16) float s[GQA][32];                   // the item's scores, head-major
 };
+
+// ---- RMS norms of one row per wave, in torch's CPU order: 32 partial sums,
+// partial a summing the squares of elements a, a + 32, a + 64, ... in order;
+// then c_l = ((s_l + s_(l+8)) + s_(l+16)) + s_(l+24) for l < 8, added in
+// order; every square and sum rounded on its own. A 128-wide row sits in the
+// wave as x[k] = element lane + 64 k (k < 2), a 256-wide row k < 4.
+__device__ __forceinline__ float xor32_f(float v) { return __shfl_xor(v, 32, 64); }
+
+__device__ __forceinline__ float wave_rinv_finish(float s, float n, float eps) {
+  const float s16 = __shfl_down(s, 16, 64);
+  const float c = add_rn(add_rn(add_rn(s, row_shl<8>(s)), s16), row_shl<8>(s16));   // lanes 0..7: c_l
+  float tot = readlane_f(c, 0);
+#pragma unroll
+  for (int l = 1; l < 8; ++l) tot = add_rn(tot, readlane_f(c, l));
+  return rsqrt_rn(add_rn(div_rn(tot, n), eps));
+}
+
+template <int K>
+__device__ __forceinline__ float wave_rinv(const float (&x)[K], float eps) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const float q = mul_rn(x[k], x[k]);
+    s = k == 0 ? q : add_rn(s, q);          // element lane + 64 k
+    s = add_rn(s, xor32_f(q));              // element lane + 64 k + 32
+  }
+  return wave_rinv_finish(s, 64.f * K, eps);
+}
+
+// rope of a normed row held as y[k] = element lane + 64 k: element e < rope
+// becomes y_e cos + (e < rope/2 ? -y_p : y_p) sin, p = e +- rope/2 (the
+// partner's normed value, from lane p % 64 of register p / 64); every multiply
+// and add rounded on its own.
+template <int K>
+__device__ __forceinline__ void wave_rope(float (&y)[K], int rope, const float (&cs)[2], const float (&sn)[2]) {
+  const int lane = threadIdx.x & 63, half = rope >> 1;
+  float out[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int e = lane + 64 * k;
+    const int pe = min(e < half ? e + half : e - half, 127);
+    const float v0 = __shfl(y[0], pe & 63, 64);
+    const float v1 = __shfl(y[1], pe & 63, 64);
+    const float yp = pe >= 64 ? v1 : v0;
+    out[k] = e < rope ? add_rn(mul_rn(y[k], cs[k]), mul_rn(e < half ? -yp : yp, sn[k])) : y[k];
+  }
+  y[0] = out[0];
+  y[1] = out[1];
+}
 
 // item -> (first token t0, visible rows [lo, hi)) of a query at position p
 __device__ __forceinline__ void item_span(int it, int n_blk_items, int gpb, int ratio, int ts, int p, const int* sel,
@@ -1392,37 +1513,6 @@ struct ItemCount {
   }
 };
 
-// the 32 partial sums of squares of rows with slots [s0, s1) (slot = 32 row + a,
-// a = 0..31 summing channels a, a+32, ... in order), then each row's 1/rms
-__device__ __forceinline__ void norm_partials(DecShared& sh, int s0, int s1) {
-  for (int s = s0 + (int)threadIdx.x; s < s1; s += DEC_NT) {
-    const int r = s >> 5, a = s & 31;
-    const float* xr = sh.x + norm_row_offset(r);
-    float acc = 0.f;
-    if (r <= NR_POOL) {
-#pragma unroll
-      for (int e = 0; e < IDX_D; e += 32) acc = add_rn(acc, mul_rn(xr[a + e], xr[a + e]));
-    } else {
-#pragma unroll
-      for (int e = 0; e < QSA_D; e += 32) acc = add_rn(acc, mul_rn(xr[a + e], xr[a + e]));
-    }
-    sh.part[s] = acc;
-  }
-}
-__device__ __forceinline__ void norm_rinv(DecShared& sh, int r0, int r1, float eps) {
-  const int r = r0 + (int)threadIdx.x;
-  if (r < r1) {
-    const float* pp = sh.part + r * 32;
-    float tot = 0.f;
-#pragma unroll
-    for (int l = 0; l < 8; ++l) {
-      const float c = add_rn(add_rn(add_rn(pp[l], pp[8 + l]), pp[16 + l]), pp[24 + l]);
-      tot = l == 0 ? c : add_rn(tot, c);
-    }
-    sh.rinv[r] = rsqrt_rn(add_rn(div_rn(tot, (float)(r <= NR_POOL ? IDX_D : QSA_D)), eps));
-  }
-}
-
 // Output slice sl = (query head h = sl / 8, channels 32 (sl % 8) ..+31) of
 // group (b, g): out[d] = round(sum_i w_i o_i[d] / sum_i w_i) *
 // round(sigmoid(gate[d])), w_i = exp(m_i - max m) l_i, over the n items (o_i
@@ -1439,7 +1529,7 @@ __device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, 
   const int h = sl / 8, d = 32 * (sl % 8) + ch;
   const int hq = D.P.hq, qh = g * GQA + h;
   float* s_w = reinterpret_cast<float*>(sh.key);           // DEC_MAX_ITEMS + 128 weights
-  float* red = sh.part;                                   // 8 x 32 partial sums, then 2 x 4 wave values
+  float* red = sh.red;                                    // 8 x 32 partial sums, then 2 x 4 wave values
   const float gate = Act<T>::load(D.P.qg, ((long)b * hq + qh) * (2 * QSA_D) + QSA_D + d);
   float ov[CHUNK];
 #pragma unroll
@@ -1518,6 +1608,7 @@ __device__ __forceinline__ void decode_merge(const DecArgs<T>& D, DecShared& sh,
     }
   }
   __syncthreads();
+  QM_PHASE(9);
   const bool poison = overflow || sh.fault != 0;
   if (item == 0 && tid == 0) st_flag(D.gen + (long)bg * DEC_GEN_STRIDE, gen + 1);
   const int step = WIDE ? DEC_SLICES : n_att;
@@ -1527,6 +1618,7 @@ __device__ __forceinline__ void decode_merge(const DecArgs<T>& D, DecShared& sh,
 template <typename T, bool WIDE>
 __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   __shared__ DecShared sh;
+  QM_PHASE_DECL
   const PrepArgs<T>& A = D.P;
   const int item = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -1534,31 +1626,32 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   const int e128 = tid & 127, hh = tid >> 7;
   const int bg = b * A.hkv + g;
 
-  // ---- 0. the loads
+  // ---- 0. the loads. Wave w takes indexer query head w and attention query
+  // heads 2w, 2w + 1 (wave 0 also the key), each row as elements lane + 64 k.
+  // Every load is unconditional, indices clamped into range, so the waits on
+  // them stay exact instead of draining the memory counter.
+  QM_PHASE(0);
   const unsigned gen = ld_flag(D.gen + (long)bg * DEC_GEN_STRIDE);
-  float iqv[2];
+  const int n_iq = A.idx_heads * IDX_D;
+  float iqx[2];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int i = tid + DEC_NT * k, n_iq = A.idx_heads * IDX_D;
-    const float v = Act<T>::load(A.iq, (long)b * n_iq + min(i, n_iq - 1));
-    iqv[k] = i < n_iq ? v : 0.f;
-  }
+  for (int k = 0; k < 2; ++k) iqx[k] = Act<T>::load(A.iq, (long)b * n_iq + min(wv * IDX_D + lane + 64 * k, n_iq - 1));
   const float ikv = Act<T>::load(A.ik, (long)b * IDX_D + e128);
-  float qx[GQA];
+  float qx[2][4], kx[4];
 #pragma unroll
-  for (int h = 0; h < GQA; ++h) qx[h] = Act<T>::load(A.qg, ((long)b * A.hq + g * GQA + h) * (2 * QSA_D) + tid);
-  const float kx = Act<T>::load(A.k_new, (long)bg * QSA_D + tid);
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      qx[j][k] = Act<T>::load(A.qg, ((long)b * A.hq + g * GQA + 2 * wv + j) * (2 * QSA_D) + lane + 64 * k);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) kx[k] = Act<T>::load(A.k_new, (long)bg * QSA_D + lane + 64 * k);
   const float vx = Act<T>::load(A.v_new, (long)bg * QSA_D + tid);
-  // norm weights of this thread's channel and of its rope partner (channel
-  // +- rope/2); 256-wide rows rope channel tid (< rope <= 128), 128-wide rows
-  // channel e128. Every load is unconditional, indices clamped into range, so
-  // the waits on them stay exact instead of draining the memory counter.
-  const int rope = A.rope, half = A.rope >> 1;
-  const bool roped = e128 < rope;
-  const int pe = e128 < half ? e128 + half : e128 - half;
-  const int ec = min(e128, rope - 1);
-  const float w_q = A.q_norm[tid], w_k = A.k_norm[tid], w_iq = A.iq_norm[e128], w_ik = A.ik_norm[e128];
-  const float w_q2 = A.q_norm[pe], w_k2 = A.k_norm[pe], w_iq2 = A.iq_norm[pe], w_ik2 = A.ik_norm[pe];
+  const int rope = A.rope;
+  float w_q[4], w_k[4], w_iq[2], w_ik[2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) { w_q[k] = A.q_norm[lane + 64 * k]; w_k[k] = A.k_norm[lane + 64 * k]; }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) { w_iq[k] = A.iq_norm[lane + 64 * k]; w_ik[k] = A.ik_norm[lane + 64 * k]; }
 
   const int p = A.positions[b];
   const int ratio = A.ratio;
@@ -1566,9 +1659,16 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   const ItemCount ic(p, ratio, topk, A.max_blocks);
   const int n_elig = ic.n_elig, n_items = ic.n_items;
   const int j_new = (p + 1) % ratio == 0 ? p / ratio : -1;
-  const float cs = A.cos[(long)p * rope + ec], sn = A.sin[(long)p * rope + ec];
-  const long t0r = (long)max(j_new, 0) * ratio * rope + ec;
-  const float cs0 = A.cos[t0r], sn0 = A.sin[t0r];
+  // rope rows: this token's position, and the start of the block it completes
+  float cs[2], sn[2], cs0[2], sn0[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int ec = min(lane + 64 * k, rope - 1);
+    cs[k] = A.cos[(long)p * rope + ec];
+    sn[k] = A.sin[(long)p * rope + ec];
+    cs0[k] = A.cos[(long)max(j_new, 0) * ratio * rope + ec];
+    sn0[k] = A.sin[(long)max(j_new, 0) * ratio * rope + ec];
+  }
   // the whole page-table row and, when this launch's positions may need
   // scoring (more items than the top-k blocks hold), the first 128 block keys,
   // whatever the position
@@ -1583,7 +1683,6 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   prefetch_block_keys<DEC_NT>(kp, bk, A.max_blocks, -1, may_score);
   // raw keys of the block this token completes: thread (e128, hh) takes the
   // 16-row chunks hh and hh + 2; the token's own row is ik (not yet stored)
-  // (loads unconditional, rows clamped, so that none waits alone)
   float rk[2][16];
   if (j_new >= 0) {
     const T* raw = A.raw_keys + ((long)b * A.max_ctx + (long)j_new * ratio) * IDX_D + e128;
@@ -1596,34 +1695,15 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
         rk[c][i] = r >= ratio ? 0.f : j_new * ratio + r == p ? ikv : v;
       }
   }
-
-  // ---- 1. the indexer query and the pooled block key
-  if (j_new >= 0) {
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int ch = hh + 2 * c;
-      if (16 * ch < ratio) {
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (16 * ch + i < ratio) acc = add_rn(acc, rk[c][i]);
-        sh.chunk[ch][e128] = acc;
-      }
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < 2; ++k) sh.x[tid + DEC_NT * k] = iqv[k];
-#pragma unroll
-  for (int h = 0; h < GQA; ++h) sh.x[X_Q + h * QSA_D + tid] = qx[h];
-  sh.x[X_K + tid] = kx;
   sh.vnb[tid] = f32_to_bf16(vx);
 #pragma unroll
   for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k) sh.pages[tid + DEC_NT * k] = pg[k];
-  // a workgroup past the position's items only merges: the waits of this
-  // launch cover only the first n_att flags
+
   // A position with more items than the launch has workgroups (a plan sized
   // for smaller positions) cannot be attended: its output is poisoned and
-  // workgroup 0 counts it in the group's word 2.
+  // workgroup 0 counts it in the group's word 2. A workgroup past the
+  // position's items only merges: the waits of this launch cover only the
+  // first n_att flags.
   const bool overflow = n_items > D.splits;
   const int n_att = min(n_items, D.splits);
   if (overflow && item == 0 && tid == 0)
@@ -1636,61 +1716,64 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
         decode_merge<WIDE>(D, sh, b, g, item, n_att, gen, overflow);
       }
     }
+    QM_PHASE_FLUSH();
     return;
   }
-  __syncthreads();
   const bool blk_item = item < ic.n_blk_items;
-  float pmean = 0.f;
+
+  // ---- 1. the indexer query (wave w: head w), and the pooled key of a block
+  // this token completes: y = round_T(x * rinv * w), then rope
+  auto nrm = [&](float xv, float ri, float w) { return Act<T>::round(mul_rn(mul_rn(xv, ri), w)); };
+  if (wv < A.idx_heads) {
+    const float ri = wave_rinv<2>(iqx, A.eps);
+    QM_PHASE(1);
+    float y[2] = {nrm(iqx[0], ri, w_iq[0]), nrm(iqx[1], ri, w_iq[1])};
+    wave_rope<2>(y, rope, cs, sn);
+    sh.iq[wv * IDX_D + lane] = y[0];
+    sh.iq[wv * IDX_D + 64 + lane] = y[1];
+  } else {
+    sh.iq[wv * IDX_D + lane] = 0.f;
+    sh.iq[wv * IDX_D + 64 + lane] = 0.f;
+  }
   if (j_new >= 0) {
     // block mean: the 16-row chunk sums in order, then divided by the count
-    if (tid < IDX_D) {
-      float total = sh.chunk[0][tid];
-      for (int ch = 1; 16 * ch < ratio; ++ch) total = add_rn(total, sh.chunk[ch][tid]);
-      pmean = Act<T>::round(div_rn(total, (float)ratio));
-      sh.x[X_POOL + tid] = pmean;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int ch = hh + 2 * c;
+      if (16 * ch < ratio) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (16 * ch + i < ratio) acc = add_rn(acc, rk[c][i]);
+        sh.chunk[ch][e128] = acc;
+      }
     }
     __syncthreads();
-  }
-  norm_partials(sh, 0, SLOTS_FRONT);
-  __syncthreads();
-  norm_rinv(sh, 0, NR_Q, A.eps);
-  __syncthreads();
-  // y = round_T(x * rinv * w); the first `rope` channels then rotate with their
-  // partner, recomputed here from its x rather than exchanged
-  auto nrm = [&](float xv, float ri, float w) { return Act<T>::round(mul_rn(mul_rn(xv, ri), w)); };
-  auto rot = [&](float y, float yp, float c, float s) {
-    return add_rn(mul_rn(y, c), mul_rn(e128 < half ? -yp : yp, s));
-  };
-  {
-    float ri[NR_Q], xp_iq[2], xp_pool = 0.f;
+    if (wv == 0) {
+      float x[2];
 #pragma unroll
-    for (int r = 0; r < NR_Q; ++r) ri[r] = sh.rinv[r];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) xp_iq[k] = sh.x[(hh + 2 * k) * IDX_D + pe];
-    if (j_new >= 0) xp_pool = sh.x[X_POOL + pe];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int r = hh + 2 * k;
-      float y = 0.f;
-      if (r < A.idx_heads) {
-        y = nrm(iqv[k], ri[r], w_iq);
-        if (roped) y = rot(y, nrm(xp_iq[k], ri[r], w_iq2), cs, sn);
+      for (int k = 0; k < 2; ++k) {
+        float total = sh.chunk[0][lane + 64 * k];
+        for (int ch = 1; 16 * ch < ratio; ++ch) total = add_rn(total, sh.chunk[ch][lane + 64 * k]);
+        x[k] = Act<T>::round(div_rn(total, (float)ratio));
       }
-      sh.iq[r * IDX_D + e128] = y;
-    }
-    if (j_new >= 0 && tid < IDX_D) {
-      float y = nrm(pmean, ri[NR_POOL], w_ik);
-      if (roped) y = rot(y, nrm(xp_pool, ri[NR_POOL], w_ik2), cs0, sn0);
-      sh.newkey[tid] = y;
+      const float ri = wave_rinv<2>(x, A.eps);
+      float y[2] = {nrm(x[0], ri, w_ik[0]), nrm(x[1], ri, w_ik[1])};
+      wave_rope<2>(y, rope, cs0, sn0);
+      sh.newkey[lane] = y[0];
+      sh.newkey[64 + lane] = y[1];
     }
   }
   __syncthreads();
 
   // ---- 2. block scores and top-k (ties to the lower index); the item of a
   // tail workgroup does not depend on them
+  QM_PHASE(2);
   if (scoring && (blk_item || item == 0)) {
-    score_blocks<DEC_NT>(sh.iq, sh.newkey, bk, n_elig, j_new, A.idx_heads, sh.key, nullptr, kp);
+    score_block_rounds<DEC_NT, score_pre<DEC_NT>()>(sh.iq, sh.newkey, bk, n_elig, j_new, A.idx_heads, sh.key, sh.dsc,
+                                                   kp);
     __syncthreads();
+    QM_PHASE(3);
     rank_topk<DEC_NT, DEC_MAX_TOPK>(sh.key, n_elig, topk, sh.sel, sh.rscr);
   } else if (!scoring) {
     for (int i = tid; i < n_elig; i += DEC_NT) sh.sel[i] = i;
@@ -1698,49 +1781,54 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   __syncthreads();
 
   // ---- 3. the item's keys/values in flight while the query heads and key are normed
+  QM_PHASE(4);
   int t0, lo, hi;
   item_span(item, ic.n_blk_items, ic.gpb, ratio, ic.ts, p, sh.sel, t0, lo, hi);
   const int page = sh.pages[t0 / A.page_size], row0 = t0 % A.page_size;
   const long pbase = ((long)page * A.hkv + g) * A.page_size * QSA_D;
+  // Every earlier load has landed by now (the selection used them): saying so
+  // lets the compiler issue the value and key loads back to back, instead of
+  // waiting on the first of them for a register an earlier load might still
+  // be writing.
+  __builtin_amdgcn_s_waitcnt(0);
   bf16x8_t kf[8], vf[4];
-  if (wv < 2) {
-    const uint16_t* kt = A.k_pool + pbase + ((row0 >> 4) + wv) * 8 * 512 + lane * 8;
-#pragma unroll
-    for (int sk = 0; sk < 8; ++sk) kf[sk] = load_bf16x8(kt + sk * 512);
-  }
   {
     const uint16_t* vt = A.v_pool + pbase + ((row0 >> 5) * 16 + 4 * wv) * 512 + lane * 8;
 #pragma unroll
     for (int i = 0; i < 4; ++i) vf[i] = load_bf16x8(vt + i * 512);
   }
-  norm_partials(sh, SLOTS_FRONT, SLOTS_ALL);
-  __syncthreads();
-  norm_rinv(sh, NR_Q, NR_ROWS, A.eps);
-  __syncthreads();
-  {
-    float ri[NR_ROWS - NR_Q], xp_q[GQA], xp_k = 0.f;
+  if (wv < 2) {
+    const uint16_t* kt = A.k_pool + pbase + ((row0 >> 4) + wv) * 8 * 512 + lane * 8;
 #pragma unroll
-    for (int r = 0; r < NR_ROWS - NR_Q; ++r) ri[r] = sh.rinv[NR_Q + r];
-#pragma unroll
-    for (int h = 0; h < GQA; ++h) xp_q[h] = 0.f;
-    if (tid < rope) {
-#pragma unroll
-      for (int h = 0; h < GQA; ++h) xp_q[h] = sh.x[X_Q + h * QSA_D + pe];
-      xp_k = sh.x[X_K + pe];
-    }
-#pragma unroll
-    for (int h = 0; h < GQA; ++h) {
-      float y = nrm(qx[h], ri[h], w_q);
-      if (tid < rope) y = rot(y, nrm(xp_q[h], ri[h], w_q2), cs, sn);
-      // the attention MFMA takes q as bf16: hi + lo carries ~16 mantissa bits
-      const uint16_t qhi = f32_to_bf16(y);
-      sh.qb[h][tid] = qhi;
-      sh.qb[GQA + h][tid] = f32_to_bf16(y - bf16_to_f32(qhi));
-    }
-    float y = nrm(kx, ri[NR_K - NR_Q], w_k);
-    if (tid < rope) y = rot(y, nrm(xp_k, ri[NR_K - NR_Q], w_k2), cs, sn);
-    sh.knb[tid] = f32_to_bf16(y);
+    for (int sk = 0; sk < 8; ++sk) kf[sk] = load_bf16x8(kt + sk * 512);
   }
+  // wave w: query heads 2w, 2w + 1 (and wave 0 the key), normed and roped;
+  // the attention MFMA takes q as bf16 hi + lo (~16 mantissa bits)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int h = 2 * wv + j;
+    const float ri = wave_rinv<4>(qx[j], A.eps);
+    float y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y[k] = nrm(qx[j][k], ri, w_q[k]);
+    wave_rope<4>(y, rope, cs, sn);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint16_t qhi = f32_to_bf16(y[k]);
+      sh.qb[h][lane + 64 * k] = qhi;
+      sh.qb[GQA + h][lane + 64 * k] = f32_to_bf16(y[k] - bf16_to_f32(qhi));
+    }
+  }
+  if (wv == 0) {
+    const float ri = wave_rinv<4>(kx, A.eps);
+    float y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y[k] = nrm(kx[k], ri, w_k[k]);
+    wave_rope<4>(y, rope, cs, sn);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sh.knb[lane + 64 * k] = f32_to_bf16(y[k]);
+  }
+  QM_PHASE(5);
   __syncthreads();
 
   // ---- 4. scores of the item's two 16-token tiles (waves 0, 1)
@@ -1774,6 +1862,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
     }
     if (col < GQA) *reinterpret_cast<float4*>(&sh.s[col][16 * wv + 4 * quad]) = sv;
   }
+  QM_PHASE(6);
   __syncthreads();
   // softmax weights: lane (col, quad) takes tokens 16t + 4quad + v of head col
   // (t = 0, 1), the k order the PV MFMA's B operand wants
@@ -1794,6 +1883,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
     pf[i] = __builtin_bit_cast(__bf16, col < GQA ? f32_to_bf16(pv) : (uint16_t)0);
   }
   lsum = xor32_sum(xor16_sum(lsum));
+  QM_PHASE(12);
   if (cur) {
     // the current token's value: one element (column kappa) of the lanes whose
     // quad holds that column
@@ -1816,16 +1906,22 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   const __amdgpu_buffer_rsrc_t ro = dev_rsrc(D.part_o + gbase * GQA * QSA_D, (long)D.splits * GQA * QSA_D * 2);
   const __amdgpu_buffer_rsrc_t rml = dev_rsrc(D.part_ml + gbase * GQA * 2, (long)D.splits * GQA * 2 * 4);
   const float linv = 1.0f / lsum;
+  // all four products before any store: a store ahead of a later load's wait
+  // would be waited for too (the counter covers both, in order)
+  f32x4_t o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const f32x4_t o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[i], pf, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    if (col < GQA) {
-      const unsigned lo = f32_to_bf16(o[0] * linv) | ((unsigned)f32_to_bf16(o[1] * linv) << 16);
-      const unsigned hi = f32_to_bf16(o[2] * linv) | ((unsigned)f32_to_bf16(o[3] * linv) << 16);
+  for (int i = 0; i < 4; ++i)
+    o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[i], pf, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+  if (col < GQA) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned lo = f32_to_bf16(o[i][0] * linv) | ((unsigned)f32_to_bf16(o[i][1] * linv) << 16);
+      const unsigned hi = f32_to_bf16(o[i][2] * linv) | ((unsigned)f32_to_bf16(o[i][3] * linv) << 16);
       st_dev_u32x2(ro, ((item * GQA + hcol) * QSA_D + 16 * (4 * wv + i) + 4 * quad) * 2, lo, hi);
     }
   }
   if (wv == 0 && quad == 0 && col < GQA) st_dev2(rml, ((item * GQA + col) * 2) * 4, make_float2(mx, lsum));
+  QM_PHASE(7);
 
   // ---- 5. the stores that outlive this step: the token's key/value into its
   // page slot (item 0 of each kv head), and per sequence (item 0 of kv head 0)
@@ -1839,7 +1935,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
     if (g == 0) {
       if (tid < IDX_D) {
         Act<T>::store(A.raw_keys, ((long)b * A.max_ctx + p) * IDX_D + tid, ikv);
-        if (j_new >= 0) A.block_keys[((long)b * A.max_blocks + j_new) * IDX_D + tid] = sh.newkey[tid];
+        if (j_new >= 0) A.block_keys[((long)b * A.max_blocks + j_new) * IDX_D + bk_index(tid)] = sh.newkey[tid];
       }
       if (D.iq_out)
         for (int i = tid; i < A.idx_heads * IDX_D; i += DEC_NT) D.iq_out[(long)b * A.idx_heads * IDX_D + i] = sh.iq[i];
@@ -1863,8 +1959,11 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   // of the group, then merge their slices
   wait_all_memory();
   __syncthreads();
+  QM_PHASE(8);
   if (tid == 0) raise_flag(D.flags + (long)bg * dec_flag_stride(D.splits) + item, gen + 1);
   if (item < DEC_SLICES) decode_merge<WIDE>(D, sh, b, g, item, n_att, gen, overflow);
+  QM_PHASE(10);
+  QM_PHASE_FLUSH();
 }
 
 int check_geom(const qm_qsa_geom* g, const char* who) {
@@ -1945,6 +2044,8 @@ size_t part_o_bytes(const qm_qsa_geom* g, int rows, int splits) {
 
 
 }  // namespace
+
+QM_PHASE_ENTRY(qsa)
 
 extern "C" int qm_v_slot(int row) { return v_slot(row); }
 

@@ -71,3 +71,4 @@ int qm_zero_words(void* p, long n_words, hipStream_t stream) {
   QM_CHECK_LAUNCH();
   return QM_OK;
 }
+

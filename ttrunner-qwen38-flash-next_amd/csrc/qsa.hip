@@ -458,44 +458,59 @@ __device__ __forceinline__ void prefetch_block_keys(float (&kp)[PRE][8], const f
   }
 }
 
-// The several-rows order: one lane per block walks the block's 128 elements in
-// order, 32 at a time, the next 32 in flight; the query rows come from LDS
-// (every lane reads the same address: a broadcast).
+// The several-rows order: one lane per (block, head) walks the block's 128
+// elements in order in one fused multiply-add chain. Wave w takes head w % 4,
+// so the query row is the same in every lane: it comes through the scalar
+// cache (s_load) as a uniform operand of the multiply-adds, not through LDS.
+// Rounds of 64 * NT / 256 blocks; each lane's relu'd dot product goes to
+// dsc[head][block of the round] (LDS), then one thread per block adds the
+// heads in order, divides and forms the key.
 template <int NT>
-__device__ void score_blocks_seq(const float* s_iq, const float* bk, int n_elig, int idx_heads,
-                                 unsigned long long* keys, float* scores_out) {
-  const int tid = threadIdx.x;
-  for (int j0 = 0; j0 < n_elig; j0 += NT) {
-    const int j = j0 + tid;
-    const bool valid = j < n_elig;
-    // float4 c of the (permuted) row holds elements c / 2 + 16 (4 (c % 2) + t),
-    // t < 4: the even ones elements 0..63, the odd ones 64..127
-    const float4* row = reinterpret_cast<const float4*>(bk + (long)(valid ? j : 0) * IDX_D);
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+__device__ void score_blocks_seq(const float* __restrict__ iq_row, const float* bk, int n_elig, int idx_heads,
+                                 unsigned long long* keys, float* scores_out, float (*dsc)[NT / 4]) {
+  constexpr int RB = NT / 4;                           // blocks per round
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = wv & 3, sub = wv >> 2;
+  // the row through the constant address space: a uniform address there is
+  // read with scalar loads into SGPRs (the kernel never writes it)
+  typedef const float __attribute__((address_space(4)))* const_ptr;
+  const unsigned long long qa = reinterpret_cast<unsigned long long>(iq_row + h * IDX_D);
+  const const_ptr qh = (const_ptr)(((unsigned long long)__builtin_amdgcn_readfirstlane((unsigned)(qa >> 32)) << 32) |
+                                   (unsigned)__builtin_amdgcn_readfirstlane((unsigned)qa));
+  for (int r0 = 0; r0 < n_elig; r0 += RB) {
+    const int jr = sub * 64 + lane, j = r0 + jr;
+    if (h < idx_heads) {
+      // float4 c of the (permuted) row holds elements c / 2 + 16 (4 (c % 2) + t),
+      // t < 4: the even ones elements 0..63, the odd ones 64..127
+      const float4* row = reinterpret_cast<const float4*>(bk + (long)(j < n_elig ? j : 0) * IDX_D);
+      float acc = 0.f;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      float4 kc[16];
+      for (int half = 0; half < 2; ++half) {
+        float4 kc[16];
 #pragma unroll
-      for (int m = 0; m < 16; ++m) kc[m] = row[2 * m + half];
+        for (int m = 0; m < 16; ++m) kc[m] = row[2 * m + half];
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int m = 0; m < 16; ++m) {
-          const int d = 64 * half + 16 * t + m;
-          const float kv = t == 0 ? kc[m].x : t == 1 ? kc[m].y : t == 2 ? kc[m].z : kc[m].w;
-#pragma unroll
-          for (int h = 0; h < 4; ++h) acc[h] = fmaf(s_iq[h * IDX_D + d], kv, acc[h]);
-        }
+          for (int m = 0; m < 16; ++m) {
+            const float kv = t == 0 ? kc[m].x : t == 1 ? kc[m].y : t == 2 ? kc[m].z : kc[m].w;
+            acc = fmaf(qh[64 * half + 16 * t + m], kv, acc);
+          }
+      }
+      dsc[h][jr] = fmaxf(acc, 0.f);
     }
-    float sc = 0.f;
+    __syncthreads();
+    if (tid < RB && r0 + tid < n_elig) {
+      float sc = 0.f;
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
-      if (h < idx_heads) sc = add_rn(sc, fmaxf(acc[h], 0.f));
-    sc = div_rn(sc, 11.313708498984761f);
-    if (valid) {
-      keys[j] = sel_key(sc, j);
-      if (scores_out) scores_out[j] = sc;
+      for (int hh = 0; hh < 4; ++hh)
+        if (hh < idx_heads) sc = add_rn(sc, dsc[hh][tid]);
+      sc = div_rn(sc, 11.313708498984761f);
+      keys[r0 + tid] = sel_key(sc, r0 + tid);
+      if (scores_out) scores_out[r0 + tid] = sc;
     }
+    __syncthreads();
   }
   const int npad = (n_elig + 31) & ~31;
   for (int j = n_elig + tid; j < npad; j += NT) keys[j] = 0ull;
@@ -692,6 +707,7 @@ struct SelArgs {
 
 struct SelShared {
   float q[4 * IDX_D];
+  float dsc[4][SELP_NT / 4];            // a scoring round's relu'd dot products (several-rows order)
   float newkey[IDX_D];
   unsigned long long key[SEL_MAX_BLOCKS];
   int pages[SEL_MAX_BLOCKS];
@@ -721,16 +737,18 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
   if (n_elig > A.topk || A.scores_out) {
     const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
     float* sc_out = A.scores_out ? A.scores_out + (long)row * A.max_blocks : nullptr;
-    if (A.seq == 1) {
-      // one query row: the first passes of block keys are in flight across the barrier
+    if (NT != SELP_NT || A.seq == 1) {
+      // one query row (the 256-thread front kernel serves decode only): the
+      // first passes of block keys are in flight across the barrier
       float kp[score_pre<NT>()][8];
       prefetch_block_keys<NT>(kp, bk, n_elig, new_j, true);
       __syncthreads();    // S.q and S.newkey visible
       score_blocks<NT>(S.q, S.newkey, bk, n_elig, new_j, A.idx_heads, S.key, sc_out, kp);
     } else {
       // several rows (a block completed in this call is already in the cache)
-      __syncthreads();
-      score_blocks_seq<NT>(S.q, bk, n_elig, A.idx_heads, S.key, sc_out);
+      if constexpr (NT == SELP_NT)
+        score_blocks_seq<NT>(A.iq + (long)row * A.idx_heads * IDX_D, bk, n_elig, A.idx_heads, S.key, sc_out,
+                             S.dsc);
     }
   }
   __syncthreads();

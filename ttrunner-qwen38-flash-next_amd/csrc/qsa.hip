@@ -459,16 +459,27 @@ __device__ __forceinline__ void prefetch_block_keys(float (&kp)[PRE][8], const f
 }
 
 // The several-rows order: one lane per (block, head) walks the block's 128
-// elements in order in one fused multiply-add chain. Wave w takes head w % 4,
-// so the query row is the same in every lane: it comes through the scalar
-// cache (s_load) as a uniform operand of the multiply-adds, not through LDS.
-// Rounds of 64 * NT / 256 blocks; each lane's relu'd dot product goes to
-// dsc[head][block of the round] (LDS), then one thread per block adds the
-// heads in order, divides and forms the key.
+// elements in order in one fused multiply-add chain. Rounds of SEQ_RB blocks:
+// the whole workgroup copies the round's block rows into LDS with coalesced
+// loads (a lane walking its own 512-byte row in global memory would touch 64
+// cache lines per load instruction), each row padded by 16 bytes so that the
+// lanes' row reads fall on distinct banks; the next round's rows are loaded
+// into registers while this round is scored. Waves 0..7 score: wave w takes
+// head w % 4 and blocks 64 (w / 4) + lane, so the query row is the same in
+// every lane and comes through the scalar cache (s_load) as a uniform operand
+// of the multiply-adds. Each lane's relu'd dot product goes to
+// dsc[head][block of the round], then one thread per block adds the heads in
+// order, divides and forms the key.
+constexpr int SEQ_RB = 128;                  // blocks per round
+constexpr int SEQ_STRIDE = IDX_D + 4;        // floats per staged row
+constexpr int SEQ_STAGE = SEQ_RB * SEQ_STRIDE;
+
 template <int NT>
 __device__ void score_blocks_seq(const float* __restrict__ iq_row, const float* bk, int n_elig, int idx_heads,
-                                 unsigned long long* keys, float* scores_out, float (*dsc)[NT / 4]) {
-  constexpr int RB = NT / 4;                           // blocks per round
+                                 unsigned long long* keys, float* scores_out, float (*dsc)[NT / 4],
+                                 float* stage) {
+  static_assert(NT == 1024 && NT / 4 >= SEQ_RB, "eight scoring waves of 64 blocks; dsc holds a round");
+  constexpr int F4 = SEQ_RB * IDX_D / 4 / NT;  // float4 of a round each thread copies
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = wv & 3, sub = wv >> 2;
@@ -478,30 +489,56 @@ __device__ void score_blocks_seq(const float* __restrict__ iq_row, const float* 
   const unsigned long long qa = reinterpret_cast<unsigned long long>(iq_row + h * IDX_D);
   const const_ptr qh = (const_ptr)(((unsigned long long)__builtin_amdgcn_readfirstlane((unsigned)(qa >> 32)) << 32) |
                                    (unsigned)__builtin_amdgcn_readfirstlane((unsigned)qa));
-  for (int r0 = 0; r0 < n_elig; r0 += RB) {
-    const int jr = sub * 64 + lane, j = r0 + jr;
-    if (h < idx_heads) {
+  const float4* src = reinterpret_cast<const float4*>(bk);
+  float4 nxt[F4];
+  auto fetch = [&](int r0) {
+#pragma unroll
+    for (int i = 0; i < F4; ++i) {
+      const int f = tid + NT * i, j = r0 + (f >> 5);
+      nxt[i] = j < n_elig ? src[(long)j * (IDX_D / 4) + (f & 31)] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  fetch(0);
+  for (int r0 = 0; r0 < n_elig; r0 += SEQ_RB) {
+#pragma unroll
+    for (int i = 0; i < F4; ++i) {
+      const int f = tid + NT * i;
+      *reinterpret_cast<float4*>(stage + (f >> 5) * SEQ_STRIDE + 4 * (f & 31)) = nxt[i];
+    }
+    __syncthreads();     // the round's rows are staged; the previous round's dsc is consumed
+    if (r0 == 0) QM_PHASE(4);
+    if (r0 + SEQ_RB < n_elig) fetch(r0 + SEQ_RB);
+    const int jr = sub * 64 + lane;
+    if (sub < SEQ_RB / 64 && h < idx_heads) {
       // float4 c of the (permuted) row holds elements c / 2 + 16 (4 (c % 2) + t),
       // t < 4: the even ones elements 0..63, the odd ones 64..127
-      const float4* row = reinterpret_cast<const float4*>(bk + (long)(j < n_elig ? j : 0) * IDX_D);
+      const float4* row = reinterpret_cast<const float4*>(stage + jr * SEQ_STRIDE);
       float acc = 0.f;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
+        // the half's query elements (scalar loads) and key elements (LDS) are
+        // all requested before the first multiply-add: scalar loads complete
+        // out of order, so any use of one waits for every LDS read in flight
+        float qv[64];
+#pragma unroll
+        for (int i = 0; i < 64; ++i) qv[i] = qh[64 * half + i];
         float4 kc[16];
 #pragma unroll
         for (int m = 0; m < 16; ++m) kc[m] = row[2 * m + half];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int m = 0; m < 16; ++m) {
             const float kv = t == 0 ? kc[m].x : t == 1 ? kc[m].y : t == 2 ? kc[m].z : kc[m].w;
-            acc = fmaf(qh[64 * half + 16 * t + m], kv, acc);
+            acc = fmaf(qv[16 * t + m], kv, acc);
           }
       }
       dsc[h][jr] = fmaxf(acc, 0.f);
     }
-    __syncthreads();
-    if (tid < RB && r0 + tid < n_elig) {
+    __syncthreads();     // dsc complete; every staged row has been read
+    if (r0 == 0) QM_PHASE(5);
+    if (tid < SEQ_RB && r0 + tid < n_elig) {
       float sc = 0.f;
 #pragma unroll
       for (int hh = 0; hh < 4; ++hh)
@@ -510,7 +547,6 @@ __device__ void score_blocks_seq(const float* __restrict__ iq_row, const float* 
       keys[r0 + tid] = sel_key(sc, r0 + tid);
       if (scores_out) scores_out[r0 + tid] = sc;
     }
-    __syncthreads();
   }
   const int npad = (n_elig + 31) & ~31;
   for (int j = n_elig + tid; j < npad; j += NT) keys[j] = 0ull;
@@ -536,26 +572,55 @@ __device__ void score_blocks_seq(const float* __restrict__ iq_row, const float* 
 constexpr int rank_scratch(int maxk) { return 256 + 40 + maxk; }
 constexpr int RANK_CAND = 128;          // candidates the bucket threshold may leave
 
+// Whole-wave reductions and scans by DPP within rows of 16 lanes and lane
+// reads across the four rows (every lane active; results in every lane).
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp_u(unsigned v) {
+  return static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, true));
+}
+template <bool MAX>
+__device__ __forceinline__ unsigned wave_minmax_u(unsigned v) {
+  auto op = [](unsigned x, unsigned y) { return MAX ? max(x, y) : min(x, y); };
+  v = op(v, dpp_u<0xB1>(v));      // quad_perm [1,0,3,2]
+  v = op(v, dpp_u<0x4E>(v));      // quad_perm [2,3,0,1]
+  v = op(v, dpp_u<0x124>(v));     // row_ror:4
+  v = op(v, dpp_u<0x128>(v));     // row_ror:8
+  return op(op(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+            op(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+// inclusive prefix sum over the wave's lanes
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  x += static_cast<int>(dpp_u<0x111>(static_cast<unsigned>(x)));    // row_shr:1
+  x += static_cast<int>(dpp_u<0x112>(static_cast<unsigned>(x)));    // row_shr:2
+  x += static_cast<int>(dpp_u<0x114>(static_cast<unsigned>(x)));    // row_shr:4
+  x += static_cast<int>(dpp_u<0x118>(static_cast<unsigned>(x)));    // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31),
+            r2 = __builtin_amdgcn_readlane(x, 47);
+  const int row = (threadIdx.x & 63) >> 4;
+  return x + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+}
+
 // The bucket threshold (above). Returns false, having written nothing to sel,
 // when more than RANK_CAND keys are at or above the threshold bucket. The
-// bucket of a key is ((score bits - min) * floor(2^40 / width)) >> 32, width =
-// max - min + 1: monotone in the key and below 256.
+// bucket of a key is ((score bits - min) * mul) >> 32 with width = max - min +
+// 1 and mul = 2^40 / width rounded down with a relative margin of 2^-20 (a
+// single-precision quotient, whose rounding the margin covers): monotone in the
+// key and below 256. Waves exchange partial results through LDS only at the
+// four barriers; within a wave, DPP and lane reads.
 template <int NT>
 __device__ bool bucket_topk(const unsigned long long* keys, int n, int topk, int* sel, int* hist, int* wtot,
                             int* state, int* cand) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int NW = NT / 64;
+  static_assert(NW <= 16 && NT >= 256, "wave totals in 16 slots; one bucket per thread");
   unsigned lo = 0xffffffffu, hi = 0u;
   for (int j = tid; j < n; j += NT) {
     const unsigned v = static_cast<unsigned>(keys[j] >> 32);
     lo = min(lo, v);
     hi = max(hi, v);
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    lo = min(lo, static_cast<unsigned>(__shfl_xor(static_cast<int>(lo), o, 64)));
-    hi = max(hi, static_cast<unsigned>(__shfl_xor(static_cast<int>(hi), o, 64)));
-  }
+  lo = wave_minmax_u<false>(lo);
+  hi = wave_minmax_u<true>(hi);
   if (tid < 256) hist[tid] = 0;
   if (tid < 8) state[tid] = 0;
   if (lane == 0) {
@@ -563,28 +628,23 @@ __device__ bool bucket_topk(const unsigned long long* keys, int n, int topk, int
     wtot[16 + wv] = static_cast<int>(hi);
   }
   __syncthreads();
-  unsigned glo = 0xffffffffu, ghi = 0u;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    glo = min(glo, static_cast<unsigned>(wtot[w]));
-    ghi = max(ghi, static_cast<unsigned>(wtot[16 + w]));
-  }
-  const unsigned long long mul = (1ull << 40) / (static_cast<unsigned long long>(ghi - glo) + 1ull);
+  QM_PHASE(6);
+  const unsigned glo = wave_minmax_u<false>(lane < NW ? static_cast<unsigned>(wtot[lane]) : 0xffffffffu);
+  const unsigned ghi = wave_minmax_u<true>(lane < NW ? static_cast<unsigned>(wtot[16 + lane]) : 0u);
+  const float width = static_cast<float>(ghi - glo) + 1.0f;
+  const unsigned long long mul =
+      static_cast<unsigned long long>(1099511627776.0f * (1.0f - 9.5367431640625e-07f) / width);
   auto bucket = [&](unsigned long long k) {
     return static_cast<int>((static_cast<unsigned long long>(static_cast<unsigned>(k >> 32) - glo) * mul) >> 32);
   };
   for (int j = tid; j < n; j += NT) atomicAdd(&hist[bucket(keys[j])], 1);
-  __syncthreads();                        // every thread has read the range: wtot is free
+  __syncthreads();                        // every wave has read the range: wtot is free
+  QM_PHASE(7);
   // suffix sums over the buckets: thread t takes bucket 255 - t
   int h = 0, incl = 0;
   if (tid < 256) {
     h = hist[255 - tid];
-    incl = h;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int x = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += x;
-    }
+    incl = wave_incl_sum(h);
     if (lane == 63) wtot[wv] = incl;
   }
   __syncthreads();
@@ -596,25 +656,50 @@ __device__ bool bucket_topk(const unsigned long long* keys, int n, int topk, int
     }
   }
   __syncthreads();
+  QM_PHASE(8);
   const int bstar = state[0], n_cand = state[1];
+#ifdef QM_PHASE_TRACE
+  if (threadIdx.x == 0) qm_ph_[14] = static_cast<unsigned long long>(n_cand);
+#endif
   if (n_cand > RANK_CAND) return false;
-  // gather, in any order (the ranks below do not depend on it); the keys go
-  // where the histogram was
+  // gather, in any order (the ranks below do not depend on it): one LDS atomic
+  // per wave reserves the wave's places, lanes take theirs by mask count. The
+  // keys go where the histogram was, zero-padded to a multiple of 32.
   unsigned long long* ckey = reinterpret_cast<unsigned long long*>(hist);
-  for (int j = tid; j < n; j += NT) {
-    const unsigned long long k = keys[j];
-    if (bucket(k) >= bstar) {
-      const int at = atomicAdd(&state[2], 1);
+  const int cpad = (n_cand + 31) & ~31;
+  for (int c = n_cand + tid; c < cpad; c += NT) ckey[c] = 0ull;
+  for (int j0 = 0; j0 < n; j0 += NT) {
+    const int j = j0 + tid;
+    const unsigned long long k = j < n ? keys[j] : 0ull;
+    const bool pick = j < n && bucket(k) >= bstar;
+    const unsigned long long m = __ballot(pick);
+    int base = 0;
+    if (lane == 0 && m) base = atomicAdd(&state[2], __popcll(m));
+    base = __builtin_amdgcn_readfirstlane(base);
+    if (pick) {
+      const int at = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(m >> 32),
+                                                                      __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(m), 0u)));
       ckey[at] = k;
       cand[at] = j;
     }
   }
   __syncthreads();
-  for (int c = tid; c < n_cand; c += NT) {
-    const unsigned long long kc = ckey[c];
+  QM_PHASE(9);
+  // rank by counting: two adjacent lanes split one candidate's comparisons
+  // (only the waves that hold candidates)
+  if (tid < 2 * cpad) {
+    const int c = tid >> 1, part = tid & 1, hc = cpad >> 1;
+    const unsigned long long kc = ckey[c < n_cand ? c : 0];
     int rank = 0;
-    for (int i = 0; i < n_cand; ++i) rank += ckey[i] > kc ? 1 : 0;
-    if (rank < topk) sel[rank] = cand[c];
+    for (int i = part * hc; i < part * hc + hc; i += 16) {
+      unsigned long long k16[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) k16[u] = ckey[i + u];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) rank += k16[u] > kc ? 1 : 0;
+    }
+    rank += __builtin_amdgcn_update_dpp(0, rank, 0xB1, 0xF, 0xF, true);
+    if (part == 0 && c < n_cand && rank < topk) sel[rank] = cand[c];
   }
   return true;
 }
@@ -720,7 +805,7 @@ struct SelShared {
 // keys come from the cache, except block new_j (>= 0 when this very launch
 // completed it), whose key is in S.newkey.
 template <int NT>
-__device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p, int new_j) {
+__device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p, int new_j, float* stage) {
   const int tid = threadIdx.x;
   const int n_elig = min((p + 1) / A.ratio, A.max_blocks);
   const int n_sel = min(n_elig, A.topk);
@@ -748,15 +833,17 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
       // several rows (a block completed in this call is already in the cache)
       if constexpr (NT == SELP_NT)
         score_blocks_seq<NT>(A.iq + (long)row * A.idx_heads * IDX_D, bk, n_elig, A.idx_heads, S.key, sc_out,
-                             S.dsc);
+                             S.dsc, stage);
     }
   }
   __syncthreads();
+  QM_PHASE(1);
   if (n_elig <= A.topk) {
     for (int i = tid; i < n_elig; i += NT) { out_ids[i] = i; S.sel[i] = i; }
   } else {
     rank_topk<NT, SEL_MAX_BLOCKS / 2>(S.key, n_elig, A.topk, S.sel, S.rscr);
     __syncthreads();
+    QM_PHASE(2);
     for (int i = tid; i < A.topk; i += NT) out_ids[i] = S.sel[i];
   }
   if (tid == 0) A.n_sel[row] = n_sel;
@@ -787,14 +874,19 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
 }
 
 __global__ __launch_bounds__(SELP_NT) void qsa_select_kernel(SelArgs A) {
+  QM_PHASE_DECL
   const int row = blockIdx.x;
   const int b = row / A.seq, s = row % A.seq;
   const int p = A.positions[b] + s;
   __shared__ SelShared S;
+  QM_PHASE(0);
   for (int i = threadIdx.x; i < 4 * IDX_D; i += SELP_NT)
     S.q[i] = i < A.idx_heads * IDX_D ? A.iq[(long)row * A.idx_heads * IDX_D + i] : 0.f;
   __syncthreads();
-  select_row<SELP_NT>(A, S, row, b, p, -1);
+  __shared__ float4 stage[SEQ_STAGE / 4];   // block rows of a scoring round (several rows per sequence)
+  select_row<SELP_NT>(A, S, row, b, p, -1, reinterpret_cast<float*>(stage));
+  QM_PHASE(3);
+  QM_PHASE_FLUSH();
 }
 
 // Decode (one token per sequence) front end in one launch: the query, key and
@@ -839,7 +931,7 @@ __global__ __launch_bounds__(SEL_NT) void qsa_front_kernel(PrepArgs<T> A, SelArg
     if (tid < IDX_D) S.newkey[tid] = y;
   }
   __syncthreads();
-  select_row<SEL_NT>(SA, S, b, b, p, new_j);
+  select_row<SEL_NT>(SA, S, b, b, p, new_j, nullptr);
 }
 
 // ---------------------------------------------------------------------------

@@ -215,20 +215,29 @@ def test_prefill_chunk_matches_golden_reference(gpu):
     assert rel_err(flat[::stride][: want.numel()], want) < OUT_TOL
 
 
-@pytest.mark.parametrize("past,seq,batch,dtype", [(0, 37, 1, torch.bfloat16), (2000, 96, 1, torch.bfloat16),
-                                                   (4030, 70, 2, torch.float32), (8100, 128, 1, torch.bfloat16)])
-def test_prefill_chunk_attention_matches_oracle(gpu, past, seq, batch, dtype):
+@pytest.mark.parametrize("past,seq,batch,dtype,shared", [(0, 37, 1, torch.bfloat16, False),
+                                                          (2000, 96, 1, torch.bfloat16, False),
+                                                          (4030, 70, 2, torch.float32, False),
+                                                          (8100, 128, 1, torch.bfloat16, False),
+                                                          (3000, 300, 1, torch.bfloat16, False),
+                                                          (2000, 96, 1, torch.bfloat16, True)])
+def test_prefill_chunk_attention_matches_oracle(gpu, past, seq, batch, dtype, shared):
     """The block-major chunk attention (qm_qsa_attend_chunk) against the oracle,
     and against the per-row item attention (qm_qsa_attend) on the same chunk:
     a ragged last tile, chunks that complete blocks part-way (rows whose tail
-    block another row has selected), a batch of two with its own pages."""
+    block another row has selected), a batch of two with its own pages, a
+    chunk of more rows than one launch takes (300), and rows that all carry the
+    same hidden state, so that every row selects (nearly) the same blocks and
+    one workgroup holds ~96 entries of a block."""
     cfg = OracleConfig()
     store = gi.FakeStore(gi.qsa_weights(3, 90, dtype))
     pasts = [gi.qsa_past(91 + b, past, dtype) for b in range(batch)]
     keys, values, idx_keys = (torch.cat([p[i] for p in pasts]) for i in range(3))
     hidden = gi.normal(gi.rng(93), (batch, seq, gi.HIDDEN)).to(dtype)
+    if shared:
+        hidden = hidden[:, :1].expand(batch, seq, gi.HIDDEN).contiguous()
     cos, sin = tables(past + seq)
-    print(f"prefill chunk past={past} seq={seq} batch={batch} {dtype}", flush=True)
+    print(f"prefill chunk past={past} seq={seq} batch={batch} {dtype} shared={shared}", flush=True)
     want, _, _, chosen = _oracle_core(cfg, store, hidden, cos, sin, keys if past else None,
                                       values if past else None, idx_keys, past)
     outs = []

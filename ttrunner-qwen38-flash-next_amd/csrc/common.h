@@ -35,6 +35,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
+// Two floats to packed bf16 (a in the low half) with the hardware conversion
+// (round to nearest even, like f32_to_bf16 for every finite value): one
+// instruction where f32_to_bf16 takes several.
+typedef float f32x2_cvt_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_cvt_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2_cvt_t{a, b}, bf16x2_cvt_t));
+}
+
 // Activation element access: load as float, store with rounding to the type.
 template <typename T> struct Act;
 template <> struct Act<float> {

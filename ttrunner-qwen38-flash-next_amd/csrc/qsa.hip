@@ -25,6 +25,15 @@
 
 namespace {
 
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
 constexpr int QSA_D = 256;     // attention head dim
 constexpr int IDX_D = 128;     // indexer head dim
 constexpr int PREP_NT = 256;
@@ -92,6 +101,58 @@ __device__ float norm_rope_row(float* s_x, float* s_y, float* s_scr, int n, cons
   return y;
 }
 
+// ---- RMS norms of one row per wave, in torch's CPU order: 32 partial sums,
+// partial a summing the squares of elements a, a + 32, a + 64, ... in order;
+// then c_l = ((s_l + s_(l+8)) + s_(l+16)) + s_(l+24) for l < 8, added in
+// order; every square and sum rounded on its own. A 128-wide row sits in the
+// wave as x[k] = element lane + 64 k (k < 2), a 256-wide row k < 4.
+template <int N>
+__device__ __forceinline__ float row_shl(float v) { return dpp_f<0x100 + N>(v); }
+
+__device__ __forceinline__ float xor32_f(float v) { return __shfl_xor(v, 32, 64); }
+
+__device__ __forceinline__ float wave_rinv_finish(float s, float n, float eps) {
+  const float s16 = __shfl_down(s, 16, 64);
+  const float c = add_rn(add_rn(add_rn(s, row_shl<8>(s)), s16), row_shl<8>(s16));   // lanes 0..7: c_l
+  float tot = readlane_f(c, 0);
+#pragma unroll
+  for (int l = 1; l < 8; ++l) tot = add_rn(tot, readlane_f(c, l));
+  return rsqrt_rn(add_rn(div_rn(tot, n), eps));
+}
+
+template <int K>
+__device__ __forceinline__ float wave_rinv(const float (&x)[K], float eps) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const float q = mul_rn(x[k], x[k]);
+    s = k == 0 ? q : add_rn(s, q);          // element lane + 64 k
+    s = add_rn(s, xor32_f(q));              // element lane + 64 k + 32
+  }
+  return wave_rinv_finish(s, 64.f * K, eps);
+}
+
+// rope of a normed row held as y[k] = element lane + 64 k: element e < rope
+// becomes y_e cos + (e < rope/2 ? -y_p : y_p) sin, p = e +- rope/2 (the
+// partner's normed value, from lane p % 64 of register p / 64); every multiply
+// and add rounded on its own.
+template <int K>
+__device__ __forceinline__ void wave_rope(float (&y)[K], int rope, const float (&cs)[2], const float (&sn)[2]) {
+  const int lane = threadIdx.x & 63, half = rope >> 1;
+  float out[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int e = lane + 64 * k;
+    const int pe = min(e < half ? e + half : e - half, 127);
+    const float v0 = __shfl(y[0], pe & 63, 64);
+    const float v1 = __shfl(y[1], pe & 63, 64);
+    const float yp = pe >= 64 ? v1 : v0;
+    out[k] = e < rope ? add_rn(mul_rn(y[k], cs[k]), mul_rn(e < half ? -yp : yp, sn[k])) : y[k];
+  }
+  y[0] = out[0];
+  y[1] = out[1];
+}
+
 // this thread's cos and sin of a table row (channel clamped into the rope range)
 __device__ __forceinline__ float2 rope_cs(const float* cos, const float* sin, long row, int rope) {
   const long i = row * rope + min((int)threadIdx.x, rope - 1);
@@ -153,80 +214,124 @@ struct PrepArgs {
   float eps;
 };
 
-// qsa_prep_kernel grid: (row, role). Roles 0..Hq-1: attention query head
-// `role` (RMS norm, rope, bf16 hi/lo). Roles Hq..Hq+Hkv-1: key/value head
-// (norm + rope the key, append both). Then one role per indexer query head,
-// and a last one that appends the raw indexer key and pools a block the row
-// completes.
+// qsa_prep_kernel, a 1-D grid of 256-thread workgroups. The first
+// batch * (seq / ratio + 1) pool the blocks the chunk's rows complete (the
+// longest work, dispatched first): workgroup x takes the (x % per)-th block
+// completed in sequence x / per, if there is one. Every later wave takes one
+// (row, role): roles 0..Hq-1 the attention query heads (RMS norm, rope, bf16
+// hi/lo), Hq..Hq+Hkv-1 a key/value head (norm + rope the key, append both to
+// the pages), then the indexer query heads (the first of which also appends
+// the row's raw indexer key). A wave normalises its row on its own (no
+// barrier); the pooled key of a block does not read the raw keys this launch
+// appends (rows of the chunk come from ik).
 template <typename T>
-__device__ void prep_head(const PrepArgs<T>& A, int b, int s, int role) {
-  __shared__ float s_x[QSA_D], s_y[QSA_D], s_scr[32];
-  const int row = b * A.seq + s;
-  const int tid = threadIdx.x;
+__device__ void prep_wave(const PrepArgs<T>& A, int row, int role) {
+  const int lane = threadIdx.x & 63;
+  const int b = row / A.seq, s = row % A.seq;
   const int pos = A.positions[b] + s;
+  const int rope = A.rope;
+  float cs[2], sn[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const long i = (long)pos * rope + min(lane + 64 * k, rope - 1);
+    cs[k] = A.cos[i];
+    sn[k] = A.sin[i];
+  }
+  auto nrm = [&](float xv, float ri, float w) { return Act<T>::round(mul_rn(mul_rn(xv, ri), w)); };
   if (role < A.hq) {
     if (!A.qg) return;
     const T* src = A.qg + ((long)row * A.hq + role) * (2 * QSA_D);
-    const float xv = Act<T>::load(src, tid);
-    const float2 csv = rope_cs(A.cos, A.sin, pos, A.rope);
-    s_x[tid] = xv;
-    const float y = norm_rope_row<T>(s_x, s_y, s_scr, QSA_D, A.q_norm, A.eps, A.rope, csv.x, csv.y);
-    // the attention MFMA takes q as bf16: keep it as hi + lo so the product
-    // carries ~16 mantissa bits (rows [2 * row] hold hi, [2 * row + 1] lo)
-    const uint16_t hi = f32_to_bf16(y);
-    A.q_out[q_index(row, A.hkv, 0, role, tid)] = hi;
-    A.q_out[q_index(row, A.hkv, 1, role, tid)] = f32_to_bf16(y - bf16_to_f32(hi));
+    float x[4], w[4], y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[k] = Act<T>::load(src, lane + 64 * k);
+      w[k] = A.q_norm[lane + 64 * k];
+    }
+    const float ri = wave_rinv<4>(x, A.eps);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y[k] = nrm(x[k], ri, w[k]);
+    wave_rope<4>(y, rope, cs, sn);
+    // the attention MFMA takes q as bf16: kept as hi + lo, the product carries
+    // ~16 mantissa bits
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int d = lane + 64 * k;
+      const uint16_t hi = f32_to_bf16(y[k]);
+      A.q_out[q_index(row, A.hkv, 0, role, d)] = hi;
+      A.q_out[q_index(row, A.hkv, 1, role, d)] = f32_to_bf16(y[k] - bf16_to_f32(hi));
+    }
     return;
   }
-  if (!A.k_new) return;
-  const int g = role - A.hq;
-  const long src = ((long)row * A.hkv + g) * QSA_D;
-  // the key, the value, the rope row and the page share one round trip
-  const float xv = Act<T>::load(A.k_new, src + tid);
-  const float vv = Act<T>::load(A.v_new, src + tid);
-  const float2 csv = rope_cs(A.cos, A.sin, pos, A.rope);
-  const int page = A.page_table[(long)b * A.max_pages + pos / A.page_size];
-  s_x[tid] = xv;
-  const float y = norm_rope_row<T>(s_x, s_y, s_scr, QSA_D, A.k_norm, A.eps, A.rope, csv.x, csv.y);
-  const int prow = pos % A.page_size;
-  const long pbase = ((long)page * A.hkv + g) * A.page_size * QSA_D;
-  A.k_pool[pbase + k_page_index(prow, tid)] = f32_to_bf16(y);
-  A.v_pool[pbase + v_page_index(prow, tid)] = f32_to_bf16(vv);
+  if (role < A.hq + A.hkv) {
+    if (!A.k_new) return;
+    const int g = role - A.hq;
+    const long src = ((long)row * A.hkv + g) * QSA_D;
+    const int page = A.page_table[(long)b * A.max_pages + pos / A.page_size];
+    float x[4], v[4], w[4], y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[k] = Act<T>::load(A.k_new, src + lane + 64 * k);
+      v[k] = Act<T>::load(A.v_new, src + lane + 64 * k);
+      w[k] = A.k_norm[lane + 64 * k];
+    }
+    const float ri = wave_rinv<4>(x, A.eps);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y[k] = nrm(x[k], ri, w[k]);
+    wave_rope<4>(y, rope, cs, sn);
+    const int prow = pos % A.page_size;
+    const long pbase = ((long)page * A.hkv + g) * A.page_size * QSA_D;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int d = lane + 64 * k;
+      A.k_pool[pbase + k_page_index(prow, d)] = f32_to_bf16(y[k]);
+      A.v_pool[pbase + v_page_index(prow, d)] = f32_to_bf16(v[k]);
+    }
+    return;
+  }
+  const int h = role - A.hq - A.hkv;
+  const long src = ((long)row * A.idx_heads + h) * IDX_D;
+  float x[2], w[2], y[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    x[k] = Act<T>::load(A.iq, src + lane + 64 * k);
+    w[k] = A.iq_norm[lane + 64 * k];
+  }
+  if (h == 0) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      A.raw_keys[((long)b * A.max_ctx + pos) * IDX_D + lane + 64 * k] = A.ik[(long)row * IDX_D + lane + 64 * k];
+  }
+  const float ri = wave_rinv<2>(x, A.eps);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) y[k] = nrm(x[k], ri, w[k]);
+  wave_rope<2>(y, rope, cs, sn);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) A.iq_out[src + lane + 64 * k] = y[k];
 }
+
+__host__ __device__ __forceinline__ int prep_pool_per_seq(int seq, int ratio) { return seq / ratio + 1; }
 
 template <typename T>
 __global__ __launch_bounds__(PREP_NT) void qsa_prep_kernel(PrepArgs<T> A) {
-  const int row = blockIdx.x;               // b * seq + s
-  const int b = row / A.seq, s = row % A.seq;
-  // workgroups start in blockIdx order: the last role (raw key append and the
-  // pooling of a completed block, the longest) goes at y = 0
-  const int role = (blockIdx.y + gridDim.y - 1) % gridDim.y;
-  const int tid = threadIdx.x;
-  const int pos0 = A.positions[b];
-  const int pos = pos0 + s;
-
-  __shared__ float s_x[QSA_D], s_y[QSA_D], s_scr[32];
-
-  if (role < A.hq + A.hkv) {
-    prep_head<T>(A, b, s, role);
+  const int per = prep_pool_per_seq(A.seq, A.ratio);
+  const int n_pool = A.batch * per;
+  const int x = blockIdx.x;
+  if (x < n_pool) {
+    // the blocks j whose last row (j + 1) ratio - 1 lies in [pos0, pos0 + seq)
+    __shared__ float s_x[IDX_D], s_y[IDX_D], s_scr[32];
+    const int b = x / per;
+    const int pos0 = A.positions[b];
+    const int j = pos0 / A.ratio + x % per;
+    if ((j + 1) * A.ratio > pos0 + A.seq) return;
+    pool_block<T>(j, A.ratio, A.rope, A.eps, A.ik_norm, A.cos, A.sin, A.raw_keys + (long)b * A.max_ctx * IDX_D,
+                  A.ik + (long)b * A.seq * IDX_D, pos0, A.block_keys + (long)b * A.max_blocks * IDX_D, s_x, s_y,
+                  s_scr);
     return;
   }
-  if (role < A.hq + A.hkv + A.idx_heads) {
-    // -------- one indexer query head
-    const int h = role - A.hq - A.hkv;
-    const float xv = Act<T>::load(A.iq, ((long)row * A.idx_heads + h) * IDX_D + min(tid, IDX_D - 1));
-    const float2 csv = rope_cs(A.cos, A.sin, pos, A.rope);
-    if (tid < IDX_D) s_x[tid] = xv;
-    const float y = norm_rope_row<T>(s_x, s_y, s_scr, IDX_D, A.iq_norm, A.eps, A.rope, csv.x, csv.y);
-    if (tid < IDX_D) A.iq_out[((long)row * A.idx_heads + h) * IDX_D + tid] = y;
-    return;
-  }
-  // -------- raw indexer key append, and the pooled key of a completed block
-  if (tid < IDX_D) A.raw_keys[((long)b * A.max_ctx + pos) * IDX_D + tid] = A.ik[(long)row * IDX_D + tid];
-  if ((pos + 1) % A.ratio != 0) return;
-  pool_block<T>(pos / A.ratio, A.ratio, A.rope, A.eps, A.ik_norm, A.cos, A.sin,
-                A.raw_keys + (long)b * A.max_ctx * IDX_D, A.ik + (long)b * A.seq * IDX_D, pos0,
-                A.block_keys + (long)b * A.max_blocks * IDX_D, s_x, s_y, s_scr);
+  const int roles = A.hq + A.hkv + A.idx_heads;
+  const long wid = (long)(x - n_pool) * (PREP_NT / 64) + (threadIdx.x >> 6);
+  if (wid >= (long)A.batch * A.seq * roles) return;
+  prep_wave<T>(A, static_cast<int>(wid / roles), static_cast<int>(wid % roles));
 }
 
 template <typename T>
@@ -293,8 +398,6 @@ __device__ __forceinline__ void load_block_part(float (&k)[8], const float* bk, 
   for (int i = 0; i < 8; ++i) k[i] = valid ? v[i] : 0.f;
 }
 
-template <int N>
-__device__ __forceinline__ float row_shl(float v) { return dpp_f<0x100 + N>(v); }
 
 // the one-row score of the block whose 16 lanes call this (valid in lane 0 of
 // the 16); q holds this lane's elements of the 4 query rows
@@ -899,7 +1002,7 @@ __global__ __launch_bounds__(SEL_NT) void qsa_front_kernel(PrepArgs<T> A, SelArg
   const int b = blockIdx.x;
   const int role = blockIdx.y;
   if (role < A.hq + A.hkv) {
-    prep_head<T>(A, b, 0, role);
+    if (threadIdx.x < 64) prep_wave<T>(A, b, role);
     return;
   }
   const int tid = threadIdx.x;
@@ -1141,329 +1244,427 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T, PO> A
 // ---------------------------------------------------------------------------
 // chunk attention (prefill), block-major
 // ---------------------------------------------------------------------------
-// The attention of a chunk of S query rows reads each key/value block once:
-//   qsa_chunk_index   one workgroup per sequence: the (row, slot) entries
-//                     (slot i < topk: the row's i-th selected block; slot topk:
-//                     its tail block, keys ts..p) counting-sorted by block, then
-//                     cut into work items of up to 8 entries of one block; slots
-//                     a row does not use get an empty partial (max -inf)
-//   qsa_chunk_attend  persistent workgroups per (kv head, sequence): a work
-//                     item's block (ratio tokens: 16 KB of key and 16 KB of
-//                     value pieces per 32 tokens, contiguous in the page's lane
-//                     order) is staged in LDS once, and each wave scores it for
-//                     two entries x 8 query heads on bf16 MFMA, writing one
-//                     partial per (row, slot, head): fp32 max and sum, and the
-//                     output normalised by the sum, in bf16
-//   qsa_combine       merges a row's topk + 1 slots and applies the gate
-constexpr int CK_NT2 = 256;
-constexpr int CI_MAX_BLOCKS = 4096;
+// The attention of a chunk of query rows reads each key/value block once. A
+// row's entries are its (row, slot) pairs: slot i < n_sel its i-th selected
+// block, slot topk its tail block (keys ts..p, when the row does not complete
+// its block). qsa_chunk_attend_kernel, grid (selected + tail workgroups, kv
+// head g, sequence b), up to CA_ROWS rows per launch:
+//   * selected workgroup x owns blocks x*bpw .. x*bpw + bpw - 1: it reads every
+//     row's ids, keeps the entries that fall in its blocks, counting-sorted by
+//     block in LDS;
+//   * tail workgroup t owns the tail entries of rows 8t .. 8t+7 (one or two
+//     blocks: the rows of a chunk share few tail blocks, and 8 rows per
+//     workgroup keeps them from piling onto one), and writes the empty
+//     partials (max -inf) of those rows' unused slots;
+//   * then, for each of its blocks in turn, its 64-token key and value pieces
+//     (16 KB of key and 16 KB of value per 32 tokens, contiguous in the page's
+//     lane order) are copied into LDS by direct global->LDS loads, the next
+//     block's while this one is scored; each wave scores two entries x 8
+//     query heads on bf16 MFMA and writes one partial per (row, slot, head):
+//     fp32 max and sum, and the output normalised by the sum, in bf16.
+// qsa_combine then merges a row's topk + 1 slots and applies the gate.
+constexpr int CA_MAX_BLOCKS = 4096;
 constexpr int CA_NT = 256;        // attention workgroup: four waves
-constexpr int CA_PER_ITEM = 8;    // entries per work item: two per wave
-constexpr int CI_NT = 1024;       // index workgroup
-
-struct ChunkIndexArgs {
-  const int* positions; const int* ids; const int* n_sel;
-  unsigned* ent; int4* work; int* n_work; float* part_ml;
-  int seq, hkv, ratio, topk, max_work;
-};
-
-// every entry's block, eight per thread at a time: entry_loads issues the
-// loads (which do not depend on the position), entry_blocks turns them into
-// blocks; j[k] = -1 for an unused slot, -2 past the end
-struct EntryLoads { int nsel[8], idv[8], s[8], i[8]; };
-
-template <int NT>
-__device__ __forceinline__ void entry_loads(const ChunkIndexArgs& A, int b, int base, EntryLoads& L) {
-  const int nslot = A.topk + 1, n_ent = A.seq * nslot;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int e = min(base + k * NT + (int)threadIdx.x, n_ent - 1);
-    L.s[k] = e / nslot;
-    L.i[k] = e - L.s[k] * nslot;
-    const long row = (long)b * A.seq + L.s[k];
-    L.nsel[k] = A.n_sel[row];
-    L.idv[k] = A.ids[row * A.topk + min(L.i[k], A.topk - 1)];
-  }
-}
-
-template <int NT>
-__device__ __forceinline__ void entry_blocks(const ChunkIndexArgs& A, int pos0, int base, const EntryLoads& L,
-                                             int (&j)[8]) {
-  const int n_ent = A.seq * (A.topk + 1);
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int p = pos0 + L.s[k];
-    const int ts = ((p + 1) / A.ratio) * A.ratio;
-    const int tail = ts <= p ? ts / A.ratio : -1;
-    const int jj = L.i[k] < A.topk ? (L.i[k] < L.nsel[k] ? L.idv[k] : -1) : tail;
-    j[k] = base + k * NT + (int)threadIdx.x < n_ent ? jj : -2;
-  }
-}
-
-__global__ __launch_bounds__(CI_NT) void qsa_chunk_index_kernel(ChunkIndexArgs A) {
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int nslot = A.topk + 1;
-  const int n_ent = A.seq * nslot;
-  // when every entry fits one pass (8 per thread), its loads are issued before
-  // the position is waited for and serve both passes below
-  const bool one_pass = n_ent <= 8 * CI_NT;
-  EntryLoads L0;
-  if (one_pass) entry_loads<CI_NT>(A, b, 0, L0);
-  const int pos0 = A.positions[b];
-  // blocks any entry can name: selected blocks are complete ones before the
-  // row, a tail block holds the row itself
-  const int NB = min((pos0 + A.seq - 1) / A.ratio + 1, CI_MAX_BLOCKS);
-  __shared__ int cnt[CI_MAX_BLOCKS], off[CI_MAX_BLOCKS], woff[CI_MAX_BLOCKS];
-  __shared__ int wsum[2][CI_NT / 64];
-  for (int j = tid; j < NB; j += CI_NT) cnt[j] = 0;
-  __syncthreads();
-  for (int base = 0; base < n_ent; base += 8 * CI_NT) {
-    EntryLoads L;
-    if (one_pass) L = L0;
-    else entry_loads<CI_NT>(A, b, base, L);
-    int j[8];
-    entry_blocks<CI_NT>(A, pos0, base, L, j);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (j[k] >= 0) {
-        atomicAdd(&cnt[j[k]], 1);
-      } else if (j[k] == -1) {
-        const long row = (long)b * A.seq + L.s[k];
-        for (int gh = 0; gh < A.hkv * GQA; ++gh) {
-          const long pb = ((row * A.hkv + gh / GQA) * nslot + L.i[k]) * GQA + gh % GQA;
-          A.part_ml[pb * 2 + 0] = -INFINITY;
-          A.part_ml[pb * 2 + 1] = 0.f;
-        }
-      }
-    }
-  }
-  __syncthreads();
-  // exclusive scans of the entry counts and of the work items per block
-  const int per = (NB + CI_NT - 1) / CI_NT;
-  const int j0 = tid * per, j1 = min(NB, j0 + per);
-  int c_tot = 0, w_tot = 0;
-  for (int j = j0; j < j1; ++j) {
-    c_tot += cnt[j];
-    w_tot += (cnt[j] + CA_PER_ITEM - 1) / CA_PER_ITEM;
-  }
-  int ci = c_tot, wi = w_tot;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int a = __shfl_up(ci, o, 64), c = __shfl_up(wi, o, 64);
-    if (lane >= o) { ci += a; wi += c; }
-  }
-  if (lane == 63) { wsum[0][wv] = ci; wsum[1][wv] = wi; }
-  __syncthreads();
-  int cb = ci - c_tot, wb = wi - w_tot;
-  for (int w = 0; w < wv; ++w) { cb += wsum[0][w]; wb += wsum[1][w]; }
-  for (int j = j0; j < j1; ++j) {
-    off[j] = cb;
-    woff[j] = wb;
-    cb += cnt[j];
-    wb += (cnt[j] + CA_PER_ITEM - 1) / CA_PER_ITEM;
-  }
-  __syncthreads();
-  // work items, then the entries (cnt becomes each block's fill cursor)
-  for (int j = tid; j < NB; j += CI_NT) {
-    const int c = cnt[j];
-    for (int k = 0; k * CA_PER_ITEM < c; ++k)
-      A.work[(long)b * A.max_work + woff[j] + k] =
-          make_int4(j, off[j] + k * CA_PER_ITEM, min(CA_PER_ITEM, c - k * CA_PER_ITEM), 0);
-  }
-  if (tid == CI_NT - 1) {
-    int tot = 0;
-    for (int w = 0; w < CI_NT / 64; ++w) tot += wsum[1][w];
-    A.n_work[b] = tot;
-  }
-  __syncthreads();
-  for (int j = tid; j < NB; j += CI_NT) cnt[j] = 0;
-  __syncthreads();
-  for (int base = 0; base < n_ent; base += 8 * CI_NT) {
-    EntryLoads L;
-    if (one_pass) L = L0;
-    else entry_loads<CI_NT>(A, b, base, L);
-    int j[8];
-    entry_blocks<CI_NT>(A, pos0, base, L, j);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (j[k] >= 0) {
-        const int c = atomicAdd(&cnt[j[k]], 1);
-        A.ent[(long)b * n_ent + off[j[k]] + c] = (static_cast<unsigned>(L.s[k]) << 16) |
-                                                  (L.i[k] == A.topk ? 1u << 9 : 0u) | static_cast<unsigned>(L.i[k]);
-      }
-    }
-  }
-}
+constexpr int CA_ROWS = 128;      // query rows per launch
+constexpr int CA_TAIL_ROWS = 8;   // rows per tail workgroup
+constexpr int CA_MAX_BPW = 8;     // blocks per selected workgroup
+constexpr int CA_MAX_ENT = CA_ROWS * CA_MAX_BPW;   // entries a workgroup can hold
 
 struct ChunkAttnArgs {
   const uint16_t* q;                      // [rows, 2 (hi, lo), hq, 256] bf16
   const uint16_t* k_pool; const uint16_t* v_pool;
-  const int* positions; const int* page_table;
-  const unsigned* ent; const int4* work; const int* n_work;
+  const int* positions; const int* page_table; const int* ids; const int* n_sel;
   uint16_t* part_o; float* part_ml;      // part_o: bf16, normalised by l
-  int seq, hq, hkv, page_size, max_pages, ratio, topk, max_work;
+  int seq, row0, rows, hq, hkv, page_size, max_pages, ratio, topk, nwg_sel, bpw;
+  unsigned topk_magic, nslot_magic;      // ceil(2^32 / d): n / d = umulhi(n, magic) for n < 2^16, d <= 2^9
   float scale;
 };
 
+// One wave's partials of a group: this lane's 4 channels of each of the 16
+// channel blocks (bf16, normalised by the sum), the (max, sum) pair and where
+// they go.
+struct GroupOut {
+  u32x2_t o[16];
+  float mx, l;
+  long pb;
+  bool ok;
+};
+
+// The wave's 16 partial rows (columns of its tiles) go out as whole 128-byte
+// lines: per 64-channel quarter, the lanes' fragments are transposed through
+// the wave's own LDS tile (16 rows of 144 bytes: padded so that the writes
+// spread over the banks) and each lane writes 16 contiguous bytes.
+constexpr int CA_TROW = 144;     // bytes per row of the transpose tile
+__device__ __forceinline__ void store_group(const ChunkAttnArgs& A, const GroupOut& R, unsigned char* tb) {
+  const int lane = threadIdx.x & 63, col = lane & 15, quad = lane >> 4;
+  long pbr[2];
+  bool okr[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (lane + 64 * i) >> 3;          // lane r holds column r's row
+    pbr[i] = (static_cast<long>(__shfl(static_cast<int>(R.pb >> 32), r, 64)) << 32) |
+             static_cast<unsigned>(__shfl(static_cast<int>(R.pb), r, 64));
+    okr[i] = __shfl(static_cast<int>(R.ok), r, 64) != 0;
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      *reinterpret_cast<u32x2_t*>(tb + col * CA_TROW + (16 * d + 4 * quad) * 2) = R.o[4 * m + d];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int f = lane + 64 * i, r = f >> 3, seg = f & 7;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(tb + r * CA_TROW + seg * 16);
+      if (okr[i]) *reinterpret_cast<u32x4_t*>(A.part_o + pbr[i] * QSA_D + 64 * m + 8 * seg) = v;
+    }
+  }
+  if (R.ok && quad == 0) *reinterpret_cast<float2*>(A.part_ml + R.pb * 2) = make_float2(R.mx, R.l);
+}
+
+// The scores and outputs of a group of up to 8 entries of block j whose keys
+// and values are in `kv` (wave: entries 2 wv, 2 wv + 1 of the group, lane
+// column il = which of the two, hh = query head of the kv head's eight).
+__device__ __forceinline__ void chunk_attend_group(const ChunkAttnArgs& A, const uint16_t (*kv)[32][64 * 8],
+                                                   const bf16x8_t (&qhi)[8], int j,
+                                                   unsigned pk, bool ok, long row_b, int pos0, int g, int nslot,
+                                                   GroupOut& R, bool mark = false) {
+  const int lane = threadIdx.x & 63, quad = lane >> 4, hh = lane & 7;
+  const int gpb = A.ratio / 32;
+  const int s = pk >> 16, slot = pk & 511;
+  const bool tail = (pk >> 9) & 1u;
+  const long row = row_b + s;
+  const int p = pos0 + s;
+  // scores of the block's groups, then one softmax over its keys
+  // a tile's eight key fragments are read from LDS before its products, so
+  // that their latencies overlap
+  f32x4_t sc[2][2];
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi) {
+    const uint16_t* kvg = &kv[gi][0][0];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+      if (gi < gpb) {
+        bf16x8_t kf[8];
+#pragma unroll
+        for (int sk = 0; sk < 8; ++sk)
+          kf[sk] = *reinterpret_cast<const bf16x8_t*>(kvg + ((t * 8 + sk) * 64 + lane) * 8);
+#pragma unroll
+        for (int sk = 0; sk < 8; ++sk) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[sk], qhi[sk], c, 0, 0, 0);
+      }
+      sc[gi][t] = c;
+    }
+  }
+  // keys of a tail entry stop at the row's own position: key gi*32 + 16t +
+  // 4quad + v of the block is visible when gi*32 + 16t + v <= lim
+  const int lim = !ok ? -1 : tail ? p - j * A.ratio - 4 * quad : 1 << 20;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float xs = (gi < gpb && gi * 32 + 16 * t + v <= lim) ? sc[gi][t][v] * A.scale : -INFINITY;
+        sc[gi][t][v] = xs;
+        mx = fmaxf(mx, xs);
+      }
+  mx = xor32_max(xor16_max(mx));
+  if (mark) QM_PHASE(9);
+  float lsum = 0.f;
+  unsigned pw[2][4];
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float pv[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        pv[v] = sc[gi][t][v] == -INFINITY ? 0.f : __expf(sc[gi][t][v] - mx);
+        lsum += pv[v];
+      }
+      pw[gi][2 * t] = pack_bf16x2(pv[0], pv[1]);
+      pw[gi][2 * t + 1] = pack_bf16x2(pv[2], pv[3]);
+    }
+  bf16x8_t pf[2];
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi) pf[gi] = __builtin_bit_cast(bf16x8_t, u32x4_t{pw[gi][0], pw[gi][1], pw[gi][2], pw[gi][3]});
+  const float l = xor32_sum(xor16_sum(lsum));
+  if (mark) QM_PHASE(10);
+  const float rl = 1.0f / l;
+  R.pb = ((row * A.hkv + g) * nslot + slot) * GQA + hh;
+  R.ok = ok;
+  R.mx = mx;
+  R.l = l;
+#pragma unroll
+  for (int db = 0; db < 16; ++db) {
+    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+    bf16x8_t vf[2];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+      if (gi < gpb) vf[gi] = *reinterpret_cast<const bf16x8_t*>(&kv[gi][16 + db][0] + lane * 8);
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+      if (gi < gpb) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[gi], pf[gi], c, 0, 0, 0);
+    R.o[db] = u32x2_t{pack_bf16x2(c[0] * rl, c[1] * rl), pack_bf16x2(c[2] * rl, c[3] * rl)};
+  }
+  if (mark) QM_PHASE(11);
+}
+
 __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArgs A) {
-  const int g = blockIdx.y, b = blockIdx.z;
+  QM_PHASE_DECL
+  QM_PHASE(0);
+  const int x = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int col = lane & 15, quad = lane >> 4;
   const int il = col >> 3, hh = col & 7;
   const int nslot = A.topk + 1;
   const int gpb = A.ratio / 32;
-  const int pos0 = A.positions[b];
-  const int n_work = A.n_work[b];
   const int* ptab = A.page_table + (long)b * A.max_pages;
+  const long row_b = (long)b * A.seq + A.row0;       // global index of the launch's row 0
   const long head_stride = (long)A.page_size * QSA_D;
-  const int4* work = A.work + (long)b * A.max_work;
-  __shared__ uint16_t kv[2][32][64 * 8];  // per 32-token group: 16 key then 16 value 1 KB pieces
 
-  // An item's descriptors are its work record, this lane's entry (column group
-  // il of the wave) and the pages of the block's groups. They are requested
-  // two items ahead: each item issues its own q and K/V loads first, then the
-  // next item's entry and pages (from the record that came in during the
-  // previous item) and the record of the item after that, so no item waits on
-  // a chain of dependent loads before its own.
-  const long ent0 = (long)b * A.seq * nslot;
-  const int e = 2 * wv + il;
-  const int pg1_off = gpb > 1 ? 32 : 0;
-  int w = blockIdx.x;
-  if (w >= n_work) return;
-  int4 item = work[w];
-  int4 item_n = work[min(w + (int)gridDim.x, n_work - 1)];
-  unsigned pk = A.ent[ent0 + item.y + min(e, item.z - 1)];
-  int pg0 = ptab[(item.x * A.ratio) / A.page_size];
-  int pg1 = ptab[(item.x * A.ratio + pg1_off) / A.page_size];
-  for (;;) {
-    const int wn = w + gridDim.x;
-    const int j = item.x, n = item.z;
-    const bool ok = e < n;
-    const int s = pk >> 16, slot = pk & 511;
-    const bool tail = (pk >> 9) & 1u;
-    const long row = (long)b * A.seq + s;
-    const int p = pos0 + s;
-    bf16x8_t qhi[8], qlo[8];
-    {
-      const int hqi = g * GQA + hh;
-      const uint16_t* qh = A.q + q_index(row, A.hkv, 0, hqi, 8 * quad);
-      const uint16_t* ql = A.q + q_index(row, A.hkv, 1, hqi, 8 * quad);
-#pragma unroll
-      for (int sk = 0; sk < 8; ++sk) {
-        qhi[sk] = load_bf16x8(qh + Q_SK_STRIDE * sk);
-        qlo[sk] = load_bf16x8(ql + Q_SK_STRIDE * sk);
-      }
-    }
-    // stage the block's groups: per group 16 KB of key and 16 KB of value
-    // pieces, both groups' loads issued before either is stored (a block of
-    // one group loads and stores it twice; the second copy is not read)
-    const int row0a = (j * A.ratio) % A.page_size, row0b = (j * A.ratio + pg1_off) % A.page_size;
-    const long pba = ((long)pg0 * A.hkv + g) * head_stride, pbb = ((long)(gpb > 1 ? pg1 : pg0) * A.hkv + g) * head_stride;
-    const uint16_t* ksa = A.k_pool + pba + (row0a >> 4) * 8 * 512;
-    const uint16_t* vsa = A.v_pool + pba + (row0a >> 5) * 16 * 512;
-    const uint16_t* ksb = A.k_pool + pbb + (row0b >> 4) * 8 * 512;
-    const uint16_t* vsb = A.v_pool + pbb + (row0b >> 5) * 16 * 512;
-    uint4 kra[4], vra[4], krb[4], vrb[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      kra[k] = *reinterpret_cast<const uint4*>(ksa + (k * CA_NT + tid) * 8);
-      vra[k] = *reinterpret_cast<const uint4*>(vsa + (k * CA_NT + tid) * 8);
-      krb[k] = *reinterpret_cast<const uint4*>(ksb + (k * CA_NT + tid) * 8);
-      vrb[k] = *reinterpret_cast<const uint4*>(vsb + (k * CA_NT + tid) * 8);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      *reinterpret_cast<uint4*>(&kv[0][0][0] + (k * CA_NT + tid) * 8) = kra[k];
-      *reinterpret_cast<uint4*>(&kv[0][16][0] + (k * CA_NT + tid) * 8) = vra[k];
-      *reinterpret_cast<uint4*>(&kv[1][0][0] + (k * CA_NT + tid) * 8) = krb[k];
-      *reinterpret_cast<uint4*>(&kv[1][16][0] + (k * CA_NT + tid) * 8) = vrb[k];
-    }
-    const unsigned pk_n = A.ent[ent0 + item_n.y + min(e, item_n.z - 1)];
-    const int pg0_n = ptab[(item_n.x * A.ratio) / A.page_size];
-    const int pg1_n = ptab[(item_n.x * A.ratio + pg1_off) / A.page_size];
-    const int4 item_nn = work[min(wn + (int)gridDim.x, n_work - 1)];
-    __syncthreads();
+  __shared__ uint16_t kv[2][32][64 * 8];      // per 32-token group: 16 key then 16 value 1 KB pieces
+  __shared__ unsigned ent[CA_MAX_ENT];         // entries by block: row << 16 | tail << 9 | slot
+  __shared__ int cnt[CA_MAX_BPW], off[CA_MAX_BPW], cur[CA_MAX_BPW], blist[CA_MAX_BPW];
+  __shared__ int pg[CA_MAX_BPW][2];
+  __shared__ int s_nb;
+  __shared__ u32x4_t tbuf[CA_NT / 64][16 * CA_TROW / 16];   // per wave: partial rows on their way out
+  unsigned char* tb = reinterpret_cast<unsigned char*>(&tbuf[wv][0]);
 
-    if (2 * wv < n) {
-      // scores of the block's groups, then one softmax over its keys
-      f32x4_t sc[2][2];
+  const bool tail_wg = x >= A.nwg_sel;
+  const int tr0 = (x - A.nwg_sel) * CA_TAIL_ROWS;
+  if (tid < CA_MAX_BPW) { cnt[tid] = 0; cur[tid] = 0; }
+
+  int pos0, jlo, nloc;
+  // a block's key and value pieces pass through registers: loaded while the
+  // previous block is scored, stored to LDS between two barriers (a block of
+  // one 32-token group loads and stores it twice; the second copy is not read)
+  // (indices of the register array are compile-time constants, so it stays in
+  // registers)
+  u32x4_t kvr[16];
+  auto kv_load_at = [&](int j, int page0, int page1) __attribute__((always_inline)) {
+    const uint16_t* src[4];
 #pragma unroll
-      for (int gi = 0; gi < 2; ++gi) {
-        const uint16_t* kvg = &kv[gi][0][0];
+    for (int gi = 0; gi < 2; ++gi) {
+      const int gg = gi < gpb ? gi : 0;
+      const int rowg = (j * A.ratio + 32 * gg) % A.page_size;
+      const long pbase = ((long)(gg ? page1 : page0) * A.hkv + g) * head_stride;
+      src[2 * gi] = A.k_pool + pbase + (rowg >> 4) * 8 * 512 + lane * 8 + wv * 512;
+      src[2 * gi + 1] = A.v_pool + pbase + (rowg >> 5) * 16 * 512 + lane * 8 + wv * 512;
+    }
+    static_for<16>([&](auto i) {
+      kvr[i] = *reinterpret_cast<const u32x4_t*>(src[i / 4] + (i % 4) * 4 * 512);
+    });
+  };
+  auto kv_load = [&](int k) __attribute__((always_inline)) {
+    const int lb = blist[k];
+    kv_load_at(jlo + lb, pg[lb][0], pg[lb][1]);
+  };
+  auto kv_store = [&]() __attribute__((always_inline)) {
+    // piece 4 pc + wv of group gi: keys at 0..15, values at 16..31
+    static_for<16>([&](auto i) {
+      constexpr int gi = i / 8, v = (i / 4) % 2, pc = i % 4;
+      *reinterpret_cast<u32x4_t*>(&kv[gi][16 * v + 4 * pc + wv][lane * 8]) = kvr[i];
+    });
+  };
+  // the chunk path scores with the query's bf16 part (hi) alone: the keys
+  // are bf16 too, and the softmax of these 64-key blocks is far inside the
+  // output tolerance either way, at half the query traffic and products
+  bf16x8_t qhi[8], qnx[8];
+  auto q_load_into = [&](bf16x8_t (&qd)[8], unsigned pk) __attribute__((always_inline)) {
+    const long row = row_b + (pk >> 16);
+    const uint16_t* qh = A.q + q_index(row, A.hkv, 0, g * GQA + hh, 8 * quad);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-          if (gi < gpb) {
+    for (int sk = 0; sk < 8; ++sk) qd[sk] = load_bf16x8(qh + Q_SK_STRIDE * sk);
+  };
+  auto q_load = [&](unsigned pk) __attribute__((always_inline)) { q_load_into(qhi, pk); };
+  // ---- this workgroup's entries, counting-sorted by local block. The first
+  // CA_SCAN * CA_NT entries' blocks stay in registers for the placement pass;
+  // every load of a round is issued before any is used.
+  constexpr int CA_SCAN = 16;
+  const int n_scan = A.rows * A.topk;
+  bool spec = false;        // the first local block's pieces are requested before its entries are known
+  auto spec_load = [&]() __attribute__((always_inline)) {
+    const int c0 = min((jlo * A.ratio) / A.page_size, A.max_pages - 1);
+    const int c1 = min((jlo * A.ratio + (gpb > 1 ? 32 : 0)) / A.page_size, A.max_pages - 1);
+    kv_load_at(jlo, ptab[c0], ptab[c1]);
+    spec = true;
+  };
+  int lb0[CA_SCAN];
+  unsigned code0[CA_SCAN];
+  auto scan_sel = [&](int base, int (&lb)[CA_SCAN], unsigned (&code)[CA_SCAN]) __attribute__((always_inline)) {
+    int nsel[CA_SCAN], jv[CA_SCAN];
 #pragma unroll
-            for (int sk = 0; sk < 8; ++sk) {
-              const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(kvg + ((t * 8 + sk) * 64 + lane) * 8);
-              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qhi[sk], c, 0, 0, 0);
-              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qlo[sk], c, 0, 0, 0);
-            }
-          }
-          sc[gi][t] = c;
-        }
-      }
-      float mx = -INFINITY;
+    for (int k = 0; k < CA_SCAN; ++k) {
+      const int e = min(base + k * CA_NT + tid, n_scan - 1);
+      nsel[k] = A.n_sel[row_b + __umulhi(e, A.topk_magic)];
+      jv[k] = A.ids[row_b * A.topk + e];
+    }
 #pragma unroll
-      for (int gi = 0; gi < 2; ++gi)
+    for (int k = 0; k < CA_SCAN; ++k) {
+      const int e = base + k * CA_NT + tid;
+      const int r = __umulhi(e, A.topk_magic), i = e - r * A.topk;
+      const int j = e < n_scan && i < nsel[k] ? jv[k] : -1;
+      lb[k] = j >= jlo && j < jlo + nloc ? j - jlo : -1;
+      code[k] = (static_cast<unsigned>(r) << 16) | static_cast<unsigned>(i);
+    }
+  };
+  if (!tail_wg) {
+    jlo = x * A.bpw;
+    nloc = A.bpw;
+    scan_sel(0, lb0, code0);
+    // the pages of the local blocks, needed only by those that hold entries
+    if (tid < 2 * nloc) {
+      const int jj = jlo + (tid >> 1), gi = tid & 1;
+      pg[tid >> 1][gi] = ptab[min((jj * A.ratio + 32 * (gi < gpb ? gi : 0)) / A.page_size, A.max_pages - 1)];
+    }
+    pos0 = A.positions[b] + A.row0;
+    // local block 0 can hold entries when it is complete before the last row
+    if ((jlo + 1) * A.ratio <= pos0 + A.rows) spec_load();
+    __syncthreads();                          // counts cleared
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+    for (int k = 0; k < CA_SCAN; ++k)
+      if (lb0[k] >= 0) atomicAdd(&cnt[lb0[k]], 1);
+    for (int base = CA_SCAN * CA_NT; base < n_scan; base += CA_SCAN * CA_NT) {
+      int lb[CA_SCAN];
+      unsigned code[CA_SCAN];
+      scan_sel(base, lb, code);
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            // keys of a tail entry stop at the row's own position
-            const int kp = j * A.ratio + gi * 32 + 16 * t + 4 * quad + v;
-            const float x = (ok && gi < gpb && (!tail || kp <= p)) ? sc[gi][t][v] * A.scale : -INFINITY;
-            sc[gi][t][v] = x;
-            mx = fmaxf(mx, x);
-          }
-      mx = xor32_max(xor16_max(mx));
-      float lsum = 0.f;
-      bf16x8_t pf[2];
+      for (int k = 0; k < CA_SCAN; ++k)
+        if (lb[k] >= 0) atomicAdd(&cnt[lb[k]], 1);
+    }
+  } else {
+    // the tail entries of rows tr0 .. tr0 + 7 (one or two blocks), and the
+    // empty partials (max -inf) of those rows' unused slots
+    pos0 = A.positions[b] + A.row0;
+    jlo = (pos0 + tr0) / A.ratio;
+    nloc = 2;
+    spec_load();
 #pragma unroll
-      for (int gi = 0; gi < 2; ++gi)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const float pv = sc[gi][t][v] == -INFINITY ? 0.f : __expf(sc[gi][t][v] - mx);
-            lsum += pv;
-            pf[gi][4 * t + v] = __builtin_bit_cast(__bf16, f32_to_bf16(pv));
-          }
-      const float l = xor32_sum(xor16_sum(lsum));
-      const float rl = 1.0f / l;
-      const long pb = ((row * A.hkv + g) * nslot + slot) * GQA + hh;
-      uint16_t* po = A.part_o + pb * QSA_D + 4 * quad;
-#pragma unroll
-      for (int db = 0; db < 16; ++db) {
-        f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int gi = 0; gi < 2; ++gi) {
-          if (gi < gpb) {
-            const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(&kv[gi][16 + db][0] + lane * 8);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[gi], c, 0, 0, 0);
-          }
-        }
-        if (ok) {
-          const unsigned lo = f32_to_bf16(c[0] * rl) | (static_cast<unsigned>(f32_to_bf16(c[1] * rl)) << 16);
-          const unsigned hi = f32_to_bf16(c[2] * rl) | (static_cast<unsigned>(f32_to_bf16(c[3] * rl)) << 16);
-          *reinterpret_cast<uint2*>(po + 16 * db) = make_uint2(lo, hi);
-        }
-      }
-      if (ok && quad == 0) {
-        A.part_ml[pb * 2 + 0] = mx;
-        A.part_ml[pb * 2 + 1] = l;
+    for (int k = 0; k < CA_SCAN; ++k) lb0[k] = -1;
+    if (tid < CA_TAIL_ROWS) {
+      const int r = tr0 + tid, p = pos0 + r;
+      if (r < A.rows && ((p + 1) / A.ratio) * A.ratio <= p) {
+        lb0[0] = p / A.ratio - jlo;
+        code0[0] = (static_cast<unsigned>(r) << 16) | (1u << 9) | static_cast<unsigned>(A.topk);
       }
     }
-    __syncthreads();
-    if (wn >= n_work) break;
-    w = wn;
-    item = item_n;
-    item_n = item_nn;
-    pk = pk_n;
-    pg0 = pg0_n;
-    pg1 = pg1_n;
+    if (tid < 4) {
+      const int gi = tid & 1;
+      pg[tid >> 1][gi] = ptab[min(((jlo + (tid >> 1)) * A.ratio + 32 * (gi < gpb ? gi : 0)) / A.page_size,
+                                  A.max_pages - 1)];
+    }
+    // (row, slot) pairs; a thread writes the pair's eight heads
+    const int n_emp = CA_TAIL_ROWS * nslot;
+    for (int e = tid; e < n_emp; e += CA_NT) {
+      const int rr = __umulhi(e, A.nslot_magic), i = e - rr * nslot;
+      const int r = tr0 + rr;
+      if (r >= A.rows) continue;
+      const long row = row_b + r;
+      const int p = pos0 + r;
+      const bool empty = i < A.topk ? i >= A.n_sel[row] : ((p + 1) / A.ratio) * A.ratio > p;
+      if (empty) {
+        const long pb = ((row * A.hkv + g) * nslot + i) * GQA;
+        float4* ml = reinterpret_cast<float4*>(A.part_ml + pb * 2);
+#pragma unroll
+        for (int h = 0; h < GQA / 2; ++h) ml[h] = make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
+      }
+    }
+    __syncthreads();                          // counts cleared
+    if (lb0[0] >= 0) atomicAdd(&cnt[lb0[0]], 1);
   }
+  __syncthreads();
+  QM_PHASE(1);
+  if (tid == 0) {
+    int o = 0, nb = 0;
+    for (int lb = 0; lb < nloc; ++lb) {
+      off[lb] = o;
+      o += cnt[lb];
+      if (cnt[lb]) blist[nb++] = lb;
+    }
+    s_nb = nb;
+  }
+  __syncthreads();
+  const int nb = s_nb;
+  if (nb == 0) {
+    QM_PHASE_FLUSH();
+    return;
+  }
+
+  if (!spec || blist[0] != 0) kv_load(0);
+  // placement: the entries in order of their local block
+  if (!tail_wg) {
+#pragma unroll
+    for (int k = 0; k < CA_SCAN; ++k)
+      if (lb0[k] >= 0) ent[off[lb0[k]] + atomicAdd(&cur[lb0[k]], 1)] = code0[k];
+    for (int base = CA_SCAN * CA_NT; base < n_scan; base += CA_SCAN * CA_NT) {
+      int lb[CA_SCAN];
+      unsigned code[CA_SCAN];
+      scan_sel(base, lb, code);
+#pragma unroll
+      for (int k = 0; k < CA_SCAN; ++k)
+        if (lb[k] >= 0) ent[off[lb[k]] + atomicAdd(&cur[lb[k]], 1)] = code[k];
+    }
+  } else if (lb0[0] >= 0) {
+    ent[off[lb0[0]] + atomicAdd(&cur[lb0[0]], 1)] = code0[0];
+  }
+  __syncthreads();
+  QM_PHASE(2);
+  {
+    const int e = 2 * wv + il, n = cnt[blist[0]];
+    q_load(ent[off[blist[0]] + min(e, n - 1)]);
+  }
+  kv_store();
+  __syncthreads();
+  QM_PHASE(3);
+
+  // ---- the blocks. A block's last partials are stored at the start of the
+  // next block: the wait for the next block's pieces (loaded after them) then
+  // finds them long written, instead of waiting for their writes to complete.
+  GroupOut R;
+  bool pending = false;
+  for (int k = 0; k < nb; ++k) {
+    const int lb = blist[k], j = jlo + lb;
+    const int n = cnt[lb], e0 = off[lb];
+    if (pending) {
+      store_group(A, R, tb);
+      pending = false;
+    }
+    // the next block's pieces and its first group's query rows are requested
+    // now, so that both have arrived when this block is done
+    if (k + 1 < nb) {
+      kv_load(k + 1);
+      const int lbn = blist[k + 1], nn = cnt[lbn];
+      q_load_into(qnx, ent[off[lbn] + min(2 * wv + il, nn - 1)]);
+    }
+    for (int g0 = 0; g0 < n; g0 += 8) {
+      const int e = g0 + 2 * wv + il;
+      const unsigned pk = ent[e0 + min(e, n - 1)];
+      if (g0 > 0) q_load(pk);
+      if (k == 0 && g0 == 0) QM_PHASE(7);
+      if (g0 + 2 * wv < n) {
+        chunk_attend_group(A, kv, qhi, j, pk, e < n, row_b, pos0, g, nslot, R, k == 0 && g0 == 0);
+        if (g0 + 8 < n) store_group(A, R, tb);
+        else pending = true;
+      }
+    }
+    if (k == 0) QM_PHASE(5);
+    if (k + 1 < nb) {
+      __syncthreads();     // every wave is done with this block's pieces
+      kv_store();
+#pragma unroll
+      for (int sk = 0; sk < 8; ++sk) qhi[sk] = qnx[sk];
+      __syncthreads();
+      if (k == 0) QM_PHASE(6);
+    }
+  }
+  if (pending) store_group(A, R, tb);
+#ifdef QM_PHASE_TRACE
+  if (tid == 0) qm_ph_[14] = static_cast<unsigned long long>(nb) | (static_cast<unsigned long long>(off[blist[nb - 1]] + cnt[blist[nb - 1]]) << 16);
+#endif
+  QM_PHASE(4);
+  QM_PHASE_FLUSH();
 }
 
 // ---------------------------------------------------------------------------
@@ -1546,55 +1747,6 @@ struct DecShared {
   alignas(16) int rscr[rank_scratch(DEC_MAX_TOPK)];
   alignas(16) float s[GQA][32];                   // the item's scores, head-major
 };
-
-// ---- RMS norms of one row per wave, in torch's CPU order: 32 partial sums,
-// partial a summing the squares of elements a, a + 32, a + 64, ... in order;
-// then c_l = ((s_l + s_(l+8)) + s_(l+16)) + s_(l+24) for l < 8, added in
-// order; every square and sum rounded on its own. A 128-wide row sits in the
-// wave as x[k] = element lane + 64 k (k < 2), a 256-wide row k < 4.
-__device__ __forceinline__ float xor32_f(float v) { return __shfl_xor(v, 32, 64); }
-
-__device__ __forceinline__ float wave_rinv_finish(float s, float n, float eps) {
-  const float s16 = __shfl_down(s, 16, 64);
-  const float c = add_rn(add_rn(add_rn(s, row_shl<8>(s)), s16), row_shl<8>(s16));   // lanes 0..7: c_l
-  float tot = readlane_f(c, 0);
-#pragma unroll
-  for (int l = 1; l < 8; ++l) tot = add_rn(tot, readlane_f(c, l));
-  return rsqrt_rn(add_rn(div_rn(tot, n), eps));
-}
-
-template <int K>
-__device__ __forceinline__ float wave_rinv(const float (&x)[K], float eps) {
-  float s = 0.f;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const float q = mul_rn(x[k], x[k]);
-    s = k == 0 ? q : add_rn(s, q);          // element lane + 64 k
-    s = add_rn(s, xor32_f(q));              // element lane + 64 k + 32
-  }
-  return wave_rinv_finish(s, 64.f * K, eps);
-}
-
-// rope of a normed row held as y[k] = element lane + 64 k: element e < rope
-// becomes y_e cos + (e < rope/2 ? -y_p : y_p) sin, p = e +- rope/2 (the
-// partner's normed value, from lane p % 64 of register p / 64); every multiply
-// and add rounded on its own.
-template <int K>
-__device__ __forceinline__ void wave_rope(float (&y)[K], int rope, const float (&cs)[2], const float (&sn)[2]) {
-  const int lane = threadIdx.x & 63, half = rope >> 1;
-  float out[2];
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int e = lane + 64 * k;
-    const int pe = min(e < half ? e + half : e - half, 127);
-    const float v0 = __shfl(y[0], pe & 63, 64);
-    const float v1 = __shfl(y[1], pe & 63, 64);
-    const float yp = pe >= 64 ? v1 : v0;
-    out[k] = e < rope ? add_rn(mul_rn(y[k], cs[k]), mul_rn(e < half ? -yp : yp, sn[k])) : y[k];
-  }
-  y[0] = out[0];
-  y[1] = out[1];
-}
 
 // item -> (first token t0, visible rows [lo, hi)) of a query at position p
 __device__ __forceinline__ void item_span(int it, int n_blk_items, int gpb, int ratio, int ts, int p, const int* sel,
@@ -2130,8 +2282,10 @@ int launch_prep(const qm_qsa_geom* g, int seq, const void* qg, const void* k_new
                 void* v_pool, void* raw_keys, float* block_keys, void* q_out, float* iq_out, hipStream_t stream) {
   PrepArgs<T> A = prep_args<T>(g, seq, qg, k_new, v_new, iq, ik, q_norm, k_norm, iq_norm, ik_norm, cos, sin,
                                positions, page_table, k_pool, v_pool, raw_keys, block_keys, q_out, iq_out);
-  dim3 grid(g->batch * seq, g->n_heads + g->n_kv_heads + g->idx_heads + 1);
-  hipLaunchKernelGGL(qsa_prep_kernel<T>, grid, dim3(PREP_NT), 0, stream, A);
+  const long waves = (long)g->batch * seq * (g->n_heads + g->n_kv_heads + g->idx_heads);
+  const long n_wg = (long)g->batch * prep_pool_per_seq(seq, g->ratio) + (waves + PREP_NT / 64 - 1) / (PREP_NT / 64);
+  if (n_wg > 0x7fffffffL) return qm_fail(QM_ERR_ARG, "qm_qsa_prep: too many rows");
+  hipLaunchKernelGGL(qsa_prep_kernel<T>, dim3(static_cast<unsigned>(n_wg)), dim3(PREP_NT), 0, stream, A);
   QM_CHECK_LAUNCH();
   return QM_OK;
 }
@@ -2281,7 +2435,7 @@ extern "C" int qm_qsa_attend(const qm_qsa_geom* g, int seq, const void* q, const
 
 namespace {
 struct ChunkWs {
-  size_t o, ml, ent, work, n_work, total;
+  size_t o, ml, total;
 };
 
 ChunkWs chunk_ws_layout(const qm_qsa_geom* g, int seq) {
@@ -2290,10 +2444,7 @@ ChunkWs chunk_ws_layout(const qm_qsa_geom* g, int seq) {
   ChunkWs w;
   w.o = 0;
   w.ml = w.o + qm_align256(rows * g->n_kv_heads * nslot * GQA * QSA_D * sizeof(uint16_t));
-  w.ent = w.ml + qm_align256(rows * g->n_kv_heads * nslot * GQA * 2 * sizeof(float));
-  w.work = w.ent + qm_align256(rows * nslot * sizeof(unsigned));
-  w.n_work = w.work + qm_align256(rows * nslot * sizeof(int4));
-  w.total = w.n_work + qm_align256((size_t)g->batch * sizeof(int));
+  w.total = w.ml + qm_align256(rows * g->n_kv_heads * nslot * GQA * 2 * sizeof(float));
   return w;
 }
 
@@ -2302,7 +2453,7 @@ int check_chunk_geom(const qm_qsa_geom* g, const char* who) {
   if (rc) return rc;
   if (g->ratio != 32 && g->ratio != 64)
     return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_attend_chunk: indexer ratio must be 32 or 64");
-  if (g->max_blocks > CI_MAX_BLOCKS || g->max_ctx > CI_MAX_BLOCKS * g->ratio)
+  if (g->max_blocks > CA_MAX_BLOCKS || g->max_ctx > CA_MAX_BLOCKS * g->ratio)
     return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_attend_chunk: more than 4096 blocks");
   if (g->budget / g->ratio + 1 > 511) return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_attend_chunk: top-k above 510");
   return QM_OK;
@@ -2332,28 +2483,28 @@ extern "C" int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q,
   const int nslot = topk + 1;
   uint16_t* part_o = reinterpret_cast<uint16_t*>(base + L.o);
   float* part_ml = reinterpret_cast<float*>(base + L.ml);
-  unsigned* ent = reinterpret_cast<unsigned*>(base + L.ent);
-  int4* work = reinterpret_cast<int4*>(base + L.work);
-  int* n_work = reinterpret_cast<int*>(base + L.n_work);
 
-  ChunkIndexArgs I;
-  I.positions = positions; I.ids = ids; I.n_sel = n_sel; I.ent = ent; I.work = work; I.n_work = n_work;
-  I.part_ml = part_ml; I.seq = seq; I.hkv = g->n_kv_heads; I.ratio = g->ratio; I.topk = topk;
-  I.max_work = seq * nslot;
-  hipLaunchKernelGGL(qsa_chunk_index_kernel, dim3(g->batch), dim3(CI_NT), 0, stream, I);
-  QM_CHECK_LAUNCH();
-
+  // blocks per selected workgroup: about 1024 selected workgroups over the kv
+  // heads and sequences (many small workgroups keep more blocks in flight)
+  const long want = ((long)g->max_blocks * g->n_kv_heads * g->batch + 1023) / 1024;
+  const int bpw = (int)(want < 1 ? 1 : want > CA_MAX_BPW ? CA_MAX_BPW : want);
   ChunkAttnArgs A;
   A.q = static_cast<const uint16_t*>(q); A.k_pool = static_cast<const uint16_t*>(k_pool);
   A.v_pool = static_cast<const uint16_t*>(v_pool); A.positions = positions; A.page_table = page_table;
-  A.ent = ent; A.work = work; A.n_work = n_work; A.part_o = part_o; A.part_ml = part_ml;
+  A.ids = ids; A.n_sel = n_sel; A.part_o = part_o; A.part_ml = part_ml;
   A.seq = seq; A.hq = g->n_heads; A.hkv = g->n_kv_heads; A.page_size = g->page_size; A.max_pages = g->max_pages;
-  A.ratio = g->ratio; A.topk = topk; A.max_work = seq * nslot;
+  A.ratio = g->ratio; A.topk = topk; A.bpw = bpw; A.nwg_sel = (g->max_blocks + bpw - 1) / bpw;
   A.scale = 1.0f / 16.0f;   // 1/sqrt(256), exact
-  int nwg = 512 / (g->n_kv_heads * g->batch);
-  nwg = nwg < 1 ? 1 : nwg > seq * nslot ? seq * nslot : nwg;
-  hipLaunchKernelGGL(qsa_chunk_attend_kernel, dim3(nwg, g->n_kv_heads, g->batch), dim3(CA_NT), 0, stream, A);
-  QM_CHECK_LAUNCH();
+  A.topk_magic = static_cast<unsigned>((0x100000000ull + topk - 1) / topk);
+  A.nslot_magic = static_cast<unsigned>((0x100000000ull + nslot - 1) / nslot);
+  for (int r0 = 0; r0 < seq; r0 += CA_ROWS) {
+    A.row0 = r0;
+    A.rows = seq - r0 < CA_ROWS ? seq - r0 : CA_ROWS;
+    const int n_tail = (A.rows + CA_TAIL_ROWS - 1) / CA_TAIL_ROWS;
+    hipLaunchKernelGGL(qsa_chunk_attend_kernel, dim3(A.nwg_sel + n_tail, g->n_kv_heads, g->batch), dim3(CA_NT), 0,
+                       stream, A);
+    QM_CHECK_LAUNCH();
+  }
   if (g->act_dtype == QM_ACT_F32) {
     CombineArgs<float, uint16_t> C{part_o, part_ml, static_cast<const float*>(qg), static_cast<float*>(out), g->n_heads,
                          g->n_kv_heads, nslot};

@@ -1707,9 +1707,11 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
 // has seen the flags of all 64, so that no workgroup reads the advanced word in
 // the launch that advances it. Otherwise the attending workgroups merge the
 // slices among themselves and only their flags are waited for.
-// Every workgroup of a group is resident at once: workgroups are dispatched in
-// order, so at most one group is ever partly dispatched, and a group (at most
-// DEC_MAX_ITEMS small workgroups) fits the device.
+// Every workgroup of a group must be resident at once for the waits to end.
+// Workgroups are dispatched in order, so at most one group is ever partly
+// dispatched; qm_qsa_decode refuses a group larger than the device's resident
+// capacity for the kernel variant (occupancy x compute units, computed on the
+// host), and callers route such plans to front + attend.
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_NT = 64 * DEC_WAVES;
 constexpr int DEC_MAX_BLOCKS = 2048;

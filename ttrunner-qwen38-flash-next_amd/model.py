@@ -43,6 +43,7 @@ class Qwen4MixModel:
         self.rope = RopeTable(self.config.rope_dim, self.config.rope_theta, self.config.mrope_section, self.device)
         self._dev = {}
         self._ws = {}
+        self._rope_copy = None  # (key, cos, sin): the device copy of the caller's host rope tables
         self._handoff = {}      # decode workspaces whose hand-off counters check_handoffs() reads
         native.load()
 
@@ -260,8 +261,18 @@ class Qwen4MixModel:
             s = sin[0] if sin.ndim == 3 else sin
             return c.contiguous(), s.contiguous()
         if cos is not None and not cos.is_cuda:
+            # the reference's forward hands the same host tables to every layer of
+            # a step: copy them once. The cache holds the tables themselves, so
+            # their storage cannot be reused by another tensor while it is kept,
+            # and an in-place change bumps their version.
+            key = (cos, sin, cos._version, sin._version, n_pos)
+            if self._rope_copy is not None:
+                k0 = self._rope_copy[0]
+                if k0[0] is cos and k0[1] is sin and k0[2:] == key[2:]:
+                    return self._rope_copy[1], self._rope_copy[2]
             c = (cos[0] if cos.ndim == 3 else cos)[:n_pos].to(self.device, torch.float32).contiguous()
             s = (sin[0] if sin.ndim == 3 else sin)[:n_pos].to(self.device, torch.float32).contiguous()
+            self._rope_copy = (key, c, s)
             return c, s
         return self.rope.get(n_pos)
 

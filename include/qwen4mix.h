@@ -334,13 +334,17 @@ size_t qm_qsa_attend_chunk_workspace(const qm_qsa_geom* g, int seq);
 /* The same attention as qm_qsa_attend for a chunk of `seq` consecutive query
  * rows per sequence (the prefill form of reference/model.py:365-382 with the
  * mask of :306-326), organised by key block instead of by row: the rows'
- * (selected block | tail block) entries are sorted by block on the device, each
+ * selected-block entries are filed under their blocks on the device, each
  * block's keys and values are read once and scored for every row that attends
  * it (a tail block only up to the row's own position), and a row's partials
  * are merged with the gate. Indexer ratio 32 or 64, at most 4096 blocks.
  *   q (qm_qsa_prep's q_out) and qg [B, S, Hq, 2*d] act as qm_qsa_attend;
  *   positions [B] = position of row 0; ids [B, S, budget/ratio] and n_sel
- *   [B, S] from qm_qsa_select; out [B, S, Hq*d] act. */
+ *   [B, S] from qm_qsa_select; out [B, S, Hq*d] act.
+ * The workspace keeps per-block entry counts between calls (double-buffered
+ * by a parity word it also holds): zero-fill it before its first use, keep
+ * it for one (batch, max_blocks) geometry (a larger `seq` may reuse a
+ * workspace sized for it), and do not let two calls on it overlap. */
 int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool,
                         const void* v_pool, const int* positions, const int* page_table, const int* ids,
                         const int* n_sel, void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);

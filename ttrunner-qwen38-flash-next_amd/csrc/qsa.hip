@@ -1184,6 +1184,7 @@ template <typename T, typename PO = float>
 struct CombineArgs {
   const PO* part_o; const float* part_ml; const T* qg; T* out;
   int hq, hkv, splits;
+  int* flip = nullptr;      // the chunk path's entry-list parity, flipped once the merge is done
 };
 
 __device__ __forceinline__ float part_value(const float* p, long i) { return p[i]; }
@@ -1201,6 +1202,7 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T, PO> A
   __shared__ float s_w[MAX_SPLITS];
   __shared__ float s_red[QSA_D / 64];
   const float gate = Act<T>::load(A.qg, ((long)row * A.hq + hq) * (2 * QSA_D) + QSA_D + d);
+  if (A.flip && hq == 0 && row == 0 && d == 0) *A.flip ^= 1;
   // every split's (max, sum) in parallel, then the weights in LDS
   float m = -INFINITY, l = 0.f;
   for (int s = d; s < A.splits; s += QSA_D) {
@@ -1247,38 +1249,83 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T, PO> A
 // The attention of a chunk of query rows reads each key/value block once. A
 // row's entries are its (row, slot) pairs: slot i < n_sel its i-th selected
 // block, slot topk its tail block (keys ts..p, when the row does not complete
-// its block). qsa_chunk_attend_kernel, grid (selected + tail workgroups, kv
-// head g, sequence b), up to CA_ROWS rows per launch:
-//   * selected workgroup x owns blocks x*bpw .. x*bpw + bpw - 1: it reads every
-//     row's ids, keeps the entries that fall in its blocks, counting-sorted by
-//     block in LDS;
-//   * tail workgroup t owns the tail entries of rows 8t .. 8t+7 (one or two
-//     blocks: the rows of a chunk share few tail blocks, and 8 rows per
-//     workgroup keeps them from piling onto one), and writes the empty
-//     partials (max -inf) of those rows' unused slots;
-//   * then, for each of its blocks in turn, its 64-token key and value pieces
-//     (16 KB of key and 16 KB of value per 32 tokens, contiguous in the page's
-//     lane order) are copied into LDS by direct global->LDS loads, the next
-//     block's while this one is scored; each wave scores two entries x 8
-//     query heads on bf16 MFMA and writes one partial per (row, slot, head):
-//     fp32 max and sum, and the output normalised by the sum, in bf16.
-// qsa_combine then merges a row's topk + 1 slots and applies the gate.
+// its block). qm_qsa_attend_chunk is three launches:
+//   qsa_chunk_bucket   one 64-thread workgroup per row: files each selected
+//                      entry under its block (an atomic count and a list of
+//                      capacity seq per block, in the workspace) and writes the
+//                      empty partials (max -inf) of the row's unused slots;
+//   qsa_chunk_attend   grid (blocks + tail workgroups, kv head, sequence): the
+//                      workgroup of block j reads its count and list with its
+//                      first loads, then the block's 64 tokens of key and value
+//                      pieces (16 KB of key and 16 KB of value per 32 tokens,
+//                      contiguous in the page's lane order) through registers
+//                      into LDS; each wave scores two entries x 8 query heads
+//                      on bf16 MFMA and writes one partial per (row, slot,
+//                      head): fp32 max and sum, and the output normalised by the
+//                      sum, in bf16. A tail workgroup takes the tail entries of
+//                      8 rows (one or two blocks), which would otherwise pile
+//                      onto two blocks' workgroups;
+//   qsa_combine        merges a row's topk + 1 slots and applies the gate.
+// The counts are double-buffered by a parity word: the bucket kernel files
+// into set p and clears set p ^ 1 (the previous call's), the merge flips p. The
+// workspace is zero-filled before its first use and left consistent by every
+// call.
 constexpr int CA_MAX_BLOCKS = 4096;
 constexpr int CA_NT = 256;        // attention workgroup: four waves
-constexpr int CA_ROWS = 128;      // query rows per launch
 constexpr int CA_TAIL_ROWS = 8;   // rows per tail workgroup
-constexpr int CA_MAX_BPW = 8;     // blocks per selected workgroup
-constexpr int CA_MAX_ENT = CA_ROWS * CA_MAX_BPW;   // entries a workgroup can hold
+constexpr int CA_MAX_BPW = 4;     // blocks per workgroup
 
 struct ChunkAttnArgs {
   const uint16_t* q;                      // [rows, 2 (hi, lo), hq, 256] bf16
   const uint16_t* k_pool; const uint16_t* v_pool;
   const int* positions; const int* page_table; const int* ids; const int* n_sel;
   uint16_t* part_o; float* part_ml;      // part_o: bf16, normalised by l
-  int seq, row0, rows, hq, hkv, page_size, max_pages, ratio, topk, nwg_sel, bpw;
-  unsigned topk_magic, nslot_magic;      // ceil(2^32 / d): n / d = umulhi(n, magic) for n < 2^16, d <= 2^9
+  unsigned* cnt;                          // [2][B][max_blocks] entry counts
+  const unsigned* list;                   // [B][max_blocks][seq]: row << 16 | slot
+  const int* parity;
+  int batch, seq, hq, hkv, page_size, max_pages, ratio, topk, max_blocks, bpw, nwg_sel;
   float scale;
 };
+
+struct ChunkBucketArgs {
+  const int* positions; const int* ids; const int* n_sel;
+  float* part_ml; unsigned* cnt; unsigned* list; const int* parity;
+  int batch, seq, hkv, ratio, topk, max_blocks;
+};
+
+__global__ __launch_bounds__(64) void qsa_chunk_bucket_kernel(ChunkBucketArgs A) {
+  const int row = blockIdx.x, lane = threadIdx.x;
+  const int b = row / A.seq, s = row % A.seq;
+  const int par = *A.parity;
+  const int nslot = A.topk + 1;
+  const int nsel = A.n_sel[row];
+  const int p = A.positions[b] + s;
+  unsigned* cnt_in = A.cnt + ((long)par * A.batch + b) * A.max_blocks;
+  // the previous call's counts, cleared for the next call
+  unsigned* cnt_old = A.cnt + ((long)(par ^ 1) * A.batch + b) * A.max_blocks;
+  for (int j = s * 64 + lane; j < A.max_blocks; j += A.seq * 64) cnt_old[j] = 0u;
+  for (int i = lane; i < nslot; i += 64) {
+    bool empty;
+    if (i < A.topk) {
+      empty = i >= nsel;
+      if (!empty) {
+        const int j = A.ids[(long)row * A.topk + i];
+        // a block is at most once among a row's selections: at < seq
+        const unsigned at = atomicAdd(&cnt_in[j], 1u);
+        if (at < static_cast<unsigned>(A.seq))
+          A.list[((long)b * A.max_blocks + j) * A.seq + at] = (static_cast<unsigned>(s) << 16) | static_cast<unsigned>(i);
+      }
+    } else {
+      empty = ((p + 1) / A.ratio) * A.ratio > p;      // the row completes its block: no tail
+    }
+    if (empty)
+      for (int g = 0; g < A.hkv; ++g) {
+        float4* ml = reinterpret_cast<float4*>(A.part_ml + (((long)row * A.hkv + g) * nslot + i) * GQA * 2);
+#pragma unroll
+        for (int h = 0; h < GQA / 2; ++h) ml[h] = make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
+      }
+  }
+}
 
 // One wave's partials of a group: this lane's 4 channels of each of the 16
 // channel blocks (bf16, normalised by the sum), the (max, sum) pair and where
@@ -1421,29 +1468,20 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
   const int nslot = A.topk + 1;
   const int gpb = A.ratio / 32;
   const int* ptab = A.page_table + (long)b * A.max_pages;
-  const long row_b = (long)b * A.seq + A.row0;       // global index of the launch's row 0
+  const long row_b = (long)b * A.seq;                 // global index of the sequence's row 0
   const long head_stride = (long)A.page_size * QSA_D;
+  const int e_w = 2 * wv + il;                        // this lane's entry within a group of 8
 
   __shared__ uint16_t kv[2][32][64 * 8];      // per 32-token group: 16 key then 16 value 1 KB pieces
-  __shared__ unsigned ent[CA_MAX_ENT];         // entries by block: row << 16 | tail << 9 | slot
-  __shared__ int cnt[CA_MAX_BPW], off[CA_MAX_BPW], cur[CA_MAX_BPW], blist[CA_MAX_BPW];
-  __shared__ int pg[CA_MAX_BPW][2];
-  __shared__ int s_nb;
   __shared__ u32x4_t tbuf[CA_NT / 64][16 * CA_TROW / 16];   // per wave: partial rows on their way out
   unsigned char* tb = reinterpret_cast<unsigned char*>(&tbuf[wv][0]);
 
-  const bool tail_wg = x >= A.nwg_sel;
-  const int tr0 = (x - A.nwg_sel) * CA_TAIL_ROWS;
-  if (tid < CA_MAX_BPW) { cnt[tid] = 0; cur[tid] = 0; }
-
-  int pos0, jlo, nloc;
-  // a block's key and value pieces pass through registers: loaded while the
-  // previous block is scored, stored to LDS between two barriers (a block of
-  // one 32-token group loads and stores it twice; the second copy is not read)
-  // (indices of the register array are compile-time constants, so it stays in
-  // registers)
+  // a block's key and value pieces pass through registers into LDS (a block of
+  // one 32-token group loads and stores it twice; the second copy is not
+  // read); indices of the register array are compile-time constants, so it
+  // stays in registers
   u32x4_t kvr[16];
-  auto kv_load_at = [&](int j, int page0, int page1) __attribute__((always_inline)) {
+  auto kv_load = [&](int j, int page0, int page1) __attribute__((always_inline)) {
     const uint16_t* src[4];
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
@@ -1457,10 +1495,6 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
       kvr[i] = *reinterpret_cast<const u32x4_t*>(src[i / 4] + (i % 4) * 4 * 512);
     });
   };
-  auto kv_load = [&](int k) __attribute__((always_inline)) {
-    const int lb = blist[k];
-    kv_load_at(jlo + lb, pg[lb][0], pg[lb][1]);
-  };
   auto kv_store = [&]() __attribute__((always_inline)) {
     // piece 4 pc + wv of group gi: keys at 0..15, values at 16..31
     static_for<16>([&](auto i) {
@@ -1471,198 +1505,133 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
   // the chunk path scores with the query's bf16 part (hi) alone: the keys
   // are bf16 too, and the softmax of these 64-key blocks is far inside the
   // output tolerance either way, at half the query traffic and products
-  bf16x8_t qhi[8], qnx[8];
-  auto q_load_into = [&](bf16x8_t (&qd)[8], unsigned pk) __attribute__((always_inline)) {
+  bf16x8_t qhi[8];
+  auto q_load = [&](unsigned pk) __attribute__((always_inline)) {
     const long row = row_b + (pk >> 16);
     const uint16_t* qh = A.q + q_index(row, A.hkv, 0, g * GQA + hh, 8 * quad);
 #pragma unroll
-    for (int sk = 0; sk < 8; ++sk) qd[sk] = load_bf16x8(qh + Q_SK_STRIDE * sk);
+    for (int sk = 0; sk < 8; ++sk) qhi[sk] = load_bf16x8(qh + Q_SK_STRIDE * sk);
   };
-  auto q_load = [&](unsigned pk) __attribute__((always_inline)) { q_load_into(qhi, pk); };
-  // ---- this workgroup's entries, counting-sorted by local block. The first
-  // CA_SCAN * CA_NT entries' blocks stay in registers for the placement pass;
-  // every load of a round is issued before any is used.
-  constexpr int CA_SCAN = 16;
-  const int n_scan = A.rows * A.topk;
-  bool spec = false;        // the first local block's pieces are requested before its entries are known
-  auto spec_load = [&]() __attribute__((always_inline)) {
-    const int c0 = min((jlo * A.ratio) / A.page_size, A.max_pages - 1);
-    const int c1 = min((jlo * A.ratio + (gpb > 1 ? 32 : 0)) / A.page_size, A.max_pages - 1);
-    kv_load_at(jlo, ptab[c0], ptab[c1]);
-    spec = true;
+  auto pages_of = [&](int j, int& page0, int& page1) __attribute__((always_inline)) {
+    page0 = ptab[min((j * A.ratio) / A.page_size, A.max_pages - 1)];
+    page1 = ptab[min((j * A.ratio + (gpb > 1 ? 32 : 0)) / A.page_size, A.max_pages - 1)];
   };
-  int lb0[CA_SCAN];
-  unsigned code0[CA_SCAN];
-  auto scan_sel = [&](int base, int (&lb)[CA_SCAN], unsigned (&code)[CA_SCAN]) __attribute__((always_inline)) {
-    int nsel[CA_SCAN], jv[CA_SCAN];
-#pragma unroll
-    for (int k = 0; k < CA_SCAN; ++k) {
-      const int e = min(base + k * CA_NT + tid, n_scan - 1);
-      nsel[k] = A.n_sel[row_b + __umulhi(e, A.topk_magic)];
-      jv[k] = A.ids[row_b * A.topk + e];
+  GroupOut R;
+
+  if (x < A.nwg_sel) {
+    // ---- blocks x bpw .. x bpw + bpw - 1: their counts (both parities' words,
+    // one of them current), first entries and pages, and the position, in one
+    // round trip; then block by block, the next nonempty block's pieces and
+    // first query rows in flight while this one is scored
+    const int j0 = x * A.bpw;
+    const int par = *A.parity;
+    // (the per-block arrays are indexed by compile-time constants only, so
+    // they stay in registers; a runtime k reads them through a select chain)
+    unsigned cw[CA_MAX_BPW], pk0[CA_MAX_BPW];
+    int pg0[CA_MAX_BPW], pg1[CA_MAX_BPW];
+    static_for<CA_MAX_BPW>([&](auto k) {
+      const int j = min(j0 + k, A.max_blocks - 1);
+      const unsigned c0 = A.cnt[(long)b * A.max_blocks + j];
+      const unsigned c1 = A.cnt[((long)A.batch + b) * A.max_blocks + j];
+      cw[k] = k < A.bpw && j0 + k < A.max_blocks ? (par ? c1 : c0) : 0u;
+      pk0[k] = A.list[((long)b * A.max_blocks + j) * A.seq + min(e_w, A.seq - 1)];
+      int a0, a1;
+      pages_of(j, a0, a1);
+      pg0[k] = a0;
+      pg1[k] = a1;
+    });
+    const int pos0 = A.positions[b];
+    // the nonempty blocks, as a bit mask taken lowest first
+    unsigned rem = 0u;
+    static_for<CA_MAX_BPW>([&](auto k) { rem |= cw[k] != 0u ? 1u << k : 0u; });
+    if (rem == 0u) {
+      QM_PHASE_FLUSH();
+      return;
     }
-#pragma unroll
-    for (int k = 0; k < CA_SCAN; ++k) {
-      const int e = base + k * CA_NT + tid;
-      const int r = __umulhi(e, A.topk_magic), i = e - r * A.topk;
-      const int j = e < n_scan && i < nsel[k] ? jv[k] : -1;
-      lb[k] = j >= jlo && j < jlo + nloc ? j - jlo : -1;
-      code[k] = (static_cast<unsigned>(r) << 16) | static_cast<unsigned>(i);
+    auto pick = [&](const auto& v, int k) __attribute__((always_inline)) {
+      auto r = v[0];
+      static_for<CA_MAX_BPW>([&](auto i) { r = k == i ? v[i] : r; });
+      return r;
+    };
+    auto first_pk = [&](int k, int n) __attribute__((always_inline)) {
+      const unsigned* lst = A.list + ((long)b * A.max_blocks + j0 + k) * A.seq;
+      return n > e_w ? pick(pk0, k) : lst[0];
+    };
+    {
+      const int k = __builtin_ctz(rem);
+      kv_load(j0 + k, pick(pg0, k), pick(pg1, k));
+      q_load(first_pk(k, static_cast<int>(pick(cw, k))));
     }
-  };
-  if (!tail_wg) {
-    jlo = x * A.bpw;
-    nloc = A.bpw;
-    scan_sel(0, lb0, code0);
-    // the pages of the local blocks, needed only by those that hold entries
-    if (tid < 2 * nloc) {
-      const int jj = jlo + (tid >> 1), gi = tid & 1;
-      pg[tid >> 1][gi] = ptab[min((jj * A.ratio + 32 * (gi < gpb ? gi : 0)) / A.page_size, A.max_pages - 1)];
-    }
-    pos0 = A.positions[b] + A.row0;
-    // local block 0 can hold entries when it is complete before the last row
-    if ((jlo + 1) * A.ratio <= pos0 + A.rows) spec_load();
-    __syncthreads();                          // counts cleared
+    kv_store();
+    __syncthreads();
+    QM_PHASE(3);
+    bf16x8_t qnx[8];
+    for (int t = 0; rem != 0u; ++t) {
+      const int k = __builtin_ctz(rem), j = j0 + k;
+      rem &= rem - 1u;
+      const int n = static_cast<int>(pick(cw, k));
+      const unsigned* lst = A.list + ((long)b * A.max_blocks + j) * A.seq;
+      if (rem != 0u) {
+        const int kn = __builtin_ctz(rem);
+        kv_load(j0 + kn, pick(pg0, kn), pick(pg1, kn));
+        const unsigned pkn = first_pk(kn, static_cast<int>(pick(cw, kn)));
+        const long rown = row_b + (pkn >> 16);
+        const uint16_t* qh = A.q + q_index(rown, A.hkv, 0, g * GQA + hh, 8 * quad);
 #pragma unroll
-    for (int k = 0; k < CA_SCAN; ++k)
-      if (lb0[k] >= 0) atomicAdd(&cnt[lb0[k]], 1);
-    for (int base = CA_SCAN * CA_NT; base < n_scan; base += CA_SCAN * CA_NT) {
-      int lb[CA_SCAN];
-      unsigned code[CA_SCAN];
-      scan_sel(base, lb, code);
+        for (int sk = 0; sk < 8; ++sk) qnx[sk] = load_bf16x8(qh + Q_SK_STRIDE * sk);
+      }
+      for (int g0 = 0; g0 < n; g0 += 8) {
+        const int e = g0 + e_w;
+        unsigned pk;
+        if (g0 > 0) {
+          pk = lst[min(e, n - 1)];
+          q_load(pk);
+        } else {
+          pk = first_pk(k, n);
+        }
+        if (g0 + 2 * wv < n) {
+          chunk_attend_group(A, kv, qhi, j, pk, e < n, row_b, pos0, g, nslot, R, t == 0 && g0 == 0);
+          store_group(A, R, tb);
+        }
+      }
+      if (rem != 0u) {
+        __syncthreads();     // every wave is done with this block's pieces
+        kv_store();
 #pragma unroll
-      for (int k = 0; k < CA_SCAN; ++k)
-        if (lb[k] >= 0) atomicAdd(&cnt[lb[k]], 1);
+        for (int sk = 0; sk < 8; ++sk) qhi[sk] = qnx[sk];
+        __syncthreads();
+      }
     }
   } else {
-    // the tail entries of rows tr0 .. tr0 + 7 (one or two blocks), and the
-    // empty partials (max -inf) of those rows' unused slots
-    pos0 = A.positions[b] + A.row0;
-    jlo = (pos0 + tr0) / A.ratio;
-    nloc = 2;
-    spec_load();
-#pragma unroll
-    for (int k = 0; k < CA_SCAN; ++k) lb0[k] = -1;
-    if (tid < CA_TAIL_ROWS) {
-      const int r = tr0 + tid, p = pos0 + r;
-      if (r < A.rows && ((p + 1) / A.ratio) * A.ratio <= p) {
-        lb0[0] = p / A.ratio - jlo;
-        code0[0] = (static_cast<unsigned>(r) << 16) | (1u << 9) | static_cast<unsigned>(A.topk);
-      }
-    }
-    if (tid < 4) {
-      const int gi = tid & 1;
-      pg[tid >> 1][gi] = ptab[min(((jlo + (tid >> 1)) * A.ratio + 32 * (gi < gpb ? gi : 0)) / A.page_size,
-                                  A.max_pages - 1)];
-    }
-    // (row, slot) pairs; a thread writes the pair's eight heads
-    const int n_emp = CA_TAIL_ROWS * nslot;
-    for (int e = tid; e < n_emp; e += CA_NT) {
-      const int rr = __umulhi(e, A.nslot_magic), i = e - rr * nslot;
-      const int r = tr0 + rr;
-      if (r >= A.rows) continue;
-      const long row = row_b + r;
-      const int p = pos0 + r;
-      const bool empty = i < A.topk ? i >= A.n_sel[row] : ((p + 1) / A.ratio) * A.ratio > p;
-      if (empty) {
-        const long pb = ((row * A.hkv + g) * nslot + i) * GQA;
-        float4* ml = reinterpret_cast<float4*>(A.part_ml + pb * 2);
-#pragma unroll
-        for (int h = 0; h < GQA / 2; ++h) ml[h] = make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
-      }
-    }
-    __syncthreads();                          // counts cleared
-    if (lb0[0] >= 0) atomicAdd(&cnt[lb0[0]], 1);
-  }
-  __syncthreads();
-  QM_PHASE(1);
-  if (tid == 0) {
-    int o = 0, nb = 0;
-    for (int lb = 0; lb < nloc; ++lb) {
-      off[lb] = o;
-      o += cnt[lb];
-      if (cnt[lb]) blist[nb++] = lb;
-    }
-    s_nb = nb;
-  }
-  __syncthreads();
-  const int nb = s_nb;
-  if (nb == 0) {
-    QM_PHASE_FLUSH();
-    return;
-  }
-
-  if (!spec || blist[0] != 0) kv_load(0);
-  // placement: the entries in order of their local block
-  if (!tail_wg) {
-#pragma unroll
-    for (int k = 0; k < CA_SCAN; ++k)
-      if (lb0[k] >= 0) ent[off[lb0[k]] + atomicAdd(&cur[lb0[k]], 1)] = code0[k];
-    for (int base = CA_SCAN * CA_NT; base < n_scan; base += CA_SCAN * CA_NT) {
-      int lb[CA_SCAN];
-      unsigned code[CA_SCAN];
-      scan_sel(base, lb, code);
-#pragma unroll
-      for (int k = 0; k < CA_SCAN; ++k)
-        if (lb[k] >= 0) ent[off[lb[k]] + atomicAdd(&cur[lb[k]], 1)] = code[k];
-    }
-  } else if (lb0[0] >= 0) {
-    ent[off[lb0[0]] + atomicAdd(&cur[lb0[0]], 1)] = code0[0];
-  }
-  __syncthreads();
-  QM_PHASE(2);
-  {
-    const int e = 2 * wv + il, n = cnt[blist[0]];
-    q_load(ent[off[blist[0]] + min(e, n - 1)]);
-  }
-  kv_store();
-  __syncthreads();
-  QM_PHASE(3);
-
-  // ---- the blocks. A block's last partials are stored at the start of the
-  // next block: the wait for the next block's pieces (loaded after them) then
-  // finds them long written, instead of waiting for their writes to complete.
-  GroupOut R;
-  bool pending = false;
-  for (int k = 0; k < nb; ++k) {
-    const int lb = blist[k], j = jlo + lb;
-    const int n = cnt[lb], e0 = off[lb];
-    if (pending) {
-      store_group(A, R, tb);
-      pending = false;
-    }
-    // the next block's pieces and its first group's query rows are requested
-    // now, so that both have arrived when this block is done
-    if (k + 1 < nb) {
-      kv_load(k + 1);
-      const int lbn = blist[k + 1], nn = cnt[lbn];
-      q_load_into(qnx, ent[off[lbn] + min(2 * wv + il, nn - 1)]);
-    }
-    for (int g0 = 0; g0 < n; g0 += 8) {
-      const int e = g0 + 2 * wv + il;
-      const unsigned pk = ent[e0 + min(e, n - 1)];
-      if (g0 > 0) q_load(pk);
-      if (k == 0 && g0 == 0) QM_PHASE(7);
-      if (g0 + 2 * wv < n) {
-        chunk_attend_group(A, kv, qhi, j, pk, e < n, row_b, pos0, g, nslot, R, k == 0 && g0 == 0);
-        if (g0 + 8 < n) store_group(A, R, tb);
-        else pending = true;
-      }
-    }
-    if (k == 0) QM_PHASE(5);
-    if (k + 1 < nb) {
-      __syncthreads();     // every wave is done with this block's pieces
+    // ---- the tail entries (keys ts..p) of rows tr0 .. tr0 + 7: block jt, then
+    // block jt + 1 when the rows cross a block boundary
+    const int tr0 = (x - A.nwg_sel) * CA_TAIL_ROWS;
+    const int pos0 = A.positions[b];
+    const int jt = (pos0 + tr0) / A.ratio;
+    const int r = tr0 + e_w, p = pos0 + r;
+    const bool has_tail = r < A.seq && ((p + 1) / A.ratio) * A.ratio <= p;
+    const int jr = has_tail ? p / A.ratio : -1;
+    const unsigned pk = (static_cast<unsigned>(min(r, A.seq - 1)) << 16) | (1u << 9) | static_cast<unsigned>(A.topk);
+    int pa0, pa1, pb0, pb1;
+    pages_of(jt, pa0, pa1);
+    pages_of(jt + 1, pb0, pb1);
+    q_load(pk);
+    for (int bi = 0; bi < 2; ++bi) {
+      const int j = jt + bi;
+      // whether any of the 8 rows has its tail in block j (every thread sees
+      // the rows of its wave's entries; the waves agree through LDS)
+      const bool mine = jr == j;
+      if (!__syncthreads_or(mine ? 1 : 0)) continue;
+      kv_load(j, bi ? pb0 : pa0, bi ? pb1 : pa1);
       kv_store();
-#pragma unroll
-      for (int sk = 0; sk < 8; ++sk) qhi[sk] = qnx[sk];
       __syncthreads();
-      if (k == 0) QM_PHASE(6);
+      if (__builtin_amdgcn_ballot_w64(mine) != 0ull) {
+        chunk_attend_group(A, kv, qhi, j, pk, mine, row_b, pos0, g, nslot, R);
+        store_group(A, R, tb);
+      }
+      __syncthreads();     // every wave is done with the pieces before the next block's
     }
   }
-  if (pending) store_group(A, R, tb);
-#ifdef QM_PHASE_TRACE
-  if (tid == 0) qm_ph_[14] = static_cast<unsigned long long>(nb) | (static_cast<unsigned long long>(off[blist[nb - 1]] + cnt[blist[nb - 1]]) << 16);
-#endif
   QM_PHASE(4);
   QM_PHASE_FLUSH();
 }
@@ -2437,14 +2406,19 @@ extern "C" int qm_qsa_attend(const qm_qsa_geom* g, int seq, const void* q, const
 
 namespace {
 struct ChunkWs {
-  size_t o, ml, total;
+  size_t parity, cnt, list, o, ml, total;
 };
 
+// the parity word and the counts first, at offsets independent of seq (a
+// workspace sized for a longer chunk serves a shorter one)
 ChunkWs chunk_ws_layout(const qm_qsa_geom* g, int seq) {
   const int nslot = g->budget / g->ratio + 1;
   const size_t rows = (size_t)g->batch * seq;
   ChunkWs w;
-  w.o = 0;
+  w.parity = 0;
+  w.cnt = 256;
+  w.list = w.cnt + qm_align256((size_t)2 * g->batch * g->max_blocks * sizeof(unsigned));
+  w.o = w.list + qm_align256((size_t)g->batch * g->max_blocks * seq * sizeof(unsigned));
   w.ml = w.o + qm_align256(rows * g->n_kv_heads * nslot * GQA * QSA_D * sizeof(uint16_t));
   w.total = w.ml + qm_align256(rows * g->n_kv_heads * nslot * GQA * 2 * sizeof(float));
   return w;
@@ -2463,7 +2437,7 @@ int check_chunk_geom(const qm_qsa_geom* g, const char* who) {
 }  // namespace
 
 extern "C" size_t qm_qsa_attend_chunk_workspace(const qm_qsa_geom* g, int seq) {
-  if (!g || g->ratio <= 0 || g->budget < g->ratio || seq <= 0 || g->batch <= 0) return 0;
+  if (!g || g->ratio <= 0 || g->budget < g->ratio || seq <= 0 || g->batch <= 0 || g->max_blocks <= 0) return 0;
   return chunk_ws_layout(g, seq).total;
 }
 
@@ -2483,37 +2457,43 @@ extern "C" int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q,
   char* base = static_cast<char*>(workspace);
   const int topk = g->budget / g->ratio;
   const int nslot = topk + 1;
+  int* parity = reinterpret_cast<int*>(base + L.parity);
+  unsigned* cnt = reinterpret_cast<unsigned*>(base + L.cnt);
+  unsigned* list = reinterpret_cast<unsigned*>(base + L.list);
   uint16_t* part_o = reinterpret_cast<uint16_t*>(base + L.o);
   float* part_ml = reinterpret_cast<float*>(base + L.ml);
 
-  // blocks per selected workgroup: about 1024 selected workgroups over the kv
-  // heads and sequences (many small workgroups keep more blocks in flight)
-  const long want = ((long)g->max_blocks * g->n_kv_heads * g->batch + 1023) / 1024;
-  const int bpw = (int)(want < 1 ? 1 : want > CA_MAX_BPW ? CA_MAX_BPW : want);
+  ChunkBucketArgs K{positions, ids, n_sel, part_ml, cnt, list, parity, g->batch, seq, g->n_kv_heads, g->ratio, topk,
+                    g->max_blocks};
+  hipLaunchKernelGGL(qsa_chunk_bucket_kernel, dim3(g->batch * seq), dim3(64), 0, stream, K);
+  QM_CHECK_LAUNCH();
+
   ChunkAttnArgs A;
   A.q = static_cast<const uint16_t*>(q); A.k_pool = static_cast<const uint16_t*>(k_pool);
   A.v_pool = static_cast<const uint16_t*>(v_pool); A.positions = positions; A.page_table = page_table;
   A.ids = ids; A.n_sel = n_sel; A.part_o = part_o; A.part_ml = part_ml;
-  A.seq = seq; A.hq = g->n_heads; A.hkv = g->n_kv_heads; A.page_size = g->page_size; A.max_pages = g->max_pages;
-  A.ratio = g->ratio; A.topk = topk; A.bpw = bpw; A.nwg_sel = (g->max_blocks + bpw - 1) / bpw;
+  A.cnt = cnt; A.list = list; A.parity = parity;
+  A.batch = g->batch; A.seq = seq; A.hq = g->n_heads; A.hkv = g->n_kv_heads; A.page_size = g->page_size;
+  A.max_pages = g->max_pages; A.ratio = g->ratio; A.topk = topk; A.max_blocks = g->max_blocks;
   A.scale = 1.0f / 16.0f;   // 1/sqrt(256), exact
-  A.topk_magic = static_cast<unsigned>((0x100000000ull + topk - 1) / topk);
-  A.nslot_magic = static_cast<unsigned>((0x100000000ull + nslot - 1) / nslot);
-  for (int r0 = 0; r0 < seq; r0 += CA_ROWS) {
-    A.row0 = r0;
-    A.rows = seq - r0 < CA_ROWS ? seq - r0 : CA_ROWS;
-    const int n_tail = (A.rows + CA_TAIL_ROWS - 1) / CA_TAIL_ROWS;
-    hipLaunchKernelGGL(qsa_chunk_attend_kernel, dim3(A.nwg_sel + n_tail, g->n_kv_heads, g->batch), dim3(CA_NT), 0,
-                       stream, A);
-    QM_CHECK_LAUNCH();
-  }
+  // blocks per workgroup: one while the grid stays within about eight
+  // workgroups per compute unit (measured at 1024 blocks x kv heads: one block
+  // per workgroup 45.0 us, two with the second's pieces loading while the
+  // first is scored 49.5 us: more workgroups in flight beat the overlap)
+  const long want = ((long)g->max_blocks * g->n_kv_heads * g->batch + 2047) / 2048;
+  A.bpw = (int)(want < 1 ? 1 : want > CA_MAX_BPW ? CA_MAX_BPW : want);
+  A.nwg_sel = (g->max_blocks + A.bpw - 1) / A.bpw;
+  const int n_tail = (seq + CA_TAIL_ROWS - 1) / CA_TAIL_ROWS;
+  hipLaunchKernelGGL(qsa_chunk_attend_kernel, dim3(A.nwg_sel + n_tail, g->n_kv_heads, g->batch), dim3(CA_NT),
+                     0, stream, A);
+  QM_CHECK_LAUNCH();
   if (g->act_dtype == QM_ACT_F32) {
     CombineArgs<float, uint16_t> C{part_o, part_ml, static_cast<const float*>(qg), static_cast<float*>(out), g->n_heads,
-                         g->n_kv_heads, nslot};
+                         g->n_kv_heads, nslot, parity};
     hipLaunchKernelGGL((qsa_combine_kernel<float, uint16_t>), dim3(g->n_heads, g->batch * seq), dim3(QSA_D), 0, stream, C);
   } else {
     CombineArgs<bf16_t, uint16_t> C{part_o, part_ml, static_cast<const bf16_t*>(qg), static_cast<bf16_t*>(out), g->n_heads,
-                          g->n_kv_heads, nslot};
+                          g->n_kv_heads, nslot, parity};
     hipLaunchKernelGGL((qsa_combine_kernel<bf16_t, uint16_t>), dim3(g->n_heads, g->batch * seq), dim3(QSA_D), 0, stream, C);
   }
   QM_CHECK_LAUNCH();

@@ -365,7 +365,10 @@ class Qwen4MixModel:
             return None
         if seq > 1 and self.chunk_attend_fits(cache):
             # a chunk of rows: each selected key block is read once for all rows that attend it
-            ws = self._workspace("qsa_attend", lib.qm_qsa_attend_chunk_workspace(ctypes.byref(g), seq))
+            # its own workspace per geometry: the entry counts it keeps between
+            # calls are laid out by batch and block count
+            ws = self._workspace(f"qsa_attend_chunk_{batch}_{cache.max_blocks}",
+                                 lib.qm_qsa_attend_chunk_workspace(ctypes.byref(g), seq))
             if out is None:
                 out = torch.empty(batch, seq, c.num_attention_heads * c.head_dim, dtype=dt, device=self.device)
             native.call("qm_qsa_attend_chunk", ctypes.byref(g), seq, native.ptr(q_out), native.ptr(qg),

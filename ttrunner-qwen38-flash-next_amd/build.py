@@ -3,7 +3,10 @@
 One hipcc invocation over csrc/*.hip, output next to this file. Every HIP
 translation unit is compiled with packed-FP32 instruction selection disabled
 (``-Xclang -target-feature -Xclang -packed-fp32-ops``); hipcc's host pass warns
-that it does not know that feature, which is harmless.
+that it does not know that feature, which is harmless. Kernels whose arguments
+are plain scalars get their first 16 argument dwords preloaded into scalar
+registers at wave start (``-amdgpu-kernarg-preload-count=16``; firmware without
+preloading runs the kernel's own argument loads instead).
 """
 
 from __future__ import annotations
@@ -38,6 +41,7 @@ def build(verbose: bool = False) -> str:
     cmd = [
         hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-mllvm", "-amdgpu-kernarg-preload-count=16",
         "-I", os.path.join(ROOT, "include"), "-I", os.path.join(PKG, "csrc"),
         "-o", tmp, *sources(),
     ]

@@ -12,15 +12,21 @@
 //
 // Work split: 4 workgroups of 256 threads per (sequence, value head), each
 // holding 32 of the head's 128 state columns (16 KB of float32, whole 128-byte
-// lines of every row): the delta rule is independent per column, so a
-// workgroup updates its columns alone and a compute unit moves 32 KB instead
-// of the head's 128 KB. Each workgroup recomputes the conv of the head's q/k
-// channels (L2-resident) and convolves its own 32 v channels. The gated RMS
-// norm needs the head's sum of squares of o: each workgroup publishes its 32
-// columns' share in one 64-bit atomic exchange that carries the launch's
-// generation number, writes its state columns back, then polls the head's 4
-// shares (one cache line) and normalises its columns. All loads are issued at
-// the start, the conv's first.
+// lines of every row, moved by 16-byte loads and stores): the delta rule is
+// independent per column, so a workgroup updates its columns alone. Each
+// workgroup recomputes the conv of the head's q/k channels and convolves its
+// own 32 v channels. The gated RMS norm needs the head's sum of squares of o:
+// each workgroup publishes its columns' share in one 64-bit word that carries
+// the launch's generation number, writes its state columns back, then polls
+// the head's 4 shares (one cache line) and normalises its columns. All loads
+// are issued at the start, before any of them is waited for, and stores wait
+// for the end (loads and stores share one in-order counter).
+//
+// Measured (MI355X, batch 1, 32 heads, HIP graph replay): about 5.0 us per
+// step with the state in the Infinity Cache, 5.8 us with it in HBM only. A
+// workgroup's own work is about 3.5 us of that; the rest is the launch's fixed
+// cost. A single 1024-thread workgroup per head needs no hand-off but moves
+// 64 KB through one compute unit, and measured 0.5 us slower.
 //
 // The conv window is a ring of K slots per channel: the input of the token at
 // position p lives in slot p % K, so the K-1 history slots read by this step are
@@ -34,24 +40,14 @@ namespace {
 constexpr int DN_D = 128;      // head dim (k and v)
 constexpr int DN_TILE = 16;    // state columns per workgroup
 constexpr int DN_NT = 256;     // threads per workgroup
-constexpr int DN_DCOLS = 32;   // state columns per decode workgroup (whole 128-byte lines)
+constexpr int DN_DEC_NT = 256;   // threads per decode workgroup: four float4 of the slice each
+constexpr int DN_DCOLS = 32;     // state columns per decode workgroup (whole 128-byte lines)
 constexpr int DN_SLICES = DN_D / DN_DCOLS;  // decode workgroups per head
 // per (sequence, head) a 128-byte line of the decode workspace: the generation
 // word, a give-up counter, then the slices' (generation, sum of squares) words
 constexpr int DN_SYNC_WORDS = 32;
-constexpr int DN_SHARE0 = 4;   // first share, in 64-bit words
+constexpr int DN_SHARE0 = 2;     // first share, in 64-bit words
 
-template <typename T>
-struct DnDecodeArgs {
-  const T* qkv; const T* z; const T* a; const T* b;
-  const float* a_neg; const float* dt_bias;
-  const T* conv_w; const float* norm_w;
-  const int* positions;
-  T* ring; float* state; T* out;
-  unsigned* sync;                  // DN_SYNC_WORDS per (sequence, head)
-  int batch, hv, hk, conv_dim, K;
-  float eps;
-};
 
 // K = 4: the ring row and the weight row of a channel are one 8-byte (bf16) or
 // 16-byte (fp32) load each, issued together with the input
@@ -65,38 +61,87 @@ __device__ __forceinline__ float vget(const uint2& v, int i) {
 }
 
 // A channel's conv inputs (K = 4): its ring row and weight row (one 8-byte or
-// 16-byte load each) and the token's input, loaded before any is used.
+// 16-byte load each) and the token's input, kept as loaded (no conversion, so
+// nothing waits for them before the kernel's other loads are issued). The
+// caller stores the input into the ring slot pos % 4.
 template <typename T>
 struct ConvIn {
   typename Vec4<T>::type r, w;
-  float x;
+  T x;
 };
 template <typename T>
-__device__ __forceinline__ ConvIn<T> conv_load4(const DnDecodeArgs<T>& A, int b, int ch) {
+__device__ __forceinline__ ConvIn<T> conv_load4(const T* ring, const T* conv_w, const T* qkv, int conv_dim, int b,
+                                                int ch) {
   typedef typename Vec4<T>::type V;
   ConvIn<T> c;
-  c.r = *reinterpret_cast<const V*>(A.ring + ((long)b * A.conv_dim + ch) * 4);
-  c.w = *reinterpret_cast<const V*>(A.conv_w + (long)ch * 4);
-  c.x = Act<T>::load(A.qkv, (long)b * A.conv_dim + ch);
+  c.r = *reinterpret_cast<const V*>(ring + ((long)b * conv_dim + ch) * 4);
+  c.w = *reinterpret_cast<const V*>(conv_w + (long)ch * 4);
+  c.x = qkv[(long)b * conv_dim + ch];
   return c;
 }
 template <typename T>
-__device__ __forceinline__ float conv_finish4(const DnDecodeArgs<T>& A, const ConvIn<T>& c, int b, int ch, int pos,
-                                              bool write_ring) {
+__device__ __forceinline__ float conv_finish4(const ConvIn<T>& c, int pos) {
+  const float x = Act<T>::load(&c.x, 0);
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < 3; ++j) acc = fmaf(vget(c.w, j), vget(c.r, (pos + 1 + j) & 3), acc);
-  acc = fmaf(vget(c.w, 3), c.x, acc);
-  if (write_ring) Act<T>::store(A.ring + ((long)b * A.conv_dim + ch) * 4, pos & 3, c.x);
+  acc = fmaf(vget(c.w, 3), x, acc);
   return Act<T>::round(silu_f(Act<T>::round(acc)));
 }
 
+// A uniform value read through the constant address space, which the compiler
+// serves with a scalar load (for buffers the launch does not write, or words
+// it writes only after the read).
+typedef const float __attribute__((address_space(4)))* cfloat_ptr;
+typedef const int __attribute__((address_space(4)))* cint_ptr;
+typedef const unsigned __attribute__((address_space(4)))* cu32_ptr;
+__device__ __forceinline__ float uniform_load(const float* p) { return *(cfloat_ptr)p; }
+__device__ __forceinline__ int uniform_load(const int* p) { return *(cint_ptr)p; }
+__device__ __forceinline__ unsigned uniform_load(const unsigned* p) { return *(cu32_ptr)p; }
+// element i of an activation buffer at a uniform index; bf16 through the
+// aligned 32-bit word that holds it (allocations are 4-byte aligned and
+// padded, so the word stays inside the buffer's allocation)
+__device__ __forceinline__ float uniform_act(const float* p, long i) { return uniform_load(p + i); }
+__device__ __forceinline__ float uniform_act(const bf16_t* p, long i) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(p + i);
+  const unsigned w = *(cu32_ptr)(a & ~3ull);
+  return bf16_to_f32(static_cast<uint16_t>((a & 2) ? (w >> 16) : (w & 0xffffu)));
+}
+
+// Hides a value's origin from the optimiser, so that work on it is not moved
+// up to where it was loaded.
+__device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void opaque(bf16_t& v) {
+  unsigned u = v.bits;
+  asm volatile("" : "+v"(u));
+  v.bits = static_cast<uint16_t>(u);
+}
+
+// v + the value of lane l ^ 16, in every lane: v_permlane16_swap exchanges the
+// odd 16-lane rows of one copy with the even rows of another.
+__device__ __forceinline__ float rows_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// the value of lane l ^ 32
+__device__ __forceinline__ float halves_swap(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+// v + the value of lane l ^ 32, in every lane, without LDS: v_permlane32_swap
+// exchanges the upper half of one copy with the lower half of another.
+__device__ __forceinline__ float halves_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <typename T>
-__device__ __forceinline__ float conv_channel(const DnDecodeArgs<T>& A, int b, int ch, int pos, bool write_ring) {
-  const int K = A.K;
-  const T* w = A.conv_w + (long)ch * K;
-  T* ring = A.ring + ((long)b * A.conv_dim + ch) * K;
-  const float x = Act<T>::load(A.qkv, (long)b * A.conv_dim + ch);
+__device__ __forceinline__ float conv_channel(T* ring_all, const T* conv_w, const T* qkv, int conv_dim, int K, int b,
+                                              int ch, int pos, bool write_ring) {
+  const T* w = conv_w + (long)ch * K;
+  T* ring = ring_all + ((long)b * conv_dim + ch) * K;
+  const float x = Act<T>::load(qkv, (long)b * conv_dim + ch);
   float acc = 0.f;
   for (int j = 0; j < K - 1; ++j) {
     int slot = (pos - (K - 1) + j) % K;
@@ -109,60 +154,94 @@ __device__ __forceinline__ float conv_channel(const DnDecodeArgs<T>& A, int b, i
   return Act<T>::round(silu_f(y));
 }
 
-// grid: batch * hv * DN_SLICES workgroups of DN_NT threads; workgroup (b, h, s)
-// owns columns 32s..32s+31. Thread t holds rows t/8 + 32k (k = 0..3) of
-// columns 32s + 4(t%8)..+3: a wave reads 8 whole rows' lines per load.
+// grid: (hv * DN_SLICES, batch) workgroups of DN_DEC_NT threads; workgroup
+// (h, s) of sequence b owns columns 32 s .. 32 s + 31 of head h (the 4 slices
+// of a head on one XCD). Thread t holds rows t / 8 + 32 i (i = 0..3), columns
+// 32 s + 4 (t % 8) .. + 3, four 16-byte loads: a wave reads 8 rows' 128-byte
+// lines per load. Four waves start together (a larger workgroup's waves start
+// in groups of four, about 0.1 us apart).
+//
+// The arguments are separate scalars, not a struct, so that the first 14
+// dwords (the pointers and sizes the first loads need, up to z) are preloaded
+// into scalar registers at wave start instead of being read from the argument
+// buffer (the library is built with kernel-argument preloading); geo packs
+// hv | n_k_heads << 8 | K << 16.
 template <typename T>
-__global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
-  const int s = blockIdx.x % DN_SLICES;
-  const int h = (blockIdx.x / DN_SLICES) % A.hv;
-  const int b = blockIdx.x / (DN_SLICES * A.hv);
-  const int hk = h % A.hk;
+__global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
+    float* state, const T* qkv, T* ring, const T* conv_w, unsigned geo, unsigned hk_magic, const int* positions,
+    const T* z, const float* norm_w, const T* ga, const T* gb, const float* a_neg_p, const float* dt_bias_p, T* out,
+    unsigned* sync, float eps) {
+  const int hv = geo & 0xff, n_hk = (geo >> 8) & 0xff, K = geo >> 16;
+  const int conv_dim = (2 * n_hk + hv) * DN_D;
+  const int wg = xcd_remap(blockIdx.x, hv * DN_SLICES);
+  const int s = wg & (DN_SLICES - 1), h = wg / DN_SLICES, b = blockIdx.y;
+  const int hk = h - (int)__umulhi((unsigned)h, hk_magic) * n_hk;   // h % n_hk, no division
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int c8 = tid & 7, r = tid >> 3;
+  const int c4 = tid & 7, r = tid >> 3;
   const int col0 = s * DN_DCOLS;
-  constexpr int NW = DN_NT / 64;
+  constexpr int NW = DN_DEC_NT / 64;          // waves: 4
+  constexpr int RPT = DN_D * 8 / DN_DEC_NT;   // rows per thread: 4
+  constexpr int RSTEP = DN_DEC_NT / 8;        // 32
 
   QM_PHASE_DECL
   QM_PHASE(0);
   __shared__ float s_q[DN_D], s_k[DN_D], s_v[DN_DCOLS];
-  __shared__ float s_red[NW][2 * DN_DCOLS];
-  __shared__ __attribute__((aligned(16))) float s_delta[DN_DCOLS];
-  __shared__ float s_w3[2][3];
+  __shared__ float4 s_red[NW][2][DN_DCOLS / 4];   // per wave: the columns' pred and qd partial sums
+  __shared__ float4 s_delta[DN_DCOLS / 4];
   __shared__ float s_scal[2];
 
-  // ---- loads, all issued before any is used: the conv inputs of q/k channel
-  // t (and of v column t < 32), the position, the gates, z, the norm weight,
-  // the state columns and last the generation word (needed last)
-  unsigned* line = A.sync + (long)(b * A.hv + h) * DN_SYNC_WORDS;
-  unsigned long long* shares = reinterpret_cast<unsigned long long*>(line) + DN_SHARE0;
-  const int key_dim = A.hk * DN_D;
+  // ---- loads, all issued before any is used and none converted before the
+  // last is issued: the conv inputs of the head's q and k channels (thread t
+  // takes channel t), the state, the conv inputs of the slice's 32 v channels,
+  // z and the norm weight of the slice's columns (wave 0), the position, the
+  // gates and the head's generation word by scalar loads (uniform).
+  const int wv = __builtin_amdgcn_readfirstlane(wid);
+  const int key_dim = n_hk * DN_D;
   const int ch_qk = tid < DN_D ? hk * DN_D + tid : key_dim + hk * DN_D + (tid - DN_D);
-  const int jt = tid & (DN_DCOLS - 1);
-  const int ch_v = 2 * key_dim + h * DN_D + col0 + jt;
-  const bool k4 = A.K == 4;
+  const int ch_v = 2 * key_dim + h * DN_D + col0 + (lane & (DN_DCOLS - 1));
+  const bool k4 = K == 4;
   ConvIn<T> cin_qk, cin_v;
-  if (k4) {
-    cin_qk = conv_load4(A, b, ch_qk);
-    cin_v = conv_load4(A, b, ch_v);
-  }
-  const int pos = A.positions[b];
-  const float gate_b = Act<T>::load(A.b, (long)b * A.hv + h), gate_a = Act<T>::load(A.a, (long)b * A.hv + h);
-  const float a_neg = A.a_neg[h], dtb = A.dt_bias[h];
-  const float zv = Act<T>::load(A.z, (long)b * A.hv * DN_D + h * DN_D + col0 + jt);
-  const float nw = A.norm_w[col0 + jt];
-  float4* S = reinterpret_cast<float4*>(A.state + ((long)(b * A.hv + h) * DN_D) * DN_D) + col0 / 4 + c8;
-  float4 st4[4];
+  if (k4) cin_qk = conv_load4(ring, conv_w, qkv, conv_dim, b, ch_qk);
+  const long head_off = (long)(b * hv + h) * DN_D * DN_D;
+  const float4* S = reinterpret_cast<const float4*>(state + head_off) + col0 / 4 + c4;
+  float4 st[RPT];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) st4[k] = S[(r + 32 * k) * (DN_D / 4)];
-  const unsigned gen = ld_flag(line);
+  for (int i = 0; i < RPT; ++i) st[i] = S[(r + RSTEP * i) * (DN_D / 4)];
+  QM_PHASE(12);
+  T zr{};
+  float nw = 0.f;
+  if (wv == 0) {
+    if (k4) cin_v = conv_load4(ring, conv_w, qkv, conv_dim, b, ch_v);
+    zr = z[(long)b * hv * DN_D + h * DN_D + col0 + (lane & (DN_DCOLS - 1))];
+    nw = norm_w[col0 + (lane & (DN_DCOLS - 1))];
+  }
+  const int pos = uniform_load(positions + b);
+  const float gate_b = uniform_act(gb, (long)b * hv + h), gate_a = uniform_act(ga, (long)b * hv + h);
+  const float a_neg = uniform_load(a_neg_p + h), dtb = uniform_load(dt_bias_p + h);
+  unsigned* line = sync + (long)(b * hv + h) * DN_SYNC_WORDS;
+  unsigned long long* shares = reinterpret_cast<unsigned long long*>(line) + DN_SHARE0;
+  // the generation word by a scalar load: it was last written in an earlier
+  // launch, and this launch's slice 0 writes it only after every slice of the
+  // head has published its share (so after this read)
+  const unsigned gen = uniform_load(line);
+  QM_PHASE(6);
 
-  // ---- conv: q/k channel t (one writer of each q/k channel's ring slot: the
-  // first slice of the head with h == hk), v column t < 32; then the gates
+  // ---- conv of the q/k channels and the slice's v channels (the q/k ring
+  // slots have one writer: slice 0 of the value head h == hk). With K = 4 the
+  // ring stores wait for the end: stores and loads share one in-order
+  // counter, so a store issued here would hold up the wait for the state.
   const bool qk_writer = h == hk && s == 0;
-  const float y_qk = k4 ? conv_finish4(A, cin_qk, b, ch_qk, pos, qk_writer) : conv_channel(A, b, ch_qk, pos, qk_writer);
-  (tid < DN_D ? s_q[tid] : s_k[tid - DN_D]) = y_qk;
-  if (tid < DN_DCOLS) s_v[tid] = k4 ? conv_finish4(A, cin_v, b, ch_v, pos, true) : conv_channel(A, b, ch_v, pos, true);
+  {
+    const float y = k4 ? conv_finish4(cin_qk, pos)
+                       : conv_channel(ring, conv_w, qkv, conv_dim, K, b, ch_qk, pos, qk_writer);
+    if (tid < DN_D) s_q[tid] = y; else s_k[tid - DN_D] = y;
+  }
+  if (wv == 0) {
+    const float y = k4 ? conv_finish4(cin_v, pos)
+                       : conv_channel(ring, conv_w, qkv, conv_dim, K, b, ch_v, pos, lane < DN_DCOLS);
+    QM_PHASE(7);
+    if (lane < DN_DCOLS) s_v[lane] = y;
+  }
   if (tid == 0) {
     s_scal[0] = Act<T>::round(sigmoid_f(gate_b));
     s_scal[1] = expf(a_neg * softplus_f(gate_a + dtb));
@@ -170,92 +249,88 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
   __syncthreads();
 
   QM_PHASE(1);
-  // ---- l2 norms of q and k and their dot product: waves 0-1 hold the 128 channels
-  if (tid < DN_D) {
-    const float qv = s_q[tid], kv = s_k[tid];
-    const float a0 = wave_sum(qv * qv), a1 = wave_sum(kv * kv), a2 = wave_sum(qv * kv);
-    if (lane == 0) { s_w3[wid][0] = a0; s_w3[wid][1] = a1; s_w3[wid][2] = a2; }
-  }
-  __syncthreads();
-  const float sq = s_w3[0][0] + s_w3[1][0], sk = s_w3[0][1] + s_w3[1][1], sqk = s_w3[0][2] + s_w3[1][2];
+  // ---- l2 norms of q and k and their dot product, computed by every wave
+  // (lane l holds channels l and l + 64): no further barrier
+  const float q0 = s_q[lane], q1 = s_q[lane + 64], k0 = s_k[lane], k1 = s_k[lane + 64];
+  const float sq = wave_sum(fmaf(q1, q1, q0 * q0));
+  const float sk = wave_sum(fmaf(k1, k1, k0 * k0));
+  const float sqk = wave_sum(fmaf(q1, k1, q0 * k0));
   const float rq = rsqrt_rn(sq + 1e-6f), rk = rsqrt_rn(sk + 1e-6f);
   const float sqrt_d = 11.313708498984761f;
   const float qk = div_rn(sqk * rq * rk, sqrt_d);       // q^ . k^
 
   QM_PHASE(2);
-  // ---- decay, then per column pred = S^T k^ and qd = S^T q^ over the rows
+  // ---- decay, then per column pred = S^T k^ and qd = S^T q^: a thread adds
+  // its 4 rows in order, the 8 rows of a wave's load are added across lanes
+  // (DPP within rows of 16 lanes, then swaps of row pairs and halves), the 4
+  // waves through LDS
   const float decay = s_scal[1];
-  float st[4][4], kr[4], pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
+  float kr[RPT];
+  float p[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int row = r + 32 * k;
-    kr[k] = mul_rn(s_k[row], rk);
+  for (int i = 0; i < RPT; ++i) {
+    const int row = r + RSTEP * i;
+    kr[i] = mul_rn(s_k[row], rk);
     const float qr = div_rn(mul_rn(s_q[row], rq), sqrt_d);
-    st[k][0] = st4[k].x * decay; st[k][1] = st4[k].y * decay;
-    st[k][2] = st4[k].z * decay; st[k][3] = st4[k].w * decay;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      pk[c] = fmaf(st[k][c], kr[k], pk[c]);
-      pq[c] = fmaf(st[k][c], qr, pq[c]);
-    }
+    st[i].x *= decay; st[i].y *= decay; st[i].z *= decay; st[i].w *= decay;
+    p[0] = fmaf(st[i].x, kr[i], p[0]); p[1] = fmaf(st[i].y, kr[i], p[1]);
+    p[2] = fmaf(st[i].z, kr[i], p[2]); p[3] = fmaf(st[i].w, kr[i], p[3]);
+    p[4] = fmaf(st[i].x, qr, p[4]); p[5] = fmaf(st[i].y, qr, p[5]);
+    p[6] = fmaf(st[i].z, qr, p[6]); p[7] = fmaf(st[i].w, qr, p[7]);
   }
-  // the 8 lanes of one c8 in a wave: lane ^ 8 within a 16-lane row (rotation
-  // by 8), then across the rows
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    pk[c] += dpp_f<0x128>(pk[c]);
-    pk[c] = xor32_sum(xor16_sum(pk[c]));
-    pq[c] += dpp_f<0x128>(pq[c]);
-    pq[c] = xor32_sum(xor16_sum(pq[c]));
-  }
+  for (int i = 0; i < 8; ++i) p[i] = halves_sum(rows_sum(p[i] + dpp_f<0x128>(p[i])));   // row_ror:8
+  QM_PHASE(9);
   if (lane < 8) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      s_red[wid][4 * lane + c] = pk[c];
-      s_red[wid][DN_DCOLS + 4 * lane + c] = pq[c];
-    }
+    s_red[wid][0][lane] = make_float4(p[0], p[1], p[2], p[3]);
+    s_red[wid][1][lane] = make_float4(p[4], p[5], p[6], p[7]);
   }
+  QM_PHASE(10);
   __syncthreads();
 
   QM_PHASE(3);
-  // ---- delta and o of the 32 columns (wave 0, lanes 0-31); their share of the
-  // head's sum of squares leaves at once
+  // ---- delta and o of the 32 columns (wave 0: lanes 0-31 add pred, lanes
+  // 32-63 qd, over the 4 waves), the slice's share of the head's sum of
+  // squares of o published with the launch's generation number
   float o = 0.f;
-  if (tid < DN_DCOLS) {
-    float pred = 0.f, qd = 0.f;
+  if (wv == 0) {
+    const float* red = reinterpret_cast<const float*>(s_red);
+    const int half = lane >> 5, col = lane & (DN_DCOLS - 1);
+    float acc = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) { pred += s_red[w][tid]; qd += s_red[w][DN_DCOLS + tid]; }
-    const float delta = (s_v[tid] - pred) * s_scal[0];
-    s_delta[tid] = delta;
-    o = Act<T>::round(fmaf(qk, delta, qd));
-  }
-  if (wid == 0) {
-    const float ss = xor16_sum(row16_sum(tid < DN_DCOLS ? o * o : 0.f));
+    for (int w = 0; w < NW; ++w) acc += red[(w * 2 + half) * DN_DCOLS + col];
+    const float pred = acc, qd = halves_swap(acc);     // lanes 0-31 receive qd
+    const float delta = (s_v[col] - pred) * s_scal[0];
+    if (lane < DN_DCOLS) reinterpret_cast<float*>(s_delta)[lane] = delta;
+    o = lane < DN_DCOLS ? Act<T>::round(fmaf(qk, delta, qd)) : 0.f;
+    const float ss = wave_sum(o * o);
     if (lane == 0) {
       const unsigned long long word = ((unsigned long long)(gen + 1) << 32) | __float_as_uint(ss);
-      raise_word(shares + s, word);
+      __hip_atomic_store(shares + s, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   __syncthreads();
 
   QM_PHASE(4);
-  // ---- rank-1 update and write-back of the columns, written through to the
-  // point of coherence: no dirty state lines are left in L2 for the end of
-  // the kernel to write back (0.35 µs less per launch)
+  // ---- rank-1 update and write-back of the slice, written through to the
+  // point of coherence (no dirty state lines are left in L2 for the end of
+  // the kernel), and the deferred ring stores
   {
-    const float4 dl = *reinterpret_cast<const float4*>(s_delta + 4 * c8);
-    const __amdgpu_buffer_rsrc_t rs = dev_rsrc(A.state + ((long)(b * A.hv + h) * DN_D) * DN_D, DN_D * DN_D * 4);
+    const float4 dl = s_delta[c4];
+    const __amdgpu_buffer_rsrc_t rsrc = dev_rsrc(state + head_off, DN_D * DN_D * 4);
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      st_dev4(rs, ((r + 32 * k) * DN_D + col0 + 4 * c8) * 4,
-              make_float4(fmaf(kr[k], dl.x, st[k][0]), fmaf(kr[k], dl.y, st[k][1]), fmaf(kr[k], dl.z, st[k][2]),
-                          fmaf(kr[k], dl.w, st[k][3])));
+    for (int i = 0; i < RPT; ++i)
+      st_dev4(rsrc, ((r + RSTEP * i) * DN_D + col0 + 4 * c4) * 4,
+              make_float4(fmaf(kr[i], dl.x, st[i].x), fmaf(kr[i], dl.y, st[i].y), fmaf(kr[i], dl.z, st[i].z),
+                          fmaf(kr[i], dl.w, st[i].w)));
   }
+  if (k4 && qk_writer) ring[((long)b * conv_dim + ch_qk) * 4 + (pos & 3)] = cin_qk.x;
+  if (k4 && wv == 0 && lane < DN_DCOLS) ring[((long)b * conv_dim + ch_v) * 4 + (pos & 3)] = cin_v.x;
 
   QM_PHASE(5);
-  // ---- the head's sum of squares from its shares (one line, polled by wave
-  // 0), then the gated RMS norm of the 32 columns
-  if (wid == 0) {
+  // ---- the head's sum of squares from its 4 shares (one line, polled by
+  // wave 0), then the gated RMS norm of the 32 columns
+  if (wv == 0) {
     float ss_all = 0.f;
     bool done = false;
     for (int it = 0; it < FLAG_SPIN_MAX && !done; ++it) {
@@ -273,16 +348,18 @@ __global__ __launch_bounds__(DN_NT) void dn_decode_kernel(DnDecodeArgs<T> A) {
     }
     // a wait that gave up counts itself (qm_dn_decode_check) and leaves NaN,
     // never an output normalised by a partial sum
-    QM_PHASE(6);
+    QM_PHASE(8);
     if (!done && lane == 0) __hip_atomic_fetch_add(line + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (s == 0 && lane == 0) st_flag(line, gen + 1);
-    if (tid < DN_DCOLS) {
-      const float rn = rsqrt_rn(ss_all / (float)DN_D + A.eps);
-      const float y = (nw * (o * rn)) * sigmoid_f(zv);
-      Act<T>::store(A.out, (long)b * A.hv * DN_D + h * DN_D + col0 + tid, done ? y : __builtin_nanf(""));
+    if (lane < DN_DCOLS) {
+      T zv = zr;
+      opaque(zv);    // converted here, not where it is loaded (that would wait for the load there)
+      const float rn = rsqrt_rn(ss_all / (float)DN_D + eps);
+      const float y = (nw * (o * rn)) * sigmoid_f(Act<T>::load(&zv, 0));
+      Act<T>::store(out, (long)b * hv * DN_D + h * DN_D + col0 + lane, done ? y : __builtin_nanf(""));
     }
   }
-  QM_PHASE(7);
+  QM_PHASE(11);
   QM_PHASE_FLUSH();
 }
 
@@ -404,19 +481,13 @@ int launch_dn_decode(const qm_dn_geom* g, const void* qkv, const void* z, const 
                      const float* a_neg, const float* dt_bias, const void* conv_w, const float* norm_w,
                      const int* positions, void* conv_ring, float* state, void* out, void* ws,
                      hipStream_t stream) {
-  DnDecodeArgs<T> A;
-  A.qkv = static_cast<const T*>(qkv); A.z = static_cast<const T*>(z);
-  A.a = static_cast<const T*>(a); A.b = static_cast<const T*>(b);
-  A.a_neg = a_neg; A.dt_bias = dt_bias;
-  A.conv_w = static_cast<const T*>(conv_w); A.norm_w = norm_w;
-  A.positions = positions;
-  A.ring = static_cast<T*>(conv_ring); A.state = state; A.out = static_cast<T*>(out);
-  A.batch = g->batch; A.hv = g->n_v_heads; A.hk = g->n_k_heads;
-  A.conv_dim = 2 * g->n_k_heads * DN_D + g->n_v_heads * DN_D;
-  A.K = g->conv_kernel; A.eps = g->eps;
-  A.sync = static_cast<unsigned*>(ws);
-  const int nwg = g->batch * g->n_v_heads * DN_SLICES;
-  hipLaunchKernelGGL(dn_decode_kernel<T>, dim3(nwg), dim3(DN_NT), 0, stream, A);
+  const unsigned geo = (unsigned)g->n_v_heads | ((unsigned)g->n_k_heads << 8) | ((unsigned)g->conv_kernel << 16);
+  const unsigned hk_magic = (unsigned)((0x100000000ull + g->n_k_heads - 1) / g->n_k_heads);
+  hipLaunchKernelGGL(dn_decode_kernel<T>, dim3(g->n_v_heads * DN_SLICES, g->batch), dim3(DN_DEC_NT), 0, stream,
+                     state, static_cast<const T*>(qkv), static_cast<T*>(conv_ring), static_cast<const T*>(conv_w),
+                     geo, hk_magic, positions, static_cast<const T*>(z), norm_w, static_cast<const T*>(a),
+                     static_cast<const T*>(b), a_neg, dt_bias, static_cast<T*>(out), static_cast<unsigned*>(ws),
+                     g->eps);
   QM_CHECK_LAUNCH();
   return QM_OK;
 }
@@ -440,8 +511,8 @@ int launch_dn_recurrent(int batch, int seq, int heads, int hk, long q_stride, lo
 QM_PHASE_ENTRY(dn)
 
 extern "C" size_t qm_dn_decode_workspace(int batch, int n_v_heads, int head_dim) {
-  // one 128-byte line per (sequence, head): generation word and the shares of
-  // the gated norm's sum of squares
+  // one 128-byte line per (sequence, head): generation word, give-up counter
+  // and the shares of the gated norm's sum of squares
   if (batch <= 0 || n_v_heads <= 0 || head_dim <= 0) return 0;
   return qm_align256((size_t)batch * n_v_heads * DN_SYNC_WORDS * sizeof(unsigned));
 }
@@ -474,6 +545,8 @@ extern "C" int qm_dn_decode(const qm_dn_geom* g, const void* qkv, const void* z,
   if (g->head_dim != DN_D) return qm_fail(QM_ERR_UNSUPPORTED, "qm_dn_decode: head_dim must be 128");
   if (g->batch <= 0 || g->n_v_heads <= 0 || g->n_k_heads <= 0 || g->n_v_heads % g->n_k_heads)
     return qm_fail(QM_ERR_ARG, "qm_dn_decode: need batch > 0 and n_v_heads a multiple of n_k_heads");
+  if (g->n_v_heads > 255 || g->n_k_heads > 255 || g->batch > 65535)
+    return qm_fail(QM_ERR_UNSUPPORTED, "qm_dn_decode: n_v_heads and n_k_heads must be below 256, batch below 65536");
   if (g->conv_kernel < 2 || g->conv_kernel > 8) return qm_fail(QM_ERR_ARG, "qm_dn_decode: conv_kernel must be 2..8");
   if (!qkv || !z || !a || !b || !a_neg || !dt_bias || !conv_w || !norm_w || !positions || !conv_ring || !state || !out)
     return qm_fail(QM_ERR_ARG, "qm_dn_decode: null tensor pointer");

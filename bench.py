@@ -203,28 +203,71 @@ def time_graph_steps(instances, steps, warmup):
 
 
 def time_kernels(instances, reps, stream_obj, batches=5):
-    """Average duration of each entry point's launches: HIP events on the launch
-    stream around `reps` back-to-back launches (rotating over the instances),
-    divided by `reps`; the median over `batches` batches. A pair of events
-    around every single launch would add the events' own cost to each."""
+    """Average duration of each entry point's launches: `reps` back-to-back
+    launches (rotating over the instances) captured in one HIP graph, replayed
+    `batches` times between HIP events on the launch stream, divided by
+    `reps`; the median over the replays. A graph keeps the host's launch cost
+    (about 5 us per launch from Python) out of the figure."""
     import torch
     n = len(instances)
-    s = stream_obj.cuda_stream
-    parts = {"qsa_decode": lambda x: x.qsa.decode(x.qg, x.k, x.v, x.iq, x.ik, s),
-             "dn_decode": lambda x: x.dn.run(x.qkv, x.z, x.a, x.b, s)}
+    parts = {"qsa_decode": lambda x, s: x.qsa.decode(x.qg, x.k, x.v, x.iq, x.ik, s),
+             "dn_decode": lambda x, s: x.dn.run(x.qkv, x.z, x.a, x.b, s)}
+    side = torch.cuda.Stream()
     out = {}
     for name, fn in parts.items():
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                for i in range(reps):
+                    fn(instances[i % n], side.cuda_stream)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
         per = []
-        for _ in range(batches):
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record(stream_obj)
-            for i in range(reps):
-                fn(instances[i % n])
-            end.record(stream_obj)
-            torch.cuda.synchronize()
-            per.append(start.elapsed_time(end) * 1000.0 / reps)     # microseconds per launch
+        with torch.cuda.stream(stream_obj):
+            for _ in range(batches):
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream_obj)
+                g.replay()
+                end.record(stream_obj)
+                torch.cuda.synchronize()
+                per.append(start.elapsed_time(end) * 1000.0 / reps)     # microseconds per launch
         out[name] = statistics.median(per)
+        del g
     return out
+
+
+def time_cold(instances, fn, flush_mb=768, launches=4, reps=20):
+    """Average duration of `launches` back-to-back launches that start after
+    `flush_mb` of other data has streamed through the caches (so their inputs
+    come from HBM): a graph of [flush, launches] minus a graph of [flush]."""
+    import torch
+    big = torch.ones(flush_mb << 18, device=instances[0].qkv.device, dtype=torch.float32)
+    side = torch.cuda.Stream()
+
+    def replay_us(body):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                body(side.cuda_stream)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            g.replay()
+            end.record()
+            torch.cuda.synchronize()
+            ts.append(start.elapsed_time(end) * 1000.0)
+        del g
+        return statistics.median(ts)
+
+    flush = replay_us(lambda s: big.mul_(1.0))
+    both = replay_us(lambda s: (big.mul_(1.0), [fn(instances[i % len(instances)], s) for i in range(launches)]))
+    del big
+    return (both - flush) / launches
 
 
 def host_cpu() -> dict:
@@ -405,6 +448,9 @@ def run_decode(qm, dev, pos, steps, warmup, instances=0, graphs=True):
     torch.cuda.synchronize()
     sec = time_steps(insts, steps, warmup, stream.cuda_stream)
     kern = time_kernels(insts, max(50, min(steps, 400)), stream)
+    # the DeltaNet launches alone rotate less than the Infinity Cache holds:
+    # also their duration with the state in HBM only
+    kern["dn_decode_hbm"] = time_cold(insts, lambda x, s: x.dn.run(x.qkv, x.z, x.a, x.b, s))
     gsec = time_graph_steps(insts, steps, warmup) if graphs else None
     del insts
     torch.cuda.synchronize()

@@ -142,6 +142,11 @@ __device__ __forceinline__ void raise_flag(unsigned* p, unsigned v) {
   const unsigned old = __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   asm volatile("" ::"v"(old));
 }
+// The same atomic, not waited for: the flag reaches the point of coherence as
+// soon, while the wave goes on (its own later loads of the flag see it).
+__device__ __forceinline__ void post_flag(unsigned* p, unsigned v) {
+  (void)__hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ void raise_word(unsigned long long* p, unsigned long long v) {
   const unsigned long long old = __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   asm volatile("" ::"v"(old));
@@ -205,10 +210,22 @@ __device__ __forceinline__ float row16_max(float v) {
 }
 // v(lane) + v(lane ^ 32) and v(lane) + v(lane ^ 16), in every lane (a single
 // cross-row step each, so one ds_bpermute is cheap enough)
-__device__ __forceinline__ float xor32_sum(float v) { return v + __shfl_xor(v, 32, 64); }
-__device__ __forceinline__ float xor16_sum(float v) { return v + __shfl_xor(v, 16, 64); }
-__device__ __forceinline__ float xor32_max(float v) { return fmaxf(v, __shfl_xor(v, 32, 64)); }
-__device__ __forceinline__ float xor16_max(float v) { return fmaxf(v, __shfl_xor(v, 16, 64)); }
+// the value of lane l ^ 32 / l ^ 16, by v_permlane32_swap / v_permlane16_swap
+// of two copies (VALU, no LDS): the 32-lane swap exchanges the upper half of
+// one copy with the lower half of the other, the 16-lane swap its odd 16-lane
+// rows with the other's even rows
+__device__ __forceinline__ float lane_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) { return v + lane_xor32(v); }
+__device__ __forceinline__ float xor16_sum(float v) { return v + lane_xor16(v); }
+__device__ __forceinline__ float xor32_max(float v) { return fmaxf(v, lane_xor32(v)); }
+__device__ __forceinline__ float xor16_max(float v) { return fmaxf(v, lane_xor16(v)); }
 // whole-wavefront sum / max, uniform result
 __device__ __forceinline__ float wave_sum(float v) {
   v = row16_sum(v);

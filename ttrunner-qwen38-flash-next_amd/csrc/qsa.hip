@@ -109,10 +109,10 @@ __device__ float norm_rope_row(float* s_x, float* s_y, float* s_scr, int n, cons
 template <int N>
 __device__ __forceinline__ float row_shl(float v) { return dpp_f<0x100 + N>(v); }
 
-__device__ __forceinline__ float xor32_f(float v) { return __shfl_xor(v, 32, 64); }
+__device__ __forceinline__ float xor32_f(float v) { return lane_xor32(v); }
 
 __device__ __forceinline__ float wave_rinv_finish(float s, float n, float eps) {
-  const float s16 = __shfl_down(s, 16, 64);
+  const float s16 = lane_xor16(s);    // lanes 0..7 read lanes 16..23
   const float c = add_rn(add_rn(add_rn(s, row_shl<8>(s)), s16), row_shl<8>(s16));   // lanes 0..7: c_l
   float tot = readlane_f(c, 0);
 #pragma unroll
@@ -139,6 +139,20 @@ __device__ __forceinline__ float wave_rinv(const float (&x)[K], float eps) {
 template <int K>
 __device__ __forceinline__ void wave_rope(float (&y)[K], int rope, const float (&cs)[2], const float (&sn)[2]) {
   const int lane = threadIdx.x & 63, half = rope >> 1;
+  if (rope == 64) {
+    // partner of element lane < 64 is lane ^ 32 of the same register; elements
+    // 64 and up are not rotated
+    const float yp = lane_xor32(y[0]);
+    y[0] = add_rn(mul_rn(y[0], cs[0]), mul_rn(lane < 32 ? -yp : yp, sn[0]));
+    return;
+  }
+  if (rope == 128) {
+    // partner of element lane + 64 k is element lane + 64 (1 - k): same lane
+    const float y0 = y[0], y1 = y[1];
+    y[0] = add_rn(mul_rn(y0, cs[0]), mul_rn(-y1, sn[0]));
+    y[1] = add_rn(mul_rn(y1, cs[1]), mul_rn(y0, sn[1]));
+    return;
+  }
   float out[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
@@ -2107,14 +2121,17 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) mx = fmaxf(mx, sv[i]);
   mx = xor32_max(xor16_max(mx));
-  bf16x8_t pf;
+  float pv[8];
   float lsum = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float pv = __expf(sv[i] - mx);
-    lsum += pv;
-    pf[i] = __builtin_bit_cast(__bf16, col < GQA ? f32_to_bf16(pv) : (uint16_t)0);
+    pv[i] = __expf(sv[i] - mx);
+    lsum += pv[i];
   }
+  u32x4_t pu;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pu[i] = col < GQA ? pack_bf16x2(pv[2 * i], pv[2 * i + 1]) : 0u;
+  const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, pu);
   lsum = xor32_sum(xor16_sum(lsum));
   QM_PHASE(12);
   if (cur) {
@@ -2148,8 +2165,8 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   if (col < GQA) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const unsigned lo = f32_to_bf16(o[i][0] * linv) | ((unsigned)f32_to_bf16(o[i][1] * linv) << 16);
-      const unsigned hi = f32_to_bf16(o[i][2] * linv) | ((unsigned)f32_to_bf16(o[i][3] * linv) << 16);
+      const unsigned lo = pack_bf16x2(o[i][0] * linv, o[i][1] * linv);
+      const unsigned hi = pack_bf16x2(o[i][2] * linv, o[i][3] * linv);
       st_dev_u32x2(ro, ((item * GQA + hcol) * QSA_D + 16 * (4 * wv + i) + 4 * quad) * 2, lo, hi);
     }
   }
@@ -2193,7 +2210,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   wait_all_memory();
   __syncthreads();
   QM_PHASE(8);
-  if (tid == 0) raise_flag(D.flags + (long)bg * dec_flag_stride(D.splits) + item, gen + 1);
+  if (tid == 0) post_flag(D.flags + (long)bg * dec_flag_stride(D.splits) + item, gen + 1);
   if (item < DEC_SLICES) decode_merge<WIDE>(D, sh, b, g, item, n_att, gen, overflow);
   QM_PHASE(10);
   QM_PHASE_FLUSH();

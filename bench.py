@@ -177,28 +177,33 @@ def time_steps(instances, steps, warmup, stream):
 
 
 def time_graph_steps(instances, steps, warmup):
-    """The same steps replayed from one HIP graph: the whole rotation (every
-    instance's step, three launches each) captured once, as a serving loop
-    captures a forward pass, then replayed until `steps` steps have run."""
+    """The same steps launched from HIP graphs, as a serving loop launches a
+    captured decode step: `warmup` steps, then exactly `steps` steps (step i
+    on instance i mod n, two launches each) captured in one graph whose single
+    replay is timed between synchronisations. The host's launch cost (about
+    5-10 us per launch from Python, which bounds the eager loop on some hosts)
+    stays out of the figure; the kernels and the gaps between them stay in."""
     import torch
     side = torch.cuda.Stream()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(side):
-        with torch.cuda.graph(g, stream=side):
-            for x in instances:
-                x.step(side.cuda_stream)
-    torch.cuda.synchronize()
     n = len(instances)
-    reps = max(1, round(steps / n))
-    for _ in range(max(1, warmup // n)):
-        g.replay()
+
+    def capture(count):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                for i in range(count):
+                    instances[i % n].step(side.cuda_stream)
+        return g
+
+    gw, g = capture(max(1, warmup)), capture(steps)
+    torch.cuda.synchronize()
+    gw.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(reps):
-        g.replay()
+    g.replay()
     torch.cuda.synchronize()
-    sec = (time.perf_counter() - t0) / (reps * n)
-    del g
+    sec = (time.perf_counter() - t0) / steps
+    del g, gw
     return sec
 
 
@@ -799,14 +804,17 @@ def main():
     head = run_decode(qm, dev, pos, args.steps, args.warmup, args.instances)
     max_ctx, n_inst, touched = head["max_ctx"], head["instances"], head["touched"]
     print(f"[bench] {n_inst} instances, {n_inst * touched / 1e6:.0f} MB touched per rotation", file=sys.stderr)
-    us_step = head["us_step"]
+    # the step as a serving loop runs it: launched from a captured graph (the
+    # eager loop's figure, bound by Python's launch cost on some hosts, is
+    # reported beside it)
+    us_step = head["graph_us_step"]
     sec = us_step * 1e-6
     kern = head["kernel_us"]
     bytes_step = touched
     kb = {"qsa_decode": qsa_bytes(pos), "dn_decode": DN_BYTES}
     dominant = max(kb, key=lambda k: kern[k])
     achieved = kb[dominant] / (kern[dominant] * 1e-6) / 1e9
-    print(f"[bench] step {us_step:.2f} us (graph replay {head['graph_us_step']:.2f} us); kernels (us): " +
+    print(f"[bench] step {us_step:.2f} us from a graph (eager launches {head['us_step']:.2f} us); kernels (us): " +
           ", ".join(f"{k} {v:.2f}" for k, v in kern.items()), file=sys.stderr)
     if args.copy_mb > 0:
         src = torch.ones(args.copy_mb << 20, dtype=torch.uint8, device=dev)
@@ -821,16 +829,17 @@ def main():
     if not args.head_only:
         # the decode step at the other positions of the benchmark's configurations
         for p in SWEEP_POSITIONS:
-            r = head if p == pos else run_decode(qm, dev, p, min(args.steps, 100), args.warmup, graphs=False)
+            r = head if p == pos else run_decode(qm, dev, p, min(args.steps, 100), args.warmup)
             qb = qsa_bytes(p)
             entry = {"workload": f"decode step at pos {p}" + (" (headline)" if p == pos else ""), "pos": p,
                      "selection": "on" if (p + 1) // 64 > 32 else "off (below the budget)",
-                     "us_per_token": round(r["us_step"], 3),
+                     "us_per_token": round(r["graph_us_step"], 3),
+                     "eager_us_per_token": round(r["us_step"], 3),
                      "qsa_us": round(r["kernel_us"]["qsa_decode"], 3), "dn_us": round(r["kernel_us"]["dn_decode"], 3),
                      "qsa_gbs": round(qb / (r["kernel_us"]["qsa_decode"] * 1e-6) / 1e9, 1),
                      "dn_gbs": round(DN_BYTES / (r["kernel_us"]["dn_decode"] * 1e-6) / 1e9, 1),
                      "step_mb": round((qb + DN_BYTES) / 1e6, 3),
-                     "step_hbm_frac": round((qb + DN_BYTES) / (r["us_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                     "step_hbm_frac": round((qb + DN_BYTES) / (r["graph_us_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
             if not args.no_cpu:
                 entry["cpu_baseline"] = cpu_baseline(p, args.cpu_seconds)
             configs.append(entry)
@@ -878,6 +887,8 @@ def main():
         "config": {"workload": f"QSA selection-on decode at pos {pos} (ctx {max_ctx}, top-32 of 64-token "
                                f"blocks) + one Gated DeltaNet decode step, batch 1",
                    "position": pos, "batch": 1, "instances_rotated": n_inst,
+                   "launch": "steps replayed from a captured HIP graph",
+                   "eager_us_per_step": round(head["us_step"], 3),
                    "step_bytes": bytes_step,
                    "step_hbm_frac": round(bytes_step / sec / 1e9 / HBM_PEAK_GBS, 4),
                    "kernel_us": {k: round(v, 3) for k, v in kern.items()}},

@@ -302,7 +302,9 @@ int qm_qsa_decode_check(const qm_qsa_geom* g, int splits, void* workspace, size_
  * (qm_qsa_decode_fits); positions whose items exceed `splits` are counted and
  * poisoned (qm_qsa_decode_check).
  *   out [B, Hq*d] act; ids [B, budget/ratio], n_sel [B], items, iq_out
- *   [B, idx_heads, idx_dim] are optional inspection outputs (may be NULL). */
+ *   [B, idx_heads, idx_dim] are optional inspection outputs (may be NULL);
+ *   ids lists the selected blocks in block order when at most 128 blocks are
+ *   eligible, in rank order otherwise (the items follow the same order). */
 int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k_new, const void* v_new, const void* iq,
                   const void* ik, const float* q_norm, const float* k_norm, const float* iq_norm,
                   const float* ik_norm, const float* cos, const float* sin, const int* positions,

@@ -27,22 +27,17 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-// round-to-nearest-even float32 -> bfloat16 (NaN kept quiet), branch-free
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t quiet = (u >> 16) | 0x40u;
-  return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
-}
-
 // Two floats to packed bf16 (a in the low half) with the hardware conversion
-// (round to nearest even, like f32_to_bf16 for every finite value): one
-// instruction where f32_to_bf16 takes several.
+// (v_cvt_pk_bf16_f32: round to nearest even; a NaN stays a quiet NaN): one
+// instruction where the integer rounding sequence takes six.
 typedef float f32x2_cvt_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_cvt_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ unsigned pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2_cvt_t{a, b}, bf16x2_cvt_t));
 }
+
+// round-to-nearest-even float32 -> bfloat16 (the hardware conversion)
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return static_cast<uint16_t>(pack_bf16x2(f, 0.f)); }
 
 // Activation element access: load as float, store with rounding to the type.
 template <typename T> struct Act;
@@ -57,6 +52,25 @@ template <> struct Act<bf16_t> {
   __device__ __forceinline__ static void store(bf16_t* p, long i, float v) { p[i].bits = f32_to_bf16(v); }
   __device__ __forceinline__ static float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 };
+
+// A uniform value read through the constant address space, which the compiler
+// serves with a scalar load (for buffers the launch does not write, or words
+// it writes only after the read).
+typedef const float __attribute__((address_space(4)))* cfloat_ptr;
+typedef const int __attribute__((address_space(4)))* cint_ptr;
+typedef const unsigned __attribute__((address_space(4)))* cu32_ptr;
+__device__ __forceinline__ float uniform_load(const float* p) { return *(cfloat_ptr)p; }
+__device__ __forceinline__ int uniform_load(const int* p) { return *(cint_ptr)p; }
+__device__ __forceinline__ unsigned uniform_load(const unsigned* p) { return *(cu32_ptr)p; }
+// element i of an activation buffer at a uniform index; bf16 through the
+// aligned 32-bit word that holds it (allocations are 4-byte aligned and
+// padded, so the word stays inside the buffer's allocation)
+__device__ __forceinline__ float uniform_act(const float* p, long i) { return uniform_load(p + i); }
+__device__ __forceinline__ float uniform_act(const bf16_t* p, long i) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(p + i);
+  const unsigned w = *(cu32_ptr)(a & ~3ull);
+  return bf16_to_f32(static_cast<uint16_t>((a & 2) ? (w >> 16) : (w & 0xffffu)));
+}
 
 // Non-contracting float ops: each rounds once, like a CPU SIMD mul/add. hipcc
 // compiles with -ffp-contract=fast, and __fmul_rn/__fadd_rn are plain operators,
@@ -117,6 +131,9 @@ __device__ __forceinline__ void st_dev_u32x2(__amdgpu_buffer_rsrc_t r, int byte_
 }
 __device__ __forceinline__ float2 ld_dev2(__amdgpu_buffer_rsrc_t r, int byte_off) {
   return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, CPOL_DEVICE));
+}
+__device__ __forceinline__ u32x4_t ld_dev_u32x4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, CPOL_DEVICE));
 }
 __device__ __forceinline__ void st_dev(__amdgpu_buffer_rsrc_t r, int byte_off, float v) {
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, byte_off, 0, CPOL_DEVICE);

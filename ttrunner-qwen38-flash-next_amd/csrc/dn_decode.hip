@@ -89,25 +89,6 @@ __device__ __forceinline__ float conv_finish4(const ConvIn<T>& c, int pos) {
   return Act<T>::round(silu_f(Act<T>::round(acc)));
 }
 
-// A uniform value read through the constant address space, which the compiler
-// serves with a scalar load (for buffers the launch does not write, or words
-// it writes only after the read).
-typedef const float __attribute__((address_space(4)))* cfloat_ptr;
-typedef const int __attribute__((address_space(4)))* cint_ptr;
-typedef const unsigned __attribute__((address_space(4)))* cu32_ptr;
-__device__ __forceinline__ float uniform_load(const float* p) { return *(cfloat_ptr)p; }
-__device__ __forceinline__ int uniform_load(const int* p) { return *(cint_ptr)p; }
-__device__ __forceinline__ unsigned uniform_load(const unsigned* p) { return *(cu32_ptr)p; }
-// element i of an activation buffer at a uniform index; bf16 through the
-// aligned 32-bit word that holds it (allocations are 4-byte aligned and
-// padded, so the word stays inside the buffer's allocation)
-__device__ __forceinline__ float uniform_act(const float* p, long i) { return uniform_load(p + i); }
-__device__ __forceinline__ float uniform_act(const bf16_t* p, long i) {
-  const unsigned long long a = reinterpret_cast<unsigned long long>(p + i);
-  const unsigned w = *(cu32_ptr)(a & ~3ull);
-  return bf16_to_f32(static_cast<uint16_t>((a & 2) ? (w >> 16) : (w & 0xffffu)));
-}
-
 // Hides a value's origin from the optimiser, so that work on it is not moved
 // up to where it was loaded.
 __device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }

@@ -132,6 +132,20 @@ __device__ __forceinline__ float wave_rinv(const float (&x)[K], float eps) {
   return wave_rinv_finish(s, 64.f * K, eps);
 }
 
+// 1/sqrt(mean(x^2) + eps) of a 256-wide row held as x[k] = element lane + 64 k,
+// for the attention query heads, whose rounding the attention's tolerance
+// absorbs: fused multiply-adds, a lane tree and the hardware reciprocal square
+// root (the rows whose bits are kept, the indexer's and the appended key, use
+// wave_rinv)
+__device__ __forceinline__ float wave_rinv_fast(const float (&x)[4], float eps) {
+  float s = x[0] * x[0];
+  s = fmaf(x[1], x[1], s);
+  s = fmaf(x[2], x[2], s);
+  s = fmaf(x[3], x[3], s);
+  s = xor32_sum(xor16_sum(row16_sum(s)));
+  return __builtin_amdgcn_rsqf(s * (1.0f / 256.0f) + eps);
+}
+
 // rope of a normed row held as y[k] = element lane + 64 k: element e < rope
 // becomes y_e cos + (e < rope/2 ? -y_p : y_p) sin, p = e +- rope/2 (the
 // partner's normed value, from lane p % 64 of register p / 64); every multiply
@@ -499,6 +513,55 @@ __device__ __forceinline__ float4 row16_dots(const float (&q)[4][8], const float
   return make_float4(p[0], p[1], p[2], p[3]);
 }
 
+// The top-k of at most 128 eligible blocks of one query row (ties to the lower
+// index) from their dot products in dsc, written to sel[0 .. topk) in block
+// order, by one wave: it forms the 128 keys in registers (lane l: blocks l and
+// 64 + l; zero past n_elig), finds the score bits t of the top-k-th largest key
+// by a bitwise search over ballot counts (the largest t with at least topk
+// keys' scores at or above it), keeps every block scored above t and, of those
+// scored exactly t, the lowest indices until there are topk, and places each
+// kept block by the count of kept blocks below it.
+__device__ __forceinline__ void select_from_dsc(const float4* dsc, int n_elig, int idx_heads, int topk, int* sel) {
+  const int lane = threadIdx.x & 63;
+  const float4 dd[2] = {dsc[lane], dsc[64 + lane]};
+  unsigned hk[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const float dv[4] = {dd[r].x, dd[r].y, dd[r].z, dd[r].w};
+    float sc = fmaxf(dv[0], 0.f);
+#pragma unroll
+    for (int h = 1; h < 4; ++h) sc = h < idx_heads ? add_rn(sc, fmaxf(dv[h], 0.f)) : sc;
+    const unsigned key = static_cast<unsigned>(sel_key(div_rn(sc, 11.313708498984761f), 0) >> 32);
+    hk[r] = lane + 64 * r < n_elig ? key : 0u;
+  }
+  auto count_ge = [&](unsigned c) {
+    return __popcll(__builtin_amdgcn_ballot_w64(hk[0] >= c)) + __popcll(__builtin_amdgcn_ballot_w64(hk[1] >= c));
+  };
+  // every eligible key has the top bit (scores are at least +0); the other 31
+  // bits two at a time: the three thresholds' counts are independent, so
+  // their compares issue back to back
+  unsigned t = 0x80000000u;
+  for (int bit = 29; bit >= 1; bit -= 2) {
+    const unsigned c1 = t | (1u << bit), c2 = t | (2u << bit), c3 = t | (3u << bit);
+    const int n1 = count_ge(c1), n2 = count_ge(c2), n3 = count_ge(c3);
+    t = n3 >= topk ? c3 : n2 >= topk ? c2 : n1 >= topk ? c1 : t;
+  }
+  t = count_ge(t | 1u) >= topk ? t | 1u : t;
+  const unsigned long long gt0 = __builtin_amdgcn_ballot_w64(hk[0] > t), gt1 = __builtin_amdgcn_ballot_w64(hk[1] > t);
+  const unsigned long long eq0 = __builtin_amdgcn_ballot_w64(hk[0] == t);
+  const int need = topk - __popcll(gt0) - __popcll(gt1);
+  auto below = [&](unsigned long long mask) {
+    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(mask >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(mask), 0u)));
+  };
+  const unsigned long long eq1 = __builtin_amdgcn_ballot_w64(hk[1] == t);
+  const int e0 = __popcll(eq0);
+  const unsigned long long s0 = gt0 | __builtin_amdgcn_ballot_w64(hk[0] == t && below(eq0) < need);
+  const unsigned long long s1 = gt1 | __builtin_amdgcn_ballot_w64(hk[1] == t && e0 + below(eq1) < need);
+  if ((s0 >> lane) & 1ull) sel[below(s0)] = lane;
+  if ((s1 >> lane) & 1ull) sel[__popcll(s0) + below(s1)] = 64 + lane;
+}
+
 // keys[j] = sel_key(score_j, j) for every eligible block j in the one-row
 // order, in rounds of PRE passes (PRE * NT / 16 blocks): the passes leave each
 // block's 4 dot products in dsc (LDS), then one thread per block forms its
@@ -506,10 +569,13 @@ __device__ __forceinline__ float4 row16_dots(const float (&q)[4][8], const float
 // than in all 16 of its lanes. kp[u] comes in holding pass u's keys; later
 // rounds load one round ahead. Block new_j's key is new_key (LDS). Ends with
 // the keys padded with zeros to a multiple of 32 (after a barrier the caller
-// issues).
+// issues). Given sel, when one round of 128 holds every eligible block, wave 0
+// selects the top-k from the round's dot products instead (select_from_dsc)
+// and the call returns true, with sel written and no keys.
 template <int NT, int PRE>
-__device__ void score_block_rounds(const float* s_iq, const float* new_key, const float* bk, int n_elig, int new_j,
-                                   int idx_heads, unsigned long long* keys, float4* dsc, float (&kp)[PRE][8]) {
+__device__ bool score_block_rounds(const float* s_iq, const float* new_key, const float* bk, int n_elig, int new_j,
+                                   int idx_heads, unsigned long long* keys, float4* dsc, float (&kp)[PRE][8],
+                                   int topk = 0, int* sel = nullptr) {
   constexpr int PASS = NT / SCORE_LANES;
   constexpr int ROUND = PASS * PRE;
   const int tid = threadIdx.x, jl = tid >> 4, m = tid & 15;
@@ -547,6 +613,10 @@ __device__ void score_block_rounds(const float* s_iq, const float* new_key, cons
     }
     QM_PHASE(13);
     __syncthreads();
+    if (sel && n_elig <= ROUND && ROUND == 128) {
+      if (tid < 64) select_from_dsc(dsc, n_elig, idx_heads, topk, sel);
+      return true;
+    }
     for (int t = tid; t < ROUND && r0 + t < n_elig; t += NT) {
       const float4 dd = dsc[t];
       const float dv[4] = {dd.x, dd.y, dd.z, dd.w};
@@ -560,6 +630,7 @@ __device__ void score_block_rounds(const float* s_iq, const float* new_key, cons
   }
   const int npad = (n_elig + 31) & ~31;
   for (int j = n_elig + tid; j < npad; j += NT) keys[j] = 0ull;
+  return false;
 }
 
 // prefetch of the first PRE passes (issued before the scores are needed)
@@ -1720,7 +1791,7 @@ struct DecShared {
   unsigned long long key[DEC_MAX_BLOCKS];         // selection keys
   float4 dsc[128];                                // a round's per-block dot products (4 heads)
   float red[264];                                 // merge: partial sums and wave values
-  int fault;                                      // the merge saw a wait give up
+  int fault[DEC_WAVES];                           // the merge's waves whose wait gave up
   float iq[4 * IDX_D];                            // the roped indexer query rows
   float newkey[IDX_D];                            // the pooled key of the block this token completes
   alignas(16) uint16_t knb[QSA_D];                // the token's roped key and its value, bf16
@@ -1760,106 +1831,156 @@ struct ItemCount {
   }
 };
 
+// flags of a group: one per workgroup that attends an item or holds a slice
+__host__ __device__ inline int dec_flag_stride(int splits) { return splits > DEC_SLICES ? splits : DEC_SLICES; }
+
+// Flags of the items a wave merges in round i0 (below): lane l polls item
+// i0 + 64 ((l >> 4) & 1) + 16 wv + (l & 15) (lanes 32..63 repeat 0..31); items
+// at or past n_wait count as raised. False if the wait gave up.
+__device__ __forceinline__ bool wait_item_flags(const unsigned* flags, int i0, int n_wait, unsigned target) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int it = i0 + 64 * ((lane >> 4) & 1) + 16 * wv + (lane & 15);
+  const bool need = it < n_wait;
+  const unsigned* f = flags + (need ? it : 0);
+  for (int k = 0; k < FLAG_SPIN_MAX; ++k) {
+    const unsigned v = ld_flag(f);
+    const bool ok = !need || (int)(v - target) >= 0;
+    if (__builtin_amdgcn_ballot_w64(!ok) == 0ull) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
 // Output slice sl = (query head h = sl / 8, channels 32 (sl % 8) ..+31) of
 // group (b, g): out[d] = round(sum_i w_i o_i[d] / sum_i w_i) *
 // round(sigmoid(gate[d])), w_i = exp(m_i - max m) l_i, over the n items (o_i
-// is the item's output divided by its sum l_i). Thread
-// (ch = tid % 32, il = tid / 32) takes items il, il + 8, ...; every load of a
-// 128-item chunk is issued before any is used, indices clamped to the last
-// item and weighted by zero past it.
+// is the item's output divided by its sum l_i). Thread (c = tid % 4, il =
+// tid / 4) takes channels 8c .. 8c + 7 of the slice (one 16-byte load) of
+// items il and il + 64 of each round of 128, so wave w merges items 16w ..
+// 16w + 15 and 64 + 16w .. of a round: it waits for those items' flags alone
+// (n_wait of them count) and loads them at once. Each thread keeps a running
+// maximum, sum and 8 channel sums; the lanes of a chunk are added by DPP row
+// rotations and lane swaps after scaling to the wave's maximum, and the four
+// waves' (sums, maximum) meet in LDS. Workgroup 0 of the group advances the
+// generation word (`word`, when given) once every wave has seen its flags.
+// A wait that gives up counts itself in the group's give-up word and poisons
+// the slice.
 template <typename T>
-__device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, int g, int sl, int n, bool poison,
+__device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, int g, int sl, int n, int n_wait,
+                                     unsigned gen, bool overflow, float gate, unsigned* word,
                                      __amdgpu_buffer_rsrc_t ro, __amdgpu_buffer_rsrc_t rml) {
-  constexpr int CHUNK = 16;                     // items per thread per round trip (128 per workgroup)
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int ch = tid & 31, il = tid >> 5;
-  const int h = sl / 8, d = 32 * (sl % 8) + ch;
-  const int hq = D.P.hq, qh = g * GQA + h;
-  float* s_w = reinterpret_cast<float*>(sh.key);           // DEC_MAX_ITEMS + 128 weights
-  float* red = sh.red;                                    // 8 x 32 partial sums, then 2 x 4 wave values
-  const float gate = Act<T>::load(D.P.qg, ((long)b * hq + qh) * (2 * QSA_D) + QSA_D + d);
-  float ov[CHUNK];
+  const int c = tid & 3, il = tid >> 2;
+  const int h = sl / 8, d0 = 32 * (sl % 8) + 8 * c;
+  const int bg = b * D.P.hkv + g;
+  const unsigned* flags = D.flags + (long)bg * dec_flag_stride(D.splits);
+  float M = -INFINITY, L = 0.f, acc[8];
 #pragma unroll
-  for (int k = 0; k < CHUNK; ++k) ov[k] = ld_dev_bf16(ro, ((min(il + 8 * k, n - 1) * GQA + h) * QSA_D + d) * 2);
-  float2 ml[DEC_MAX_ITEMS / DEC_NT];
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  bool ok = true;
+  const int n_rounds = max(n, n_wait);
+  for (int i0 = 0; i0 < n_rounds; i0 += 128) {
+    ok = ok & wait_item_flags(flags, i0, n_wait, gen + 1);
+    if (i0 >= n) continue;
+    const int ia = i0 + il, ib = ia + 64;
+    const int ca = min(ia, n - 1), cb = min(ib, n - 1);
+    const u32x4_t oa = ld_dev_u32x4(ro, ((ca * GQA + h) * QSA_D + d0) * 2);
+    const u32x4_t ob = ld_dev_u32x4(ro, ((cb * GQA + h) * QSA_D + d0) * 2);
+    const float2 ma = ld_dev2(rml, ((ca * GQA + h) * 2) * 4);
+    const float2 mb = ld_dev2(rml, ((cb * GQA + h) * 2) * 4);
+    const float xa = ia < n ? ma.x : -INFINITY, xb = ib < n ? mb.x : -INFINITY;
+    const float mn = fmaxf(M, fmaxf(xa, xb));
+    const float f = M == -INFINITY ? 0.f : __expf(M - mn);
+    const float wa = ia < n ? __expf(xa - mn) * ma.y : 0.f;
+    const float wb = ib < n ? __expf(xb - mn) * mb.y : 0.f;
+    L = L * f + wa + wb;
 #pragma unroll
-  for (int k = 0; k < DEC_MAX_ITEMS / DEC_NT; ++k) ml[k] = ld_dev2(rml, ((min(tid + DEC_NT * k, n - 1) * GQA + h) * 2) * 4);
-  float M = -INFINITY;
-#pragma unroll
-  for (int k = 0; k < DEC_MAX_ITEMS / DEC_NT; ++k)
-    if (tid + DEC_NT * k < n) M = fmaxf(M, ml[k].x);
-  M = wave_max(M);
-  if (lane == 0) red[256 + wv] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(red[256], red[257]), fmaxf(red[258], red[259]));
-  float L = 0.f;
-  const int n_pad = (n + 127) & ~127;
-#pragma unroll
-  for (int k = 0; k < DEC_MAX_ITEMS / DEC_NT; ++k) {
-    const int i = tid + DEC_NT * k;
-    const float w = i < n ? __expf(ml[k].x - M) * ml[k].y : 0.f;
-    if (i < n_pad) s_w[i] = w;
-    L += w;
+    for (int e = 0; e < 8; ++e) {
+      const float va = __uint_as_float(e & 1 ? oa[e >> 1] & 0xffff0000u : oa[e >> 1] << 16);
+      const float vb = __uint_as_float(e & 1 ? ob[e >> 1] & 0xffff0000u : ob[e >> 1] << 16);
+      acc[e] = acc[e] * f + wa * va + wb * vb;
+    }
+    M = mn;
   }
-  L = wave_sum(L);
-  if (lane == 0) red[260 + wv] = L;
-  __syncthreads();
-  L = (red[260] + red[261]) + (red[262] + red[263]);
-  float acc = 0.f;
-  for (int i0 = 0;; i0 += 8 * CHUNK) {
+  // to the wave's maximum, then the sums over the wave's items (lanes of one c)
+  const float Mw = wave_max(M);
+  const float fw = M == -INFINITY ? 0.f : __expf(M - Mw);
+  float v[9];
 #pragma unroll
-    for (int k = 0; k < CHUNK; ++k) acc += ov[k] * s_w[i0 + il + 8 * k];
-    if (i0 + 8 * CHUNK >= n) break;
+  for (int e = 0; e < 8; ++e) v[e] = acc[e] * fw;
+  v[8] = L * fw;
 #pragma unroll
-    for (int k = 0; k < CHUNK; ++k)
-      ov[k] = ld_dev_bf16(ro, ((min(i0 + 8 * CHUNK + il + 8 * k, n - 1) * GQA + h) * QSA_D + d) * 2);
+  for (int e = 0; e < 9; ++e) {
+    v[e] += dpp_f<0x124>(v[e]);     // row_ror:4
+    v[e] += dpp_f<0x128>(v[e]);     // row_ror:8
+    v[e] = xor32_sum(xor16_sum(v[e]));
   }
-  red[il * 32 + ch] = acc;
+  float* red = sh.red;              // [wave][chunk][8 sums, L, M]
+  if (lane < 4) {
+#pragma unroll
+    for (int e = 0; e < 9; ++e) red[(wv * 4 + lane) * 10 + e] = v[e];
+    red[(wv * 4 + lane) * 10 + 9] = Mw;
+  }
+  if (lane == 0) {
+    if (!ok) __hip_atomic_fetch_add(D.gen + (long)bg * DEC_GEN_STRIDE + 1, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    sh.fault[wv] = ok ? 0 : 1;
+  }
   __syncthreads();
+  QM_PHASE(9);
+  if (word && tid == 0) st_flag(word, gen + 1);
   if (tid < 32) {
-    float o = red[ch];
+    const int cc = tid >> 3, e = tid & 7;
+    float mw[DEC_WAVES], Mx = -INFINITY;
 #pragma unroll
-    for (int k = 1; k < 8; ++k) o += red[k * 32 + ch];
-    const float y = Act<T>::round(o / L) * Act<T>::round(sigmoid_f(gate));
-    Act<T>::store(D.out, ((long)b * hq + qh) * QSA_D + d, poison ? __builtin_nanf("") : y);
+    for (int w = 0; w < DEC_WAVES; ++w) {
+      mw[w] = red[(w * 4 + cc) * 10 + 9];
+      Mx = fmaxf(Mx, mw[w]);
+    }
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < DEC_WAVES; ++w) {
+      const float s = mw[w] == -INFINITY ? 0.f : __expf(mw[w] - Mx);
+      num += red[(w * 4 + cc) * 10 + e] * s;
+      den += red[(w * 4 + cc) * 10 + 8] * s;
+    }
+    const bool poison = overflow || (sh.fault[0] | sh.fault[1] | sh.fault[2] | sh.fault[3]) != 0;
+    const int hq = D.P.hq, qh = g * GQA + h;
+    const float y = Act<T>::round(num / den) * Act<T>::round(sigmoid_f(gate));
+    Act<T>::store(D.out, ((long)b * hq + qh) * QSA_D + 32 * (sl % 8) + tid, poison ? __builtin_nanf("") : y);
   }
   __syncthreads();
 }
 
-// flags of a group: one per workgroup that attends an item or holds a slice
-__host__ __device__ inline int dec_flag_stride(int splits) { return splits > DEC_SLICES ? splits : DEC_SLICES; }
-
-// Workgroup `item` < DEC_SLICES of group (b, g): wait (wave 0 polling) until
-// the flags of the n_att attending workgroups (workgroup 0 of a widened grid:
-// of all 64 slice holders) have reached gen + 1, advance the generation word
-// (workgroup 0), then merge output slices item, item + step, ... A wait that
-// gives up counts itself in the group's give-up word and the slices this
-// workgroup merges become NaN (never a merge of missing partials); so do all
-// slices when the position has more items than the launch has workgroups
+// Workgroup `item` < DEC_SLICES of group (b, g): merge output slices item,
+// item + step, ... once the flags of the n_att attending workgroups have
+// reached gen + 1 (workgroup 0 of a widened grid waits for all 64 slice
+// holders' flags, then advances the generation word). A wait that gives up
+// counts itself in the group's give-up word and the slices this workgroup
+// merges become NaN (never a merge of missing partials); so do all slices
+// when the position has more items than the launch has workgroups
 // (`overflow`). qm_qsa_decode_check reads and resets both counters.
 template <bool WIDE, typename T>
 __device__ __forceinline__ void decode_merge(const DecArgs<T>& D, DecShared& sh, int b, int g, int item, int n_att,
                                              unsigned gen, bool overflow) {
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x;
   const int bg = b * D.P.hkv + g;
   const long gbase = (long)bg * D.splits;
   const __amdgpu_buffer_rsrc_t ro = dev_rsrc(D.part_o + gbase * GQA * QSA_D, (long)D.splits * GQA * QSA_D * 2);
   const __amdgpu_buffer_rsrc_t rml = dev_rsrc(D.part_ml + gbase * GQA * 2, (long)D.splits * GQA * 2 * 4);
   const int n_wait = WIDE && item == 0 ? DEC_SLICES : n_att;
-  if (wv == 0) {
-    const bool ok = wait_flags<DEC_MAX_ITEMS>(D.flags + (long)bg * dec_flag_stride(D.splits), n_wait, gen + 1);
-    if (lane == 0) {
-      if (!ok) __hip_atomic_fetch_add(D.gen + (long)bg * DEC_GEN_STRIDE + 1, 1u, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-      sh.fault = ok ? 0 : 1;
-    }
-  }
-  __syncthreads();
-  QM_PHASE(9);
-  const bool poison = overflow || sh.fault != 0;
-  if (item == 0 && tid == 0) st_flag(D.gen + (long)bg * DEC_GEN_STRIDE, gen + 1);
   const int step = WIDE ? DEC_SLICES : n_att;
-  for (int sl = item; sl < DEC_SLICES; sl += step) decode_combine_slice(D, sh, b, g, sl, n_att, poison, ro, rml);
+  const int hq = D.P.hq;
+  auto gate_of = [&](int sl) {
+    return Act<T>::load(D.P.qg, ((long)b * hq + g * GQA + sl / 8) * (2 * QSA_D) + QSA_D + 32 * (sl % 8) + (tid & 31));
+  };
+  // the first slice's gate is loaded before the wait
+  const float gate0 = gate_of(item);
+  unsigned* word = item == 0 ? D.gen + (long)bg * DEC_GEN_STRIDE : nullptr;
+  for (int sl = item; sl < DEC_SLICES; sl += step) {
+    decode_combine_slice(D, sh, b, g, sl, n_att, n_wait, gen, overflow, sl == item ? gate0 : gate_of(sl),
+                         sl == item ? word : nullptr, ro, rml);
+  }
 }
 
 template <typename T, bool WIDE>
@@ -2017,11 +2138,12 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   // tail workgroup does not depend on them
   QM_PHASE(2);
   if (scoring && (blk_item || item == 0)) {
-    score_block_rounds<DEC_NT, score_pre<DEC_NT>()>(sh.iq, sh.newkey, bk, n_elig, j_new, A.idx_heads, sh.key, sh.dsc,
-                                                   kp);
-    __syncthreads();
-    QM_PHASE(3);
-    rank_topk<DEC_NT, DEC_MAX_TOPK>(sh.key, n_elig, topk, sh.sel, sh.rscr);
+    if (!score_block_rounds<DEC_NT, score_pre<DEC_NT>()>(sh.iq, sh.newkey, bk, n_elig, j_new, A.idx_heads, sh.key,
+                                                         sh.dsc, kp, topk, sh.sel)) {
+      __syncthreads();
+      QM_PHASE(3);
+      rank_topk<DEC_NT, DEC_MAX_TOPK>(sh.key, n_elig, topk, sh.sel, sh.rscr);
+    }
   } else if (!scoring) {
     for (int i = tid; i < n_elig; i += DEC_NT) sh.sel[i] = i;
   }
@@ -2049,12 +2171,15 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
 #pragma unroll
     for (int sk = 0; sk < 8; ++sk) kf[sk] = load_bf16x8(kt + sk * 512);
   }
-  // wave w: query heads 2w, 2w + 1 (and wave 0 the key), normed and roped;
-  // the attention MFMA takes q as bf16 hi + lo (~16 mantissa bits)
+  const bool cur = p >= t0 && p < t0 + 32;          // the item holds the current token
+  const int rcur = p - t0;
+  // wave w: query heads 2w, 2w + 1 (and, in the workgroups that use it, wave 0
+  // the key), normed and roped; the attention MFMA takes q as bf16 hi + lo
+  // (~16 mantissa bits)
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int h = 2 * wv + j;
-    const float ri = wave_rinv<4>(qx[j], A.eps);
+    const float ri = wave_rinv_fast(qx[j], A.eps);
     float y[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) y[k] = nrm(qx[j][k], ri, w_q[k]);
@@ -2066,7 +2191,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
       sh.qb[GQA + h][lane + 64 * k] = f32_to_bf16(y[k] - bf16_to_f32(qhi));
     }
   }
-  if (wv == 0) {
+  if (wv == 0 && (item == 0 || cur)) {
     const float ri = wave_rinv<4>(kx, A.eps);
     float y[4];
 #pragma unroll
@@ -2079,8 +2204,6 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   __syncthreads();
 
   // ---- 4. scores of the item's two 16-token tiles (waves 0, 1)
-  const bool cur = p >= t0 && p < t0 + 32;          // the item holds the current token
-  const int rcur = p - t0;
   if (wv < 2) {
     if (cur && (rcur >> 4) == wv) {
       // the current token's key replaces whole 8-channel vectors of one lane

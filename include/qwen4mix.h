@@ -351,6 +351,24 @@ int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void
                         const void* v_pool, const int* positions, const int* page_table, const int* ids,
                         const int* n_sel, void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* qm_qsa_select for a chunk of `seq` rows that also files every row's
+ * selection into a qm_qsa_attend_chunk workspace (the step qm_qsa_attend_chunk
+ * otherwise runs as a kernel of its own), for qm_qsa_attend_chunk_filed. Same
+ * ids and n_sel as qm_qsa_select; the conditions and the workspace rules of
+ * qm_qsa_attend_chunk. No counterpart in the reference: it composes the
+ * selection (reference/model.py:248-327) with the chunk attention's own
+ * bookkeeping, to save a launch per chunk. */
+int qm_qsa_select_chunk(const qm_qsa_geom* g, int seq, const float* iq, const float* block_keys,
+                        const int* positions, int* ids, int* n_sel, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+/* qm_qsa_attend_chunk over a workspace that qm_qsa_select_chunk has just
+ * filed (the same call's rows and geometry): the attention and the merge
+ * only. No counterpart in the reference (see qm_qsa_select_chunk). */
+int qm_qsa_attend_chunk_filed(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool,
+                              const void* v_pool, const int* positions, const int* page_table, void* out,
+                              void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* The layer projections at small M (the F.linear calls of
  * reference/model.py:184-187, 244, 270, 274, 345-352, 383 for decode):
  * y[m][n] = sum_k w[n][k] x[m][k] for m < M <= 4, one stream over w.

@@ -222,8 +222,10 @@ def test_prefill_chunk_matches_golden_reference(gpu):
                                                           (3000, 300, 1, torch.bfloat16, False),
                                                           (2000, 96, 1, torch.bfloat16, True)])
 def test_prefill_chunk_attention_matches_oracle(gpu, past, seq, batch, dtype, shared):
-    """The block-major chunk attention (qm_qsa_attend_chunk) against the oracle,
-    and against the per-row item attention (qm_qsa_attend) on the same chunk:
+    """The block-major chunk attention against the oracle, with the entries
+    filed by the selection (qm_qsa_select_chunk + qm_qsa_attend_chunk_filed)
+    and by the attention (qm_qsa_select + qm_qsa_attend_chunk), and against
+    the per-row item attention (qm_qsa_attend) on the same chunk:
     a ragged last tile, chunks that complete blocks part-way (rows whose tail
     block another row has selected), a batch of two with its own pages, a
     chunk of more rows than one launch takes (300), and rows that all carry the
@@ -241,8 +243,9 @@ def test_prefill_chunk_attention_matches_oracle(gpu, past, seq, batch, dtype, sh
     want, _, _, chosen = _oracle_core(cfg, store, hidden, cos, sin, keys if past else None,
                                       values if past else None, idx_keys, past)
     outs = []
-    for chunked in (True, False):
+    for chunked, fused in ((True, True), (True, False), (False, False)):
         model, cache = _model_and_cache(gpu, store, dtype, past + seq + 64, batch=batch)
+        model.fuse_chunk_select = fused
         if not chunked:
             model.chunk_attend_fits = lambda cache: False
         if past:
@@ -250,9 +253,10 @@ def test_prefill_chunk_attention_matches_oracle(gpu, past, seq, batch, dtype, sh
         qg, k, v, iq, ik = (t.to(DEV) for t in _projections(store, hidden))
         got = model.qsa_core(qg, k, v, iq, ik, 3, cache, past, cos.to(DEV), sin.to(DEV))
         assert _got_sets(cache[3]) == chosen
-        assert rel_err(got, want) < OUT_TOL, "chunked" if chunked else "items"
+        assert rel_err(got, want) < OUT_TOL, ("chunked" if chunked else "items", fused)
         outs.append(got.float())
-    assert rel_err(outs[0], outs[1]) < 1e-2
+    assert torch.equal(outs[0], outs[1])           # the same entries either way
+    assert rel_err(outs[0], outs[2]) < 1e-2
 
 
 def test_small_ratio_several_blocks_per_page(gpu):

@@ -35,6 +35,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 constexpr int QSA_D = 256;     // attention head dim
+constexpr int GQA = 8;          // query heads per kv head the attention kernels handle
 constexpr int IDX_D = 128;     // indexer head dim
 constexpr int PREP_NT = 256;
 
@@ -976,6 +977,9 @@ struct SelArgs {
   const float* iq; const float* block_keys; const int* positions; const int* page_table;
   int* ids; int* n_sel; int2* items; float* scores_out;
   int batch, seq, idx_heads, ratio, topk, max_blocks, page_size, max_pages, max_items;
+  // the chunk path's entry lists (qm_qsa_select_chunk), or null
+  unsigned* cnt = nullptr; unsigned* list = nullptr; float* part_ml = nullptr; const int* parity = nullptr;
+  int hkv = 0;
 };
 
 struct SelShared {
@@ -1035,6 +1039,40 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
     for (int i = tid; i < A.topk; i += NT) out_ids[i] = S.sel[i];
   }
   if (tid == 0) A.n_sel[row] = n_sel;
+  if (A.cnt) {
+    // the chunk path's entry lists, as qsa_chunk_bucket_kernel files them:
+    // every selected block files (row, slot) under the block, the slots this
+    // row leaves empty get (max, sum) = (-inf, 0), and the previous call's
+    // counts (the other parity) are cleared, spread over the rows
+    __syncthreads();
+    const int s = row % A.seq;
+    const int par = *A.parity;
+    unsigned* cnt_in = A.cnt + ((long)par * A.batch + b) * A.max_blocks;
+    unsigned* cnt_old = A.cnt + ((long)(par ^ 1) * A.batch + b) * A.max_blocks;
+    for (int j = s * NT + tid; j < A.max_blocks; j += A.seq * NT) cnt_old[j] = 0u;
+    const int nslot = A.topk + 1;
+    for (int i = tid; i < nslot; i += NT) {
+      bool empty;
+      if (i < A.topk) {
+        empty = i >= n_sel;
+        if (!empty) {
+          const int j = S.sel[i];
+          // a block is at most once among a row's selections: at < seq
+          const unsigned at = atomicAdd(&cnt_in[j], 1u);
+          if (at < static_cast<unsigned>(A.seq))
+            A.list[((long)b * A.max_blocks + j) * A.seq + at] = (static_cast<unsigned>(s) << 16) | static_cast<unsigned>(i);
+        }
+      } else {
+        empty = ((p + 1) / A.ratio) * A.ratio > p;      // the row completes its block: no tail
+      }
+      if (empty)
+        for (int g = 0; g < A.hkv; ++g) {
+          float4* ml = reinterpret_cast<float4*>(A.part_ml + (((long)row * A.hkv + g) * nslot + i) * GQA * 2);
+#pragma unroll
+          for (int h = 0; h < GQA / 2; ++h) ml[h] = make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
+        }
+    }
+  }
   if (!A.items) return;
   __syncthreads();
   // attention items: the groups of every selected block in rank order, then the tail's
@@ -1125,7 +1163,6 @@ __global__ __launch_bounds__(SEL_NT) void qsa_front_kernel(PrepArgs<T> A, SelArg
 // ---------------------------------------------------------------------------
 // decode attention
 // ---------------------------------------------------------------------------
-constexpr int GQA = 8;          // query heads per kv head this kernel handles
 constexpr int ATT_WAVES = 2;    // waves (one 32-token item each) per workgroup
 
 struct AttnArgs {
@@ -2581,13 +2618,13 @@ extern "C" size_t qm_qsa_attend_chunk_workspace(const qm_qsa_geom* g, int seq) {
   return chunk_ws_layout(g, seq).total;
 }
 
-extern "C" int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool,
-                                   const void* v_pool, const int* positions, const int* page_table, const int* ids,
-                                   const int* n_sel, void* out, void* workspace, size_t workspace_bytes,
-                                   hipStream_t stream) {
+namespace {
+int attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool, const void* v_pool,
+                 const int* positions, const int* page_table, const int* ids, const int* n_sel, void* out,
+                 void* workspace, size_t workspace_bytes, bool filed, hipStream_t stream) {
   int rc = check_chunk_geom(g, "qm_qsa_attend_chunk: null geometry");
   if (rc) return rc;
-  if (!q || !qg || !k_pool || !v_pool || !positions || !page_table || !ids || !n_sel || !out)
+  if (!q || !qg || !k_pool || !v_pool || !positions || !page_table || (!filed && (!ids || !n_sel)) || !out)
     return qm_fail(QM_ERR_ARG, "qm_qsa_attend_chunk: null pointer");
   if (seq <= 0 || seq > 65535 || (long)g->batch * seq > 65535)
     return qm_fail(QM_ERR_ARG, "qm_qsa_attend_chunk: bad seq");
@@ -2603,10 +2640,12 @@ extern "C" int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q,
   uint16_t* part_o = reinterpret_cast<uint16_t*>(base + L.o);
   float* part_ml = reinterpret_cast<float*>(base + L.ml);
 
-  ChunkBucketArgs K{positions, ids, n_sel, part_ml, cnt, list, parity, g->batch, seq, g->n_kv_heads, g->ratio, topk,
-                    g->max_blocks};
-  hipLaunchKernelGGL(qsa_chunk_bucket_kernel, dim3(g->batch * seq), dim3(64), 0, stream, K);
-  QM_CHECK_LAUNCH();
+  if (!filed) {
+    ChunkBucketArgs K{positions, ids, n_sel, part_ml, cnt, list, parity, g->batch, seq, g->n_kv_heads, g->ratio, topk,
+                      g->max_blocks};
+    hipLaunchKernelGGL(qsa_chunk_bucket_kernel, dim3(g->batch * seq), dim3(64), 0, stream, K);
+    QM_CHECK_LAUNCH();
+  }
 
   ChunkAttnArgs A;
   A.q = static_cast<const uint16_t*>(q); A.k_pool = static_cast<const uint16_t*>(k_pool);
@@ -2638,6 +2677,49 @@ extern "C" int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q,
   }
   QM_CHECK_LAUNCH();
   return QM_OK;
+}
+}  // namespace
+
+extern "C" int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool,
+                                   const void* v_pool, const int* positions, const int* page_table, const int* ids,
+                                   const int* n_sel, void* out, void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream) {
+  return attend_chunk(g, seq, q, qg, k_pool, v_pool, positions, page_table, ids, n_sel, out, workspace,
+                      workspace_bytes, false, stream);
+}
+
+extern "C" int qm_qsa_select_chunk(const qm_qsa_geom* g, int seq, const float* iq, const float* block_keys,
+                                   const int* positions, int* ids, int* n_sel, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream) {
+  int rc = check_chunk_geom(g, "qm_qsa_select_chunk: null geometry");
+  if (rc) return rc;
+  if (!iq || !block_keys || !positions || !ids || !n_sel) return qm_fail(QM_ERR_ARG, "qm_qsa_select_chunk: null pointer");
+  if (seq <= 0 || seq > 65535 || (long)g->batch * seq > 65535)
+    return qm_fail(QM_ERR_ARG, "qm_qsa_select_chunk: bad seq");
+  if (g->max_pages > SEL_MAX_BLOCKS || g->budget / g->ratio > SEL_MAX_BLOCKS / 2)
+    return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_select_chunk: more than 4096 blocks or pages");
+  const ChunkWs L = chunk_ws_layout(g, seq);
+  if (!workspace || workspace_bytes < L.total)
+    return qm_fail(QM_ERR_WORKSPACE, "qm_qsa_select_chunk: workspace too small");
+  char* base = static_cast<char*>(workspace);
+  SelArgs A = sel_args(g, seq, iq, block_keys, positions, nullptr, ids, n_sel, nullptr, nullptr);
+  A.parity = reinterpret_cast<const int*>(base + L.parity);
+  A.cnt = reinterpret_cast<unsigned*>(base + L.cnt);
+  A.list = reinterpret_cast<unsigned*>(base + L.list);
+  A.part_ml = reinterpret_cast<float*>(base + L.ml);
+  A.hkv = g->n_kv_heads;
+  hipLaunchKernelGGL(qsa_select_kernel, dim3(g->batch * seq), dim3(SELP_NT), 0, stream, A);
+  QM_CHECK_LAUNCH();
+  return QM_OK;
+}
+
+extern "C" int qm_qsa_attend_chunk_filed(const qm_qsa_geom* g, int seq, const void* q, const void* qg,
+                                         const void* k_pool, const void* v_pool, const int* positions,
+                                         const int* page_table, void* out, void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream) {
+  // the entry lists come from qm_qsa_select_chunk: no ids or counts to read
+  return attend_chunk(g, seq, q, qg, k_pool, v_pool, positions, page_table, nullptr, nullptr, out, workspace,
+                      workspace_bytes, true, stream);
 }
 
 extern "C" int qm_qsa_pool_blocks(const qm_qsa_geom* g, const void* raw_keys, const float* k_norm, const float* cos,

@@ -35,6 +35,11 @@ from .rope import RopeTable
 
 
 class Qwen4MixModel:
+    # a prefill chunk's selection files its entries for the chunk attention
+    # (qm_qsa_select_chunk + qm_qsa_attend_chunk_filed) rather than the
+    # attention filing them itself (qm_qsa_select + qm_qsa_attend_chunk)
+    fuse_chunk_select = True
+
     def __init__(self, config, store, device=None, max_ctx: int = 8192):
         self.config = config if isinstance(config, MixConfig) else MixConfig.from_reference(config)
         self.store = store
@@ -354,26 +359,40 @@ class Qwen4MixModel:
                         native.ptr(pos), native.ptr(lc.page_table), native.ptr(lc.k_pool), native.ptr(lc.v_pool),
                         native.ptr(lc.raw_keys), native.ptr(lc.block_keys), native.ptr(q_out), native.ptr(iq_out),
                         stream)
-            native.call("qm_qsa_select", ctypes.byref(g), seq, native.ptr(iq_out), native.ptr(lc.block_keys),
-                        native.ptr(pos), native.ptr(lc.page_table), native.ptr(ids), native.ptr(n_sel),
-                        native.ptr(items), None, stream)
+            if chunked:
+                # the chunk attention's own workspace per geometry: the entry
+                # counts it keeps between calls are laid out by batch and block count
+                chunk_ws = self._workspace(f"qsa_attend_chunk_{batch}_{cache.max_blocks}",
+                                           lib.qm_qsa_attend_chunk_workspace(ctypes.byref(g), seq))
+            if chunked and self.fuse_chunk_select:
+                # the selection also files each row's blocks into that workspace
+                # (one launch fewer per chunk)
+                native.call("qm_qsa_select_chunk", ctypes.byref(g), seq, native.ptr(iq_out),
+                            native.ptr(lc.block_keys), native.ptr(pos), native.ptr(ids), native.ptr(n_sel),
+                            native.ptr(chunk_ws), chunk_ws.numel(), stream)
+            else:
+                native.call("qm_qsa_select", ctypes.byref(g), seq, native.ptr(iq_out), native.ptr(lc.block_keys),
+                            native.ptr(pos), native.ptr(lc.page_table), native.ptr(ids), native.ptr(n_sel),
+                            native.ptr(items), None, stream)
         lc.blocks_valid = max(lc.blocks_valid, (query_offset + seq) // c.indexer_compress_ratio)
         if k is not None:
             lc.n_tokens = query_offset + seq
         lc.last_ids, lc.last_n_sel, lc.last_iq, lc.last_q = ids, n_sel, iq_out, q_out
         if not attend:
             return None
-        if seq > 1 and self.chunk_attend_fits(cache):
+        if chunked:
             # a chunk of rows: each selected key block is read once for all rows that attend it
-            # its own workspace per geometry: the entry counts it keeps between
-            # calls are laid out by batch and block count
-            ws = self._workspace(f"qsa_attend_chunk_{batch}_{cache.max_blocks}",
-                                 lib.qm_qsa_attend_chunk_workspace(ctypes.byref(g), seq))
             if out is None:
                 out = torch.empty(batch, seq, c.num_attention_heads * c.head_dim, dtype=dt, device=self.device)
-            native.call("qm_qsa_attend_chunk", ctypes.byref(g), seq, native.ptr(q_out), native.ptr(qg),
-                        native.ptr(lc.k_pool), native.ptr(lc.v_pool), native.ptr(pos), native.ptr(lc.page_table),
-                        native.ptr(ids), native.ptr(n_sel), native.ptr(out), native.ptr(ws), ws.numel(), stream)
+            if self.fuse_chunk_select:
+                native.call("qm_qsa_attend_chunk_filed", ctypes.byref(g), seq, native.ptr(q_out), native.ptr(qg),
+                            native.ptr(lc.k_pool), native.ptr(lc.v_pool), native.ptr(pos),
+                            native.ptr(lc.page_table), native.ptr(out), native.ptr(chunk_ws), chunk_ws.numel(), stream)
+            else:
+                native.call("qm_qsa_attend_chunk", ctypes.byref(g), seq, native.ptr(q_out), native.ptr(qg),
+                            native.ptr(lc.k_pool), native.ptr(lc.v_pool), native.ptr(pos),
+                            native.ptr(lc.page_table), native.ptr(ids), native.ptr(n_sel), native.ptr(out),
+                            native.ptr(chunk_ws), chunk_ws.numel(), stream)
             return out
         splits = lib.qm_qsa_attend_splits(ctypes.byref(g), query_offset, query_offset + seq - 1)
         ws = self._workspace("qsa_attend", lib.qm_qsa_attend_workspace(ctypes.byref(g), seq, splits))

@@ -71,6 +71,8 @@ SIGNATURES = {
     "qm_qsa_attend": (_i, [ctypes.POINTER(QsaGeom), _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _sz, _vp]),
     "qm_qsa_attend_chunk_workspace": (_sz, [ctypes.POINTER(QsaGeom), _i]),
     "qm_qsa_attend_chunk": (_i, [ctypes.POINTER(QsaGeom), _i] + [_vp] * 9 + [_vp, _sz, _vp]),
+    "qm_qsa_select_chunk": (_i, [ctypes.POINTER(QsaGeom), _i] + [_vp] * 5 + [_vp, _sz, _vp]),
+    "qm_qsa_attend_chunk_filed": (_i, [ctypes.POINTER(QsaGeom), _i] + [_vp] * 7 + [_vp, _sz, _vp]),
     "qm_qsa_pool_blocks": (_i, [ctypes.POINTER(QsaGeom), _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "qm_gemv": (_i, [_i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp]),
     "qm_gemv_reinject": (_i, [_i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp]),

@@ -239,6 +239,7 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   const float rq = rsqrt_rn(sq + 1e-6f), rk = rsqrt_rn(sk + 1e-6f);
   const float sqrt_d = 11.313708498984761f;
   const float qk = div_rn(sqk * rq * rk, sqrt_d);       // q^ . k^
+  const float rqd = div_rn(rq, sqrt_d);                 // q's scale, one division for the four rows
 
   QM_PHASE(2);
   // ---- decay, then per column pred = S^T k^ and qd = S^T q^: a thread adds
@@ -252,7 +253,7 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   for (int i = 0; i < RPT; ++i) {
     const int row = r + RSTEP * i;
     kr[i] = mul_rn(s_k[row], rk);
-    const float qr = div_rn(mul_rn(s_q[row], rq), sqrt_d);
+    const float qr = s_q[row] * rqd;
     st[i].x *= decay; st[i].y *= decay; st[i].z *= decay; st[i].w *= decay;
     p[0] = fmaf(st[i].x, kr[i], p[0]); p[1] = fmaf(st[i].y, kr[i], p[1]);
     p[2] = fmaf(st[i].z, kr[i], p[2]); p[3] = fmaf(st[i].w, kr[i], p[3]);
@@ -335,8 +336,10 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
     if (lane < DN_DCOLS) {
       T zv = zr;
       opaque(zv);    // converted here, not where it is loaded (that would wait for the load there)
-      const float rn = rsqrt_rn(ss_all / (float)DN_D + eps);
-      const float y = (nw * (o * rn)) * sigmoid_f(Act<T>::load(&zv, 0));
+      // the output is rounded to the activation type: the hardware reciprocal
+      // square root and a reciprocal-based sigmoid are well inside that
+      const float rn = __builtin_amdgcn_rsqf(ss_all * (1.0f / DN_D) + eps);
+      const float y = (nw * (o * rn)) * __builtin_amdgcn_rcpf(1.0f + __expf(-Act<T>::load(&zv, 0)));
       Act<T>::store(out, (long)b * hv * DN_D + h * DN_D + col0 + lane, done ? y : __builtin_nanf(""));
     }
   }

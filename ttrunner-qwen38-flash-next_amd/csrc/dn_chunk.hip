@@ -125,6 +125,8 @@ struct PrepShared {
 template <typename T>
 __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A) {
   __shared__ PrepShared sh;
+  QM_PHASE_DECL
+  QM_PHASE(0);
   // A.parts workgroups per chunk: each forms L and T, then writes its share
   // (all of it, or a quarter) of qk, q_dec, k_dec^T and of the w / u columns
   const int part = blockIdx.x % A.parts;
@@ -207,7 +209,9 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
       }
     }
   }
+  QM_PHASE(1);
   __syncthreads();
+  QM_PHASE(2);
 
   // L = (k k^T) * beta_i * exp(cum_i - cum_j) for j < i
   for (int ti = wid; ti < 10; ti += 4) {
@@ -221,7 +225,9 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
       sh.L[i][j] = i > j ? (acc[v] * sh.beta[i]) * expf(sh.cum[i] - sh.cum[j]) : 0.f;
     }
   }
+  QM_PHASE(3);
   __syncthreads();
+  QM_PHASE(4);
 
   if (wid == 0) {
     // (I + L_II)^-1 for the four diagonal blocks; lane = (block, column):
@@ -257,6 +263,7 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
     }
   }
 
+  QM_PHASE(5);
   // q e^cum as [token][dim] and (k e^(cum_last - cum))^T as [dim][token]
   for (int it = 2 * span * part; it < 2 * span * (part + 1); ++it) {
     const int idx = tid + CK_NT * it;
@@ -274,6 +281,7 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   }
   __syncthreads();
 
+  QM_PHASE(6);
   // blocks of T below the diagonal, one sub-diagonal at a time:
   // T_IJ = -T_II sum_{K=J}^{I-1} L_IK T_KJ
   for (int dist = 1; dist < 4; ++dist) {
@@ -294,6 +302,7 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
     __syncthreads();
   }
 
+  QM_PHASE(7);
   // w = T (k beta e^cum) and u = T (v beta): quarter r holds column tiles 2r
   // and 2r + 1 of each, one (matrix, tile) per wave
   for (int kq = 0; kq < span; ++kq) {
@@ -323,6 +332,8 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
       }
     }
   }
+  QM_PHASE(8);
+  QM_PHASE_FLUSH();
 }
 
 template <typename T>
@@ -481,6 +492,8 @@ int run_chunked(int act_dtype, int batch, int seq, int heads, int hk, long q_str
 }
 
 }  // namespace
+
+QM_PHASE_ENTRY(dnc)
 
 namespace {
 size_t chunk_records_bytes(int batch, int seq, int heads) {

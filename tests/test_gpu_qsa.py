@@ -154,6 +154,46 @@ def test_decode_core_matches_oracle(gpu, pos, dtype):
     assert torch.equal(cache[3].page_row("v", page, pos % P).cpu(), v_new[0, :, 0].to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("pos", [8128, 4032, 9000])
+def test_decode_selection_ties_go_to_lower_index(gpu, pos):
+    """Exactly tied block scores at the top-k boundary, through the one-launch
+    decode: the indexer query's roped dims are zero (their projection rows
+    zeroed), and the raw indexer keys repeat every 20 blocks, so the repeated
+    blocks' pooled keys agree outside the roped dims and score bit-identically;
+    of a tied group the lower block indices must be selected (the oracle's
+    stable descending sort). 8128 and 4032 take
+    the kernel's ballot search over at most 128 blocks, 9000 its radix
+    select."""
+    cfg = OracleConfig()
+    dtype = torch.bfloat16
+    store = gi.FakeStore(gi.qsa_weights(3, 71, dtype))
+    wq = store.get("blk.3.indexer.q_proj.weight")
+    for h in range(wq.shape[0] // 128):
+        wq[h * 128: h * 128 + cfg.rope_dim] = 0
+    keys, values, idx_keys = gi.qsa_past(72, pos, dtype)
+    n_blocks = pos // 64
+    for j in range(20, n_blocks):
+        idx_keys[:, 64 * j: 64 * j + 64] = idx_keys[:, 64 * (j % 20): 64 * (j % 20) + 64]
+    hidden = gi.normal(gi.rng(73), (1, 1, gi.HIDDEN)).to(dtype)
+    cos, sin = tables(pos + 1)
+    print(f"decode ties pos={pos}", flush=True)
+    want, _, _, chosen = _oracle_core(cfg, store, hidden, cos, sin, keys, values, idx_keys, pos)
+    model, cache = _model_and_cache(gpu, store, dtype, pos + 128)
+    cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
+    qg, k, v, iq, ik = (t.to(DEV) for t in _projections(store, hidden))
+    got = model.qsa_core(qg, k, v, iq, ik, 3, cache, pos, cos.to(DEV), sin.to(DEV))
+    # the tie really sits at the boundary: the k-th and (k+1)-th scores are
+    # equal (no block completes at these positions: every eligible block is
+    # pooled from the past keys)
+    om = OracleMixer(cfg, store)
+    q = om.indexer_query(hidden, 3, cos, sin)
+    sc = om.indexer_scores(q, om.indexer_pooled(idx_keys, 3, cos, sin, (pos + 1) // 64)).flatten()
+    top = torch.sort(sc, descending=True).values
+    assert top[31] == top[32], "no tie at the top-k boundary"
+    assert _got_sets(cache[3]) == chosen
+    assert rel_err(got, want) < OUT_TOL
+
+
 def test_page_gather_round_trip_is_bit_exact(gpu):
     store = gi.FakeStore(gi.qsa_weights(3, 64, torch.bfloat16))
     keys, values, idx = gi.qsa_past(65, 1000, torch.bfloat16)

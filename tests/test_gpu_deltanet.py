@@ -211,3 +211,46 @@ def test_chunked_4096_tokens_against_reference_golden(gpu):
     ws = torch.from_numpy(z["chunk_state"])
     stride = max(1, s.numel() // ws.numel())
     assert abs_err(s[::stride][: ws.numel()], ws) < STATE_TOL
+
+
+@pytest.mark.parametrize("hk,hv", [(1, 4), (3, 6), (2, 8)])
+def test_decode_core_other_key_head_counts(gpu, hk, hv):
+    """Value head h reads q/k head h % hk for any key-head count, one key head
+    included (the decode kernel's division-free h % hk): four decode steps and
+    a 5-token prefill against the oracle, conv window bit-exact."""
+    qm = gpu
+    dtype = torch.bfloat16
+    ocfg = OracleConfig(linear_num_k_heads=hk, linear_num_v_heads=hv)
+    cfg = qm.MixConfig(linear_num_k_heads=hk, linear_num_v_heads=hv)
+    r = gi.rng(60 + hk)
+    d, conv_dim = 128, ocfg.conv_dim
+    w = {"blk.0.ssm_conv1d.weight": gi.normal(r, (conv_dim, 4), 0.5, dtype),
+         "blk.0.ssm_a": -(gi.normal(r, (hv,)).abs() + 0.5),
+         "blk.0.ssm_dt.bias": gi.normal(r, (hv,), 0.1),
+         "blk.0.ssm_norm.weight": 1.0 + gi.normal(r, (d,), 0.1)}
+    store = gi.FakeStore(w)
+    conv = gi.normal(r, (1, conv_dim, 3)).to(dtype)
+    state = gi.normal(r, (1, hv, d, d), 0.02)
+    ocache = OracleHybridCache(1)
+    ocache[0].conv_state, ocache[0].recurrent_state = conv.clone(), state.clone()
+    model = qm.Qwen4MixModel(cfg, store, device=DEV)
+    cache = qm.MixHybridCache(1, cfg, 1, 256, DEV, dtype)
+    cache[0].conv_state = conv.to(DEV)
+    cache[0].recurrent_state = state.to(DEV).clone()
+    omix = OracleMixer(ocfg, store)
+    worst_out = worst_state = 0.0
+    for t, seq in enumerate((1, 1, 5, 1, 1)):
+        mixed = gi.normal(r, (1, seq, conv_dim)).to(dtype)
+        z = gi.normal(r, (1, seq, hv * d)).to(dtype)
+        b = gi.normal(r, (1, seq, hv)).to(dtype)
+        a = gi.normal(r, (1, seq, hv)).to(dtype)
+        want = omix.dn_core(mixed, z, b, a, 0, ocache)
+        got = model.dn_core(mixed.to(DEV), z.to(DEV), a.to(DEV), b.to(DEV), 0, cache[0])
+        torch.cuda.synchronize()
+        worst_out = max(worst_out, rel_err(got, want))
+        worst_state = max(worst_state, abs_err(cache[0].recurrent_state, ocache[0].recurrent_state))
+        assert torch.equal(cache[0].conv_state.cpu(), ocache[0].conv_state), (hk, hv, t)
+    print(f"hk={hk} hv={hv}: worst out rel {worst_out:.2e} (bar {OUT_TOL}), "
+          f"worst state abs {worst_state:.2e} (bar {STATE_TOL})", flush=True)
+    assert worst_out < OUT_TOL and worst_state < STATE_TOL
+    model.check_handoffs()

@@ -156,7 +156,9 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   const int conv_dim = (2 * n_hk + hv) * DN_D;
   const int wg = xcd_remap(blockIdx.x, hv * DN_SLICES);
   const int s = wg & (DN_SLICES - 1), h = wg / DN_SLICES, b = blockIdx.y;
-  const int hk = h - (int)__umulhi((unsigned)h, hk_magic) * n_hk;   // h % n_hk, no division
+  // h % n_hk without a division: hk_magic = ceil(2^32 / n_hk) is exact for
+  // h < 256, but one key head (magic 2^32) does not fit the word
+  const int hk = n_hk == 1 ? 0 : h - (int)__umulhi((unsigned)h, hk_magic) * n_hk;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c4 = tid & 7, r = tid >> 3;
   const int col0 = s * DN_DCOLS;
@@ -174,8 +176,8 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   // ---- loads, all issued before any is used and none converted before the
   // last is issued: the conv inputs of the head's q and k channels (thread t
   // takes channel t), the state, the conv inputs of the slice's 32 v channels,
-  // z and the norm weight of the slice's columns (wave 0), the position, the
-  // gates and the head's generation word by scalar loads (uniform).
+  // z, the norm weight of the slice's columns and the head's generation word
+  // (wave 0), the position and the gates by scalar loads (uniform).
   const int wv = __builtin_amdgcn_readfirstlane(wid);
   const int key_dim = n_hk * DN_D;
   const int ch_qk = tid < DN_D ? hk * DN_D + tid : key_dim + hk * DN_D + (tid - DN_D);
@@ -191,20 +193,22 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   QM_PHASE(12);
   T zr{};
   float nw = 0.f;
+  unsigned* line = sync + (long)(b * hv + h) * DN_SYNC_WORDS;
+  unsigned long long* shares = reinterpret_cast<unsigned long long*>(line) + DN_SHARE0;
+  unsigned gen = 0;
   if (wv == 0) {
     if (k4) cin_v = conv_load4(ring, conv_w, qkv, conv_dim, b, ch_v);
     zr = z[(long)b * hv * DN_D + h * DN_D + col0 + (lane & (DN_DCOLS - 1))];
     nw = norm_w[col0 + (lane & (DN_DCOLS - 1))];
+    // the generation word, an atomic load issued last (loads complete in
+    // order, so nothing earlier waits for it): it was last written in an
+    // earlier launch, and this launch's slice 0 writes it only after every
+    // slice of the head has published its share
+    gen = ld_flag(line);
   }
   const int pos = uniform_load(positions + b);
   const float gate_b = uniform_act(gb, (long)b * hv + h), gate_a = uniform_act(ga, (long)b * hv + h);
   const float a_neg = uniform_load(a_neg_p + h), dtb = uniform_load(dt_bias_p + h);
-  unsigned* line = sync + (long)(b * hv + h) * DN_SYNC_WORDS;
-  unsigned long long* shares = reinterpret_cast<unsigned long long*>(line) + DN_SHARE0;
-  // the generation word by a scalar load: it was last written in an earlier
-  // launch, and this launch's slice 0 writes it only after every slice of the
-  // head has published its share (so after this read)
-  const unsigned gen = uniform_load(line);
   QM_PHASE(6);
 
   // ---- conv of the q/k channels and the slice's v channels (the q/k ring

@@ -515,52 +515,99 @@ __device__ __forceinline__ float4 row16_dots(const float (&q)[4][8], const float
 }
 
 // The top-k of at most 128 eligible blocks of one query row (ties to the lower
-// index) from their dot products in dsc, written to sel[0 .. topk) in block
-// order, by one wave: it forms the 128 keys in registers (lane l: blocks l and
-// 64 + l; zero past n_elig), finds the score bits t of the top-k-th largest key
-// by a bitwise search over ballot counts (the largest t with at least topk
-// keys' scores at or above it), keeps every block scored above t and, of those
-// scored exactly t, the lowest indices until there are topk, and places each
-// kept block by the count of kept blocks below it.
-__device__ __forceinline__ void select_from_dsc(const float4* dsc, int n_elig, int idx_heads, int topk, int* sel) {
-  const int lane = threadIdx.x & 63;
-  const float4 dd[2] = {dsc[lane], dsc[64 + lane]};
-  unsigned hk[2];
+// index) from their dot products in dsc, by all 256 threads, written to
+// sel[0 .. topk) in block order; returns the want-th selected block (block
+// order; -1 for want < 0), the same in every thread. Ranking by counting:
+// thread (wave w, lane l) takes block i = 32 w + (l & 31) and half h = l >> 5
+// of the blocks. It forms block i's score key (relu, the heads added in order,
+// the division by sqrt(128), then the order-preserving bits of sel_key; zero
+// past n_elig, below every eligible key), the h = 0 lanes store it to LDS,
+// and after a barrier each thread counts the keys of half h strictly above
+// its own (four keys per broadcast LDS read, one 32-bit compare each). The
+// halves' counts meet by a lane swap (l ^ 32). A block with fewer than topk
+// keys above it is kept; each wave's kept blocks are one 32-bit ballot,
+// published in masks (LDS, 4 words) behind a second barrier. When exactly
+// topk blocks are kept there is no tie at the boundary and the set is final.
+// Otherwise blocks with equal scores straddle the boundary, and every thread
+// counts again with 64-bit keys (score bits over the reversed index, so that
+// the lower index ranks higher), which orders every pair; a third barrier
+// publishes those masks. A kept block's place in sel is the count of kept
+// blocks below it; sel is published by the caller's next barrier.
+__device__ __forceinline__ int select128(const float4* dsc, int n_elig, int idx_heads, int topk, int* sel,
+                                         unsigned long long* keys, unsigned* masks, int want) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = 32 * wv + (lane & 31), h = lane >> 5;
+  const float4 dd = dsc[i];
+  const float dv[4] = {dd.x, dd.y, dd.z, dd.w};
+  float sc = fmaxf(dv[0], 0.f);
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const float dv[4] = {dd[r].x, dd[r].y, dd[r].z, dd[r].w};
-    float sc = fmaxf(dv[0], 0.f);
+  for (int hh = 1; hh < 4; ++hh) sc = hh < idx_heads ? add_rn(sc, fmaxf(dv[hh], 0.f)) : sc;
+  const unsigned long long key = i < n_elig ? sel_key(div_rn(sc, 11.313708498984761f), i) : 0ull;
+  const unsigned hk = static_cast<unsigned>(key >> 32);
+  unsigned* hkeys = masks + 8;                       // 128 score keys after the mask words
+  if (h == 0) { hkeys[i] = hk; keys[i] = key; }
+  __syncthreads();
+  QM_PHASE(3);
+  // the 64 score keys of half h, all requested before the first compare
+  {
+    const uint4* kh = reinterpret_cast<const uint4*>(hkeys + 64 * h);
+    uint4 kk[16];
 #pragma unroll
-    for (int h = 1; h < 4; ++h) sc = h < idx_heads ? add_rn(sc, fmaxf(dv[h], 0.f)) : sc;
-    const unsigned key = static_cast<unsigned>(sel_key(div_rn(sc, 11.313708498984761f), 0) >> 32);
-    hk[r] = lane + 64 * r < n_elig ? key : 0u;
+    for (int q = 0; q < 16; ++q) kk[q] = kh[q];
+    __builtin_amdgcn_sched_barrier(0);
+    unsigned cnt = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      cnt += (kk[q].x > hk ? 1u : 0u) + (kk[q].y > hk ? 1u : 0u) + (kk[q].z > hk ? 1u : 0u) +
+             (kk[q].w > hk ? 1u : 0u);
+    const auto sw = __builtin_amdgcn_permlane32_swap(cnt, cnt, false, false);
+    const unsigned above = sw[0] + sw[1];
+    const unsigned mine = static_cast<unsigned>(
+        __builtin_amdgcn_ballot_w64(lane < 32 && i < n_elig && above < static_cast<unsigned>(topk)));
+    if (lane == 0) masks[wv] = mine;
   }
-  auto count_ge = [&](unsigned c) {
-    return __popcll(__builtin_amdgcn_ballot_w64(hk[0] >= c)) + __popcll(__builtin_amdgcn_ballot_w64(hk[1] >= c));
-  };
-  // every eligible key has the top bit (scores are at least +0); the other 31
-  // bits two at a time: the three thresholds' counts are independent, so
-  // their compares issue back to back
-  unsigned t = 0x80000000u;
-  for (int bit = 29; bit >= 1; bit -= 2) {
-    const unsigned c1 = t | (1u << bit), c2 = t | (2u << bit), c3 = t | (3u << bit);
-    const int n1 = count_ge(c1), n2 = count_ge(c2), n3 = count_ge(c3);
-    t = n3 >= topk ? c3 : n2 >= topk ? c2 : n1 >= topk ? c1 : t;
+  __syncthreads();
+  unsigned m[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) m[w] = masks[w];
+  if (__popc(m[0]) + __popc(m[1]) + __popc(m[2]) + __popc(m[3]) != static_cast<unsigned>(topk)) {
+    // equal scores at the boundary: rank by the full keys
+    const ulonglong2* kh = reinterpret_cast<const ulonglong2*>(keys + 64 * h);
+    unsigned cnt = 0;
+#pragma unroll 4
+    for (int q = 0; q < 32; ++q) {
+      const ulonglong2 kk = kh[q];
+      cnt += (kk.x > key ? 1u : 0u) + (kk.y > key ? 1u : 0u);
+    }
+    const auto sw = __builtin_amdgcn_permlane32_swap(cnt, cnt, false, false);
+    const unsigned rank = sw[0] + sw[1];
+    const unsigned mine = static_cast<unsigned>(
+        __builtin_amdgcn_ballot_w64(lane < 32 && i < n_elig && rank < static_cast<unsigned>(topk)));
+    __syncthreads();                     // every thread has read the first masks
+    if (lane == 0) masks[wv] = mine;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < 4; ++w) m[w] = masks[w];
   }
-  t = count_ge(t | 1u) >= topk ? t | 1u : t;
-  const unsigned long long gt0 = __builtin_amdgcn_ballot_w64(hk[0] > t), gt1 = __builtin_amdgcn_ballot_w64(hk[1] > t);
-  const unsigned long long eq0 = __builtin_amdgcn_ballot_w64(hk[0] == t);
-  const int need = topk - __popcll(gt0) - __popcll(gt1);
-  auto below = [&](unsigned long long mask) {
-    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(mask >> 32),
-                                                      __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(mask), 0u)));
-  };
-  const unsigned long long eq1 = __builtin_amdgcn_ballot_w64(hk[1] == t);
-  const int e0 = __popcll(eq0);
-  const unsigned long long s0 = gt0 | __builtin_amdgcn_ballot_w64(hk[0] == t && below(eq0) < need);
-  const unsigned long long s1 = gt1 | __builtin_amdgcn_ballot_w64(hk[1] == t && e0 + below(eq1) < need);
-  if ((s0 >> lane) & 1ull) sel[below(s0)] = lane;
-  if ((s1 >> lane) & 1ull) sel[__popcll(s0) + below(s1)] = 64 + lane;
+  unsigned below = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) below += w < wv ? __popc(m[w]) : 0u;
+  const unsigned mw = m[wv];
+  if (lane < 32 && ((mw >> lane) & 1u)) sel[below + __builtin_amdgcn_mbcnt_lo(mw, 0u)] = i;
+  if (want < 0) return -1;
+  // the want-th kept block: its word, then its bit (the lane whose count of
+  // kept bits below it is the remainder)
+  int w = 0, n = want;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int c = __popc(m[w]);
+    if (n >= c) { n -= c; ++w; }
+  }
+  const unsigned word = m[w];
+  const unsigned long long hit = __builtin_amdgcn_ballot_w64(
+      lane < 32 && ((word >> lane) & 1u) && __builtin_amdgcn_mbcnt_lo(word, 0u) == static_cast<unsigned>(n));
+  return 32 * w + static_cast<int>(__builtin_ctzll(hit));
 }
 
 // keys[j] = sel_key(score_j, j) for every eligible block j in the one-row
@@ -570,13 +617,15 @@ __device__ __forceinline__ void select_from_dsc(const float4* dsc, int n_elig, i
 // than in all 16 of its lanes. kp[u] comes in holding pass u's keys; later
 // rounds load one round ahead. Block new_j's key is new_key (LDS). Ends with
 // the keys padded with zeros to a multiple of 32 (after a barrier the caller
-// issues). Given sel, when one round of 128 holds every eligible block, wave 0
-// selects the top-k from the round's dot products instead (select_from_dsc)
-// and the call returns true, with sel written and no keys.
+// issues). Given sel, when one round of 128 holds every eligible block, the
+// workgroup (NT = 256) selects the top-k from the round's dot products instead
+// (select128) and the call returns true, with sel written (published by the
+// caller's next barrier) and *blk = the want-th selected block in block order
+// (want >= 0); keys[0 .. 128) and the 1 KB after them are then scratch.
 template <int NT, int PRE>
 __device__ bool score_block_rounds(const float* s_iq, const float* new_key, const float* bk, int n_elig, int new_j,
                                    int idx_heads, unsigned long long* keys, float4* dsc, float (&kp)[PRE][8],
-                                   int topk = 0, int* sel = nullptr) {
+                                   int topk = 0, int* sel = nullptr, int want = -1, int* blk = nullptr) {
   constexpr int PASS = NT / SCORE_LANES;
   constexpr int ROUND = PASS * PRE;
   const int tid = threadIdx.x, jl = tid >> 4, m = tid & 15;
@@ -614,9 +663,12 @@ __device__ bool score_block_rounds(const float* s_iq, const float* new_key, cons
     }
     QM_PHASE(13);
     __syncthreads();
-    if (sel && n_elig <= ROUND && ROUND == 128) {
-      if (tid < 64) select_from_dsc(dsc, n_elig, idx_heads, topk, sel);
-      return true;
+    QM_PHASE(14);
+    if constexpr (NT == 256 && ROUND == 128) {
+      if (sel && n_elig <= ROUND) {
+        *blk = select128(dsc, n_elig, idx_heads, topk, sel, keys, reinterpret_cast<unsigned*>(keys + ROUND), want);
+        return true;
+      }
     }
     for (int t = tid; t < ROUND && r0 + t < n_elig; t += NT) {
       const float4 dd = dsc[t];
@@ -1853,6 +1905,18 @@ __device__ __forceinline__ void item_span(int it, int n_blk_items, int gpb, int 
   }
 }
 
+// item_span with the item's selected block given (blk, for it < n_blk_items)
+__device__ __forceinline__ void item_span_blk(int it, int n_blk_items, int gpb, int ratio, int ts, int p, int blk,
+                                              int& t0, int& lo, int& hi) {
+  if (it < n_blk_items) {
+    const int bs = blk * ratio;
+    if (ratio >= 32) { t0 = bs + (it % gpb) * 32; lo = 0; hi = 32; }
+    else { t0 = bs & ~31; lo = bs - t0; hi = lo + ratio; }
+  } else {
+    t0 = (ts & ~31) + (it - n_blk_items) * 32; lo = max(ts - t0, 0); hi = min(p + 1 - t0, 32);
+  }
+}
+
 // attention items of a query at position p (the selected blocks' 32-token
 // groups, then the tail's)
 struct ItemCount {
@@ -2173,23 +2237,29 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
 
   // ---- 2. block scores and top-k (ties to the lower index); the item of a
   // tail workgroup does not depend on them
+  // The item's block is known without reading sel back when the selection
+  // is select128's (it returns the block) or there is none (block i is the
+  // i-th); after the counting ranks of rank_topk, sel is read behind a barrier.
   QM_PHASE(2);
+  int blk = blk_item && !scoring ? item / ic.gpb : -1;
   if (scoring && (blk_item || item == 0)) {
     if (!score_block_rounds<DEC_NT, score_pre<DEC_NT>()>(sh.iq, sh.newkey, bk, n_elig, j_new, A.idx_heads, sh.key,
-                                                         sh.dsc, kp, topk, sh.sel)) {
+                                                         sh.dsc, kp, topk, sh.sel, blk_item ? item / ic.gpb : -1,
+                                                         &blk)) {
       __syncthreads();
       QM_PHASE(3);
       rank_topk<DEC_NT, DEC_MAX_TOPK>(sh.key, n_elig, topk, sh.sel, sh.rscr);
+      __syncthreads();
+      blk = blk_item ? sh.sel[item / ic.gpb] : -1;
     }
   } else if (!scoring) {
     for (int i = tid; i < n_elig; i += DEC_NT) sh.sel[i] = i;
   }
-  __syncthreads();
 
   // ---- 3. the item's keys/values in flight while the query heads and key are normed
   QM_PHASE(4);
   int t0, lo, hi;
-  item_span(item, ic.n_blk_items, ic.gpb, ratio, ic.ts, p, sh.sel, t0, lo, hi);
+  item_span_blk(item, ic.n_blk_items, ic.gpb, ratio, ic.ts, p, blk, t0, lo, hi);
   const int page = sh.pages[t0 / A.page_size], row0 = t0 % A.page_size;
   const long pbase = ((long)page * A.hkv + g) * A.page_size * QSA_D;
   // Every earlier load has landed by now (the selection used them): saying so

@@ -13,7 +13,7 @@ namespace {
 constexpr int MAX_DEVICES = 64;
 
 struct CapacityCache {
-  const void* kernel;
+  std::atomic<const void*> kernel;
   std::atomic<int> value[MAX_DEVICES];
 };
 
@@ -33,11 +33,14 @@ int qm_resident_workgroups(const void* kernel, int block_threads, size_t dyn_lds
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return qm_fail(QM_ERR_LAUNCH, "no current HIP device");
   // one cache slot per kernel, claimed on first use (lookups are lock-free;
-  // two threads claiming at once may both compute the same value)
-  int n = g_n_kernels.load(std::memory_order_acquire);
+  // two threads claiming at once may both compute the same value). A slot's
+  // kernel is published with release order after its values are cleared, so
+  // a reader that sees the kernel sees cleared or computed values; a slot
+  // still being claimed reads as empty (nullptr) and costs a recompute.
+  const int n = g_n_kernels.load(std::memory_order_acquire);
   CapacityCache* slot = nullptr;
-  for (int i = 0; i < n; ++i)
-    if (g_capacity[i].kernel == kernel) slot = &g_capacity[i];
+  for (int i = 0; i < n && i < MAX_KERNELS; ++i)
+    if (g_capacity[i].kernel.load(std::memory_order_acquire) == kernel) slot = &g_capacity[i];
   if (slot) {
     const int v = slot->value[dev].load(std::memory_order_relaxed);
     if (v > 0) { *out = v; return QM_OK; }
@@ -52,8 +55,8 @@ int qm_resident_workgroups(const void* kernel, int block_threads, size_t dyn_lds
     static std::atomic<int> claim{0};
     int mine = claim.fetch_add(1);
     if (mine < MAX_KERNELS) {
-      g_capacity[mine].kernel = kernel;
       for (int d = 0; d < MAX_DEVICES; ++d) g_capacity[mine].value[d].store(0, std::memory_order_relaxed);
+      g_capacity[mine].kernel.store(kernel, std::memory_order_release);
       slot = &g_capacity[mine];
       g_n_kernels.fetch_add(1, std::memory_order_release);
     }

@@ -136,7 +136,7 @@ class MixDecoder:
     first when the cache draws its pages from a pool."""
 
     def __init__(self, model, cache, layers=None, dtype=torch.bfloat16, min_bucket: int = 1024, positions=None,
-                 check_every: int = 64):
+                 check_every: int = 0):
         c = model.config
         self.model, self.cache, self.dtype = model, cache, dtype
         self.layers = list(range(len(cache.layers))) if layers is None else list(layers)
@@ -159,8 +159,9 @@ class MixDecoder:
         self.positions = torch.tensor(rows, dtype=torch.int32, device=dev)
         self._steps = {}
         self._graphs = {}
-        # every check_every steps (0: never by itself) the decode kernels'
-        # hand-off counters are read back (a sync) and a fault raises QmError
+        # every check_every steps (default 0: only when check_handoffs is
+        # called) the decode kernels' hand-off counters are read back, which
+        # synchronises the stream, and a fault raises QmError
         self.check_every = check_every
         self._since_check = 0
 
@@ -209,10 +210,17 @@ class MixDecoder:
         self.positions.add_(1)
 
     def seek(self, positions) -> None:
-        """Set every row's position (an int, or one per row) on the host and in
-        the device tensor the graphs read, without touching the caches: a
-        replay then runs at those positions (the bench repeats one position
-        this way; a server rewinds a row it refilled)."""
+        """Set every row's position (an int, or one per row) on the host, in
+        the device tensor the graphs read, and in each layer cache's
+        bookkeeping (``n_tokens`` becomes the largest row position, pooled
+        blocks past it stop counting, ``slot_tokens`` follows the rows). The
+        cache contents (pages, keys, states, rings) are not touched: a replay
+        then runs at those positions (the bench repeats one position this way;
+        a server rewinds a row it refilled). A rewind is always safe. A seek
+        forward past the old ``n_tokens`` declares the history up to the new
+        position present: the caller must have filled it (K/V pages, raw
+        indexer keys), since the layer methods (``step_n``) then pool blocks
+        from those raw keys and attend to those pages."""
         rows = [int(positions)] * len(self.row_positions) if isinstance(positions, int) else [int(p) for p in positions]
         if len(rows) != len(self.row_positions) or min(rows) < 0:
             raise ValueError(f"need {len(self.row_positions)} non-negative row positions, got {rows}")

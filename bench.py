@@ -7,7 +7,12 @@ selection, paged GQA attention over the 2049 selected keys, sigmoid gate) plus
 one DeltaNet decode core (conv ring, gates, delta-rule update of the
 [32,128,128] float32 state, gated norm). Inputs are synthetic (seeded), already
 resident in HBM, and rotated over enough independent layer instances that the
-data touched per rotation exceeds twice the 256 MB Infinity Cache.
+data touched per rotation exceeds twice the 256 MB Infinity Cache. Every timed
+figure starts cold: 768 MB of other traffic passes through the caches right
+before the timed steps, the per-launch kernel times (`*_cold`) and the prefill
+calls, as a layer's data is cold when a decode step reaches it after the other
+layers' weights have streamed through. Back-to-back warm launch times
+(`*_warm`) are reported beside them.
 
 Prints one JSON line (see the driver contract). Besides the headline, its
 "configs" list holds every workload of the benchmark's configuration set, each
@@ -163,11 +168,31 @@ def weights_store(dtype):
     return Store()
 
 
-def time_steps(instances, steps, warmup, stream):
+FLUSH_MB = 768      # other traffic streamed through the caches before a cold timing (3x the Infinity Cache)
+
+
+class Flusher:
+    """A buffer of FLUSH_MB that one elementwise kernel reads and writes: after
+    it, the caches (L2 and the 256 MB Infinity Cache) hold none of the data a
+    timed launch reads."""
+
+    def __init__(self, dev):
+        import torch
+        self.buf = torch.ones(FLUSH_MB << 18, device=dev, dtype=torch.float32)
+
+    def __call__(self):
+        self.buf.mul_(1.0)
+
+
+def time_steps(instances, steps, warmup, stream, flush):
+    """The steps launched eagerly from Python (two launches each): `warmup`
+    steps on the last instances, the caches flushed, then exactly `steps`
+    steps from instance 0 on, timed between synchronisations."""
     import torch
     n = len(instances)
     for i in range(warmup):
-        instances[i % n].step(stream)
+        instances[(n - 1 - i) % n].step(stream)
+    flush()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
@@ -176,28 +201,35 @@ def time_steps(instances, steps, warmup, stream):
     return (time.perf_counter() - t0) / steps
 
 
-def time_graph_steps(instances, steps, warmup):
+def time_graph_steps(instances, steps, warmup, flush):
     """The same steps launched from HIP graphs, as a serving loop launches a
-    captured decode step: `warmup` steps, then exactly `steps` steps (step i
-    on instance i mod n, two launches each) captured in one graph whose single
-    replay is timed between synchronisations. The host's launch cost (about
-    5-10 us per launch from Python, which bounds the eager loop on some hosts)
-    stays out of the figure; the kernels and the gaps between them stay in."""
+    captured decode step. `steps` steps (step i on instance i mod n, two
+    launches each) are captured in one graph, and `warmup` steps on the last
+    instances (disjoint from the timed ones while steps + warmup <= n) in
+    another. The timed graph is replayed once untimed (a graph's first replay
+    also uploads it), then the warmup graph, then FLUSH_MB of other traffic
+    empties the caches, so every timed step reads its instance from HBM; the
+    timed graph's single replay is then timed between synchronisations. The
+    host's launch cost stays out of the figure; the kernels, the gaps between
+    them and the replay's own start stay in."""
     import torch
     side = torch.cuda.Stream()
     n = len(instances)
 
-    def capture(count):
+    def capture(count, first, stride):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(side):
             with torch.cuda.graph(g, stream=side):
                 for i in range(count):
-                    instances[i % n].step(side.cuda_stream)
+                    instances[(first + stride * i) % n].step(side.cuda_stream)
         return g
 
-    gw, g = capture(max(1, warmup)), capture(steps)
+    g = capture(steps, 0, 1)
+    gw = capture(max(1, warmup), n - 1, -1)
     torch.cuda.synchronize()
+    g.replay()
     gw.replay()
+    flush()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     g.replay()
@@ -207,19 +239,23 @@ def time_graph_steps(instances, steps, warmup):
     return sec
 
 
+def kernel_parts():
+    return {"qsa_decode": lambda x, s: x.qsa.decode(x.qg, x.k, x.v, x.iq, x.ik, s),
+            "dn_decode": lambda x, s: x.dn.run(x.qkv, x.z, x.a, x.b, s)}
+
+
 def time_kernels(instances, reps, stream_obj, batches=5):
-    """Average duration of each entry point's launches: `reps` back-to-back
-    launches (rotating over the instances) captured in one HIP graph, replayed
+    """Average duration of each entry point's launches back to back (warm: the
+    data a launch reads may sit in the Infinity Cache): `reps` launches
+    (rotating over the instances) captured in one HIP graph, replayed
     `batches` times between HIP events on the launch stream, divided by
     `reps`; the median over the replays. A graph keeps the host's launch cost
     (about 5 us per launch from Python) out of the figure."""
     import torch
     n = len(instances)
-    parts = {"qsa_decode": lambda x, s: x.qsa.decode(x.qg, x.k, x.v, x.iq, x.ik, s),
-             "dn_decode": lambda x, s: x.dn.run(x.qkv, x.z, x.a, x.b, s)}
     side = torch.cuda.Stream()
     out = {}
-    for name, fn in parts.items():
+    for name, fn in kernel_parts().items():
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(side):
             with torch.cuda.graph(g, stream=side):
@@ -242,13 +278,14 @@ def time_kernels(instances, reps, stream_obj, batches=5):
     return out
 
 
-def time_cold(instances, fn, flush_mb=768, launches=4, reps=20):
-    """Average duration of `launches` back-to-back launches that start after
-    `flush_mb` of other data has streamed through the caches (so their inputs
-    come from HBM): a graph of [flush, launches] minus a graph of [flush]."""
+def time_cold(instances, fn, flush, launches=8, reps=15):
+    """Average duration of `launches` back-to-back launches, each on its own
+    instance, that start right after FLUSH_MB of other traffic (so everything
+    they read comes from HBM): the event time of a graph of [flush, launches]
+    minus that of a graph of [flush], medians over `reps` replays."""
     import torch
-    big = torch.ones(flush_mb << 18, device=instances[0].qkv.device, dtype=torch.float32)
     side = torch.cuda.Stream()
+    n = len(instances)
 
     def replay_us(body):
         g = torch.cuda.CUDAGraph()
@@ -269,10 +306,9 @@ def time_cold(instances, fn, flush_mb=768, launches=4, reps=20):
         del g
         return statistics.median(ts)
 
-    flush = replay_us(lambda s: big.mul_(1.0))
-    both = replay_us(lambda s: (big.mul_(1.0), [fn(instances[i % len(instances)], s) for i in range(launches)]))
-    del big
-    return (both - flush) / launches
+    only = replay_us(lambda s: flush())
+    both = replay_us(lambda s: (flush(), [fn(instances[i % n], s) for i in range(launches)]))
+    return (both - only) / launches
 
 
 def host_cpu() -> dict:
@@ -450,14 +486,16 @@ def run_decode(qm, dev, pos, steps, warmup, instances=0, graphs=True):
     n_inst = instances or max(8, int(2 * 256e6 / touched) + 1)
     insts = [Instance(qm, model, pos, max_ctx, 1000 + i) for i in range(n_inst)]
     stream = torch.cuda.current_stream(dev)
+    flush = Flusher(dev)
     torch.cuda.synchronize()
-    sec = time_steps(insts, steps, warmup, stream.cuda_stream)
-    kern = time_kernels(insts, max(50, min(steps, 400)), stream)
-    # the DeltaNet launches alone rotate less than the Infinity Cache holds:
-    # also their duration with the state in HBM only
-    kern["dn_decode_hbm"] = time_cold(insts, lambda x, s: x.dn.run(x.qkv, x.z, x.a, x.b, s))
-    gsec = time_graph_steps(insts, steps, warmup) if graphs else None
-    del insts
+    sec = time_steps(insts, steps, warmup, stream.cuda_stream, flush)
+    warm = time_kernels(insts, max(50, min(steps, 400)), stream)
+    kern = {}
+    for name, fn in kernel_parts().items():
+        kern[name + "_cold"] = time_cold(insts, fn, flush)
+        kern[name + "_warm"] = warm[name]
+    gsec = time_graph_steps(insts, steps, warmup, flush) if graphs else None
+    del insts, flush
     torch.cuda.synchronize()
     return {"pos": pos, "us_step": sec * 1e6, "kernel_us": kern, "instances": n_inst, "touched": touched,
             "max_ctx": max_ctx, "graph_us_step": None if gsec is None else gsec * 1e6}
@@ -503,12 +541,16 @@ class PrefillInstance:
 
 
 def run_prefill(qm, dev, reps=20, n_inst=4):
+    """Event time of each layer's chunk call, each call starting after
+    FLUSH_MB of other traffic (its K/V, keys and state come from HBM), median
+    over `reps` calls rotating over `n_inst` instances."""
     import torch
     model = qm.Qwen4MixModel(qm.MixConfig(), weights_store(torch.bfloat16), device=dev, max_ctx=PREFILL_CTX)
     insts = [PrefillInstance(qm, model, 2000 + i) for i in range(n_inst)]
     for x in insts:          # first calls pool the block cache and size the workspaces
         x.qsa()
         x.dn()
+    flush = Flusher(dev)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     out = {}
@@ -516,12 +558,13 @@ def run_prefill(qm, dev, reps=20, n_inst=4):
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
         for i in range(reps):
             x = insts[i % n_inst]
+            flush()
             evs[i][0].record(stream)
             getattr(x, name)()
             evs[i][1].record(stream)
         torch.cuda.synchronize()
         out[name] = statistics.median(sorted(a.elapsed_time(b) for a, b in evs))   # ms
-    del insts
+    del insts, flush
     torch.cuda.synchronize()
     flops = qsa_chunk_flops(PREFILL_START, PREFILL_LEN)
     dflops = dn_rule_flops(PREFILL_LEN)
@@ -812,10 +855,13 @@ def main():
     kern = head["kernel_us"]
     bytes_step = touched
     kb = {"qsa_decode": qsa_bytes(pos), "dn_decode": DN_BYTES}
-    dominant = max(kb, key=lambda k: kern[k])
-    achieved = kb[dominant] / (kern[dominant] * 1e-6) / 1e9
+    # the dominant kernel and its roofline from the cold launches (data from HBM)
+    dominant = max(kb, key=lambda k: kern[k + "_cold"])
+    achieved = kb[dominant] / (kern[dominant + "_cold"] * 1e-6) / 1e9
+    gap = us_step - kern["qsa_decode_cold"] - kern["dn_decode_cold"]
     print(f"[bench] step {us_step:.2f} us from a graph (eager launches {head['us_step']:.2f} us); kernels (us): " +
-          ", ".join(f"{k} {v:.2f}" for k, v in kern.items()), file=sys.stderr)
+          ", ".join(f"{k} {v:.2f}" for k, v in kern.items()) + f"; step minus cold kernels {gap:.2f}",
+          file=sys.stderr)
     if args.copy_mb > 0:
         src = torch.ones(args.copy_mb << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -835,9 +881,12 @@ def main():
                      "selection": "on" if (p + 1) // 64 > 32 else "off (below the budget)",
                      "us_per_token": round(r["graph_us_step"], 3),
                      "eager_us_per_token": round(r["us_step"], 3),
-                     "qsa_us": round(r["kernel_us"]["qsa_decode"], 3), "dn_us": round(r["kernel_us"]["dn_decode"], 3),
-                     "qsa_gbs": round(qb / (r["kernel_us"]["qsa_decode"] * 1e-6) / 1e9, 1),
-                     "dn_gbs": round(DN_BYTES / (r["kernel_us"]["dn_decode"] * 1e-6) / 1e9, 1),
+                     "qsa_us": round(r["kernel_us"]["qsa_decode_cold"], 3),
+                     "dn_us": round(r["kernel_us"]["dn_decode_cold"], 3),
+                     "qsa_warm_us": round(r["kernel_us"]["qsa_decode_warm"], 3),
+                     "dn_warm_us": round(r["kernel_us"]["dn_decode_warm"], 3),
+                     "qsa_gbs": round(qb / (r["kernel_us"]["qsa_decode_cold"] * 1e-6) / 1e9, 1),
+                     "dn_gbs": round(DN_BYTES / (r["kernel_us"]["dn_decode_cold"] * 1e-6) / 1e9, 1),
                      "step_mb": round((qb + DN_BYTES) / 1e6, 3),
                      "step_hbm_frac": round((qb + DN_BYTES) / (r["graph_us_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
             if not args.no_cpu:
@@ -887,12 +936,14 @@ def main():
         "config": {"workload": f"QSA selection-on decode at pos {pos} (ctx {max_ctx}, top-32 of 64-token "
                                f"blocks) + one Gated DeltaNet decode step, batch 1",
                    "position": pos, "batch": 1, "instances_rotated": n_inst,
-                   "launch": "steps replayed from a captured HIP graph",
+                   "launch": "steps replayed from a captured HIP graph, caches flushed before the timed replay",
                    "eager_us_per_step": round(head["us_step"], 3),
                    "step_bytes": bytes_step,
                    "step_hbm_frac": round(bytes_step / sec / 1e9 / HBM_PEAK_GBS, 4),
-                   "kernel_us": {k: round(v, 3) for k, v in kern.items()}},
-        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                   "kernel_us": {k: round(v, 3) for k, v in kern.items()},
+                   "step_minus_cold_kernels_us": round(gap, 3)},
+        "roofline": {"bound": "hbm", "kernel": dominant, "launch": "cold (caches flushed, data from HBM)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(pos, dominant)},
         "cpu_baseline": cpu,

@@ -142,10 +142,17 @@ class Instance:
         self.dn = plan.DnDecodePlan(model, self.cache, 0, bf)
         self.qsa.positions.fill_(pos)
         self.dn.positions.fill_(pos)
+        # the same two launches with their arguments converted once (the eager loop's launcher)
+        self.bound = [self.qsa.bind(self.qg, self.k, self.v, self.iq, self.ik),
+                      self.dn.bind(self.qkv, self.z, self.a, self.b)]
 
     def step(self, stream):
         self.qsa.run(self.qg, self.k, self.v, self.iq, self.ik, stream)
         self.dn.run(self.qkv, self.z, self.a, self.b, stream)
+
+    def step_bound(self, stream):
+        for c in self.bound:
+            c(stream)
 
 
 def weights_store(dtype):
@@ -185,18 +192,20 @@ class Flusher:
 
 
 def time_steps(instances, steps, warmup, stream, flush):
-    """The steps launched eagerly from Python (two launches each): `warmup`
-    steps on the last instances, the caches flushed, then exactly `steps`
-    steps from instance 0 on, timed between synchronisations."""
+    """The steps launched eagerly from Python, two launches each through their
+    prebound calls (plan.BoundCall: arguments converted once, so the host's
+    cost per launch is one foreign call): `warmup` steps on the last
+    instances, the caches flushed, then exactly `steps` steps from instance 0
+    on, timed between synchronisations."""
     import torch
     n = len(instances)
     for i in range(warmup):
-        instances[(n - 1 - i) % n].step(stream)
+        instances[(n - 1 - i) % n].step_bound(stream)
     flush()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        instances[i % n].step(stream)
+        instances[i % n].step_bound(stream)
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / steps
 
@@ -817,14 +826,41 @@ def run_stack(qm, dev, pos=8128, n_layers=STACK_LAYERS, steps=30, warmup=5):
         out[mode] = (time.perf_counter() - t0) / steps * 1e6
         for l in range(n_layers):
             cache[l].n_tokens = pos
+    # the verify step: 4 tokens of the sequence replayed from one captured
+    # graph (every per-token stage over 4 rows, the cores on their chunk
+    # paths), against 4 single-token graph steps (out["graph"] each)
+    x4 = torch.randn(1, 4, HC_STREAMS * HIDDEN, generator=g, device=dev).to(bf)
+    for _ in range(warmup):
+        dec.seek(pos)
+        dec.step_n_graph(x4)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dec.seek(pos)
+        dec.step_n_graph(x4)
+    torch.cuda.synchronize()
+    out["verify4"] = (time.perf_counter() - t0) / steps * 1e6
+    for l in range(n_layers):
+        cache[l].n_tokens = pos
     nbytes = stack_bytes(pos, n_layers)
     res = {"layers": n_layers, "pos": pos, "mb_per_token": round(nbytes / 1e6, 1),
            "eager_us": round(out["eager"], 1), "graph_us": round(out["graph"], 1),
            "graph_gbs": round(nbytes / (out["graph"] * 1e-6) / 1e9, 1),
-           "graph_hbm_frac": round(nbytes / (out["graph"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+           "graph_hbm_frac": round(nbytes / (out["graph"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+           "verify_k4_graph_us": round(out["verify4"], 1), "four_graph_steps_us": round(4 * out["graph"], 1)}
     del dec, cache, model
     torch.cuda.synchronize()
     return res
+
+
+def best_launch(r):
+    """(us per step, how launched): the faster of the graph replay and the
+    eager loop of prebound calls, both timed over the same steps from cold
+    caches."""
+    g, e = r["graph_us_step"], r["us_step"]
+    if g is not None and g <= e:
+        return g, "steps replayed from one captured HIP graph, caches flushed before the timed replay"
+    return e, "steps launched eagerly through prebound calls, caches flushed before the timed steps"
 
 
 def main():
@@ -847,10 +883,12 @@ def main():
     head = run_decode(qm, dev, pos, args.steps, args.warmup, args.instances)
     max_ctx, n_inst, touched = head["max_ctx"], head["instances"], head["touched"]
     print(f"[bench] {n_inst} instances, {n_inst * touched / 1e6:.0f} MB touched per rotation", file=sys.stderr)
-    # the step as a serving loop runs it: launched from a captured graph (the
-    # eager loop's figure, bound by Python's launch cost on some hosts, is
-    # reported beside it)
-    us_step = head["graph_us_step"]
+    # the step as a serving loop runs it: replayed from a captured graph, or
+    # launched eagerly through prebound calls; both time the same steps from
+    # cold caches, and the faster is the value (a graph replay starts ~30 us
+    # after its launch on this runtime; an eager loop keeps up with the GPU
+    # only where the host's foreign calls are fast)
+    us_step, launch = best_launch(head)
     sec = us_step * 1e-6
     kern = head["kernel_us"]
     bytes_step = touched
@@ -859,7 +897,7 @@ def main():
     dominant = max(kb, key=lambda k: kern[k + "_cold"])
     achieved = kb[dominant] / (kern[dominant + "_cold"] * 1e-6) / 1e9
     gap = us_step - kern["qsa_decode_cold"] - kern["dn_decode_cold"]
-    print(f"[bench] step {us_step:.2f} us from a graph (eager launches {head['us_step']:.2f} us); kernels (us): " +
+    print(f"[bench] step {us_step:.2f} us (graph {head['graph_us_step']:.2f}, eager {head['us_step']:.2f}); kernels (us): " +
           ", ".join(f"{k} {v:.2f}" for k, v in kern.items()) + f"; step minus cold kernels {gap:.2f}",
           file=sys.stderr)
     if args.copy_mb > 0:
@@ -879,7 +917,8 @@ def main():
             qb = qsa_bytes(p)
             entry = {"workload": f"decode step at pos {p}" + (" (headline)" if p == pos else ""), "pos": p,
                      "selection": "on" if (p + 1) // 64 > 32 else "off (below the budget)",
-                     "us_per_token": round(r["graph_us_step"], 3),
+                     "us_per_token": round(best_launch(r)[0], 3),
+                     "graph_us_per_token": round(r["graph_us_step"], 3),
                      "eager_us_per_token": round(r["us_step"], 3),
                      "qsa_us": round(r["kernel_us"]["qsa_decode_cold"], 3),
                      "dn_us": round(r["kernel_us"]["dn_decode_cold"], 3),
@@ -888,7 +927,7 @@ def main():
                      "qsa_gbs": round(qb / (r["kernel_us"]["qsa_decode_cold"] * 1e-6) / 1e9, 1),
                      "dn_gbs": round(DN_BYTES / (r["kernel_us"]["dn_decode_cold"] * 1e-6) / 1e9, 1),
                      "step_mb": round((qb + DN_BYTES) / 1e6, 3),
-                     "step_hbm_frac": round((qb + DN_BYTES) / (r["graph_us_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                     "step_hbm_frac": round((qb + DN_BYTES) / (best_launch(r)[0] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
             if not args.no_cpu:
                 entry["cpu_baseline"] = cpu_baseline(p, args.cpu_seconds)
             configs.append(entry)
@@ -936,7 +975,8 @@ def main():
         "config": {"workload": f"QSA selection-on decode at pos {pos} (ctx {max_ctx}, top-32 of 64-token "
                                f"blocks) + one Gated DeltaNet decode step, batch 1",
                    "position": pos, "batch": 1, "instances_rotated": n_inst,
-                   "launch": "steps replayed from a captured HIP graph, caches flushed before the timed replay",
+                   "launch": launch,
+                   "graph_us_per_step": round(head["graph_us_step"], 3),
                    "eager_us_per_step": round(head["us_step"], 3),
                    "step_bytes": bytes_step,
                    "step_hbm_frac": round(bytes_step / sec / 1e9 / HBM_PEAK_GBS, 4),

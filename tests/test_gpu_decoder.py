@@ -376,3 +376,95 @@ def test_rows_at_different_positions_match_single_rows(stack):
     assert dec.positions.cpu().tolist() == list(ROWS) and dec.position == max(ROWS)
     dec.seek(500)
     assert dec.positions.cpu().tolist() == [500, 500] and dec.row_positions == [500, 500]
+
+
+def _dn_state(cache):
+    return [(lc.recurrent_state.clone(), lc.conv_ring.clone()) for lc in cache.layers if lc.recurrent_state is not None]
+
+
+def test_captured_step_n_matches_eager_step_n(stack):
+    """The verify step replayed from its graph runs the layer methods' kernels:
+    the same residual rows and caches, bit for bit, over two replays."""
+    qm, model, cache = stack
+    snap = snapshot(cache)
+    xs = inputs(2, k=3, seed=31)
+    print("eager step_n k=3, twice", flush=True)
+    dec = qm.decoder.MixDecoder(model, cache)
+    eager = [dec.step_n(x).clone() for x in xs]
+    torch.cuda.synchronize()
+    after_eager = snapshot(cache)
+    restore(cache, snap)
+    print("captured step_n k=3, twice", flush=True)
+    dec = qm.decoder.MixDecoder(model, cache)
+    for x, want in zip(xs, eager):
+        got = dec.step_n_graph(x).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+    assert dec.position == START + 6 and int(dec.positions.item()) == START + 6
+    for l, ((a, na, ba), (b, nb, bb)) in enumerate(zip(after_eager, snapshot(cache))):
+        assert na == nb == START + 6 and ba == bb
+        for f in a:
+            assert torch.equal(a[f], b[f]), f"layer {l} {f}"
+    restore(cache, snap)
+
+
+def test_rewound_verify_step_matches_a_fresh_one(stack):
+    """Speculation: snapshot, verify k = 4 drafts from the graph, restore, then
+    commit j = 2 of them from the graph of j: the residual rows, the DeltaNet
+    states and rings and every K/V page row up to the new position equal, bit
+    for bit, a decoder that verified only those 2; a single graph step after
+    either agrees bit for bit too. The snapshot reuses its buffers on the
+    second call."""
+    qm, model, cache = stack
+    snap = snapshot(cache)
+    x4 = inputs(1, k=4, seed=41)[0]
+    x1 = inputs(1, k=1, seed=42)[0]
+    print("verify 4, rewind, commit 2", flush=True)
+    dec = qm.decoder.MixDecoder(model, cache)
+    keep = dec.snapshot()
+    ptrs = {n: t.data_ptr() for n, t in keep["tensors"].items()}
+    dec.step_n_graph(x4)
+    assert dec.position == START + 4
+    dec.restore(keep)
+    assert dec.position == START and int(dec.positions.item()) == START
+    assert all(cache[l].n_tokens == START for l in range(N_LAYERS))
+    got2 = dec.step_n_graph(x4[:, :2]).clone()
+    got_state = _dn_state(cache)
+    got_step = dec.step(x1).clone()
+    torch.cuda.synchronize()
+    got_after = snapshot(cache)
+    got_kv = [(lc.keys.clone(), lc.values.clone()) for lc in cache.layers if lc.k_pool is not None]
+    keep2 = dec.snapshot(into=keep)
+    assert keep2 is keep and all(t.data_ptr() == ptrs[n] for n, t in keep["tensors"].items())
+
+    restore(cache, snap)
+    print("fresh commit 2", flush=True)
+    dec = qm.decoder.MixDecoder(model, cache)
+    want2 = dec.step_n_graph(x4[:, :2]).clone()
+    want_state = _dn_state(cache)
+    want_step = dec.step(x1).clone()
+    torch.cuda.synchronize()
+    want_after = snapshot(cache)
+    want_kv = [(lc.keys.clone(), lc.values.clone()) for lc in cache.layers if lc.k_pool is not None]
+    assert torch.equal(got2, want2)
+    for (a, b), (c, d) in zip(got_state, want_state):
+        assert torch.equal(a, c) and torch.equal(b, d)
+    assert torch.equal(got_step, want_step)
+    # K/V up to the committed position (rows past it hold the rejected drafts', never read)
+    for (a, b), (c, d) in zip(got_kv, want_kv):
+        assert a.shape[2] == START + 3 and torch.equal(a, c) and torch.equal(b, d)
+    n_blocks = (START + 3) // model.config.indexer_compress_ratio
+    for l, ((a, na, ba), (b, nb, bb)) in enumerate(zip(got_after, want_after)):
+        assert na == nb == START + 3 and ba == bb
+        for f in a:
+            if f in ("k_pool", "v_pool"):
+                continue
+            if f == "raw_keys":
+                assert torch.equal(a[f][:, :START + 3], b[f][:, :START + 3]), f"layer {l} raw_keys"
+            elif f == "block_keys":
+                # a block a rejected draft completed is pooled again when a token completes it
+                assert torch.equal(a[f][:, :n_blocks], b[f][:, :n_blocks]), f"layer {l} block_keys"
+            else:
+                assert torch.equal(a[f], b[f]), f"layer {l} {f}"
+    dec.check_handoffs()
+    restore(cache, snap)

@@ -18,6 +18,26 @@ import torch
 from . import native
 
 
+class BoundCall:
+    """One entry point with every argument but the trailing stream converted
+    to its ctypes type once: a call is one foreign call and an error check,
+    for a host loop that launches the same step many times (a plan's buffers
+    never move). The referenced geometry and tensors must outlive it."""
+
+    def __init__(self, name: str, *args):
+        self.name = name
+        self.fn = getattr(native.load(), name)
+        types = self.fn.argtypes[:-1]
+        if len(args) != len(types):
+            raise ValueError(f"{name} takes {len(types)} arguments before the stream, got {len(args)}")
+        self.args = tuple(a if not isinstance(a, int) and a is not None else t(a) for a, t in zip(args, types))
+
+    def __call__(self, stream: int) -> None:
+        rc = self.fn(*self.args, stream)
+        if rc:
+            raise native.QmError(f"{self.name} failed ({rc}): {native.load().qm_last_error().decode(errors='replace')}")
+
+
 class DnDecodePlan:
     """One DeltaNet decode step of ``layer`` for a ``batch``-row cache."""
 
@@ -43,15 +63,21 @@ class DnDecodePlan:
         return native.dn_decode_faults(self.geom.batch, c.linear_num_v_heads, c.linear_head_dim, self.ws, reset,
                                        f"layer {self.layer}", self.model.device)
 
-    def run(self, qkv, z, a, b, stream=None):
+    def _args(self, qkv, z, a, b):
         w, lc = self.w, self.lc
-        native.call("qm_dn_decode", ctypes.byref(self.geom), qkv.data_ptr(), z.data_ptr(), a.data_ptr(),
-                    b.data_ptr(), w["ssm_a"].data_ptr(), w["ssm_dt.bias"].data_ptr(),
-                    w["ssm_conv1d.weight"].data_ptr(), w["ssm_norm.weight"].data_ptr(), self.positions.data_ptr(),
-                    lc.conv_ring.data_ptr(), lc.recurrent_state.data_ptr(), self.out.data_ptr(),
-                    self.ws.data_ptr(), self.ws.numel(),
+        return (ctypes.byref(self.geom), qkv.data_ptr(), z.data_ptr(), a.data_ptr(), b.data_ptr(),
+                w["ssm_a"].data_ptr(), w["ssm_dt.bias"].data_ptr(), w["ssm_conv1d.weight"].data_ptr(),
+                w["ssm_norm.weight"].data_ptr(), self.positions.data_ptr(), lc.conv_ring.data_ptr(),
+                lc.recurrent_state.data_ptr(), self.out.data_ptr(), self.ws.data_ptr(), self.ws.numel())
+
+    def run(self, qkv, z, a, b, stream=None):
+        native.call("qm_dn_decode", *self._args(qkv, z, a, b),
                     stream if stream is not None else native.stream_handle(self.model.device))
         return self.out
+
+    def bind(self, qkv, z, a, b) -> BoundCall:
+        """The step on these inputs as a BoundCall (stream at call time)."""
+        return BoundCall("qm_dn_decode", *self._args(qkv, z, a, b))
 
 
 class QsaDecodePlan:
@@ -121,16 +147,25 @@ class QsaDecodePlan:
                     lc.k_pool.data_ptr(), lc.v_pool.data_ptr(), self.items.data_ptr(), self.out.data_ptr(),
                     self.splits, self.ws.data_ptr(), self.ws.numel(), stream)
 
+    def _decode_args(self, qg, k, v, iq, ik):
+        lc, w = self.lc, self.w
+        return (ctypes.byref(self.geom), qg.data_ptr(), k.data_ptr(), v.data_ptr(), iq.data_ptr(), ik.data_ptr(),
+                w["attn_q_norm.weight"].data_ptr(), w["attn_k_norm.weight"].data_ptr(),
+                w["indexer.q_norm.weight"].data_ptr(), w["indexer.k_norm.weight"].data_ptr(), self.cos.data_ptr(),
+                self.sin.data_ptr(), self.positions.data_ptr(), lc.page_table.data_ptr(), lc.k_pool.data_ptr(),
+                lc.v_pool.data_ptr(), lc.raw_keys.data_ptr(), lc.block_keys.data_ptr(), self.out.data_ptr(),
+                self.dec_splits, self.dec_ws.data_ptr(), self.dec_ws.numel(), None, None, None, None)
+
     def decode(self, qg, k, v, iq, ik, stream):
         """The whole step in one qm_qsa_decode launch."""
-        lc, w = self.lc, self.w
-        native.call("qm_qsa_decode", ctypes.byref(self.geom), qg.data_ptr(), k.data_ptr(), v.data_ptr(),
-                    iq.data_ptr(), ik.data_ptr(), w["attn_q_norm.weight"].data_ptr(),
-                    w["attn_k_norm.weight"].data_ptr(), w["indexer.q_norm.weight"].data_ptr(),
-                    w["indexer.k_norm.weight"].data_ptr(), self.cos.data_ptr(), self.sin.data_ptr(),
-                    self.positions.data_ptr(), lc.page_table.data_ptr(), lc.k_pool.data_ptr(),
-                    lc.v_pool.data_ptr(), lc.raw_keys.data_ptr(), lc.block_keys.data_ptr(), self.out.data_ptr(),
-                    self.dec_splits, self.dec_ws.data_ptr(), self.dec_ws.numel(), None, None, None, None, stream)
+        native.call("qm_qsa_decode", *self._decode_args(qg, k, v, iq, ik), stream)
+
+    def bind(self, qg, k, v, iq, ik) -> BoundCall:
+        """The one-launch step on these inputs as a BoundCall (stream at call
+        time); plans that do not fit one launch are refused."""
+        if not self.fused:
+            raise native.QmError(f"layer {self.layer}: this plan runs as front + attend, not one launch")
+        return BoundCall("qm_qsa_decode", *self._decode_args(qg, k, v, iq, ik))
 
     def check(self, reset: bool = True) -> list:
         """Hand-off faults of this plan's fused launches since the last check

@@ -4,6 +4,9 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HERE = os.path.dirname(os.path.abspath(__file__))
+if HERE not in sys.path:
+    sys.path.insert(0, HERE)
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
@@ -34,3 +37,15 @@ def gpu(qm):
         pytest.skip("no GPU in this environment")
     qm.native.load()  # raises if the HIP library is missing: no silent fallback
     return qm
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The achieved parity margins (tests/margins.py), one line per test and kind."""
+    from margins import summary
+    rows = summary()
+    if not rows:
+        return
+    terminalreporter.section("parity margins (worst per test; bar where the test names it)")
+    for test, kind, v, bar in rows:
+        tail = f"  bar {bar:g}  ({v / bar:.1%} of it)" if isinstance(bar, (int, float)) and bar > 0 else ""
+        terminalreporter.write_line(f"{kind:>4} {v:.3e}{tail}  {test}")

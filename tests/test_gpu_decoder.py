@@ -35,16 +35,13 @@ import torch
 sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
 import inputs as gi  # noqa: E402
 
+from margins import rel_err  # noqa: E402
+
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 BF = torch.bfloat16
 N_LAYERS = 4
 START = 1020
-
-
-def rel_err(got, want):
-    got, want = got.float().cpu(), want.float().cpu()
-    return ((got - want).abs().max() / want.abs().max().clamp_min(1e-30)).item()
 
 
 @pytest.fixture(scope="module")
@@ -158,7 +155,7 @@ def test_decoder_step_matches_layer_methods(stack):
                 branch = model._linear_attention(mixed, l, cache)
             h = model._reinject(h, branch, inject)
         torch.cuda.synchronize()
-        assert rel_err(got[i], h) < 2e-2, f"step {i}"
+        assert rel_err(got[i], h, 2e-2) < 2e-2, f"step {i}"
     restore(cache, snap)
 
 
@@ -178,7 +175,7 @@ def test_step_n_matches_single_steps(stack, k):
     singles = [dec.step_eager(x[:, i:i + 1]).clone() for i in range(k)]
     torch.cuda.synchronize()
     for i in range(k):
-        assert rel_err(rows[:, i:i + 1], singles[i]) < 2e-2, f"row {i}"
+        assert rel_err(rows[:, i:i + 1], singles[i], 2e-2) < 2e-2, f"row {i}"
     for l, ((a, na, _), (b, nb, _)) in enumerate(zip(after_n, snapshot(cache))):
         assert na == nb == START + k
         for f in a:
@@ -188,7 +185,7 @@ def test_step_n_matches_single_steps(stack, k):
                 # same inputs on both paths: the fp32 state bar
                 assert (a[f] - b[f]).abs().max().item() < 1e-3, f"layer {l}"
             else:
-                assert rel_err(a[f], b[f]) < 2e-2, f"layer {l} {f}"
+                assert rel_err(a[f], b[f], 2e-2) < 2e-2, f"layer {l} {f}"
     restore(cache, snap)
 
 
@@ -245,12 +242,12 @@ def test_decoder_matches_oracle_chain(stack, k):
     dec = qm.decoder.MixDecoder(model, cache)
     got = dec.step(x).clone() if k == 1 else dec.step_n(x).clone()
     torch.cuda.synchronize()
-    assert rel_err(got, want) < 2e-2, rel_err(got, want)
+    assert rel_err(got, want, 2e-2) < 2e-2, rel_err(got, want)
     got_oc = _export(cache)
     for l in range(N_LAYERS):
         if model.config.is_full_attention(l):
-            assert rel_err(got_oc[l].keys[:, :, -k:], oc[l].keys[:, :, -k:]) < 2e-2, l
-            assert rel_err(got_oc[l].values[:, :, -k:], oc[l].values[:, :, -k:]) < 2e-2, l
+            assert rel_err(got_oc[l].keys[:, :, -k:], oc[l].keys[:, :, -k:], 2e-2) < 2e-2, l
+            assert rel_err(got_oc[l].values[:, :, -k:], oc[l].values[:, :, -k:], 2e-2) < 2e-2, l
             assert got_oc[l].indexer_keys.shape == oc[l].indexer_keys.shape
         else:
             bar = 1e-3 if l == 0 else None
@@ -258,8 +255,8 @@ def test_decoder_matches_oracle_chain(stack, k):
             if bar is not None:
                 assert diff < bar, (l, diff)
             else:
-                assert rel_err(got_oc[l].recurrent_state, oc[l].recurrent_state) < 2e-2, l
-            assert rel_err(got_oc[l].conv_state, oc[l].conv_state) < 2e-2, l
+                assert rel_err(got_oc[l].recurrent_state, oc[l].recurrent_state, 2e-2) < 2e-2, l
+            assert rel_err(got_oc[l].conv_state, oc[l].conv_state, 2e-2) < 2e-2, l
     dec.check_handoffs()
     restore(cache, snap)
 

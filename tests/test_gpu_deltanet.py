@@ -26,18 +26,11 @@ HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 sys.path.insert(0, HERE)
 import inputs as gi  # noqa: E402
 
+from margins import abs_err, rel_err  # noqa: E402
+
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 OUT_TOL, STATE_TOL = 2e-2, 1e-3
-
-
-def rel_err(got, want):
-    got, want = got.detach().float().cpu(), want.detach().float().cpu()
-    return ((got - want).abs().max() / want.abs().max().clamp_min(1e-30)).item()
-
-
-def abs_err(got, want):
-    return (got.detach().float().cpu() - want.detach().float().cpu()).abs().max().item()
 
 
 def _setup(gpu, dtype, wseed, sseed, batch=1):
@@ -80,8 +73,8 @@ def test_decode_core_matches_oracle(gpu, dtype, batch):
     print(f"decode core dtype={dtype} batch={batch}", flush=True)
     got, want = _core_step(model, cache, OracleMixer(OracleConfig(), store), ocache, store, hidden)
     torch.cuda.synchronize()
-    assert rel_err(got, want) < OUT_TOL
-    assert abs_err(cache[0].recurrent_state, ocache[0].recurrent_state) < STATE_TOL
+    assert rel_err(got, want, OUT_TOL) < OUT_TOL
+    assert abs_err(cache[0].recurrent_state, ocache[0].recurrent_state, STATE_TOL) < STATE_TOL
     assert torch.equal(cache[0].conv_state.cpu(), ocache[0].conv_state)
 
 
@@ -92,8 +85,8 @@ def test_decode_layer_matches_oracle(gpu, dtype):
     hidden = gi.normal(gi.rng(26), (1, 1, gi.HIDDEN)).to(dtype)
     want = OracleMixer(OracleConfig(), store)._linear_attention(hidden, 0, ocache)
     got = model._linear_attention(hidden.to(DEV), 0, cache)
-    assert rel_err(got, want) < OUT_TOL
-    assert abs_err(cache[0].recurrent_state, ocache[0].recurrent_state) < STATE_TOL
+    assert rel_err(got, want, OUT_TOL) < OUT_TOL
+    assert abs_err(cache[0].recurrent_state, ocache[0].recurrent_state, STATE_TOL) < STATE_TOL
 
 
 def test_decode_core_matches_golden_reference(gpu):
@@ -110,11 +103,11 @@ def test_decode_core_matches_golden_reference(gpu):
         flat = y.float().reshape(-1).cpu()
         want = torch.from_numpy(z["dn_out"])
         stride = max(1, flat.numel() // want.numel())
-        assert rel_err(flat[::stride][: want.numel()], want) < OUT_TOL, tag
+        assert rel_err(flat[::stride][: want.numel()], want, OUT_TOL) < OUT_TOL, tag
         st = cache[0].recurrent_state.reshape(-1).cpu()
         ws = torch.from_numpy(z["dn_state"])
         stride = max(1, st.numel() // ws.numel())
-        assert abs_err(st[::stride][: ws.numel()], ws) < STATE_TOL, tag
+        assert abs_err(st[::stride][: ws.numel()], ws, STATE_TOL) < STATE_TOL, tag
 
 
 def test_64_compounding_decode_steps_stay_within_tolerance(gpu):
@@ -150,13 +143,13 @@ def test_prefill_core_matches_oracle(gpu, seq):
     hidden = gi.normal(gi.rng(43), (1, seq, gi.HIDDEN)).to(dtype)
     print(f"prefill core seq={seq}", flush=True)
     got, want = _core_step(model, cache, omix, ocache, store, hidden)
-    assert rel_err(got, want) < OUT_TOL
-    assert abs_err(cache[0].recurrent_state, ocache[0].recurrent_state) < STATE_TOL
+    assert rel_err(got, want, OUT_TOL) < OUT_TOL
+    assert abs_err(cache[0].recurrent_state, ocache[0].recurrent_state, STATE_TOL) < STATE_TOL
     assert torch.equal(cache[0].conv_state.cpu(), ocache[0].conv_state)
     # a decode step continues from the prefilled state and ring
     h1 = gi.normal(gi.rng(44), (1, 1, gi.HIDDEN)).to(dtype)
     got, want = _core_step(model, cache, omix, ocache, store, h1)
-    assert rel_err(got, want) < OUT_TOL
+    assert rel_err(got, want, OUT_TOL) < OUT_TOL
     assert torch.equal(cache[0].conv_state.cpu(), ocache[0].conv_state)
 
 
@@ -170,11 +163,11 @@ def test_prefill_chunk_matches_golden_reference(gpu):
     y = model._linear_attention(hidden.to(DEV), 0, cache).float().reshape(-1).cpu()
     want = torch.from_numpy(z["dn_out"])
     stride = max(1, y.numel() // want.numel())
-    assert rel_err(y[::stride][: want.numel()], want) < OUT_TOL
+    assert rel_err(y[::stride][: want.numel()], want, OUT_TOL) < OUT_TOL
     st = cache[0].recurrent_state.reshape(-1).cpu()
     ws = torch.from_numpy(z["dn_state"])
     stride = max(1, st.numel() // ws.numel())
-    assert abs_err(st[::stride][: ws.numel()], ws) < STATE_TOL
+    assert abs_err(st[::stride][: ws.numel()], ws, STATE_TOL) < STATE_TOL
 
 
 @pytest.mark.parametrize("fn", ["recurrent", "chunked"])
@@ -187,8 +180,8 @@ def test_free_function_rules_match_oracle(gpu, fn, seq):
     want_o, want_s = o_rec(q, k, v, g, beta, initial_state=s0)
     rule = layers.recurrent_gated_delta_rule if fn == "recurrent" else layers.chunk_gated_delta_rule
     got_o, got_s = rule(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), beta.to(DEV), initial_state=s0.to(DEV))
-    assert abs_err(got_o, want_o) < 1e-3
-    assert abs_err(got_s, want_s) < STATE_TOL
+    assert abs_err(got_o, want_o, 1e-3) < 1e-3
+    assert abs_err(got_s, want_s, STATE_TOL) < STATE_TOL
     # and the float64 twin bounds both
     o64, s64 = f64.delta_rule_f64(q[0], k[0], v[0], g[0], beta[0], s0[0])
     assert np.abs(got_s[0].cpu().numpy() - s64).max() < STATE_TOL
@@ -206,11 +199,16 @@ def test_chunked_4096_tokens_against_reference_golden(gpu):
     o = got_o.reshape(-1).cpu()
     want = torch.from_numpy(z["chunk_out"])
     stride = max(1, o.numel() // want.numel())
-    assert abs_err(o[::stride][: want.numel()], want) < 2e-3
+    assert abs_err(o[::stride][: want.numel()], want, 2e-3) < 2e-3
     s = got_s.reshape(-1).cpu()
     ws = torch.from_numpy(z["chunk_state"])
     stride = max(1, s.numel() // ws.numel())
-    assert abs_err(s[::stride][: ws.numel()], ws) < STATE_TOL
+    assert abs_err(s[::stride][: ws.numel()], ws, STATE_TOL) < STATE_TOL
+    # every output and state element against the oracle's chunked rule, whose
+    # output and state digests equal the reference's (tests/test_golden.py)
+    want_o, want_s = o_chunk(q, k, v, g, beta, initial_state=s0)
+    assert abs_err(got_o, want_o, 2e-3) < 2e-3
+    assert abs_err(got_s, want_s, STATE_TOL) < STATE_TOL
 
 
 @pytest.mark.parametrize("hk,hv", [(1, 4), (3, 6), (2, 8)])

@@ -18,13 +18,10 @@ import torch.nn.functional as F
 sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
 import inputs as gi  # noqa: E402
 
+from margins import rel_err  # noqa: E402
+
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-
-
-def rel_err(got, want):
-    got, want = got.float().cpu(), want.float().cpu()
-    return ((got - want).abs().max() / want.abs().max().clamp_min(1e-30)).item()
 
 
 def run_gemv(qm, w, x, rows):
@@ -55,7 +52,7 @@ def test_gemv_matches_fp32_product(gpu, dtype, k, m):
         tol = 1e-2 if dtype == torch.bfloat16 else 1e-5
         start = 0
         for o, r in zip(got, rows):
-            assert rel_err(o, want[:, start:start + r]) < tol, (rows, r)
+            assert rel_err(o, want[:, start:start + r], tol) < tol, (rows, r)
             start += r
 
 
@@ -72,7 +69,7 @@ def test_layer_projections_take_the_gemv(gpu):
         got = model.project(hidden, 0, "dn_in")
         for t, name in zip(got, model.PROJ_GROUPS["dn_in"]):
             want = F.linear(hidden.float(), store.get(f"blk.0.{name}").to(DEV).float())
-            assert rel_err(t, want) < 1e-2, (seq, name)
+            assert rel_err(t, want, 1e-2) < 1e-2, (seq, name)
 
 
 @pytest.mark.parametrize("dtype,k", [(torch.bfloat16, 4096), (torch.float32, 2048)])

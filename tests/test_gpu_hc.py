@@ -23,13 +23,10 @@ import inputs as gi  # noqa: E402
 from oracle.config import OracleConfig  # noqa: E402
 from oracle.mixing import OracleMixer  # noqa: E402
 
+from margins import rel_err  # noqa: E402
+
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-
-
-def rel_err(got, want):
-    got, want = got.float().cpu(), want.float().cpu()
-    return ((got - want).abs().max() / want.abs().max().clamp_min(1e-30)).item()
 
 
 def tol(dtype):
@@ -58,12 +55,12 @@ def test_gated_residual_matches_oracle(gpu, dtype, hidden, rows):
         mixed, hyper_out, inject = model._gated_residual(hyper.to(DEV), layer, "attn")
         torch.cuda.synchronize()
         assert mixed.shape == want_mixed.shape and mixed.dtype == dtype
-        assert rel_err(mixed, want_mixed) < tol(dtype)
+        assert rel_err(mixed, want_mixed, tol(dtype)) < tol(dtype)
         if layer is None:
             assert inject is None
         else:
             assert inject.shape == want_inject.shape
-            assert rel_err(inject, want_inject) < tol(dtype)
+            assert rel_err(inject, want_inject, tol(dtype)) < tol(dtype)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

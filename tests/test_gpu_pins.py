@@ -43,6 +43,8 @@ HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 sys.path.insert(0, HERE)
 import inputs as gi  # noqa: E402
 
+from margins import abs_err, record, rel_err  # noqa: E402
+
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 OUT_TOL, STATE_TOL = 2e-2, 1e-3
@@ -53,15 +55,6 @@ ROT = RotaryEmbedding(64, 1e7, [11, 11, 10])
 def tables(n):
     p = torch.arange(n)[None]
     return ROT(p[None].expand(3, -1, -1))
-
-
-def rel_err(got, want):
-    got, want = got.detach().float().cpu(), want.detach().float().cpu()
-    return ((got - want).abs().max() / want.abs().max().clamp_min(1e-30)).item()
-
-
-def abs_err(got, want):
-    return (got.detach().float().cpu() - want.detach().float().cpu()).abs().max().item()
 
 
 def _layers(qm):
@@ -120,6 +113,7 @@ def test_block_scores_bit_exact_vs_reference(gpu, tag):
                    qm.native.stream_handle())
     want = z["scores"].reshape(seq, -1).astype(np.float32)
     got = scores.cpu().numpy()[:, : want.shape[1]]
+    record("ulps", _ulps(got, want), 0)
     same = got.view(np.int32) == want.view(np.int32)
     if not same.all():
         bad = np.argwhere(~same)
@@ -170,8 +164,8 @@ def test_delta_rules_under_extreme_decay(gpu, scale, seq):
     for rule in (lay.chunk_gated_delta_rule, lay.recurrent_gated_delta_rule):
         got_o, got_s = rule(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), beta.to(DEV), initial_state=s0.to(DEV))
         assert torch.isfinite(got_o).all() and torch.isfinite(got_s).all(), rule.__name__
-        assert abs_err(got_o, want_o) < 1e-3, rule.__name__
-        assert abs_err(got_s, want_s) < STATE_TOL, rule.__name__
+        assert abs_err(got_o, want_o, 1e-3) < 1e-3, rule.__name__
+        assert abs_err(got_s, want_s, STATE_TOL) < STATE_TOL, rule.__name__
 
 
 @pytest.mark.parametrize("seq", [1, 128])
@@ -202,8 +196,8 @@ def test_layer_cores_under_extreme_decay(gpu, seq):
         got = model.dn_core(p[0].to(DEV), p[1].to(DEV), p[3].to(DEV), p[2].to(DEV), 0, cache[0])
         st = cache[0].recurrent_state
         assert torch.isfinite(got).all() and torch.isfinite(st).all()
-        assert rel_err(got, want) < OUT_TOL
-        assert abs_err(st, ocache[0].recurrent_state) < STATE_TOL
+        assert rel_err(got, want, OUT_TOL) < OUT_TOL
+        assert abs_err(st, ocache[0].recurrent_state, STATE_TOL) < STATE_TOL
 
 
 # -- config 4 against the sequential recurrence -----------------------------------------
@@ -221,11 +215,11 @@ def test_config4_against_reference_recurrence(gpu, rule_name):
     o = got_o.reshape(-1).cpu()
     want = torch.from_numpy(z["rec_out"])
     stride = max(1, o.numel() // want.numel())
-    assert abs_err(o[::stride][: want.numel()], want) < 2e-3
+    assert abs_err(o[::stride][: want.numel()], want, 2e-3) < 2e-3
     s = got_s.reshape(-1).cpu()
     ws = torch.from_numpy(z["rec_state"])
     stride = max(1, s.numel() // ws.numel())
-    assert abs_err(s[::stride][: ws.numel()], ws) < STATE_TOL
+    assert abs_err(s[::stride][: ws.numel()], ws, STATE_TOL) < STATE_TOL
 
 
 # -- the free conv functions ------------------------------------------------------------
@@ -244,13 +238,13 @@ def test_causal_conv1d_free_functions(gpu, dtype, seq):
     print(f"causal conv seq={seq} {dtype}", flush=True)
     want_o, want_s = ol.causal_conv1d_step(x, state, w)
     got_o, got_s = lay.causal_conv1d_step(x.to(DEV), state.to(DEV), w.to(DEV))
-    assert rel_err(got_o, want_o) < tol
+    assert rel_err(got_o, want_o, tol) < tol
     assert torch.equal(got_s.cpu(), want_s)                  # the window only moves inputs
     want = ol.causal_conv1d(x, w)
     got = lay.causal_conv1d(x.to(DEV), w.to(DEV))
-    assert rel_err(got, want) < tol
+    assert rel_err(got, want, tol) < tol
     got_lin = lay.causal_conv1d(x.to(DEV), w.to(DEV), activation=False)
-    assert rel_err(got_lin, ol.causal_conv1d(x, w, activation=False)) < tol
+    assert rel_err(got_lin, ol.causal_conv1d(x, w, activation=False), tol) < tol
 
 
 # -- _indexer_mask through the product method -------------------------------------------
@@ -323,7 +317,7 @@ def test_front_then_attend_decode_matches_oracle(gpu):
     print("front + attend decode pos=8128", flush=True)
     got = model._full_attention(hidden.to(DEV), 3, cos.to(DEV), sin.to(DEV), cache, pos)
     assert "qsa_decode_3_1" not in model._ws           # the one-launch kernel never ran
-    assert rel_err(got, want) < OUT_TOL
+    assert rel_err(got, want, OUT_TOL) < OUT_TOL
     # the selection the two launches made is the oracle's
     ids, n = cache[3].last_ids.cpu()[0, 0], int(cache[3].last_n_sel.cpu()[0, 0])
     oc2 = OracleHybridCache(4)

@@ -214,8 +214,9 @@ def test_chunked_4096_tokens_against_reference_golden(gpu):
 @pytest.mark.parametrize("hk,hv", [(1, 4), (3, 6), (2, 8)])
 def test_decode_core_other_key_head_counts(gpu, hk, hv):
     """Value head h reads q/k head h % hk for any key-head count, one key head
-    included (the decode kernel's division-free h % hk): four decode steps and
-    a 5-token prefill against the oracle, conv window bit-exact."""
+    included (the decode kernel's division-free h % hk): decode steps between
+    prefills of 5 tokens (the token loop), 20 and 70 tokens (the chunked rule
+    with the conv inside its prep) against the oracle, conv window bit-exact."""
     qm = gpu
     dtype = torch.bfloat16
     ocfg = OracleConfig(linear_num_k_heads=hk, linear_num_v_heads=hv)
@@ -237,7 +238,7 @@ def test_decode_core_other_key_head_counts(gpu, hk, hv):
     cache[0].recurrent_state = state.to(DEV).clone()
     omix = OracleMixer(ocfg, store)
     worst_out = worst_state = 0.0
-    for t, seq in enumerate((1, 1, 5, 1, 1)):
+    for t, seq in enumerate((1, 1, 5, 20, 1, 70, 1)):
         mixed = gi.normal(r, (1, seq, conv_dim)).to(dtype)
         z = gi.normal(r, (1, seq, hv * d)).to(dtype)
         b = gi.normal(r, (1, seq, hv)).to(dtype)

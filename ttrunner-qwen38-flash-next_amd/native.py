@@ -90,12 +90,14 @@ _lib = None
 _lock = threading.Lock()
 
 
-def load(path: str = LIB_PATH) -> ctypes.CDLL:
-    """Load the library (once) and bind every entry point; raise if absent."""
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load the library (once) and bind every entry point; raise if absent.
+    The path defaults to QM_LIB from the environment, else the in-tree build."""
     global _lib
     with _lock:
         if _lib is not None:
             return _lib
+        path = path or os.environ.get("QM_LIB") or LIB_PATH
         if not os.path.exists(path):
             raise QmError(f"{path} is missing: build it with __graft_entry__.build() "
                           "(there is no fallback implementation)")

@@ -94,9 +94,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=5.0, help="CPU oracle time per decode config")
     ap.add_argument("--head-only", action="store_true",
                     help="time only the headline workload (no other configs), e.g. under a profiler")
-    ap.add_argument("--part", choices=("stack", "hc"), default=None,
-                    help="time only this part (the token-mixing layer stack, or the hyper-connection mix) and "
-                         "print its result as one JSON line")
+    ap.add_argument("--part", choices=("stack", "hc", "prefill"), default=None,
+                    help="time only this part (the token-mixing layer stack, the hyper-connection mix, or the "
+                         "128-token prefill chunk) and print its result as one JSON line")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="after timing, copy a buffer of this many MiB device to device three times (a kernel of "
                          "known traffic that scales hardware byte counters)")
@@ -853,6 +853,20 @@ def run_stack(qm, dev, pos=8128, n_layers=STACK_LAYERS, steps=30, warmup=5):
     return res
 
 
+def copy_buffer(mb: int, dev):
+    """Three device-to-device copies of `mb` MiB: a kernel of known traffic
+    (mb MiB read and mb MiB written per call) that scales the hardware byte
+    counters of a profiled run."""
+    import torch
+    src = torch.ones(mb << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def best_launch(r):
     """(us per step, how launched): the faster of the graph replay and the
     eager loop of prebound calls, both timed over the same steps from cold
@@ -877,8 +891,11 @@ def main():
     torch.cuda.set_device(dev)
     pos = args.position
     if args.part is not None:
-        res = run_stack(qm, dev, pos) if args.part == "stack" else run_hc(qm, dev)
-        print(json.dumps({"part": args.part, **res}))
+        run = {"stack": lambda: run_stack(qm, dev, pos), "hc": lambda: run_hc(qm, dev),
+               "prefill": lambda: run_prefill(qm, dev)}[args.part]
+        print(json.dumps({"part": args.part, **run()}))
+        if args.copy_mb > 0:
+            copy_buffer(args.copy_mb, dev)
         return
     head = run_decode(qm, dev, pos, args.steps, args.warmup, args.instances)
     max_ctx, n_inst, touched = head["max_ctx"], head["instances"], head["touched"]
@@ -901,13 +918,7 @@ def main():
           ", ".join(f"{k} {v:.2f}" for k, v in kern.items()) + f"; step minus cold kernels {gap:.2f}",
           file=sys.stderr)
     if args.copy_mb > 0:
-        src = torch.ones(args.copy_mb << 20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        copy_buffer(args.copy_mb, dev)
 
     configs = []
     if not args.head_only:

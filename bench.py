@@ -8,7 +8,7 @@ one DeltaNet decode core (conv ring, gates, delta-rule update of the
 [32,128,128] float32 state, gated norm). Inputs are synthetic (seeded), already
 resident in HBM, and rotated over enough independent layer instances that the
 data touched per rotation exceeds twice the 256 MB Infinity Cache. Every timed
-figure starts cold: 768 MB of other traffic passes through the caches right
+figure starts cold: 768 MB of other data is read through the caches right
 before the timed steps, the per-launch kernel times (`*_cold`) and the prefill
 calls, as a layer's data is cold when a decode step reaches it after the other
 layers' weights have streamed through. Back-to-back warm launch times
@@ -175,20 +175,30 @@ def weights_store(dtype):
     return Store()
 
 
-FLUSH_MB = 768      # other traffic streamed through the caches before a cold timing (3x the Infinity Cache)
+FLUSH_MB = 768      # other data read through the caches before a cold timing (3x the Infinity Cache)
 
 
 class Flusher:
-    """A buffer of FLUSH_MB that one elementwise kernel reads and writes: after
-    it, the caches (L2 and the 256 MB Infinity Cache) hold none of the data a
-    timed launch reads."""
+    """FLUSH_MB of other data read through the caches by one matrix-vector
+    product ([FLUSH_MB << 8, 1024] float32 times a vector): after it, the L2s
+    and the 256 MB Infinity Cache hold none of the data a timed launch reads,
+    and only clean lines (a flush that also wrote its buffer, as an in-place
+    elementwise update does, leaves hundreds of MB of dirty lines whose
+    write-back then lands in the timed launches: 1 us more per step and per
+    QSA launch when measured). The library's handle is set up here, outside
+    any graph capture."""
 
     def __init__(self, dev):
         import torch
-        self.buf = torch.ones(FLUSH_MB << 18, device=dev, dtype=torch.float32)
+        self.buf = torch.ones(FLUSH_MB << 8, 1024, device=dev, dtype=torch.float32)
+        self.vec = torch.ones(1024, device=dev, dtype=torch.float32)
+        self.out = torch.empty(FLUSH_MB << 8, device=dev, dtype=torch.float32)
+        self()
+        torch.cuda.synchronize(dev)
 
     def __call__(self):
-        self.buf.mul_(1.0)
+        import torch
+        torch.mv(self.buf, self.vec, out=self.out)
 
 
 def time_steps(instances, steps, warmup, stream, flush):
@@ -216,7 +226,7 @@ def time_graph_steps(instances, steps, warmup, flush):
     launches each) are captured in one graph, and `warmup` steps on the last
     instances (disjoint from the timed ones while steps + warmup <= n) in
     another. The timed graph is replayed once untimed (a graph's first replay
-    also uploads it), then the warmup graph, then FLUSH_MB of other traffic
+    also uploads it), then the warmup graph, then FLUSH_MB of other data read through the caches
     empties the caches, so every timed step reads its instance from HBM; the
     timed graph's single replay is then timed between synchronisations. The
     host's launch cost stays out of the figure; the kernels, the gaps between
@@ -289,7 +299,7 @@ def time_kernels(instances, reps, stream_obj, batches=5):
 
 def time_cold(instances, fn, flush, launches=8, reps=15):
     """Average duration of `launches` back-to-back launches, each on its own
-    instance, that start right after FLUSH_MB of other traffic (so everything
+    instance, that start right after FLUSH_MB of other data is read (so everything
     they read comes from HBM): the event time of a graph of [flush, launches]
     minus that of a graph of [flush], medians over `reps` replays."""
     import torch
@@ -551,7 +561,7 @@ class PrefillInstance:
 
 def run_prefill(qm, dev, reps=20, n_inst=4):
     """Event time of each layer's chunk call, each call starting after
-    FLUSH_MB of other traffic (its K/V, keys and state come from HBM), median
+    FLUSH_MB of other data read (its K/V, keys and state come from HBM), median
     over `reps` calls rotating over `n_inst` instances."""
     import torch
     model = qm.Qwen4MixModel(qm.MixConfig(), weights_store(torch.bfloat16), device=dev, max_ctx=PREFILL_CTX)

@@ -293,11 +293,12 @@ __device__ __forceinline__ float torch_row_sumsq(const float* x, int n, float* s
 }
 
 // Phase markers (a build compiled with -DQM_PHASE_TRACE, for timing a
-// kernel's stages; in every other build all three are nothing):
+// kernel's stages; in every other build they are all nothing):
 // QM_PHASE_DECL declares a workgroup's 16 LDS time slots; QM_PHASE(slot) has
 // thread 0 record the wall clock (100 MHz) in one of them (an LDS write: no
 // global store that a later barrier would wait for); QM_PHASE_FLUSH writes the
-// slots to the workgroup's row of the translation unit's qm_phase_buf, and
+// slots to the workgroup's row of the translation unit's qm_phase_buf (rows
+// from first_row on with QM_PHASE_FLUSH_AT), and
 // QM_PHASE_ENTRY(tag) defines qm_phase_read_<tag> / qm_phase_clear_<tag> for
 // the host. Slot 15 holds the workgroup's XCC id.
 #ifdef QM_PHASE_TRACE
@@ -310,10 +311,11 @@ static __shared__ unsigned long long qm_ph_[16];
   do {                                                           \
     if (threadIdx.x == 0) qm_ph_[(slot)] = wall_clock64() | (1ull << 63); \
   } while (0)
-#define QM_PHASE_FLUSH()                                                                                   \
+#define QM_PHASE_FLUSH() QM_PHASE_FLUSH_AT(0u)
+#define QM_PHASE_FLUSH_AT(first_row)                                                                       \
   do {                                                                                                     \
     if (threadIdx.x == 0) {                                                                                \
-      const unsigned row_ = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);                \
+      const unsigned row_ = (first_row) + blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);  \
       qm_ph_[15] = (unsigned long long)__builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)) | (1ull << 63); \
       if (row_ < QM_PHASE_ROWS)                                                                            \
         for (int s_ = 0; s_ < 16; ++s_) qm_phase_buf[row_ * 16 + s_] = qm_ph_[s_];                         \
@@ -335,6 +337,9 @@ static __shared__ unsigned long long qm_ph_[16];
   } while (0)
 #define QM_PHASE_FLUSH() \
   do {                 \
+  } while (0)
+#define QM_PHASE_FLUSH_AT(first_row) \
+  do {                             \
   } while (0)
 #define QM_PHASE_ENTRY(tag)
 #endif

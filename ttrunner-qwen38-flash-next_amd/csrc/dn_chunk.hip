@@ -375,6 +375,8 @@ template <typename T>
 __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A) {
   __shared__ float sST[CK_COLS][CK_LD];  // the state slice, transposed: [column][d_k]
   __shared__ float sVT[CK_COLS][CK_LT];  // v_new of the chunk, transposed: [column][token]
+  QM_PHASE_DECL
+  QM_PHASE(0);
   constexpr int NSL = CK_D / CK_COLS;
   const int nwg = A.batch * A.heads * NSL;
   const int wg = xcd_remap(blockIdx.x, nwg);
@@ -401,6 +403,7 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
     *reinterpret_cast<float4*>(&sST[r16][row]) = make_float4(st[t][0], st[t][1], st[t][2], st[t][3]);
   }
 
+  QM_PHASE(1);
   auto chunk = [&](int ci, const ScanOps& cur, ScanOps& ahead) {
     // chunk ci + 2's operands fly during this one (clamped at the last chunk)
     load_scan_ops(recs + (long)min(ci + 2, A.n_chunks - 1) * CK_REC, wid, g4, r16, col0, ahead);
@@ -440,6 +443,7 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
       st[t] = acc;
       *reinterpret_cast<float4*>(&sST[r16][row + 4 * g4]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     }
+    if (ci < 12) QM_PHASE(2 + ci);
   };
 
   for (int ci = 0; ci < A.n_chunks; ci += 3) {
@@ -454,6 +458,8 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
 #pragma unroll
     for (int v = 0; v < 4; ++v) S[(long)(row + v) * CK_D] = st[t][v];
   }
+  QM_PHASE(14);
+  QM_PHASE_FLUSH_AT(4096u);
 }
 
 template <typename T>

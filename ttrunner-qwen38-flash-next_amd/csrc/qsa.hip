@@ -1032,6 +1032,9 @@ struct SelArgs {
   // the chunk path's entry lists (qm_qsa_select_chunk), or null
   unsigned* cnt = nullptr; unsigned* list = nullptr; float* part_ml = nullptr; const int* parity = nullptr;
   int hkv = 0;
+  // the rows' block scores from qsa_score_rows_kernel ([row][max_blocks]), or
+  // null when the selection scores the blocks itself
+  const float* scores_in = nullptr;
 };
 
 struct SelShared {
@@ -1063,7 +1066,14 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
     for (int j = tid; j < A.max_blocks; j += NT)
       if (j >= n_elig) A.scores_out[(long)row * A.max_blocks + j] = -INFINITY;
 
-  if (n_elig > A.topk || A.scores_out) {
+  if (A.scores_in) {
+    if (n_elig > A.topk) {
+      const float* sc = A.scores_in + (long)row * A.max_blocks;
+      for (int j = tid; j < n_elig; j += NT) S.key[j] = sel_key(sc[j], j);
+      const int npad = (n_elig + 31) & ~31;
+      for (int j = n_elig + tid; j < npad; j += NT) S.key[j] = 0ull;
+    }
+  } else if (n_elig > A.topk || A.scores_out) {
     const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
     float* sc_out = A.scores_out ? A.scores_out + (long)row * A.max_blocks : nullptr;
     if (NT != SELP_NT || A.seq == 1) {
@@ -1149,6 +1159,119 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
     items[1 + it] = make_item(page * A.page_size + t0 % A.page_size, lo, hi);
   }
   if (tid == 0) items[0] = make_int2(n_items, 0);
+}
+
+// Block scores of the query rows of a chunk (several rows per sequence) in the
+// reference's several-rows summation order: one fused multiply-add chain over
+// the 128 elements per (row, block, head), then relu, the heads added in order
+// and the division by sqrt(128), as score_blocks_seq forms them. Workgroup
+// (tile of 64 blocks, 4 rows, sequence): the tile's block rows are staged in
+// LDS with coalesced loads (rows padded by 16 bytes, so that the lanes' row
+// reads fall on distinct banks); wave w takes row 4 y + w and lane l block
+// 64 x + l, running the idx_heads chains side by side (each key element read
+// once feeds every head); the 4 query rows are staged in LDS beside the block
+// rows. Scores past a row's eligible blocks are -inf when `fill` is set and
+// left unwritten otherwise.
+constexpr int SCR_BLK = 64;                 // blocks per workgroup, one per lane
+constexpr int SCR_ROWS = 4;                 // query rows per workgroup, one per wave
+constexpr int SCR_STRIDE = IDX_D / 4 + 1;   // float4 per staged block row
+
+struct ScoreRowsArgs {
+  const float* iq; const float* block_keys; const int* positions; float* scores;
+  int seq, idx_heads, ratio, max_blocks;
+  int fill;
+};
+
+__global__ __launch_bounds__(64 * SCR_ROWS) void qsa_score_rows_kernel(ScoreRowsArgs A) {
+  __shared__ float4 rows_lds[SCR_BLK * SCR_STRIDE];
+  __shared__ float4 q_lds[SCR_ROWS][IDX_D];      // 4 heads x 128 per row, zeros past idx_heads
+  const int b = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j0 = blockIdx.x * SCR_BLK, s0 = blockIdx.y * SCR_ROWS;
+  const int pos0 = A.positions[b];
+  const int s_last = min(s0 + SCR_ROWS, A.seq) - 1;
+  const int elig_max = min((pos0 + s_last + 1) / A.ratio, A.max_blocks);   // the group's last row sees the most
+  const int s = s0 + wv, j = j0 + lane;
+  float* out = A.scores + ((long)b * A.seq + s) * A.max_blocks;
+  if (j0 >= elig_max) {
+    // no row of the group has an eligible block in this tile
+    if (A.fill && s < A.seq && j < A.max_blocks) out[j] = -INFINITY;
+    return;
+  }
+  const float4* src = reinterpret_cast<const float4*>(A.block_keys + ((long)b * A.max_blocks + j0) * IDX_D);
+  const float4* qsrc = reinterpret_cast<const float4*>(A.iq + ((long)b * A.seq + s0) * A.idx_heads * IDX_D);
+  constexpr int F4 = SCR_BLK * IDX_D / 4 / (64 * SCR_ROWS);
+  float4 kv[F4], qv[SCR_ROWS];
+#pragma unroll
+  for (int i = 0; i < F4; ++i) {
+    const int f = tid + 64 * SCR_ROWS * i, r = f >> 5;
+    kv[i] = j0 + r < elig_max ? src[(long)r * (IDX_D / 4) + (f & 31)] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // the group's query rows: thread t < 128 takes float4 t of each row's
+  // idx_heads x 128 (zeros past them)
+#pragma unroll
+  for (int r = 0; r < SCR_ROWS; ++r)
+    qv[r] = s0 + r < A.seq && tid < A.idx_heads * IDX_D / 4 ? qsrc[(long)r * A.idx_heads * (IDX_D / 4) + tid]
+                                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < F4; ++i) {
+    const int f = tid + 64 * SCR_ROWS * i;
+    rows_lds[(f >> 5) * SCR_STRIDE + (f & 31)] = kv[i];
+  }
+  if (tid < IDX_D)
+#pragma unroll
+    for (int r = 0; r < SCR_ROWS; ++r) q_lds[r][tid] = qv[r];
+  __syncthreads();
+  if (s >= A.seq) return;
+  const int n_elig = min((pos0 + s + 1) / A.ratio, A.max_blocks);
+  const int nh = A.idx_heads;
+  const float4* row = &rows_lds[lane * SCR_STRIDE];
+  const float* qrow = reinterpret_cast<const float*>(&q_lds[wv][0]);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    // float4 c of the (permuted) row holds elements c / 2 + 16 (4 (c % 2) + t),
+    // t < 4: the even ones elements 0..63, the odd ones 64..127
+    float4 kc[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) kc[m] = row[2 * m + half];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      // elements d = 64 half + 16 t + m, m < 16, in order; the step's query
+      // elements come from LDS at one address per wave (a broadcast), all
+      // requested before the step's first multiply-add. Heads past idx_heads
+      // multiply the staged zeros and stay out of the sum (a condition on the
+      // head count inside the loops would have the compiler copy them per count).
+      float4 qv4[4][4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int m4 = 0; m4 < 4; ++m4)
+          qv4[h][m4] = *reinterpret_cast<const float4*>(qrow + h * IDX_D + 64 * half + 16 * t + 4 * m4);
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        const float kvv = t == 0 ? kc[m].x : t == 1 ? kc[m].y : t == 2 ? kc[m].z : kc[m].w;
+        const int e = m & 3;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const float4 q4 = qv4[h][m >> 2];
+          acc[h] = fmaf(e == 0 ? q4.x : e == 1 ? q4.y : e == 2 ? q4.z : q4.w, kvv, acc[h]);
+        }
+      }
+      // the step's products complete here and the next step's reads stay
+      // behind them (an empty asm that takes the sums and clobbers memory):
+      // requested all at once, the reads would need registers for every step,
+      // and the other waves of the SIMD cover their latency
+      asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]) : : "memory");
+    }
+  }
+  float sc = 0.f;
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+    if (h < nh) sc = add_rn(sc, fmaxf(acc[h], 0.f));
+  sc = div_rn(sc, 11.313708498984761f);
+  if (j < n_elig) out[j] = sc;
+  else if (A.fill && j < A.max_blocks) out[j] = -INFINITY;
 }
 
 __global__ __launch_bounds__(SELP_NT) void qsa_select_kernel(SelArgs A) {
@@ -2508,6 +2631,17 @@ int launch_prep(const qm_qsa_geom* g, int seq, const void* qg, const void* k_new
   return QM_OK;
 }
 
+// the several-rows block scores of batch x seq rows into scores [row][max_blocks]
+int launch_score_rows(const qm_qsa_geom* g, int seq, const float* iq, const float* block_keys, const int* positions,
+                      float* scores, bool fill, hipStream_t stream) {
+  if ((seq + SCR_ROWS - 1) / SCR_ROWS > 65535) return qm_fail(QM_ERR_UNSUPPORTED, "qsa: more than 262140 rows");
+  ScoreRowsArgs A{iq, block_keys, positions, scores, seq, g->idx_heads, g->ratio, g->max_blocks, fill ? 1 : 0};
+  const dim3 grid((g->max_blocks + SCR_BLK - 1) / SCR_BLK, (seq + SCR_ROWS - 1) / SCR_ROWS, g->batch);
+  hipLaunchKernelGGL(qsa_score_rows_kernel, grid, dim3(64 * SCR_ROWS), 0, stream, A);
+  QM_CHECK_LAUNCH();
+  return QM_OK;
+}
+
 SelArgs sel_args(const qm_qsa_geom* g, int seq, const float* iq, const float* block_keys, const int* positions,
                  const int* page_table, int* ids, int* n_sel, void* items, float* scores_out) {
   SelArgs A;
@@ -2578,6 +2712,14 @@ extern "C" int qm_qsa_select(const qm_qsa_geom* g, int seq, const float* iq, con
   if (g->max_blocks > SEL_MAX_BLOCKS || g->max_pages > SEL_MAX_BLOCKS || g->budget / g->ratio > SEL_MAX_BLOCKS / 2)
     return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_select: more than 4096 blocks or pages");
   SelArgs A = sel_args(g, seq, iq, block_keys, positions, page_table, ids, n_sel, items, scores_out);
+  if (seq > 1 && scores_out) {
+    // several rows: the scores come from their own launch over every compute
+    // unit, and the selection ranks them
+    rc = launch_score_rows(g, seq, iq, block_keys, positions, scores_out, true, stream);
+    if (rc) return rc;
+    A.scores_in = scores_out;
+    A.scores_out = nullptr;
+  }
   hipLaunchKernelGGL(qsa_select_kernel, dim3(g->batch * seq), dim3(SELP_NT), 0, stream, A);
   QM_CHECK_LAUNCH();
   return QM_OK;
@@ -2666,7 +2808,11 @@ ChunkWs chunk_ws_layout(const qm_qsa_geom* g, int seq) {
   w.cnt = 256;
   w.list = w.cnt + qm_align256((size_t)2 * g->batch * g->max_blocks * sizeof(unsigned));
   w.o = w.list + qm_align256((size_t)g->batch * g->max_blocks * seq * sizeof(unsigned));
-  w.ml = w.o + qm_align256(rows * g->n_kv_heads * nslot * GQA * QSA_D * sizeof(uint16_t));
+  // the partials' space first holds the rows' block scores, which the
+  // selection reads before the attention writes partials over them
+  const size_t o_bytes = rows * g->n_kv_heads * nslot * GQA * QSA_D * sizeof(uint16_t);
+  const size_t score_bytes = rows * g->max_blocks * sizeof(float);
+  w.ml = w.o + qm_align256(o_bytes > score_bytes ? o_bytes : score_bytes);
   w.total = w.ml + qm_align256(rows * g->n_kv_heads * nslot * GQA * 2 * sizeof(float));
   return w;
 }
@@ -2773,6 +2919,12 @@ extern "C" int qm_qsa_select_chunk(const qm_qsa_geom* g, int seq, const float* i
     return qm_fail(QM_ERR_WORKSPACE, "qm_qsa_select_chunk: workspace too small");
   char* base = static_cast<char*>(workspace);
   SelArgs A = sel_args(g, seq, iq, block_keys, positions, nullptr, ids, n_sel, nullptr, nullptr);
+  if (seq > 1) {
+    float* scores = reinterpret_cast<float*>(base + L.o);
+    rc = launch_score_rows(g, seq, iq, block_keys, positions, scores, false, stream);
+    if (rc) return rc;
+    A.scores_in = scores;
+  }
   A.parity = reinterpret_cast<const int*>(base + L.parity);
   A.cnt = reinterpret_cast<unsigned*>(base + L.cnt);
   A.list = reinterpret_cast<unsigned*>(base + L.list);

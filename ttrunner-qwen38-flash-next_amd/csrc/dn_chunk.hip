@@ -8,18 +8,23 @@
 //                   CPU cumsum accumulates), forms L = (k beta k^T) * decay
 //                   below the diagonal and (q k^T) * decay on and below it,
 //                   inverts I + L (16x16 diagonal blocks by substitution, the
-//                   blocks below by MFMA, one sub-diagonal at a time) and writes
-//                   w = T (k beta e^cum), u = T (v beta), q e^cum and
-//                   (k e^(cum_last - cum))^T to the workspace
+//                   blocks below by fp32 MFMA, one sub-diagonal at a time) and
+//                   writes w = T (k beta e^cum), u = T (v beta), q e^cum and
+//                   k e^(cum_last - cum) to the workspace
 //   dn_chunk_scan   one workgroup per (sequence, head, 16 columns of d_v): the
-//                   state slice [128 x 16] stays on chip while the chunks pass:
+//                   state slice stays on chip while the chunks pass:
 //                   v_new = u - w S, out = q_dec S + qk v_new,
 //                   S = S e^cum_last + k_dec^T v_new
-// Every product is a v_mfma_f32_16x16x4_f32 (fp32 in, fp32 accumulate); its
-// operand lanes are A[row l%16][k l/16], B[k l/16][col l%16] and the result
-// rows 4(l/16)+i, col l%16. K runs in the order 16j + 4(l/16) + e over float4
-// operand loads, the same for both operands, so an accumulator's four rows
-// feed the next product's B operand without a trip through LDS.
+// The products over d_k and over tokens run on v_mfma_f32_16x16x32_bf16 with
+// each fp32 operand split into bf16 high and low parts, x = hi + lo to 16
+// significant bits: a b = hi hi + hi lo + lo hi, the lo lo term (2^-18 of the
+// product) dropped, every sum accumulated in fp32. One such product costs
+// three bf16 MFMAs where the same 16x16x32 product takes eight fp32
+// 16x16x4 MFMAs of twice the cycles each. Operand lanes: A[row l%16][k 8(l/16)
+// + e], B[k 8(l/16) + e][col l%16], e < 8; result rows 4(l/16)+i, col l%16.
+// The scan works on transposed products (S^T w^T, S^T q_dec^T, v_new^T qk^T,
+// v_new^T k_dec), so that the state's A operand and every record operand are
+// runs of 8 consecutive elements in memory.
 #include "common.h"
 #include "qwen4mix_internal.h"
 
@@ -34,29 +39,91 @@ constexpr int CK_COLS = 16;       // d_v columns per scan workgroup
 constexpr int CK_MIN_SEQ = 16;    // shorter prefill chunks take the token loop
 constexpr int CK_PARTS = 4;       // prep workgroups per chunk when chunks are few
 
-// One fp32 record per (sequence, head, chunk):
-//   w   [64][128]   T (k beta e^cum)                               fragment order
-//   u   [64][128]   T (v beta)                                     row-major
-//   qd  [64][128]   q e^cum (q l2-normalised and scaled by d^-1/2) fragment order
-//   kdT [128][64]   (k e^(cum_last - cum))^T                       fragment order
-//   qk  [64][64]    (q k^T) * decay on and below the diagonal      fragment order
-//   ecl [64]        e^cum_last in element 0
-// Fragment order (frag_index) stores each 16x16 block as the A operands of its
-// four 16x16x4 MFMA steps in lane order: every wave-wide float4 load of the
-// scan reads 1 KB of contiguous memory.
+// One record per (sequence, head, chunk), in floats. A fragment pair is the
+// bf16 high parts of one 16x32 MFMA operand (64 lanes x 8, 1 KB) followed by
+// its low parts: FRAG2 floats. Fragment (b, s) of a matrix holds rows 16 b ..
+// 16 b + 15 and k-step s (k = 32 s .. 32 s + 31) in operand lane order, so a
+// wave's operand load reads 1 KB of contiguous memory.
+//   W    w[tok][dk] = T (k beta e^cum)          (token block, dk step)  4 x 4
+//   QD   q e^cum [tok][dk] (q l2-normalised, scaled by d^-1/2)          4 x 4
+//   QK   (q k^T)[i][j] * decay, j <= i          (i block, j step)       4 x 2
+//   KD   k e^(cum_last - cum), as [dk][tok]     (dk block, token step)  8 x 2
+//   U    u = T (v beta) [tok][dv], fp32 row-major
+//   ECL  e^cum_last in element 0
+constexpr long FRAG2 = 512;
 constexpr long CK_W = 0;
-constexpr long CK_U = CK_W + CK_C * CK_D;
-constexpr long CK_QD = CK_U + CK_C * CK_D;
-constexpr long CK_KDT = CK_QD + CK_C * CK_D;
-constexpr long CK_QK = CK_KDT + CK_C * CK_D;
-constexpr long CK_ECL = CK_QK + CK_C * CK_C;
+constexpr long CK_QD = CK_W + 16 * FRAG2;
+constexpr long CK_QK = CK_QD + 16 * FRAG2;
+constexpr long CK_KD = CK_QK + 8 * FRAG2;
+constexpr long CK_U = CK_KD + 16 * FRAG2;
+constexpr long CK_ECL = CK_U + CK_C * CK_D;
 constexpr long CK_REC = CK_ECL + 64;
 static_assert((CK_REC * 4) % 256 == 0, "records stay 256-byte aligned");
 
-// offset of element (row, col) of a [rows][ncol] matrix in fragment order:
-// 16x16 block, then lane 16 * ((col % 16) / 4) + row % 16, then col % 4
-__device__ __forceinline__ int frag_index(int row, int col, int ncol) {
-  return ((((row >> 4) * (ncol >> 4) + (col >> 4)) * 64 + ((col & 15) >> 2) * 16 + (row & 15)) << 2) + (col & 3);
+// An fp32 MFMA operand as bf16 high and low parts.
+struct Frag {
+  bf16x8_t hi, lo;
+};
+
+__device__ __forceinline__ float bf16_lo_half(unsigned w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi_half(unsigned w) { return __uint_as_float(w & 0xffff0000u); }
+
+// x = hi + lo: hi rounds x to bf16, lo rounds the (exact) remainder
+__device__ __forceinline__ void split2(float a, float b, unsigned& h, unsigned& l) {
+  h = pack_bf16x2(a, b);
+  l = pack_bf16x2(a - bf16_lo_half(h), b - bf16_hi_half(h));
+}
+
+__device__ __forceinline__ Frag split8(const float (&x)[8]) {
+  u32x4_t h, l;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    unsigned hh, ll;
+    split2(x[2 * i], x[2 * i + 1], hh, ll);
+    h[i] = hh;
+    l[i] = ll;
+  }
+  return Frag{__builtin_bit_cast(bf16x8_t, h), __builtin_bit_cast(bf16x8_t, l)};
+}
+
+// c + a b over one k-step, the small terms first
+__device__ __forceinline__ f32x4_t mfma3(const Frag& a, const Frag& b, f32x4_t c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, b.hi, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.lo, c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.hi, c, 0, 0, 0);
+}
+
+// lane's operand from a record fragment pair
+__device__ __forceinline__ Frag ld_frag(const float* pair, int lane) {
+  const char* p = reinterpret_cast<const char*>(pair) + lane * 16;
+  return Frag{*reinterpret_cast<const bf16x8_t*>(p), *reinterpret_cast<const bf16x8_t*>(p + 1024)};
+}
+
+// the lane's 8 elements of a fragment pair, from fp32 values
+__device__ __forceinline__ void st_frag8(float* pair, int lane, const float (&x)[8]) {
+  const Frag f = split8(x);
+  char* p = reinterpret_cast<char*>(pair) + lane * 16;
+  *reinterpret_cast<bf16x8_t*>(p) = f.hi;
+  *reinterpret_cast<bf16x8_t*>(p + 1024) = f.lo;
+}
+
+// 4 of a lane's 8 elements (e0 .. e0 + 3, e0 = 0 or 4) of a fragment pair
+__device__ __forceinline__ void st_frag4(float* pair, int lane, int e0, float a, float b, float c, float d) {
+  unsigned h0, l0, h1, l1;
+  split2(a, b, h0, l0);
+  split2(c, d, h1, l1);
+  char* p = reinterpret_cast<char*>(pair) + lane * 16 + e0 * 2;
+  *reinterpret_cast<u32x2_t*>(p) = u32x2_t{h0, h1};
+  *reinterpret_cast<u32x2_t*>(p + 1024) = u32x2_t{l0, l1};
+}
+
+// A result tile's lane holds rows 4 g + v (v < 4) of column r16; when the rows
+// are the k index of a fragment pair whose k-step starts at row 32 s of the
+// result's block b (rows 16 b ..), its 4 values are elements e0 .. e0 + 3 of
+// lane r16 + 16 g' of fragment step s = b / 2
+__device__ __forceinline__ void frag_slot(int blk, int g4, int& lane_g, int& e0) {
+  lane_g = 2 * (blk & 1) + (g4 >> 1);
+  e0 = 4 * (g4 & 1);
 }
 
 __device__ __forceinline__ f32x4_t mfma4(float a, float b, f32x4_t c) {
@@ -95,12 +162,35 @@ __device__ __forceinline__ void tile_ij(int t, int& I, int& J) {
   J = t - I * (I + 1) / 2;
 }
 
-// 16x16 tile of X Y^T over 128 dims: a = &X[row0 + l%16][4(l/16)], b likewise
-__device__ __forceinline__ f32x4_t gram_tile(const float* a, const float* b) {
+// a lane's operand from a [row][k] bf16 hi / lo LDS tile pair (row stride
+// CK_HS): row `row`, k = 32 s + 8 g4 .. + 7
+constexpr int CK_HS = CK_D + 8;   // bf16 row stride of the [token][dim] tiles
+__device__ __forceinline__ Frag tile_frag(const uint16_t* hi, const uint16_t* lo, int row, int s, int g4) {
+  const int o = row * CK_HS + 32 * s + 8 * g4;
+  return Frag{*reinterpret_cast<const bf16x8_t*>(hi + o), *reinterpret_cast<const bf16x8_t*>(lo + o)};
+}
+
+// 16x16 tile of X Y^T over the 128 dims from split [token][dim] tiles:
+// rows xr + l%16 of X and yr + l%16 of Y
+__device__ __forceinline__ f32x4_t gram16(const uint16_t* xh, const uint16_t* xl, int xr, const uint16_t* yh,
+                                          const uint16_t* yl, int yr, int g4) {
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc = mfma4x4(lds4(a + 16 * j), lds4(b + 16 * j), acc);
+  for (int s = 0; s < 4; ++s) acc = mfma3(tile_frag(xh, xl, xr, s, g4), tile_frag(yh, yl, yr, s, g4), acc);
   return acc;
+}
+
+// a lane's operand of an fp32 LDS row: elements 32 s + 8 g4 .. + 7, each times
+// scale[element] when SCALED
+template <bool SCALED>
+__device__ __forceinline__ Frag row_frag(const float* row, int s, int g4, const float* scale) {
+  const int c = 32 * s + 8 * g4;
+  const float4 a = lds4(row + c), b = lds4(row + c + 4);
+  float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  if (SCALED)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] *= scale[c + e];
+  return split8(x);
 }
 
 template <typename T>
@@ -113,12 +203,19 @@ struct ChunkPrepArgs {
   long q_stride, v_stride;
 };
 
-struct PrepShared {
-  float q[CK_C][CK_LD];    // normalised q * d^-1/2
-  float k[CK_C][CK_LD];    // normalised k
-  float v[CK_C][CK_LD];    // v * beta
-  float L[CK_C][CK_LT];    // (k beta k^T) * decay, strictly lower
-  float Tm[CK_C][CK_LT];   // (I + L)^-1, lower
+struct alignas(16) PrepShared {
+  union {
+    struct {
+      uint16_t h[CK_C * CK_HS], l[CK_C * CK_HS];   // normalised q * d^-1/2, split
+    } q;
+    struct {
+      float L[CK_C][CK_LT];    // (k beta k^T) * decay, strictly lower
+      float Tm[CK_C][CK_LT];   // (I + L)^-1, lower
+    } t;                       // after the q k^T tiles are done with q
+  } u;
+  uint16_t kh[CK_C * CK_HS], kl[CK_C * CK_HS];     // normalised k, split
+  float kT[CK_D][CK_LT];       // normalised k, [dim][token]
+  float vT[CK_D][CK_LT];       // v * beta, [dim][token]
   float cum[CK_C], beta[CK_C], ecum[CK_C], bec[CK_C], kds[CK_C];
 };
 
@@ -128,7 +225,7 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   QM_PHASE_DECL
   QM_PHASE(0);
   // A.parts workgroups per chunk: each forms L and T, then writes its share
-  // (all of it, or a quarter) of qk, q_dec, k_dec^T and of the w / u columns
+  // (all of it, or a quarter) of the record
   const int part = blockIdx.x % A.parts;
   const int c = (blockIdx.x / A.parts) % A.n_chunks;
   const int bh = blockIdx.x / A.parts / A.n_chunks;
@@ -139,73 +236,83 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int g4 = lane >> 4, r16 = lane & 15;
   float* rec = A.ws + ((long)bh * A.n_chunks + c) * CK_REC;
-
-  // gates; padding tokens carry g = 0 and beta = 0
-  if (wid == 0) {
-    const bool ok = lane < n_valid;
-    const long gi = ((long)b * A.seq + t0 + (ok ? lane : 0)) * A.heads + h;
-    const float gv = ok ? A.g[gi] : 0.f;
-    const float bv = ok ? A.beta[gi] : 0.f;
-    double s = gv;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const double o = __shfl_up(s, off, 64);
-      if (lane >= off) s += o;
-    }
-    const float cum = static_cast<float>(s);
-    const float last = __shfl(cum, 63, 64);
-    const float ec = expf(cum);
-    sh.cum[lane] = cum;
-    sh.beta[lane] = bv;
-    sh.ecum[lane] = ec;
-    sh.bec[lane] = bv * ec;
-    sh.kds[lane] = expf(last - cum);
-    if (lane == 0 && part == 0) rec[CK_ECL] = expf(last);
-  }
+  auto mine = [&](int quarter) __attribute__((always_inline)) { return quarter / span == part; };
 
   // q, k, v rows: four threads per token, 32 dims each as four runs of 8
+  const int t = tid >> 2, p = tid & 3;
+  const bool tok_ok = t < n_valid;
+  float qn[32];
   {
-    const int t = tid >> 2, p = tid & 3;
-    const bool ok = t < n_valid;
-    const long tok = (long)b * A.seq + t0 + (ok ? t : 0);
+    const long tok = (long)b * A.seq + t0 + (tok_ok ? t : 0);
     const long qo = tok * A.q_stride + (long)(h % A.hk) * CK_D;
     const long vo = tok * A.v_stride + (long)h * CK_D;
-    const float bv = ok ? A.beta[tok * A.heads + h] : 0.f;
-    float qv[32], kv[32], vv[32];
+    const float bv = tok_ok ? A.beta[tok * A.heads + h] : 0.f;
+    float kv[32], vv[32];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int d = 8 * (p + 4 * j);
-      load8(A.q + qo + d, qv + 8 * j);
+      load8(A.q + qo + d, qn + 8 * j);
       load8(A.k + qo + d, kv + 8 * j);
       load8(A.v + vo + d, vv + 8 * j);
     }
+
+    // gates; padding tokens carry g = 0 and beta = 0
+    if (wid == 0) {
+      const bool ok = lane < n_valid;
+      const long gi = ((long)b * A.seq + t0 + (ok ? lane : 0)) * A.heads + h;
+      const float gv = ok ? A.g[gi] : 0.f;
+      const float bl = ok ? A.beta[gi] : 0.f;
+      double s = gv;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const double o = __shfl_up(s, off, 64);
+        if (lane >= off) s += o;
+      }
+      const float cum = static_cast<float>(s);
+      const float last = __shfl(cum, 63, 64);
+      const float ec = expf(cum);
+      sh.cum[lane] = cum;
+      sh.beta[lane] = bl;
+      sh.ecum[lane] = ec;
+      sh.bec[lane] = bl * ec;
+      sh.kds[lane] = expf(last - cum);
+      if (lane == 0 && part == 0) rec[CK_ECL] = expf(last);
+    }
+
     float sq = 0.f, sk = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      sq = fmaf(qv[i], qv[i], sq);
+      sq = fmaf(qn[i], qn[i], sq);
       sk = fmaf(kv[i], kv[i], sk);
     }
     sq += __shfl_xor(sq, 1, 64);
     sk += __shfl_xor(sk, 1, 64);
     sq += __shfl_xor(sq, 2, 64);
     sk += __shfl_xor(sk, 2, 64);
-    const float rq = ok ? rsqrt_rn(sq + 1e-6f) : 0.f;
-    const float rk = ok ? rsqrt_rn(sk + 1e-6f) : 0.f;
+    const float rq = tok_ok ? rsqrt_rn(sq + 1e-6f) : 0.f;
+    const float rk = tok_ok ? rsqrt_rn(sk + 1e-6f) : 0.f;
     const float qscale = 0.08838834764831845f;  // 128^-1/2
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int i = 0; i < 32; ++i) {
+      qn[i] = mul_rn(mul_rn(qn[i], rq), qscale);
+      kv[i] = mul_rn(kv[i], rk);
+      vv[i] = vv[i] * bv;
+    }
 #pragma unroll
-      for (int e = 0; e < 8; e += 4) {
-        const int d = 8 * (p + 4 * j) + e;
-        const float* x = qv + 8 * j + e;
-        const float* y = kv + 8 * j + e;
-        const float* z = vv + 8 * j + e;
-        *reinterpret_cast<float4*>(&sh.q[t][d]) =
-            make_float4(mul_rn(mul_rn(x[0], rq), qscale), mul_rn(mul_rn(x[1], rq), qscale),
-                        mul_rn(mul_rn(x[2], rq), qscale), mul_rn(mul_rn(x[3], rq), qscale));
-        *reinterpret_cast<float4*>(&sh.k[t][d]) =
-            make_float4(mul_rn(y[0], rk), mul_rn(y[1], rk), mul_rn(y[2], rk), mul_rn(y[3], rk));
-        *reinterpret_cast<float4*>(&sh.v[t][d]) = make_float4(z[0] * bv, z[1] * bv, z[2] * bv, z[3] * bv);
+    for (int j = 0; j < 4; ++j) {
+      const int d = 8 * (p + 4 * j);
+      float xq[8], xk[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { xq[e] = qn[8 * j + e]; xk[e] = kv[8 * j + e]; }
+      const Frag fq = split8(xq), fk = split8(xk);
+      *reinterpret_cast<bf16x8_t*>(&sh.u.q.h[t * CK_HS + d]) = fq.hi;
+      *reinterpret_cast<bf16x8_t*>(&sh.u.q.l[t * CK_HS + d]) = fq.lo;
+      *reinterpret_cast<bf16x8_t*>(&sh.kh[t * CK_HS + d]) = fk.hi;
+      *reinterpret_cast<bf16x8_t*>(&sh.kl[t * CK_HS + d]) = fk.lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sh.kT[d + e][t] = kv[8 * j + e];
+        sh.vT[d + e][t] = vv[8 * j + e];
       }
     }
   }
@@ -213,21 +320,75 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   __syncthreads();
   QM_PHASE(2);
 
+  // q e^cum fragments (QD: token block t / 16, dk step j) from the thread's
+  // own q values: its run j of 8 dims is lane t % 16 + 16 p of fragment j
+  if (mine(t >> 4)) {
+    const float e = sh.ecum[t];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = qn[8 * j + i] * e;
+      st_frag8(rec + CK_QD + ((t >> 4) * 4 + j) * FRAG2, (t & 15) + 16 * p, x);
+    }
+  }
+  QM_PHASE(10);
+  // qk = (q k^T) * exp(cum_i - cum_j) for j <= i, as QK fragments: tile
+  // (I, J) is computed as k_J q_I^T, so that a lane holds 4 consecutive j of
+  // one i; tiles 10 and 11 are the zero blocks (0, 1) and (2, 3) above the
+  // diagonal that the scan's 32-wide k-steps read. Tile ti belongs to quarter
+  // ti % 4; this workgroup's tiles go round-robin to its waves
+  {
+    int k = 0;
+    for (int ti = 0; ti < 12; ++ti) {
+      if (!mine(ti & 3)) continue;
+      if (k++ % 4 != wid) continue;
+      int I, J;
+      if (ti < 10) tile_ij(ti, I, J);
+      else { I = ti == 10 ? 0 : 2; J = I + 1; }
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      if (ti < 10) acc = gram16(sh.kh, sh.kl, 16 * J + r16, sh.u.q.h, sh.u.q.l, 16 * I + r16, g4);
+      // the decays' operands are read before any exponential, outside the
+      // masks, so that their LDS latencies overlap
+      const int i = 16 * I + r16;
+      const float ci = sh.cum[i];
+      const float4 cj = lds4(&sh.cum[16 * J + 4 * g4]);
+      const float cjv[4] = {cj.x, cj.y, cj.z, cj.w};
+      float x[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float val = acc[v] * expf(ci - cjv[v]);
+        x[v] = ti < 10 && i >= 16 * J + 4 * g4 + v ? val : 0.f;
+      }
+      int lg, e0;
+      frag_slot(J, g4, lg, e0);
+      st_frag4(rec + CK_QK + (I * 2 + J / 2) * FRAG2, r16 + 16 * lg, e0, x[0], x[1], x[2], x[3]);
+    }
+  }
+  QM_PHASE(3);
+  __syncthreads();   // q is done with: L and T take its space
+  QM_PHASE(9);
+
+  float (&L)[CK_C][CK_LT] = sh.u.t.L;
+  float (&Tm)[CK_C][CK_LT] = sh.u.t.Tm;
   // L = (k k^T) * beta_i * exp(cum_i - cum_j) for j < i
   for (int ti = wid; ti < 10; ti += 4) {
     int I, J;
     tile_ij(ti, I, J);
-    const f32x4_t acc = gram_tile(&sh.k[16 * I + r16][4 * g4], &sh.k[16 * J + r16][4 * g4]);
+    const f32x4_t acc = gram16(sh.kh, sh.kl, 16 * I + r16, sh.kh, sh.kl, 16 * J + r16, g4);
     const int j = 16 * J + r16;
+    const float cj = sh.cum[j];
+    const float4 ci = lds4(&sh.cum[16 * I + 4 * g4]), bi = lds4(&sh.beta[16 * I + 4 * g4]);
+    const float civ[4] = {ci.x, ci.y, ci.z, ci.w}, biv[4] = {bi.x, bi.y, bi.z, bi.w};
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int i = 16 * I + 4 * g4 + v;
-      sh.L[i][j] = i > j ? (acc[v] * sh.beta[i]) * expf(sh.cum[i] - sh.cum[j]) : 0.f;
+      const float val = (acc[v] * biv[v]) * expf(civ[v] - cj);
+      L[i][j] = i > j ? val : 0.f;
     }
   }
-  QM_PHASE(3);
-  __syncthreads();
   QM_PHASE(4);
+  __syncthreads();
 
   if (wid == 0) {
     // (I + L_II)^-1 for the four diagonal blocks; lane = (block, column):
@@ -236,49 +397,39 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float* Lr = &sh.L[16 * I + i][16 * I];
+      const float* Lr = &L[16 * I + i][16 * I];
       float acc = i == col ? 1.f : 0.f;
 #pragma unroll
       for (int kk = 0; kk < i; ++kk) acc = fmaf(-Lr[kk], x[kk], acc);
       x[i] = acc;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sh.Tm[16 * I + i][16 * I + col] = x[i];
+    for (int i = 0; i < 16; ++i) Tm[16 * I + i][16 * I + col] = x[i];
   } else {
-    // qk = (q k^T) * exp(cum_i - cum_j) for j <= i: tile ti belongs to quarter
-    // ti % 4; this workgroup's tiles go round-robin to waves 1-3
+    // the zero blocks (0, 1) and (2, 3) of T, which the 32-wide k-steps of
+    // the w and u products read
+    for (int idx = tid - 64; idx < 2 * 256; idx += CK_NT - 64) {
+      const int blk = idx >> 8, r = (idx >> 4) & 15, cc = idx & 15;
+      Tm[32 * blk + r][32 * blk + 16 + cc] = 0.f;
+    }
+    // k_dec fragments (KD: dk blocks 2 quarter, 2 quarter + 1, token steps
+    // 0..1): lane (dk 16 D + r16, tokens 32 s + 8 g4 ..), round-robin over
+    // waves 1-3
     int k = 0;
-    for (int ti = 0; ti < 10; ++ti) {
-      if ((ti & 3) / span != part) continue;
+    for (int f = 0; f < 16; ++f) {
+      const int D = f >> 1, s = f & 1;
+      if (!mine(D >> 1)) continue;
       if (k++ % 3 != wid - 1) continue;
-      int I, J;
-      tile_ij(ti, I, J);
-      const f32x4_t acc = gram_tile(&sh.q[16 * I + r16][4 * g4], &sh.k[16 * J + r16][4 * g4]);
-      const int j = 16 * J + r16;
+      const int c0 = 32 * s + 8 * g4;
+      const float* row = &sh.kT[16 * D + r16][0];
+      const float4 x0 = lds4(row + c0), x1 = lds4(row + c0 + 4);
+      float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int i = 16 * I + 4 * g4 + v;
-        rec[CK_QK + frag_index(i, j, CK_C)] = i >= j ? acc[v] * expf(sh.cum[i] - sh.cum[j]) : 0.f;
-      }
+      for (int e = 0; e < 8; ++e) x[e] *= sh.kds[c0 + e];
+      st_frag8(rec + CK_KD + f * FRAG2, lane, x);
     }
   }
-
   QM_PHASE(5);
-  // q e^cum as [token][dim] and (k e^(cum_last - cum))^T as [dim][token]
-  for (int it = 2 * span * part; it < 2 * span * (part + 1); ++it) {
-    const int idx = tid + CK_NT * it;
-    const int t = idx >> 5, d = 4 * (idx & 31);
-    const float4 x = lds4(&sh.q[t][d]);
-    const float e = sh.ecum[t];
-    *reinterpret_cast<float4*>(rec + CK_QD + frag_index(t, d, CK_D)) = make_float4(x.x * e, x.y * e, x.z * e, x.w * e);
-  }
-  for (int it = 2 * span * part; it < 2 * span * (part + 1); ++it) {
-    const int idx = tid + CK_NT * it;
-    const int t = 4 * (idx & 15), d = idx >> 4;
-    *reinterpret_cast<float4*>(rec + CK_KDT + frag_index(d, t, CK_C)) =
-        make_float4(sh.k[t][d] * sh.kds[t], sh.k[t + 1][d] * sh.kds[t + 1], sh.k[t + 2][d] * sh.kds[t + 2],
-                    sh.k[t + 3][d] * sh.kds[t + 3]);
-  }
   __syncthreads();
 
   QM_PHASE(6);
@@ -287,48 +438,48 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   for (int dist = 1; dist < 4; ++dist) {
     if (wid < 4 - dist) {
       const int J = wid, I = wid + dist;
-      f32x4_t p = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t pp = {0.f, 0.f, 0.f, 0.f};
       for (int K = J; K < I; ++K) {
-        const float4 a = lds4(&sh.L[16 * I + r16][16 * K + 4 * g4]);
-        const float* tb = &sh.Tm[16 * K + 4 * g4][16 * J + r16];
-        p = mfma4x4(a, make_float4(tb[0], tb[CK_LT], tb[2 * CK_LT], tb[3 * CK_LT]), p);
+        const float4 a = lds4(&L[16 * I + r16][16 * K + 4 * g4]);
+        const float* tb = &Tm[16 * K + 4 * g4][16 * J + r16];
+        pp = mfma4x4(a, make_float4(tb[0], tb[CK_LT], tb[2 * CK_LT], tb[3 * CK_LT]), pp);
       }
-      const float4 xa = lds4(&sh.Tm[16 * I + r16][16 * I + 4 * g4]);
+      const float4 xa = lds4(&Tm[16 * I + r16][16 * I + 4 * g4]);
       f32x4_t x = {0.f, 0.f, 0.f, 0.f};
-      x = mfma4x4(xa, make_float4(p[0], p[1], p[2], p[3]), x);
+      x = mfma4x4(xa, make_float4(pp[0], pp[1], pp[2], pp[3]), x);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) sh.Tm[16 * I + 4 * g4 + v][16 * J + r16] = -x[v];
+      for (int v = 0; v < 4; ++v) Tm[16 * I + 4 * g4 + v][16 * J + r16] = -x[v];
     }
     __syncthreads();
   }
 
   QM_PHASE(7);
-  // w = T (k beta e^cum) and u = T (v beta): quarter r holds column tiles 2r
-  // and 2r + 1 of each, one (matrix, tile) per wave
-  for (int kq = 0; kq < span; ++kq) {
-    const bool is_u = wid >= 2;
-    const int col = 16 * (2 * (span * part + kq) + (wid & 1)) + r16;
-    float bo[4][4];
+  // w = T (k beta e^cum) and u = T (v beta), as w^T = (k beta e^cum)^T T^T so
+  // that a lane holds 4 consecutive dims of one token: quarter r holds column
+  // tiles 4 r .. 4 r + 3 of the 16 (w: 0..7, u: 8..15, 16 dims each), one per
+  // wave; T is lower triangular, so row block I needs k-steps 0 .. I / 2
+  for (int qr = span * part; qr < span * (part + 1); ++qr) {
+    const int tile = 4 * qr + wid;
+    const bool is_u = tile >= 8;
+    const int D = tile & 7;
+    const float* arow = is_u ? &sh.vT[16 * D + r16][0] : &sh.kT[16 * D + r16][0];
+    Frag a[2];
 #pragma unroll
-    for (int K = 0; K < 4; ++K) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t = 16 * K + 4 * g4 + e;
-        bo[K][e] = is_u ? sh.v[t][col] : sh.k[t][col] * sh.bec[t];
-      }
-    }
-    float* dst = rec + (is_u ? CK_U : CK_W);
+    for (int s2 = 0; s2 < 2; ++s2)
+      a[s2] = is_u ? row_frag<false>(arow, s2, g4, nullptr) : row_frag<true>(arow, s2, g4, sh.bec);
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int K = 0; K <= I; ++K)
-        acc = mfma4x4(lds4(&sh.Tm[16 * I + r16][16 * K + 4 * g4]), make_float4(bo[K][0], bo[K][1], bo[K][2], bo[K][3]),
-                      acc);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = 16 * I + 4 * g4 + v;
-        dst[is_u ? row * CK_D + col : frag_index(row, col, CK_D)] = acc[v];
+      for (int s2 = 0; s2 <= I / 2; ++s2) acc = mfma3(a[s2], row_frag<false>(&Tm[16 * I + r16][0], s2, g4, nullptr), acc);
+      // acc[v]: dim 16 D + 4 g4 + v of token 16 I + r16
+      if (is_u) {
+        *reinterpret_cast<float4*>(rec + CK_U + (16 * I + r16) * CK_D + 16 * D + 4 * g4) =
+            make_float4(acc[0], acc[1], acc[2], acc[3]);
+      } else {
+        int lg, e0;
+        frag_slot(D, g4, lg, e0);
+        st_frag4(rec + CK_W + (I * 4 + D / 2) * FRAG2, r16 + 16 * lg, e0, acc[0], acc[1], acc[2], acc[3]);
       }
     }
   }
@@ -344,37 +495,59 @@ struct ChunkScanArgs {
   int batch, seq, heads, n_chunks;
 };
 
-// A wave's operands of one chunk, none of which depends on the state: its 16
-// rows of w and q_dec, its row block of qk (blocks j <= wave used), its two
-// 16-row blocks of k_dec^T, its 4 values of u, and e^cum_last.
+// A wave's record operands of one chunk, none of which depends on the
+// state: the W and QD fragments of its token block (dk steps 0..3), the QK
+// fragments of its token block (j steps 0..1), the KD fragments of its two dk
+// blocks (token steps 0..1), its 4 values of u and e^cum_last.
 struct ScanOps {
-  float4 w[8], qd[8], qk[4], kd[2][4];
-  float u[4], ecl;
+  Frag w[4], qd[4], qk[2], kd[2][2];
+  float4 u;
+  float ecl;
 };
 
-__device__ __forceinline__ void load_scan_ops(const float* rec, int wid, int g4, int r16, int col0, ScanOps& o) {
-  const int lane4 = (16 * g4 + r16) * 4;
+__device__ __forceinline__ void load_scan_ops(const float* rec, int wid, int lane, int r16, int g4, int col0,
+                                              ScanOps& o) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    o.w[j] = ld4(rec + CK_W + (wid * 8 + j) * 256 + lane4);
-    o.qd[j] = ld4(rec + CK_QD + (wid * 8 + j) * 256 + lane4);
+  for (int s = 0; s < 4; ++s) {
+    o.w[s] = ld_frag(rec + CK_W + (wid * 4 + s) * FRAG2, lane);
+    o.qd[s] = ld_frag(rec + CK_QD + (wid * 4 + s) * FRAG2, lane);
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) o.qk[j] = ld4(rec + CK_QK + (wid * 4 + j) * 256 + lane4);
+  for (int s = 0; s < 2; ++s) o.qk[s] = ld_frag(rec + CK_QK + (wid * 2 + s) * FRAG2, lane);
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o.kd[t][j] = ld4(rec + CK_KDT + ((2 * wid + t) * 4 + j) * 256 + lane4);
-  const float* ur = rec + CK_U + (16 * wid + 4 * g4) * CK_D + col0 + r16;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) o.u[v] = ur[v * CK_D];
+    for (int s = 0; s < 2; ++s) o.kd[t][s] = ld_frag(rec + CK_KD + ((2 * wid + t) * 2 + s) * FRAG2, lane);
+  o.u = *reinterpret_cast<const float4*>(rec + CK_U + (16 * wid + r16) * CK_D + col0 + 4 * g4);
   o.ecl = rec[CK_ECL];
+}
+
+constexpr int SC_SS = CK_D + 8;   // bf16 row stride of the state tile [column][dk]
+constexpr int SC_SV = CK_C + 8;   // bf16 row stride of the v_new tile [column][token]
+
+// lane's A operand of row r16 of a bf16 hi / lo LDS tile pair, k = 32 s + 8 g4 ..
+__device__ __forceinline__ Frag lds_frag(const uint16_t* hi, const uint16_t* lo, int stride, int r16, int s, int g4) {
+  const int o = r16 * stride + 32 * s + 8 * g4;
+  return Frag{*reinterpret_cast<const bf16x8_t*>(hi + o), *reinterpret_cast<const bf16x8_t*>(lo + o)};
+}
+
+// columns c and c + 1 of row `r` of a [column][.] bf16 hi / lo tile pair from
+// two split values
+__device__ __forceinline__ void put2(uint16_t* hi, uint16_t* lo, int stride, int c, int r, float a, float b) {
+  unsigned hh, ll;
+  split2(a, b, hh, ll);
+  hi[c * stride + r] = static_cast<uint16_t>(hh);
+  hi[(c + 1) * stride + r] = static_cast<uint16_t>(hh >> 16);
+  lo[c * stride + r] = static_cast<uint16_t>(ll);
+  lo[(c + 1) * stride + r] = static_cast<uint16_t>(ll >> 16);
 }
 
 template <typename T>
 __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A) {
-  __shared__ float sST[CK_COLS][CK_LD];  // the state slice, transposed: [column][d_k]
-  __shared__ float sVT[CK_COLS][CK_LT];  // v_new of the chunk, transposed: [column][token]
+  // the state slice S^T [column][dk] and the chunk's v_new^T [column][token],
+  // as bf16 high and low parts (the A operands of the transposed products)
+  __shared__ __attribute__((aligned(16))) uint16_t sSh[CK_COLS * SC_SS], sSl[CK_COLS * SC_SS];
+  __shared__ __attribute__((aligned(16))) uint16_t sVh[CK_COLS * SC_SV], sVl[CK_COLS * SC_SV];
   QM_PHASE_DECL
   QM_PHASE(0);
   constexpr int NSL = CK_D / CK_COLS;
@@ -390,58 +563,60 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
   // operands two chunks ahead: three register sets, the loop unrolled by
   // three so that no set is copied while its loads are in flight
   ScanOps o0, o1, o2;
-  load_scan_ops(recs, wid, g4, r16, col0, o0);
-  load_scan_ops(recs + (long)min(1, A.n_chunks - 1) * CK_REC, wid, g4, r16, col0, o1);
-  // wave wid keeps d_k rows 32wid .. 32wid+31 of the slice as two result tiles
-  float* S = A.state + (long)bh * CK_D * CK_D + col0 + r16;
+  load_scan_ops(recs, wid, lane, r16, g4, col0, o0);
+  load_scan_ops(recs + (long)min(1, A.n_chunks - 1) * CK_REC, wid, lane, r16, g4, col0, o1);
+  // wave wid keeps dk rows 32 wid .. 32 wid + 31 of the slice as two result
+  // tiles of S^T: st[t][i] = S[dk 32 wid + 16 t + r16][column 4 g4 + i]
+  float* S = A.state + (long)bh * CK_D * CK_D + col0 + 4 * g4;
   f32x4_t st[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int row = 32 * wid + 16 * t + 4 * g4;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) st[t][v] = S[(long)(row + v) * CK_D];
-    *reinterpret_cast<float4*>(&sST[r16][row]) = make_float4(st[t][0], st[t][1], st[t][2], st[t][3]);
+    const float4 x = *reinterpret_cast<const float4*>(S + (long)(32 * wid + 16 * t + r16) * CK_D);
+    st[t] = f32x4_t{x.x, x.y, x.z, x.w};
+    put2(sSh, sSl, SC_SS, 4 * g4, 32 * wid + 16 * t + r16, st[t][0], st[t][1]);
+    put2(sSh, sSl, SC_SS, 4 * g4 + 2, 32 * wid + 16 * t + r16, st[t][2], st[t][3]);
   }
-
   QM_PHASE(1);
+
   auto chunk = [&](int ci, const ScanOps& cur, ScanOps& ahead) {
     // chunk ci + 2's operands fly during this one (clamped at the last chunk)
-    load_scan_ops(recs + (long)min(ci + 2, A.n_chunks - 1) * CK_REC, wid, g4, r16, col0, ahead);
+    load_scan_ops(recs + (long)min(ci + 2, A.n_chunks - 1) * CK_REC, wid, lane, r16, g4, col0, ahead);
     __syncthreads();
-    // rows 16wid.. of w S and q_dec S
+    // (w S)^T and (q_dec S)^T for tokens 16 wid ..: rows = columns 4 g4 + i,
+    // column = token 16 wid + r16
     f32x4_t aw = {0.f, 0.f, 0.f, 0.f}, ao = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float4 sb = lds4(&sST[r16][16 * j + 4 * g4]);
-      aw = mfma4x4(cur.w[j], sb, aw);
-      ao = mfma4x4(cur.qd[j], sb, ao);
+    for (int s = 0; s < 4; ++s) {
+      const Frag sa = lds_frag(sSh, sSl, SC_SS, r16, s, g4);
+      aw = mfma3(sa, cur.w[s], aw);
+      ao = mfma3(sa, cur.qd[s], ao);
     }
-    *reinterpret_cast<float4*>(&sVT[r16][16 * wid + 4 * g4]) =
-        make_float4(cur.u[0] - aw[0], cur.u[1] - aw[1], cur.u[2] - aw[2], cur.u[3] - aw[3]);
+    put2(sVh, sVl, SC_SV, 4 * g4, 16 * wid + r16, cur.u.x - aw[0], cur.u.y - aw[1]);
+    put2(sVh, sVl, SC_SV, 4 * g4 + 2, 16 * wid + r16, cur.u.z - aw[2], cur.u.w - aw[3]);
     __syncthreads();
 
-    // out rows 16wid..: q_dec S + qk v_new over the causal blocks j <= wid
-    float4 vb[4];
+    // out^T += v_new^T qk^T over the causal token steps (j <= i: steps 0 ..
+    // wid / 2; the record's QK holds zeros above the diagonal)
+    const Frag va0 = lds_frag(sVh, sVl, SC_SV, r16, 0, g4), va1 = lds_frag(sVh, sVl, SC_SV, r16, 1, g4);
+    ao = mfma3(va0, cur.qk[0], ao);
+    if (wid >= 2) ao = mfma3(va1, cur.qk[1], ao);
+    const int tok = ci * CK_C + 16 * wid + r16;
+    if (tok < A.seq) {
+      T* o = A.out + (((long)b * A.seq + tok) * A.heads + h) * CK_D + col0 + 4 * g4;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) vb[j] = lds4(&sVT[r16][16 * j + 4 * g4]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (j <= wid) ao = mfma4x4(cur.qk[j], vb[j], ao);
-    const int tok0 = ci * CK_C + 16 * wid + 4 * g4;
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-      if (tok0 + v < A.seq)
-        Act<T>::store(A.out, (((long)b * A.seq + tok0 + v) * A.heads + h) * CK_D + col0 + r16, ao[v]);
+      for (int i = 0; i < 4; ++i) Act<T>::store(o, i, ao[i]);
+    }
 
-    // S = S e^cum_last + k_dec^T v_new on this wave's rows
+    // S^T = S^T e^cum_last + v_new^T k_dec on this wave's dk rows (the tile
+    // is only read again after the next chunk's first barrier)
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const int row = 32 * wid + 16 * t;
       f32x4_t acc = {st[t][0] * cur.ecl, st[t][1] * cur.ecl, st[t][2] * cur.ecl, st[t][3] * cur.ecl};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc = mfma4x4(cur.kd[t][j], vb[j], acc);
+      acc = mfma3(va0, cur.kd[t][0], acc);
+      acc = mfma3(va1, cur.kd[t][1], acc);
       st[t] = acc;
-      *reinterpret_cast<float4*>(&sST[r16][row + 4 * g4]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      put2(sSh, sSl, SC_SS, 4 * g4, 32 * wid + 16 * t + r16, acc[0], acc[1]);
+      put2(sSh, sSl, SC_SS, 4 * g4 + 2, 32 * wid + 16 * t + r16, acc[2], acc[3]);
     }
     if (ci < 12) QM_PHASE(2 + ci);
   };
@@ -453,11 +628,9 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
   }
 
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int row = 32 * wid + 16 * t + 4 * g4;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) S[(long)(row + v) * CK_D] = st[t][v];
-  }
+  for (int t = 0; t < 2; ++t)
+    *reinterpret_cast<float4*>(S + (long)(32 * wid + 16 * t + r16) * CK_D) =
+        make_float4(st[t][0], st[t][1], st[t][2], st[t][3]);
   QM_PHASE(14);
   QM_PHASE_FLUSH_AT(4096u);
 }

@@ -1624,75 +1624,43 @@ __global__ __launch_bounds__(64) void qsa_chunk_bucket_kernel(ChunkBucketArgs A)
   }
 }
 
-// One wave's partials of a group: this lane's 4 channels of each of the 16
-// channel blocks (bf16, normalised by the sum), the (max, sum) pair and where
-// they go.
-struct GroupOut {
-  u32x2_t o[16];
-  float mx, l;
-  long pb;
-  bool ok;
+// Workgroup LDS of the chunk attention: the block's keys, the softmax weights
+// and sums every wave hands to the others, where each column's partial goes,
+// and a per-wave tile through which partial rows leave as whole lines.
+constexpr int CA_TROW = 144;     // bytes per row of the transpose tile (padded: the writes spread over the banks)
+struct ChunkShared {
+  uint16_t k[2][16][64 * 8];     // per 32-token group: 16 key pieces of 1 KB (16 tokens x 32 channels)
+  bf16x8_t p[2][4][64];          // softmax weights: [group][column block = wave that formed it][lane]
+  float rl[64];                  // 1 / sum per column (entry, query head)
+  long pb[64];                   // partial row of each column, -1 for none
+  u32x4_t tbuf[CA_NT / 64][16 * CA_TROW / 16];
 };
 
-// The wave's 16 partial rows (columns of its tiles) go out as whole 128-byte
-// lines: per 64-channel quarter, the lanes' fragments are transposed through
-// the wave's own LDS tile (16 rows of 144 bytes: padded so that the writes
-// spread over the banks) and each lane writes 16 contiguous bytes.
-constexpr int CA_TROW = 144;     // bytes per row of the transpose tile
-__device__ __forceinline__ void store_group(const ChunkAttnArgs& A, const GroupOut& R, unsigned char* tb) {
-  const int lane = threadIdx.x & 63, col = lane & 15, quad = lane >> 4;
-  long pbr[2];
-  bool okr[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = (lane + 64 * i) >> 3;          // lane r holds column r's row
-    pbr[i] = (static_cast<long>(__shfl(static_cast<int>(R.pb >> 32), r, 64)) << 32) |
-             static_cast<unsigned>(__shfl(static_cast<int>(R.pb), r, 64));
-    okr[i] = __shfl(static_cast<int>(R.ok), r, 64) != 0;
-  }
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-#pragma unroll
-    for (int d = 0; d < 4; ++d)
-      *reinterpret_cast<u32x2_t*>(tb + col * CA_TROW + (16 * d + 4 * quad) * 2) = R.o[4 * m + d];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int f = lane + 64 * i, r = f >> 3, seg = f & 7;
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(tb + r * CA_TROW + seg * 16);
-      if (okr[i]) *reinterpret_cast<u32x4_t*>(A.part_o + pbr[i] * QSA_D + 64 * m + 8 * seg) = v;
-    }
-  }
-  if (R.ok && quad == 0) *reinterpret_cast<float2*>(A.part_ml + R.pb * 2) = make_float2(R.mx, R.l);
-}
-
-// The scores and outputs of a group of up to 8 entries of block j whose keys
-// and values are in `kv` (wave: entries 2 wv, 2 wv + 1 of the group, lane
-// column il = which of the two, hh = query head of the kv head's eight).
-__device__ __forceinline__ void chunk_attend_group(const ChunkAttnArgs& A, const uint16_t (*kv)[32][64 * 8],
-                                                   const bf16x8_t (&qhi)[8], int j,
-                                                   unsigned pk, bool ok, long row_b, int pos0, int g, int nslot,
-                                                   GroupOut& R, bool mark = false) {
-  const int lane = threadIdx.x & 63, quad = lane >> 4, hh = lane & 7;
+// One wave's scores over the block for its two entries x 8 query heads (lane
+// column il = which entry, hh = query head): the softmax weights of its 16
+// columns go to S.p as the PV product's operands, their sums' reciprocals and
+// partial rows to S.rl / S.pb, the (max, sum) pairs to the workspace.
+__device__ __forceinline__ void chunk_scores(const ChunkAttnArgs& A, ChunkShared& S, const bf16x8_t (&qhi)[8],
+                                             int j, unsigned pk, bool ok, long row_b, int pos0, int g, int nslot,
+                                             bool mark = false) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, quad = lane >> 4, col = lane & 15, hh = lane & 7;
   const int gpb = A.ratio / 32;
   const int s = pk >> 16, slot = pk & 511;
   const bool tail = (pk >> 9) & 1u;
   const long row = row_b + s;
   const int p = pos0 + s;
-  // scores of the block's groups, then one softmax over its keys
   // a tile's eight key fragments are read from LDS before its products, so
   // that their latencies overlap
   f32x4_t sc[2][2];
 #pragma unroll
   for (int gi = 0; gi < 2; ++gi) {
-    const uint16_t* kvg = &kv[gi][0][0];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       f32x4_t c = {0.f, 0.f, 0.f, 0.f};
       if (gi < gpb) {
         bf16x8_t kf[8];
 #pragma unroll
-        for (int sk = 0; sk < 8; ++sk)
-          kf[sk] = *reinterpret_cast<const bf16x8_t*>(kvg + ((t * 8 + sk) * 64 + lane) * 8);
+        for (int sk = 0; sk < 8; ++sk) kf[sk] = *reinterpret_cast<const bf16x8_t*>(&S.k[gi][t * 8 + sk][lane * 8]);
 #pragma unroll
         for (int sk = 0; sk < 8; ++sk) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[sk], qhi[sk], c, 0, 0, 0);
       }
@@ -1716,9 +1684,9 @@ __device__ __forceinline__ void chunk_attend_group(const ChunkAttnArgs& A, const
   mx = xor32_max(xor16_max(mx));
   if (mark) QM_PHASE(9);
   float lsum = 0.f;
-  unsigned pw[2][4];
 #pragma unroll
-  for (int gi = 0; gi < 2; ++gi)
+  for (int gi = 0; gi < 2; ++gi) {
+    unsigned pw[4];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       float pv[4];
@@ -1727,35 +1695,73 @@ __device__ __forceinline__ void chunk_attend_group(const ChunkAttnArgs& A, const
         pv[v] = sc[gi][t][v] == -INFINITY ? 0.f : __expf(sc[gi][t][v] - mx);
         lsum += pv[v];
       }
-      pw[gi][2 * t] = pack_bf16x2(pv[0], pv[1]);
-      pw[gi][2 * t + 1] = pack_bf16x2(pv[2], pv[3]);
+      pw[2 * t] = pack_bf16x2(pv[0], pv[1]);
+      pw[2 * t + 1] = pack_bf16x2(pv[2], pv[3]);
     }
-  bf16x8_t pf[2];
-#pragma unroll
-  for (int gi = 0; gi < 2; ++gi) pf[gi] = __builtin_bit_cast(bf16x8_t, u32x4_t{pw[gi][0], pw[gi][1], pw[gi][2], pw[gi][3]});
+    S.p[gi][wv][lane] = __builtin_bit_cast(bf16x8_t, u32x4_t{pw[0], pw[1], pw[2], pw[3]});
+  }
   const float l = xor32_sum(xor16_sum(lsum));
   if (mark) QM_PHASE(10);
-  const float rl = 1.0f / l;
-  R.pb = ((row * A.hkv + g) * nslot + slot) * GQA + hh;
-  R.ok = ok;
-  R.mx = mx;
-  R.l = l;
+  const long pb = ((row * A.hkv + g) * nslot + slot) * GQA + hh;
+  if (quad == 0) {
+    S.rl[wv * 16 + col] = ok ? 1.0f / l : 0.f;
+    S.pb[wv * 16 + col] = ok ? pb : -1;
+    if (ok) *reinterpret_cast<float2*>(A.part_ml + pb * 2) = make_float2(mx, l);
+  }
+}
+
+// A wave with no entry in the group: its columns hold no partial.
+__device__ __forceinline__ void chunk_no_scores(ChunkShared& S) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const bf16x8_t zero = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
+  S.p[0][wv][lane] = zero;
+  S.p[1][wv][lane] = zero;
+  if (lane < 16) {
+    S.rl[wv * 16 + lane] = 0.f;
+    S.pb[wv * 16 + lane] = -1;
+  }
+}
+
+// The outputs of a group's 64 columns (4 waves' entries x 8 query heads) in
+// this wave's 64 channels (16 wv ..: value blocks 4 wv .. 4 wv + 3, whose
+// pieces `vr` the wave holds), divided by the sums and written out: per column
+// block the lanes' fragments pass through the wave's LDS tile, and each lane
+// writes 16 contiguous bytes of a 128-byte line.
+__device__ __forceinline__ void chunk_outputs(const ChunkAttnArgs& A, ChunkShared& S, const bf16x8_t (&vr)[2][4],
+                                              int gpb, bool mark = false) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, quad = lane >> 4, col = lane & 15;
+  unsigned char* tb = reinterpret_cast<unsigned char*>(&S.tbuf[wv][0]);
 #pragma unroll
-  for (int db = 0; db < 16; ++db) {
-    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-    bf16x8_t vf[2];
+  for (int cw = 0; cw < 4; ++cw) {
+    f32x4_t acc[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi)
-      if (gi < gpb) vf[gi] = *reinterpret_cast<const bf16x8_t*>(&kv[gi][16 + db][0] + lane * 8);
+      if (gi < gpb) {
+        const bf16x8_t pf = S.p[gi][cw][lane];
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi)
-      if (gi < gpb) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[gi], pf[gi], c, 0, 0, 0);
-    R.o[db] = u32x2_t{pack_bf16x2(c[0] * rl, c[1] * rl), pack_bf16x2(c[2] * rl, c[3] * rl)};
+        for (int cb = 0; cb < 4; ++cb) acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vr[gi][cb], pf, acc[cb], 0, 0, 0);
+      }
+    // acc[cb][v]: channel 64 wv + 16 cb + 4 quad + v of column 16 cw + col
+    const float rl = S.rl[cw * 16 + col];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+      *reinterpret_cast<u32x2_t*>(tb + col * CA_TROW + (16 * cb + 4 * quad) * 2) =
+          u32x2_t{pack_bf16x2(acc[cb][0] * rl, acc[cb][1] * rl), pack_bf16x2(acc[cb][2] * rl, acc[cb][3] * rl)};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int f = lane + 64 * i, r = f >> 3, seg = f & 7;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(tb + r * CA_TROW + seg * 16);
+      const long pbr = S.pb[cw * 16 + r];
+      if (pbr >= 0) *reinterpret_cast<u32x4_t*>(A.part_o + pbr * QSA_D + 64 * wv + 8 * seg) = v;
+    }
   }
   if (mark) QM_PHASE(11);
 }
 
-__global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArgs A) {
+// Three workgroups per compute unit (about 50 KB of LDS each).
+__global__ __launch_bounds__(CA_NT, 3) void qsa_chunk_attend_kernel(ChunkAttnArgs A) {
   QM_PHASE_DECL
   QM_PHASE(0);
   const int x = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
@@ -1769,35 +1775,33 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
   const long head_stride = (long)A.page_size * QSA_D;
   const int e_w = 2 * wv + il;                        // this lane's entry within a group of 8
 
-  __shared__ uint16_t kv[2][32][64 * 8];      // per 32-token group: 16 key then 16 value 1 KB pieces
-  __shared__ u32x4_t tbuf[CA_NT / 64][16 * CA_TROW / 16];   // per wave: partial rows on their way out
-  unsigned char* tb = reinterpret_cast<unsigned char*>(&tbuf[wv][0]);
+  __shared__ ChunkShared S;
 
-  // a block's key and value pieces pass through registers into LDS (a block of
-  // one 32-token group loads and stores it twice; the second copy is not
-  // read); indices of the register array are compile-time constants, so it
-  // stays in registers
-  u32x4_t kvr[16];
+  // A block's keys pass through registers into LDS (the thread's 8 of the 32
+  // pieces); the wave's value pieces (channel blocks 4 wv .. 4 wv + 3 of each
+  // 32-token group) stay in registers. A block of one 32-token group loads
+  // its pieces twice; the second copy is not used.
+  u32x4_t kr[8];
+  bf16x8_t vr[2][4];
   auto kv_load = [&](int j, int page0, int page1) __attribute__((always_inline)) {
-    const uint16_t* src[4];
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
       const int gg = gi < gpb ? gi : 0;
       const int rowg = (j * A.ratio + 32 * gg) % A.page_size;
       const long pbase = ((long)(gg ? page1 : page0) * A.hkv + g) * head_stride;
-      src[2 * gi] = A.k_pool + pbase + (rowg >> 4) * 8 * 512 + lane * 8 + wv * 512;
-      src[2 * gi + 1] = A.v_pool + pbase + (rowg >> 5) * 16 * 512 + lane * 8 + wv * 512;
+      const uint16_t* ks = A.k_pool + pbase + (rowg >> 4) * 8 * 512 + lane * 8;
+      const uint16_t* vs = A.v_pool + pbase + (rowg >> 5) * 16 * 512 + lane * 8;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kr[4 * gi + i] = *reinterpret_cast<const u32x4_t*>(ks + (wv + 4 * i) * 512);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) vr[gi][cb] = *reinterpret_cast<const bf16x8_t*>(vs + (4 * wv + cb) * 512);
     }
-    static_for<16>([&](auto i) {
-      kvr[i] = *reinterpret_cast<const u32x4_t*>(src[i / 4] + (i % 4) * 4 * 512);
-    });
   };
-  auto kv_store = [&]() __attribute__((always_inline)) {
-    // piece 4 pc + wv of group gi: keys at 0..15, values at 16..31
-    static_for<16>([&](auto i) {
-      constexpr int gi = i / 8, v = (i / 4) % 2, pc = i % 4;
-      *reinterpret_cast<u32x4_t*>(&kv[gi][16 * v + 4 * pc + wv][lane * 8]) = kvr[i];
-    });
+  auto k_store = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(&S.k[gi][wv + 4 * i][lane * 8]) = kr[4 * gi + i];
   };
   // the chunk path scores with the query's bf16 part (hi) alone: the keys
   // are bf16 too, and the softmax of these 64-key blocks is far inside the
@@ -1813,13 +1817,11 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
     page0 = ptab[min((j * A.ratio) / A.page_size, A.max_pages - 1)];
     page1 = ptab[min((j * A.ratio + (gpb > 1 ? 32 : 0)) / A.page_size, A.max_pages - 1)];
   };
-  GroupOut R;
 
   if (x < A.nwg_sel) {
     // ---- blocks x bpw .. x bpw + bpw - 1: their counts (both parities' words,
     // one of them current), first entries and pages, and the position, in one
-    // round trip; then block by block, the next nonempty block's pieces and
-    // first query rows in flight while this one is scored
+    // round trip; then block by block
     const int j0 = x * A.bpw;
     const int par = *A.parity;
     // (the per-block arrays are indexed by compile-time constants only, so
@@ -1850,53 +1852,29 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
       static_for<CA_MAX_BPW>([&](auto i) { r = k == i ? v[i] : r; });
       return r;
     };
-    auto first_pk = [&](int k, int n) __attribute__((always_inline)) {
-      const unsigned* lst = A.list + ((long)b * A.max_blocks + j0 + k) * A.seq;
-      return n > e_w ? pick(pk0, k) : lst[0];
-    };
-    {
-      const int k = __builtin_ctz(rem);
-      kv_load(j0 + k, pick(pg0, k), pick(pg1, k));
-      q_load(first_pk(k, static_cast<int>(pick(cw, k))));
-    }
-    kv_store();
-    __syncthreads();
-    QM_PHASE(3);
-    bf16x8_t qnx[8];
     for (int t = 0; rem != 0u; ++t) {
       const int k = __builtin_ctz(rem), j = j0 + k;
       rem &= rem - 1u;
       const int n = static_cast<int>(pick(cw, k));
       const unsigned* lst = A.list + ((long)b * A.max_blocks + j) * A.seq;
-      if (rem != 0u) {
-        const int kn = __builtin_ctz(rem);
-        kv_load(j0 + kn, pick(pg0, kn), pick(pg1, kn));
-        const unsigned pkn = first_pk(kn, static_cast<int>(pick(cw, kn)));
-        const long rown = row_b + (pkn >> 16);
-        const uint16_t* qh = A.q + q_index(rown, A.hkv, 0, g * GQA + hh, 8 * quad);
-#pragma unroll
-        for (int sk = 0; sk < 8; ++sk) qnx[sk] = load_bf16x8(qh + Q_SK_STRIDE * sk);
-      }
+      kv_load(j, pick(pg0, k), pick(pg1, k));
+      unsigned pk = n > e_w ? pick(pk0, k) : lst[0];
+      q_load(pk);
+      if (t > 0) __syncthreads();   // every wave is done with the previous block's keys
+      k_store();
+      __syncthreads();
+      if (t == 0) QM_PHASE(3);
       for (int g0 = 0; g0 < n; g0 += 8) {
         const int e = g0 + e_w;
-        unsigned pk;
         if (g0 > 0) {
           pk = lst[min(e, n - 1)];
           q_load(pk);
-        } else {
-          pk = first_pk(k, n);
         }
-        if (g0 + 2 * wv < n) {
-          chunk_attend_group(A, kv, qhi, j, pk, e < n, row_b, pos0, g, nslot, R, t == 0 && g0 == 0);
-          store_group(A, R, tb);
-        }
-      }
-      if (rem != 0u) {
-        __syncthreads();     // every wave is done with this block's pieces
-        kv_store();
-#pragma unroll
-        for (int sk = 0; sk < 8; ++sk) qhi[sk] = qnx[sk];
+        if (g0 + 2 * wv < n) chunk_scores(A, S, qhi, j, pk, e < n, row_b, pos0, g, nslot, t == 0 && g0 == 0);
+        else chunk_no_scores(S);
         __syncthreads();
+        chunk_outputs(A, S, vr, gpb, t == 0 && g0 == 0);
+        __syncthreads();   // every wave is done with the weights before the next group's
       }
     }
   } else {
@@ -1920,13 +1898,13 @@ __global__ __launch_bounds__(CA_NT, 2) void qsa_chunk_attend_kernel(ChunkAttnArg
       const bool mine = jr == j;
       if (!__syncthreads_or(mine ? 1 : 0)) continue;
       kv_load(j, bi ? pb0 : pa0, bi ? pb1 : pa1);
-      kv_store();
+      k_store();
       __syncthreads();
-      if (__builtin_amdgcn_ballot_w64(mine) != 0ull) {
-        chunk_attend_group(A, kv, qhi, j, pk, mine, row_b, pos0, g, nslot, R);
-        store_group(A, R, tb);
-      }
-      __syncthreads();     // every wave is done with the pieces before the next block's
+      if (__builtin_amdgcn_ballot_w64(mine) != 0ull) chunk_scores(A, S, qhi, j, pk, mine, row_b, pos0, g, nslot);
+      else chunk_no_scores(S);
+      __syncthreads();
+      chunk_outputs(A, S, vr, gpb);
+      __syncthreads();     // every wave is done with the keys and weights before the next block's
     }
   }
   QM_PHASE(4);

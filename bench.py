@@ -142,9 +142,10 @@ class Instance:
         self.dn = plan.DnDecodePlan(model, self.cache, 0, bf)
         self.qsa.positions.fill_(pos)
         self.dn.positions.fill_(pos)
-        # the same two launches with their arguments converted once (the eager loop's launcher)
+        # the same two launches with their arguments converted once (the eager
+        # loop's launcher; a plan past the one-launch decode's limits has none)
         self.bound = [self.qsa.bind(self.qg, self.k, self.v, self.iq, self.ik),
-                      self.dn.bind(self.qkv, self.z, self.a, self.b)]
+                      self.dn.bind(self.qkv, self.z, self.a, self.b)] if self.qsa.fused else None
 
     def step(self, stream):
         self.qsa.run(self.qg, self.k, self.v, self.iq, self.ik, stream)
@@ -518,6 +519,31 @@ def run_decode(qm, dev, pos, steps, warmup, instances=0, graphs=True):
     torch.cuda.synchronize()
     return {"pos": pos, "us_step": sec * 1e6, "kernel_us": kern, "instances": n_inst, "touched": touched,
             "max_ctx": max_ctx, "graph_us_step": None if gsec is None else gsec * 1e6}
+
+
+LONG_POS, LONG_CTX = 196544, 196608   # 3072 blocks: past the one-launch decode's 2048
+
+
+def run_long_decode(qm, dev, reps=15, n_inst=8):
+    """QSA decode at position 196544 of a 196608-token context (3071 eligible
+    blocks, top-32): past the one-launch kernel's 2048 blocks, so the plan takes
+    qm_qsa_prep, the one-row scores spread over the blocks, the ranking
+    (qm_qsa_select with a score buffer) and qm_qsa_attend. Each figure is the median over `reps`
+    batches of one launch per instance (`n_inst` instances, 430 MB each), every
+    batch after FLUSH_MB of other data read, minus the flush alone."""
+    import torch
+    model = qm.Qwen4MixModel(qm.MixConfig(), weights_store(torch.bfloat16), device=dev, max_ctx=LONG_CTX)
+    insts = [Instance(qm, model, LONG_POS, LONG_CTX, 3000 + i) for i in range(n_inst)]
+    assert not insts[0].qsa.fused
+    flush = Flusher(dev)
+    torch.cuda.synchronize()
+    qsa = time_cold(insts, lambda x, s: x.qsa.run(x.qg, x.k, x.v, x.iq, x.ik, s), flush, launches=n_inst, reps=reps)
+    step = time_cold(insts, lambda x, s: x.step(s), flush, launches=n_inst, reps=reps)
+    del insts, flush
+    torch.cuda.synchronize()
+    return {"pos": LONG_POS, "ctx": LONG_CTX, "path": "qm_qsa_prep + scores over the blocks + qm_qsa_select + qm_qsa_attend",
+            "qsa_us_cold": round(qsa, 2), "step_us_cold": round(step, 2),
+            "qsa_gbs": round(qsa_bytes(LONG_POS) / (qsa * 1e-6) / 1e9, 1)}
 
 
 class PrefillInstance:
@@ -974,6 +1000,8 @@ def main():
         print(f"[sweep] hyper_connections {json.dumps(sweep['hyper_connections'])}", file=sys.stderr)
         sweep["layer_stack"] = run_stack(qm, dev, pos)
         print(f"[sweep] layer_stack {json.dumps(sweep['layer_stack'])}", file=sys.stderr)
+        sweep["long_context_decode"] = run_long_decode(qm, dev)
+        print(f"[sweep] long_context_decode {json.dumps(sweep['long_context_decode'])}", file=sys.stderr)
 
     cpu = None
     if not args.no_cpu:

@@ -233,7 +233,10 @@ int qm_qsa_items_stride(const qm_qsa_geom* g);
  * rule is this library's; torch leaves tie order unspecified).
  *   iq [B, S, idx_heads, idx_dim] f32; block_keys as above; positions [B] first
  *   row's position; ids [B, S, budget/ratio] int32 in rank order; n_sel [B, S];
- *   scores_out [B, S, max_blocks] f32 or NULL (ineligible entries -inf).
+ *   scores_out [B, S, max_blocks] f32 or NULL (ineligible entries -inf). Given
+ *   scores_out, the scores are computed by a launch of their own spread over
+ *   the blocks (the way to select among many blocks: a long-context decode
+ *   row), and the ranking launch reads them back.
  *   items [B, S, qm_qsa_items_stride(g)] int2 or NULL: the attention work list
  *   of each row -- entry 0 holds the count, then one entry per 32-token group
  *   of the selected blocks (rank order) and of the row's tail block: physical

@@ -295,9 +295,10 @@ def test_indexer_mask_matches_oracle(gpu, past, seq, dtype):
 # -- the decode path of two launches ---------------------------------------------------
 
 
-def test_front_then_attend_decode_matches_oracle(gpu):
-    """pos 8128 through qm_qsa_decode_front + qm_qsa_attend, forced the way a
-    plan too large for one resident group is routed."""
+def test_split_decode_matches_oracle(gpu):
+    """pos 8128 through qm_qsa_prep, the one-row scores spread over the blocks,
+    the ranking (qm_qsa_select with a score buffer) and qm_qsa_attend, forced
+    the way a plan too large for one resident group is routed."""
     qm = gpu
     dtype = torch.bfloat16
     pos = 8128
@@ -314,7 +315,7 @@ def test_front_then_attend_decode_matches_oracle(gpu):
     model.decode_group_fits = lambda splits, dt: False
     cache = qm.MixHybridCache(4, model.config, 1, pos + 128, DEV, dtype, page_table="random", seed=5)
     cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
-    print("front + attend decode pos=8128", flush=True)
+    print("split decode pos=8128", flush=True)
     got = model._full_attention(hidden.to(DEV), 3, cos.to(DEV), sin.to(DEV), cache, pos)
     assert "qsa_decode_3_1" not in model._ws           # the one-launch kernel never ran
     assert rel_err(got, want, OUT_TOL) < OUT_TOL
@@ -325,3 +326,68 @@ def test_front_then_attend_decode_matches_oracle(gpu):
     mask = om._indexer_mask(hidden, 3, cos, sin, oc2, pos + 1, pos)
     chosen = sorted(j for j in range((pos + 1) // 64) if bool(mask[0, 0, 0, j * 64]))
     assert sorted(ids[:n].tolist()) == chosen
+
+
+def _decode_case(qm, pos, seed):
+    dtype = torch.bfloat16
+    store = gi.FakeStore(gi.qsa_weights(3, seed, dtype))
+    keys, values, idx_keys = gi.qsa_past(seed + 1, pos, dtype)
+    hidden = gi.normal(gi.rng(seed + 2), (1, 1, gi.HIDDEN)).to(dtype)
+    cos, sin = tables(pos + 1)
+    om = OracleMixer(OracleConfig(), store)
+    oc = OracleHybridCache(4)
+    oc[3].keys, oc[3].values, oc[3].indexer_keys = keys, values, idx_keys
+    want = om._full_attention(hidden, 3, cos, sin, oc, pos)
+    oc2 = OracleHybridCache(4)
+    oc2[3].indexer_keys = idx_keys
+    mask = om._indexer_mask(hidden, 3, cos, sin, oc2, pos + 1, pos)
+    chosen = sorted(j for j in range((pos + 1) // 64) if bool(mask[0, 0, 0, j * 64]))
+    model = qm.Qwen4MixModel(qm.MixConfig(), store, device=DEV, max_ctx=pos + 128)
+    cache = qm.MixHybridCache(4, model.config, 1, pos + 128, DEV, dtype, page_table="random", seed=5)
+    cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
+    return model, cache, hidden, cos, sin, want, chosen
+
+
+def test_decode_front_entry_point_matches_oracle(gpu):
+    """qm_qsa_decode_front (prep and selection in one launch) + qm_qsa_attend
+    at pos 8128, called through a decode plan: output and selected blocks
+    against the oracle."""
+    import ctypes
+    from importlib import import_module
+    qm = gpu
+    plan_mod = import_module(qm.__name__ + ".plan")
+    pos = 8128
+    model, cache, hidden, cos, sin, want, chosen = _decode_case(qm, pos, 71)
+    lc = cache[3]
+    g = model.qsa_geom(cache, torch.bfloat16)
+    cos_t, sin_t = model._rope(cos.to(DEV), sin.to(DEV), pos + 1)
+    model._sync_blocks(lc, g, cos_t, sin_t, pos, 3)
+    qg, k, v, iq, ik = (t.contiguous() for t in model.project(hidden.to(DEV), 3, "qsa_in"))
+    plan = plan_mod.QsaDecodePlan(model, cache, 3, pos, torch.bfloat16, fused=False)
+    plan.cos, plan.sin = cos_t, sin_t
+    plan.positions.fill_(pos)
+    print("front + attend decode pos=8128", flush=True)
+    s = qm.native.stream_handle(torch.device(DEV))
+    plan.front(qg, k, v, iq, ik, s)
+    plan.attend(qg, s)
+    got = model.project(plan.out, 3, "qsa_out")[0]
+    assert rel_err(got, want, OUT_TOL) < OUT_TOL
+    n = int(plan.n_sel.cpu()[0, 0])
+    assert sorted(plan.ids.cpu()[0, 0, :n].tolist()) == chosen
+
+
+def test_long_context_decode_matches_oracle(gpu):
+    """pos 131200 of a 131328-token context (2050 eligible blocks, past the
+    one-launch kernel's 2048): the model's decode step takes prep, the scores
+    spread over the blocks, the ranking and the attention; output and the
+    selected blocks against the oracle."""
+    qm = gpu
+    pos = 131200
+    model, cache, hidden, cos, sin, want, chosen = _decode_case(qm, pos, 81)
+    assert not model.fused_decode_fits(cache)
+    print("long-context decode pos=131200", flush=True)
+    got = model._full_attention(hidden.to(DEV), 3, cos.to(DEV), sin.to(DEV), cache, pos)
+    assert rel_err(got, want, OUT_TOL) < OUT_TOL
+    lc = cache[3]
+    n = int(lc.last_n_sel.cpu()[0, 0])
+    assert sorted(lc.last_ids.cpu()[0, 0, :n].tolist()) == chosen

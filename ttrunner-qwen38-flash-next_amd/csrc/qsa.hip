@@ -1274,6 +1274,52 @@ __global__ __launch_bounds__(64 * SCR_ROWS) void qsa_score_rows_kernel(ScoreRows
   else if (A.fill && j < A.max_blocks) out[j] = -INFINITY;
 }
 
+// Block scores of one query row per sequence (decode) in the reference's
+// one-row summation order (row16_block_score, the order of the front and
+// decode kernels), spread over the blocks: workgroup (64 blocks, sequence),
+// 16 lanes per block, the 4 passes' key loads all issued before the first
+// product. Scores past the row's eligible blocks are -inf (up to max_blocks).
+constexpr int SC1_BLK = 64;                    // blocks per workgroup
+constexpr int SC1_NT = 256;
+
+struct ScoreRowArgs {
+  const float* iq; const float* block_keys; const int* positions; float* scores;
+  int idx_heads, ratio, max_blocks;
+};
+
+__global__ __launch_bounds__(SC1_NT) void qsa_score_row_kernel(ScoreRowArgs A) {
+  constexpr int PASS = SC1_NT / SCORE_LANES;   // blocks per pass: 16
+  constexpr int NPASS = SC1_BLK / PASS;        // 4
+  const int b = blockIdx.y, tid = threadIdx.x, m = tid & 15, jl = tid >> 4;
+  const int j0 = blockIdx.x * SC1_BLK;
+  const int n_elig = min((A.positions[b] + 1) / A.ratio, A.max_blocks);
+  float* out = A.scores + (long)b * A.max_blocks;
+  if (j0 >= n_elig) {
+    for (int j = j0 + tid; j < min(j0 + SC1_BLK, A.max_blocks); j += SC1_NT) out[j] = -INFINITY;
+    return;
+  }
+  const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
+  float kp[NPASS][8];
+#pragma unroll
+  for (int u = 0; u < NPASS; ++u) {
+    const int j = j0 + u * PASS + jl;
+    load_block_part(kp[u], bk, j, j < n_elig);
+  }
+  // this lane's elements 16 i + m of the 4 query rows (heads past idx_heads zero)
+  const float* q_row = A.iq + (long)b * A.idx_heads * IDX_D;
+  float q[4][8];
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[h][i] = h < A.idx_heads ? q_row[h * IDX_D + 16 * i + m] : 0.f;
+#pragma unroll
+  for (int u = 0; u < NPASS; ++u) {
+    const int j = j0 + u * PASS + jl;
+    const float sc = row16_block_score(q, kp[u], A.idx_heads);
+    if (m == 0 && j < A.max_blocks) out[j] = j < n_elig ? sc : -INFINITY;
+  }
+}
+
 __global__ __launch_bounds__(SELP_NT) void qsa_select_kernel(SelArgs A) {
   QM_PHASE_DECL
   const int row = blockIdx.x;
@@ -2690,11 +2736,19 @@ extern "C" int qm_qsa_select(const qm_qsa_geom* g, int seq, const float* iq, con
   if (g->max_blocks > SEL_MAX_BLOCKS || g->max_pages > SEL_MAX_BLOCKS || g->budget / g->ratio > SEL_MAX_BLOCKS / 2)
     return qm_fail(QM_ERR_UNSUPPORTED, "qm_qsa_select: more than 4096 blocks or pages");
   SelArgs A = sel_args(g, seq, iq, block_keys, positions, page_table, ids, n_sel, items, scores_out);
-  if (seq > 1 && scores_out) {
-    // several rows: the scores come from their own launch over every compute
-    // unit, and the selection ranks them
-    rc = launch_score_rows(g, seq, iq, block_keys, positions, scores_out, true, stream);
-    if (rc) return rc;
+  if (scores_out) {
+    // with a score buffer the scores come from their own launch over every
+    // compute unit (in the several-rows order for several rows, the one-row
+    // order for one), and the selection ranks them
+    if (seq > 1) {
+      rc = launch_score_rows(g, seq, iq, block_keys, positions, scores_out, true, stream);
+      if (rc) return rc;
+    } else {
+      ScoreRowArgs S{iq, block_keys, positions, scores_out, g->idx_heads, g->ratio, g->max_blocks};
+      hipLaunchKernelGGL(qsa_score_row_kernel, dim3((g->max_blocks + SC1_BLK - 1) / SC1_BLK, g->batch),
+                         dim3(SC1_NT), 0, stream, S);
+      QM_CHECK_LAUNCH();
+    }
     A.scores_in = scores_out;
     A.scores_out = nullptr;
   }

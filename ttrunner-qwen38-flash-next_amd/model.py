@@ -327,7 +327,7 @@ class Qwen4MixModel:
         norms = [native.ptr(self._dw(layer, n, torch.float32)) for n in
                  ("attn_q_norm.weight", "attn_k_norm.weight", "indexer.q_norm.weight", "indexer.k_norm.weight")]
         splits = lib.qm_qsa_decode_splits(ctypes.byref(g), query_offset) if seq == 1 else 0
-        if (seq == 1 and qg is not None and k is not None and attend and self.fused_decode_fits(cache)
+        if (seq == 1 and qg is not None and k is not None and attend and self.fused_decode_fits(cache, query_offset)
                 and self.decode_group_fits(splits, dt)):
             # decode: the whole QSA step in one qm_qsa_decode launch; its workspace
             # (generation words, flags, partials) is kept per layer and batch
@@ -346,34 +346,31 @@ class Qwen4MixModel:
             lc.n_tokens = query_offset + seq
             lc.last_ids, lc.last_n_sel, lc.last_iq, lc.last_q = ids, n_sel, iq_out, None
             return out
-        if seq == 1 and qg is not None and k is not None and attend:
-            # decode: prep and selection in one launch
-            native.call("qm_qsa_decode_front", ctypes.byref(g), native.ptr(qg), native.ptr(k), native.ptr(v),
-                        native.ptr(iq), native.ptr(ik), *norms, native.ptr(cos_t), native.ptr(sin_t),
-                        native.ptr(pos), native.ptr(lc.page_table), native.ptr(lc.k_pool), native.ptr(lc.v_pool),
-                        native.ptr(lc.raw_keys), native.ptr(lc.block_keys), native.ptr(q_out), native.ptr(iq_out),
-                        native.ptr(ids), native.ptr(n_sel), native.ptr(items), stream)
+        # every other case: prep, then the selection, then the attention below
+        native.call("qm_qsa_prep", ctypes.byref(g), seq, native.ptr(qg), native.ptr(k), native.ptr(v),
+                    native.ptr(iq), native.ptr(ik), *norms, native.ptr(cos_t), native.ptr(sin_t),
+                    native.ptr(pos), native.ptr(lc.page_table), native.ptr(lc.k_pool), native.ptr(lc.v_pool),
+                    native.ptr(lc.raw_keys), native.ptr(lc.block_keys), native.ptr(q_out), native.ptr(iq_out),
+                    stream)
+        if chunked:
+            # the chunk attention's own workspace per geometry: the entry
+            # counts it keeps between calls are laid out by batch and block count
+            chunk_ws = self._workspace(f"qsa_attend_chunk_{batch}_{cache.max_blocks}",
+                                       lib.qm_qsa_attend_chunk_workspace(ctypes.byref(g), seq))
+        if chunked and self.fuse_chunk_select:
+            # the selection also files each row's blocks into that workspace
+            # (one launch fewer per chunk)
+            native.call("qm_qsa_select_chunk", ctypes.byref(g), seq, native.ptr(iq_out),
+                        native.ptr(lc.block_keys), native.ptr(pos), native.ptr(ids), native.ptr(n_sel),
+                        native.ptr(chunk_ws), chunk_ws.numel(), stream)
         else:
-            native.call("qm_qsa_prep", ctypes.byref(g), seq, native.ptr(qg), native.ptr(k), native.ptr(v),
-                        native.ptr(iq), native.ptr(ik), *norms, native.ptr(cos_t), native.ptr(sin_t),
-                        native.ptr(pos), native.ptr(lc.page_table), native.ptr(lc.k_pool), native.ptr(lc.v_pool),
-                        native.ptr(lc.raw_keys), native.ptr(lc.block_keys), native.ptr(q_out), native.ptr(iq_out),
-                        stream)
-            if chunked:
-                # the chunk attention's own workspace per geometry: the entry
-                # counts it keeps between calls are laid out by batch and block count
-                chunk_ws = self._workspace(f"qsa_attend_chunk_{batch}_{cache.max_blocks}",
-                                           lib.qm_qsa_attend_chunk_workspace(ctypes.byref(g), seq))
-            if chunked and self.fuse_chunk_select:
-                # the selection also files each row's blocks into that workspace
-                # (one launch fewer per chunk)
-                native.call("qm_qsa_select_chunk", ctypes.byref(g), seq, native.ptr(iq_out),
-                            native.ptr(lc.block_keys), native.ptr(pos), native.ptr(ids), native.ptr(n_sel),
-                            native.ptr(chunk_ws), chunk_ws.numel(), stream)
-            else:
-                native.call("qm_qsa_select", ctypes.byref(g), seq, native.ptr(iq_out), native.ptr(lc.block_keys),
-                            native.ptr(pos), native.ptr(lc.page_table), native.ptr(ids), native.ptr(n_sel),
-                            native.ptr(items), None, stream)
+            # one row (a decode step past the one-launch kernel's range): a
+            # score buffer makes qm_qsa_select spread the scores over the blocks
+            scores = (self._workspace(f"qsa_scores_{batch}_{cache.max_blocks}", batch * cache.max_blocks * 4)
+                      if seq == 1 else None)
+            native.call("qm_qsa_select", ctypes.byref(g), seq, native.ptr(iq_out), native.ptr(lc.block_keys),
+                        native.ptr(pos), native.ptr(lc.page_table), native.ptr(ids), native.ptr(n_sel),
+                        native.ptr(items), native.ptr(scores), stream)
         lc.blocks_valid = max(lc.blocks_valid, (query_offset + seq) // c.indexer_compress_ratio)
         if k is not None:
             lc.n_tokens = query_offset + seq
@@ -409,16 +406,27 @@ class Qwen4MixModel:
         return (c.indexer_compress_ratio in (32, 64) and cache.max_blocks <= 4096
                 and cache.max_ctx <= 4096 * c.indexer_compress_ratio and c.block_topk <= 510)
 
-    def fused_decode_fits(self, cache) -> bool:
-        """Whether qm_qsa_decode covers this cache's geometry."""
+    # Up to this many eligible blocks the one-launch decode is the faster path:
+    # each of its workgroups scores and ranks every eligible block itself, so
+    # its time grows with the context (cold, MI355X: 11.0 us at 127 blocks,
+    # 25.3 at 511, 36.8 at 1023, 60.6 at 2047), while prep + the scores spread
+    # over the blocks + the ranking + the attention stay near 28-35 us.
+    FUSED_MAX_BLOCKS = 640
+
+    def fused_decode_fits(self, cache, max_position=None) -> bool:
+        """Whether qm_qsa_decode covers this cache's geometry (and, given a
+        position, whether it is the faster path there)."""
         c = self.config
-        return (cache.max_blocks <= 2048 and cache.max_pages <= 2048 and c.block_topk <= 256
+        fits = (cache.max_blocks <= 2048 and cache.max_pages <= 2048 and c.block_topk <= 256
                 and c.indexer_compress_ratio <= 64)
+        if max_position is not None:
+            fits = fits and (max_position + 1) // c.indexer_compress_ratio <= self.FUSED_MAX_BLOCKS
+        return fits
 
     def decode_group_fits(self, splits: int, dtype) -> bool:
         """Whether a qm_qsa_decode group of ``splits`` workgroups can be resident
         on the device at once (its workgroups wait for one another); larger
-        plans go through qm_qsa_decode_front + qm_qsa_attend."""
+        plans go through prep + select + attend."""
         lib = native.load()
         resident = lib.qm_qsa_decode_resident(native.act_code(dtype), splits)
         if resident < 0:

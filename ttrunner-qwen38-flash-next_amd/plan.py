@@ -84,7 +84,7 @@ class QsaDecodePlan:
     """One QSA decode step (prep, select, attend) of ``layer``, sized for
     positions up to ``max_position``."""
 
-    def __init__(self, model, cache, layer: int, max_position: int, dtype=torch.bfloat16):
+    def __init__(self, model, cache, layer: int, max_position: int, dtype=torch.bfloat16, fused=None):
         c = model.config
         self.model, self.layer, self.cache = model, layer, cache
         self.lc = cache[layer]
@@ -98,8 +98,16 @@ class QsaDecodePlan:
                               dtype=torch.uint8, device=dev)
         self.dec_splits = lib.qm_qsa_decode_splits(ctypes.byref(self.geom), max_position)
         # one launch when the geometry allows it and a group of dec_splits
-        # workgroups fits the device at once; else the front + attend launches
-        self.fused = model.fused_decode_fits(cache) and model.decode_group_fits(self.dec_splits, dtype)
+        # workgroups fits the device at once; else prep + select + attend
+        can_fuse = model.fused_decode_fits(cache) and model.decode_group_fits(self.dec_splits, dtype)
+        faster = model.fused_decode_fits(cache, max_position)
+        if fused and not can_fuse:
+            raise native.QmError(f"layer {layer}: this geometry does not fit one qm_qsa_decode launch")
+        self.fused = (can_fuse and faster) if fused is None else bool(fused)
+        # the other path: prep, the scores spread over the blocks, the ranking,
+        # and the attention (the scores' buffer makes qm_qsa_select split them)
+        self.scores = None if self.fused else torch.empty(batch, 1, cache.max_blocks, dtype=torch.float32,
+                                                           device=dev)
         self.dec_ws = torch.zeros(lib.qm_qsa_decode_workspace(ctypes.byref(self.geom), self.dec_splits),
                                   dtype=torch.uint8, device=dev)
         self.positions = torch.zeros(batch, dtype=torch.int32, device=dev)
@@ -139,7 +147,8 @@ class QsaDecodePlan:
     def select(self, stream):
         native.call("qm_qsa_select", ctypes.byref(self.geom), 1, self.iq_out.data_ptr(),
                     self.lc.block_keys.data_ptr(), self.positions.data_ptr(), self.lc.page_table.data_ptr(),
-                    self.ids.data_ptr(), self.n_sel.data_ptr(), self.items.data_ptr(), None, stream)
+                    self.ids.data_ptr(), self.n_sel.data_ptr(), self.items.data_ptr(),
+                    None if self.scores is None else self.scores.data_ptr(), stream)
 
     def attend(self, qg, stream):
         lc = self.lc
@@ -164,7 +173,7 @@ class QsaDecodePlan:
         """The one-launch step on these inputs as a BoundCall (stream at call
         time); plans that do not fit one launch are refused."""
         if not self.fused:
-            raise native.QmError(f"layer {self.layer}: this plan runs as front + attend, not one launch")
+            raise native.QmError(f"layer {self.layer}: this plan runs as prep + select + attend, not one launch")
         return BoundCall("qm_qsa_decode", *self._decode_args(qg, k, v, iq, ik))
 
     def check(self, reset: bool = True) -> list:
@@ -180,6 +189,7 @@ class QsaDecodePlan:
         if self.fused:
             self.decode(qg, k, v, iq, ik, s)
         else:
-            self.front(qg, k, v, iq, ik, s)
+            self.prep(qg, k, v, iq, ik, s)
+            self.select(s)
             self.attend(qg, s)
         return self.out

@@ -89,9 +89,26 @@ __device__ __forceinline__ float conv_finish4(const ConvIn<T>& c, int pos) {
   return Act<T>::round(silu_f(Act<T>::round(acc)));
 }
 
+// The decay e^g, g = a * softplus(x) (a = -exp(A_log) < 0), in a short chain
+// of hardware exponentials and a logarithm: e^x and the final exponential as
+// 2^(y log2 e); log1p(t) as a series t - t^2/2 + t^3/3 - t^4/4 below t = 2^-5
+// (truncation below 2e-7 relative), else as log(1 + t) (1 + t rounded to
+// float: below 2e-6 relative). The decay's relative error stays below about
+// 2e-6 |g|, far inside the state's tolerance; the precise library chain (three
+// dependent calls) took most of a microsecond on the step's critical path.
+__device__ __forceinline__ float decay_fast(float a_neg, float x) {
+  float sp = x;
+  if (x <= 20.0f) {
+    const float t = __expf(x);
+    sp = t < 0.03125f ? t * (1.0f - t * (0.5f - t * (0.33333334f - t * 0.25f))) : __logf(1.0f + t);
+  }
+  return __expf(a_neg * sp);
+}
+
 // Hides a value's origin from the optimiser, so that work on it is not moved
 // up to where it was loaded.
 __device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void opaque(unsigned& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void opaque(bf16_t& v) {
   unsigned u = v.bits;
   asm volatile("" : "+v"(u));
@@ -171,12 +188,12 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   __shared__ float s_q[DN_D], s_k[DN_D], s_v[DN_DCOLS];
   __shared__ float4 s_red[NW][2][DN_DCOLS / 4];   // per wave: the columns' pred and qd partial sums
   __shared__ float4 s_delta[DN_DCOLS / 4];
-  __shared__ float s_scal[2];
+  __shared__ float s_scal[1];
 
   // ---- loads, all issued before any is used and none converted before the
   // last is issued: the conv inputs of the head's q and k channels (thread t
-  // takes channel t), the state, the conv inputs of the slice's 32 v channels,
-  // z, the norm weight of the slice's columns and the head's generation word
+  // takes channel t) and of the slice's 32 v channels (wave 0), the state, z,
+  // the norm weight of the slice's columns and the head's generation word
   // (wave 0), the position and the gates by scalar loads (uniform).
   const int wv = __builtin_amdgcn_readfirstlane(wid);
   const int key_dim = n_hk * DN_D;
@@ -185,6 +202,9 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   const bool k4 = K == 4;
   ConvIn<T> cin_qk, cin_v;
   if (k4) cin_qk = conv_load4(ring, conv_w, qkv, conv_dim, b, ch_qk);
+  // wave 0's v channels ahead of the state, so that their conv waits for
+  // nothing else (loads complete in order)
+  if (k4 && wv == 0) cin_v = conv_load4(ring, conv_w, qkv, conv_dim, b, ch_v);
   const long head_off = (long)(b * hv + h) * DN_D * DN_D;
   const float4* S = reinterpret_cast<const float4*>(state + head_off) + col0 / 4 + c4;
   float4 st[RPT];
@@ -197,7 +217,6 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   unsigned long long* shares = reinterpret_cast<unsigned long long*>(line) + DN_SHARE0;
   unsigned gen = 0;
   if (wv == 0) {
-    if (k4) cin_v = conv_load4(ring, conv_w, qkv, conv_dim, b, ch_v);
     zr = z[(long)b * hv * DN_D + h * DN_D + col0 + (lane & (DN_DCOLS - 1))];
     nw = norm_w[col0 + (lane & (DN_DCOLS - 1))];
     // the generation word, an atomic load issued last (loads complete in
@@ -210,12 +229,20 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   const float gate_b = uniform_act(gb, (long)b * hv + h), gate_a = uniform_act(ga, (long)b * hv + h);
   const float a_neg = uniform_load(a_neg_p + h), dtb = uniform_load(dt_bias_p + h);
   QM_PHASE(6);
+  // the decay, in every wave while its conv inputs are in flight
+  const float decay = decay_fast(a_neg, gate_a + dtb);
 
   // ---- conv of the q/k channels and the slice's v channels (the q/k ring
   // slots have one writer: slice 0 of the value head h == hk). With K = 4 the
   // ring stores wait for the end: stores and loads share one in-order
   // counter, so a store issued here would hold up the wait for the state.
   const bool qk_writer = h == hk && s == 0;
+  // beta = sigmoid(b), rounded to the activation type as the reference rounds
+  // it, in wave 1 (a chain of an exponential and a division); it is first
+  // needed after the column sums (below), so no barrier waits for it before
+  // that.
+  float beta_v = 0.f;
+  if (tid == 64) beta_v = Act<T>::round(sigmoid_f(gate_b));
   {
     const float y = k4 ? conv_finish4(cin_qk, pos)
                        : conv_channel(ring, conv_w, qkv, conv_dim, K, b, ch_qk, pos, qk_writer);
@@ -226,10 +253,6 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
                        : conv_channel(ring, conv_w, qkv, conv_dim, K, b, ch_v, pos, lane < DN_DCOLS);
     QM_PHASE(7);
     if (lane < DN_DCOLS) s_v[lane] = y;
-  }
-  if (tid == 0) {
-    s_scal[0] = Act<T>::round(sigmoid_f(gate_b));
-    s_scal[1] = expf(a_neg * softplus_f(gate_a + dtb));
   }
   __syncthreads();
 
@@ -246,11 +269,11 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   const float rqd = div_rn(rq, sqrt_d);                 // q's scale, one division for the four rows
 
   QM_PHASE(2);
-  // ---- decay, then per column pred = S^T k^ and qd = S^T q^: a thread adds
-  // its 4 rows in order, the 8 rows of a wave's load are added across lanes
-  // (DPP within rows of 16 lanes, then swaps of row pairs and halves), the 4
-  // waves through LDS
-  const float decay = s_scal[1];
+  // ---- per column S^T k^ and S^T q^ of the state before its decay (which
+  // scales both sums after they are formed): a thread adds its 4 rows in
+  // order, the 8 rows of a wave's load are added across lanes (DPP within
+  // rows of 16 lanes, then swaps of row pairs and halves), the 4 waves
+  // through LDS
   float kr[RPT];
   float p[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -258,7 +281,6 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
     const int row = r + RSTEP * i;
     kr[i] = mul_rn(s_k[row], rk);
     const float qr = s_q[row] * rqd;
-    st[i].x *= decay; st[i].y *= decay; st[i].z *= decay; st[i].w *= decay;
     p[0] = fmaf(st[i].x, kr[i], p[0]); p[1] = fmaf(st[i].y, kr[i], p[1]);
     p[2] = fmaf(st[i].z, kr[i], p[2]); p[3] = fmaf(st[i].w, kr[i], p[3]);
     p[4] = fmaf(st[i].x, qr, p[4]); p[5] = fmaf(st[i].y, qr, p[5]);
@@ -271,12 +293,14 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
     s_red[wid][0][lane] = make_float4(p[0], p[1], p[2], p[3]);
     s_red[wid][1][lane] = make_float4(p[4], p[5], p[6], p[7]);
   }
+  if (tid == 64) s_scal[0] = beta_v;
   QM_PHASE(10);
   __syncthreads();
 
   QM_PHASE(3);
   // ---- delta and o of the 32 columns (wave 0: lanes 0-31 add pred, lanes
-  // 32-63 qd, over the 4 waves), the slice's share of the head's sum of
+  // 32-63 qd, over the 4 waves, then scale them by the decay: pred =
+  // (S e^g)^T k^, qd = (S e^g)^T q^), the slice's share of the head's sum of
   // squares of o published with the launch's generation number
   float o = 0.f;
   if (wv == 0) {
@@ -285,11 +309,13 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
     float acc = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) acc += red[(w * 2 + half) * DN_DCOLS + col];
+    acc *= decay;
     const float pred = acc, qd = halves_swap(acc);     // lanes 0-31 receive qd
     const float delta = (s_v[col] - pred) * s_scal[0];
     if (lane < DN_DCOLS) reinterpret_cast<float*>(s_delta)[lane] = delta;
     o = lane < DN_DCOLS ? Act<T>::round(fmaf(qk, delta, qd)) : 0.f;
     const float ss = wave_sum(o * o);
+    opaque(gen);     // used from here on, not where it is loaded (that would wait for every load there)
     if (lane == 0) {
       const unsigned long long word = ((unsigned long long)(gen + 1) << 32) | __float_as_uint(ss);
       __hip_atomic_store(shares + s, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -298,17 +324,17 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   __syncthreads();
 
   QM_PHASE(4);
-  // ---- rank-1 update and write-back of the slice, written through to the
-  // point of coherence (no dirty state lines are left in L2 for the end of
-  // the kernel), and the deferred ring stores
+  // ---- decay and rank-1 update (S e^g + k^ delta^T) and write-back of the
+  // slice, written through to the point of coherence (no dirty state lines
+  // are left in L2 for the end of the kernel), and the deferred ring stores
   {
     const float4 dl = s_delta[c4];
     const __amdgpu_buffer_rsrc_t rsrc = dev_rsrc(state + head_off, DN_D * DN_D * 4);
 #pragma unroll
     for (int i = 0; i < RPT; ++i)
       st_dev4(rsrc, ((r + RSTEP * i) * DN_D + col0 + 4 * c4) * 4,
-              make_float4(fmaf(kr[i], dl.x, st[i].x), fmaf(kr[i], dl.y, st[i].y), fmaf(kr[i], dl.z, st[i].z),
-                          fmaf(kr[i], dl.w, st[i].w)));
+              make_float4(fmaf(kr[i], dl.x, st[i].x * decay), fmaf(kr[i], dl.y, st[i].y * decay),
+                          fmaf(kr[i], dl.z, st[i].z * decay), fmaf(kr[i], dl.w, st[i].w * decay)));
   }
   if (k4 && qk_writer) ring[((long)b * conv_dim + ch_qk) * 4 + (pos & 3)] = cin_qk.x;
   if (k4 && wv == 0 && lane < DN_DCOLS) ring[((long)b * conv_dim + ch_v) * 4 + (pos & 3)] = cin_v.x;

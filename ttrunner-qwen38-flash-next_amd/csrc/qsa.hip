@@ -2231,8 +2231,21 @@ __device__ __forceinline__ void decode_merge(const DecArgs<T>& D, DecShared& sh,
   }
 }
 
+// The arguments the first loads need come first, as plain scalars: the library
+// is built with kernel-argument preloading, so these 14 dwords are in scalar
+// registers at wave start and the position, the indexer query and its norm
+// weight and the block keys are requested at once, then the rope rows as soon
+// as the position is in; the rest of the arguments (D) arrive by the kernel's
+// own scalar loads while those are in flight. dims0 = max_blocks | rope << 16
+// | idx_heads << 24 | may_score << 28, where may_score says the launch's
+// positions may need scoring (more items than the top-k blocks hold), so the
+// first 128 block keys are prefetched whatever the position; dims1 =
+// log2(ratio) | topk << 8.
 template <typename T, bool WIDE>
-__global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
+__global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(const int* positions0, const T* iq0,
+                                                            const float* iq_norm0, const float* bk0,
+                                                            const float* cos0, const float* sin0, unsigned dims0,
+                                                            unsigned dims1, DecArgs<T> D) {
   __shared__ DecShared sh;
   QM_PHASE_DECL
   const PrepArgs<T>& A = D.P;
@@ -2240,18 +2253,54 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int col = lane & 15, quad = lane >> 4;
   const int e128 = tid & 127, hh = tid >> 7;
-  const int bg = b * A.hkv + g;
+  const int max_blocks = dims0 & 0xffff, rope = (dims0 >> 16) & 0xff, idx_heads = (dims0 >> 24) & 0xf;
+  const bool may_score = (dims0 >> 28) & 1;
+  const int ratio_log2 = dims1 & 0xff, ratio = 1 << ratio_log2, topk = dims1 >> 8;
 
   // ---- 0. the loads. Wave w takes indexer query head w and attention query
   // heads 2w, 2w + 1 (wave 0 also the key), each row as elements lane + 64 k.
   // Every load is unconditional, indices clamped into range, so the waits on
-  // them stay exact instead of draining the memory counter.
+  // them stay exact instead of draining the memory counter. First the ones
+  // the scalar arguments address: the position (a vector load, issued first:
+  // a scalar load would be issued after the scalar loads of D and waited for
+  // with them), the indexer query and its norm weight, the first 128 block
+  // keys, then the rope rows of this token's position and of the start of the
+  // block it completes.
   QM_PHASE(0);
-  const unsigned gen = ld_flag(D.gen + (long)bg * DEC_GEN_STRIDE);
-  const int n_iq = A.idx_heads * IDX_D;
-  float iqx[2];
+  const int p = __builtin_amdgcn_readfirstlane(
+      (int)__builtin_amdgcn_raw_buffer_load_b32(dev_rsrc(positions0 + b, 4), 0, 0, 0));
+  const int n_iq = idx_heads * IDX_D;
+  float iqx[2], w_iq[2];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) iqx[k] = Act<T>::load(A.iq, (long)b * n_iq + min(wv * IDX_D + lane + 64 * k, n_iq - 1));
+  for (int k = 0; k < 2; ++k) iqx[k] = Act<T>::load(iq0, (long)b * n_iq + min(wv * IDX_D + lane + 64 * k, n_iq - 1));
+#pragma unroll
+  for (int k = 0; k < 2; ++k) w_iq[k] = iq_norm0[lane + 64 * k];
+  const float* bk = bk0 + (long)b * max_blocks * IDX_D;
+  float kp[score_pre<DEC_NT>()][8];
+  prefetch_block_keys<DEC_NT>(kp, bk, max_blocks, -1, may_score);
+  // every block-key load issued before the wait for the position
+  __builtin_amdgcn_sched_barrier(0);
+  const int j_new = ((p + 1) & (ratio - 1)) == 0 ? p >> ratio_log2 : -1;
+  float cs[2], sn[2], cs0[2], sn0[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int ec = min(lane + 64 * k, rope - 1);
+    cs[k] = cos0[(long)p * rope + ec];
+    sn[k] = sin0[(long)p * rope + ec];
+    cs0[k] = cos0[(long)max(j_new, 0) * ratio * rope + ec];
+    sn0[k] = sin0[(long)max(j_new, 0) * ratio * rope + ec];
+  }
+  // nothing addressed through D moves above this point: its scalar loads'
+  // waits would hold up the rope rows
+  __builtin_amdgcn_sched_barrier(0);
+  // then the loads addressed through D: the page-table row (for after the
+  // selection), the generation word, the token's inputs and norm weights
+  int pg[DEC_MAX_PAGES / DEC_NT];
+#pragma unroll
+  for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k)
+    pg[k] = A.page_table[(long)b * A.max_pages + min(tid + DEC_NT * k, A.max_pages - 1)];
+  const int bg = b * A.hkv + g;
+  const unsigned gen = ld_flag(D.gen + (long)bg * DEC_GEN_STRIDE);
   const float ikv = Act<T>::load(A.ik, (long)b * IDX_D + e128);
   float qx[2][4], kx[4];
 #pragma unroll
@@ -2262,41 +2311,15 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) kx[k] = Act<T>::load(A.k_new, (long)bg * QSA_D + lane + 64 * k);
   const float vx = Act<T>::load(A.v_new, (long)bg * QSA_D + tid);
-  const int rope = A.rope;
-  float w_q[4], w_k[4], w_iq[2], w_ik[2];
+  float w_q[4], w_k[4], w_ik[2];
 #pragma unroll
   for (int k = 0; k < 4; ++k) { w_q[k] = A.q_norm[lane + 64 * k]; w_k[k] = A.k_norm[lane + 64 * k]; }
 #pragma unroll
-  for (int k = 0; k < 2; ++k) { w_iq[k] = A.iq_norm[lane + 64 * k]; w_ik[k] = A.ik_norm[lane + 64 * k]; }
+  for (int k = 0; k < 2; ++k) w_ik[k] = A.ik_norm[lane + 64 * k];
 
-  const int p = A.positions[b];
-  const int ratio = A.ratio;
-  const int topk = D.topk;
-  const ItemCount ic(p, ratio, topk, A.max_blocks);
+  const ItemCount ic(p, ratio, topk, max_blocks);
   const int n_elig = ic.n_elig, n_items = ic.n_items;
-  const int j_new = (p + 1) % ratio == 0 ? p / ratio : -1;
-  // rope rows: this token's position, and the start of the block it completes
-  float cs[2], sn[2], cs0[2], sn0[2];
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int ec = min(lane + 64 * k, rope - 1);
-    cs[k] = A.cos[(long)p * rope + ec];
-    sn[k] = A.sin[(long)p * rope + ec];
-    cs0[k] = A.cos[(long)max(j_new, 0) * ratio * rope + ec];
-    sn0[k] = A.sin[(long)max(j_new, 0) * ratio * rope + ec];
-  }
-  // the whole page-table row and, when this launch's positions may need
-  // scoring (more items than the top-k blocks hold), the first 128 block keys,
-  // whatever the position
-  int pg[DEC_MAX_PAGES / DEC_NT];
-#pragma unroll
-  for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k)
-    pg[k] = A.page_table[(long)b * A.max_pages + min(tid + DEC_NT * k, A.max_pages - 1)];
-  const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
   const bool scoring = n_elig > topk;
-  float kp[score_pre<DEC_NT>()][8];
-  const bool may_score = D.splits > topk * (ratio >= 32 ? ratio / 32 : 1);
-  prefetch_block_keys<DEC_NT>(kp, bk, A.max_blocks, -1, may_score);
   // raw keys of the block this token completes: thread (e128, hh) takes the
   // 16-row chunks hh and hh + 2; the token's own row is ik (not yet stored)
   float rk[2][16];
@@ -2311,9 +2334,6 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
         rk[c][i] = r >= ratio ? 0.f : j_new * ratio + r == p ? ikv : v;
       }
   }
-  sh.vnb[tid] = f32_to_bf16(vx);
-#pragma unroll
-  for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k) sh.pages[tid + DEC_NT * k] = pg[k];
 
   // A position with more items than the launch has workgroups (a plan sized
   // for smaller positions) cannot be attended: its output is poisoned and
@@ -2340,7 +2360,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   // ---- 1. the indexer query (wave w: head w), and the pooled key of a block
   // this token completes: y = round_T(x * rinv * w), then rope
   auto nrm = [&](float xv, float ri, float w) { return Act<T>::round(mul_rn(mul_rn(xv, ri), w)); };
-  if (wv < A.idx_heads) {
+  if (wv < idx_heads) {
     const float ri = wave_rinv<2>(iqx, A.eps);
     QM_PHASE(1);
     float y[2] = {nrm(iqx[0], ri, w_iq[0]), nrm(iqx[1], ri, w_iq[1])};
@@ -2380,6 +2400,11 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
       sh.newkey[64 + lane] = y[1];
     }
   }
+  // the token's value and the page-table row, for after the selection (the
+  // rope above has waited for the loads issued before the rope rows)
+  sh.vnb[tid] = f32_to_bf16(vx);
+#pragma unroll
+  for (int k = 0; k < DEC_MAX_PAGES / DEC_NT; ++k) sh.pages[tid + DEC_NT * k] = pg[k];
   __syncthreads();
 
   // ---- 2. block scores and top-k (ties to the lower index); the item of a
@@ -2390,7 +2415,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(DecArgs<T> D) {
   QM_PHASE(2);
   int blk = blk_item && !scoring ? item / ic.gpb : -1;
   if (scoring && (blk_item || item == 0)) {
-    if (!score_block_rounds<DEC_NT, score_pre<DEC_NT>()>(sh.iq, sh.newkey, bk, n_elig, j_new, A.idx_heads, sh.key,
+    if (!score_block_rounds<DEC_NT, score_pre<DEC_NT>()>(sh.iq, sh.newkey, bk, n_elig, j_new, idx_heads, sh.key,
                                                          sh.dsc, kp, topk, sh.sel, blk_item ? item / ic.gpb : -1,
                                                          &blk)) {
       __syncthreads();
@@ -3166,8 +3191,18 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
     D.part_o = part_o; D.part_ml = part_ml; D.gen = gen; D.flags = flags; D.out = static_cast<T*>(out);
     D.ids = ids; D.n_sel = n_sel; D.items = static_cast<int2*>(items); D.iq_out = iq_out;
     D.splits = splits; D.topk = g->budget / g->ratio; D.max_items = item_stride(g);
-    if (wide) hipLaunchKernelGGL((qsa_decode_kernel<T, true>), grid, dim3(DEC_NT), 0, stream, D);
-    else hipLaunchKernelGGL((qsa_decode_kernel<T, false>), grid, dim3(DEC_NT), 0, stream, D);
+    const int gpb = g->ratio >= 32 ? g->ratio / 32 : 1;
+    const unsigned may_score = splits > D.topk * gpb ? 1u : 0u;
+    const unsigned dims0 = (unsigned)g->max_blocks | ((unsigned)g->rope_dim << 16) |
+                           ((unsigned)g->idx_heads << 24) | (may_score << 28);
+    const unsigned dims1 = (unsigned)__builtin_ctz((unsigned)g->ratio) | ((unsigned)D.topk << 8);
+    const T* iq_t = static_cast<const T*>(iq);
+    if (wide)
+      hipLaunchKernelGGL((qsa_decode_kernel<T, true>), grid, dim3(DEC_NT), 0, stream, positions, iq_t, iq_norm,
+                         static_cast<const float*>(block_keys), cos, sin, dims0, dims1, D);
+    else
+      hipLaunchKernelGGL((qsa_decode_kernel<T, false>), grid, dim3(DEC_NT), 0, stream, positions, iq_t, iq_norm,
+                         static_cast<const float*>(block_keys), cos, sin, dims0, dims1, D);
     QM_CHECK_LAUNCH();
     return QM_OK;
   };

@@ -521,14 +521,16 @@ __device__ __forceinline__ float4 row16_dots(const float (&q)[4][8], const float
 // thread (wave w, lane l) takes block i = 32 w + (l & 31) and half h = l >> 5
 // of the blocks. It forms block i's score key (relu, the heads added in order,
 // the division by sqrt(128), then the order-preserving bits of sel_key; zero
-// past n_elig, below every eligible key), the h = 0 lanes store it to LDS,
-// and after a barrier each thread counts the keys of half h strictly above
-// its own (four keys per broadcast LDS read, one 32-bit compare each). The
-// halves' counts meet by a lane swap (l ^ 32). A block with fewer than topk
-// keys above it is kept; each wave's kept blocks are one 32-bit ballot,
-// published in masks (LDS, 4 words) behind a second barrier. When exactly
-// topk blocks are kept there is no tie at the boundary and the set is final.
-// Otherwise blocks with equal scores straddle the boundary, and every thread
+// past n_elig, below every eligible key), the h = 0 lanes store the top 31
+// bits of that key to LDS, and after a barrier each thread counts the keys of
+// half h strictly above its own (four keys per broadcast LDS read; 31-bit
+// keys, so a comparison is the sign bit of a difference). The halves' counts
+// meet by a lane swap (l ^ 32). A block with fewer than topk keys above it is
+// kept; each wave's kept blocks are one 32-bit ballot, published in masks
+// (LDS, 4 words) behind a second barrier. The kept set holds every block
+// above any kept one (its coarse key is at least as high, so fewer keys are
+// above it), so when exactly topk blocks are kept it is the top-k and final.
+// Otherwise blocks with equal coarse keys straddle the boundary, and every thread
 // counts again with 64-bit keys (score bits over the reversed index, so that
 // the lower index ranks higher), which orders every pair; a third barrier
 // publishes those masks. A kept block's place in sel is the count of kept
@@ -544,23 +546,31 @@ __device__ __forceinline__ int select128(const float4* dsc, int n_elig, int idx_
 #pragma unroll
   for (int hh = 1; hh < 4; ++hh) sc = hh < idx_heads ? add_rn(sc, fmaxf(dv[hh], 0.f)) : sc;
   const unsigned long long key = i < n_elig ? sel_key(div_rn(sc, 11.313708498984761f), i) : 0ull;
-  const unsigned hk = static_cast<unsigned>(key >> 32);
+  // the score key's top 31 bits: a coarser order, which keeps the set exact
+  // (below), and lets a comparison be a subtraction's sign bit
+  const unsigned hk = static_cast<unsigned>(key >> 33);
   unsigned* hkeys = masks + 8;                       // 128 score keys after the mask words
   if (h == 0) { hkeys[i] = hk; keys[i] = key; }
   __syncthreads();
   QM_PHASE(3);
-  // the 64 score keys of half h, all requested before the first compare
+  // the 64 score keys of half h, all requested before the first compare;
+  // (hk - k) >> 31 is 1 exactly when k > hk (both below 2^31), four
+  // independent counts with no compare-and-carry chain through vcc
   {
     const uint4* kh = reinterpret_cast<const uint4*>(hkeys + 64 * h);
     uint4 kk[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) kk[q] = kh[q];
     __builtin_amdgcn_sched_barrier(0);
-    unsigned cnt = 0;
+    unsigned c4[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int q = 0; q < 16; ++q)
-      cnt += (kk[q].x > hk ? 1u : 0u) + (kk[q].y > hk ? 1u : 0u) + (kk[q].z > hk ? 1u : 0u) +
-             (kk[q].w > hk ? 1u : 0u);
+    for (int q = 0; q < 16; ++q) {
+      c4[0] += (hk - kk[q].x) >> 31;
+      c4[1] += (hk - kk[q].y) >> 31;
+      c4[2] += (hk - kk[q].z) >> 31;
+      c4[3] += (hk - kk[q].w) >> 31;
+    }
+    const unsigned cnt = (c4[0] + c4[1]) + (c4[2] + c4[3]);
     const auto sw = __builtin_amdgcn_permlane32_swap(cnt, cnt, false, false);
     const unsigned above = sw[0] + sw[1];
     const unsigned mine = static_cast<unsigned>(
@@ -2082,17 +2092,21 @@ struct ItemCount {
 // flags of a group: one per workgroup that attends an item or holds a slice
 __host__ __device__ inline int dec_flag_stride(int splits) { return splits > DEC_SLICES ? splits : DEC_SLICES; }
 
-// Flags of the items a wave merges in round i0 (below): lane l polls item
-// i0 + 64 ((l >> 4) & 1) + 16 wv + (l & 15) (lanes 32..63 repeat 0..31); items
-// at or past n_wait count as raised. False if the wait gave up.
+// Flags of the 128 items of round i0, polled by one wave (the caller's wave
+// 0; its workgroup waits at a barrier): lane l polls items i0 + l and
+// i0 + 64 + l, both loads issued together; items at or past n_wait count as
+// raised. One polling wave per merging workgroup, not four: every poll of
+// every merging workgroup reads the same few lines at the point of coherence,
+// and fewer polls reach it sooner. False if the wait gave up.
 __device__ __forceinline__ bool wait_item_flags(const unsigned* flags, int i0, int n_wait, unsigned target) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int it = i0 + 64 * ((lane >> 4) & 1) + 16 * wv + (lane & 15);
-  const bool need = it < n_wait;
-  const unsigned* f = flags + (need ? it : 0);
+  const int lane = threadIdx.x & 63;
+  const int ia = i0 + lane, ib = ia + 64;
+  const bool need_a = ia < n_wait, need_b = ib < n_wait;
+  const unsigned* fa = flags + (need_a ? ia : 0);
+  const unsigned* fb = flags + (need_b ? ib : 0);
   for (int k = 0; k < FLAG_SPIN_MAX; ++k) {
-    const unsigned v = ld_flag(f);
-    const bool ok = !need || (int)(v - target) >= 0;
+    const unsigned va = ld_flag(fa), vb = ld_flag(fb);
+    const bool ok = (!need_a || (int)(va - target) >= 0) && (!need_b || (int)(vb - target) >= 0);
     if (__builtin_amdgcn_ballot_w64(!ok) == 0ull) return true;
     __builtin_amdgcn_s_sleep(1);
   }
@@ -2105,8 +2119,9 @@ __device__ __forceinline__ bool wait_item_flags(const unsigned* flags, int i0, i
 // is the item's output divided by its sum l_i). Thread (c = tid % 4, il =
 // tid / 4) takes channels 8c .. 8c + 7 of the slice (one 16-byte load) of
 // items il and il + 64 of each round of 128, so wave w merges items 16w ..
-// 16w + 15 and 64 + 16w .. of a round: it waits for those items' flags alone
-// (n_wait of them count) and loads them at once. Each thread keeps a running
+// 16w + 15 and 64 + 16w .. of a round; wave 0 waits for the round's flags
+// (n_wait of them count), the workgroup meets at a barrier, and each wave
+// loads its items' partials at once. Each thread keeps a running
 // maximum, sum and 8 channel sums; the lanes of a chunk are added by DPP row
 // rotations and lane swaps after scaling to the wave's maximum, and the four
 // waves' (sums, maximum) meet in LDS. Workgroup 0 of the group advances the
@@ -2126,9 +2141,13 @@ __device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, 
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
   bool ok = true;
+  // the gate's sigmoid is formed while the first round's partials are in flight
+  float gsig = 0.f;
+  bool have_gate = false;
   const int n_rounds = max(n, n_wait);
   for (int i0 = 0; i0 < n_rounds; i0 += 128) {
-    ok = ok & wait_item_flags(flags, i0, n_wait, gen + 1);
+    if (wv == 0) ok = ok & wait_item_flags(flags, i0, n_wait, gen + 1);
+    __syncthreads();
     if (i0 >= n) continue;
     const int ia = i0 + il, ib = ia + 64;
     const int ca = min(ia, n - 1), cb = min(ib, n - 1);
@@ -2136,6 +2155,10 @@ __device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, 
     const u32x4_t ob = ld_dev_u32x4(ro, ((cb * GQA + h) * QSA_D + d0) * 2);
     const float2 ma = ld_dev2(rml, ((ca * GQA + h) * 2) * 4);
     const float2 mb = ld_dev2(rml, ((cb * GQA + h) * 2) * 4);
+    if (!have_gate) {
+      gsig = Act<T>::round(sigmoid_f(gate));
+      have_gate = true;
+    }
     const float xa = ia < n ? ma.x : -INFINITY, xb = ib < n ? mb.x : -INFINITY;
     const float mn = fmaxf(M, fmaxf(xa, xb));
     const float f = M == -INFINITY ? 0.f : __expf(M - mn);
@@ -2150,6 +2173,7 @@ __device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, 
     }
     M = mn;
   }
+  if (!have_gate) gsig = Act<T>::round(sigmoid_f(gate));
   // to the wave's maximum, then the sums over the wave's items (lanes of one c)
   const float Mw = wave_max(M);
   const float fw = M == -INFINITY ? 0.f : __expf(M - Mw);
@@ -2194,7 +2218,7 @@ __device__ void decode_combine_slice(const DecArgs<T>& D, DecShared& sh, int b, 
     }
     const bool poison = overflow || (sh.fault[0] | sh.fault[1] | sh.fault[2] | sh.fault[3]) != 0;
     const int hq = D.P.hq, qh = g * GQA + h;
-    const float y = Act<T>::round(num / den) * Act<T>::round(sigmoid_f(gate));
+    const float y = Act<T>::round(num / den) * gsig;
     Act<T>::store(D.out, ((long)b * hq + qh) * QSA_D + 32 * (sl % 8) + tid, poison ? __builtin_nanf("") : y);
   }
   __syncthreads();
@@ -2470,7 +2494,10 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(const int* positions
       sh.qb[GQA + h][lane + 64 * k] = f32_to_bf16(y[k] - bf16_to_f32(qhi));
     }
   }
-  if (wv == 0 && (item == 0 || cur)) {
+  // the token's roped key, in the bits appended to the cache: before the
+  // scores in the workgroup whose item holds the token; item 0, which appends
+  // it, forms it after raising its flag (below) when it does not hold it
+  auto key_bits = [&]() {
     const float ri = wave_rinv<4>(kx, A.eps);
     float y[4];
 #pragma unroll
@@ -2478,7 +2505,8 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(const int* positions
     wave_rope<4>(y, rope, cs, sn);
 #pragma unroll
     for (int k = 0; k < 4; ++k) sh.knb[lane + 64 * k] = f32_to_bf16(y[k]);
-  }
+  };
+  if (wv == 0 && cur) key_bits();
   QM_PHASE(5);
   __syncthreads();
 
@@ -2575,11 +2603,24 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(const int* positions
   if (wv == 0 && quad == 0 && col < GQA) st_dev2(rml, ((item * GQA + col) * 2) * 4, make_float2(mx, lsum));
   QM_PHASE(7);
 
-  // ---- 5. the stores that outlive this step: the token's key/value into its
-  // page slot (item 0 of each kv head), and per sequence (item 0 of kv head 0)
-  // its raw indexer key, the pooled key of a completed block and the optional
+  // ---- 5. arrive: the partial's stores acknowledged, then the flag; the
+  // workgroups holding output slices then wait for every item of the group
+  // and merge their slices (6)
+  wait_all_memory();
+  __syncthreads();
+  QM_PHASE(8);
+  if (tid == 0) post_flag(D.flags + (long)bg * dec_flag_stride(D.splits) + item, gen + 1);
+
+  // the stores that outlive this step, after the flag (no merge waits for
+  // them; the launch's end does): the token's key/value into its page slot
+  // (item 0 of each kv head), and per sequence (item 0 of kv head 0) its raw
+  // indexer key, the pooled key of a completed block and the optional
   // inspection outputs
   if (item == 0) {
+    if (!cur) {
+      if (wv == 0) key_bits();
+      __syncthreads();
+    }
     const int pg_cur = sh.pages[p / A.page_size], prow = p % A.page_size;
     const long cbase = ((long)pg_cur * A.hkv + g) * A.page_size * QSA_D;
     A.k_pool[cbase + k_page_index(prow, tid)] = sh.knb[tid];
@@ -2607,12 +2648,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(const int* positions
     }
   }
 
-  // ---- 6. arrive; the workgroups holding output slices wait for every item
-  // of the group, then merge their slices
-  wait_all_memory();
-  __syncthreads();
-  QM_PHASE(8);
-  if (tid == 0) post_flag(D.flags + (long)bg * dec_flag_stride(D.splits) + item, gen + 1);
+  // ---- 6. the merge of this workgroup's output slices
   if (item < DEC_SLICES) decode_merge<WIDE>(D, sh, b, g, item, n_att, gen, overflow);
   QM_PHASE(10);
   QM_PHASE_FLUSH();

@@ -709,6 +709,25 @@ __device__ __forceinline__ void prefetch_block_keys(float (&kp)[PRE][8], const f
   }
 }
 
+// the decode kernel's prefetch of the first PRE passes: no zeroing (a block
+// past the eligible ones is scored but never ranked, and the block this launch
+// completes takes its key from LDS), rows past max_blocks, or every row when
+// the launch never scores, read row 0
+template <int NT, int PRE>
+__device__ __forceinline__ void prefetch_block_keys_raw(float (&kp)[PRE][8], const float* bk, int max_blocks, bool on) {
+  constexpr int SCORE_PASS = NT / SCORE_LANES;
+  const int jl = threadIdx.x >> 4;
+#pragma unroll
+  for (int u = 0; u < PRE; ++u) {
+    const int j = u * SCORE_PASS + jl;
+    const float4* src =
+        reinterpret_cast<const float4*>(bk + (long)(on && j < max_blocks ? j : 0) * IDX_D + 8 * (threadIdx.x & 15));
+    const float4 a = src[0], c = src[1];
+    kp[u][0] = a.x; kp[u][1] = a.y; kp[u][2] = a.z; kp[u][3] = a.w;
+    kp[u][4] = c.x; kp[u][5] = c.y; kp[u][6] = c.z; kp[u][7] = c.w;
+  }
+}
+
 // The several-rows order: one lane per (block, head) walks the block's 128
 // elements in order in one fused multiply-add chain. Rounds of SEQ_RB blocks:
 // the whole workgroup copies the round's block rows into LDS with coalesced
@@ -2301,7 +2320,7 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(const int* positions
   for (int k = 0; k < 2; ++k) w_iq[k] = iq_norm0[lane + 64 * k];
   const float* bk = bk0 + (long)b * max_blocks * IDX_D;
   float kp[score_pre<DEC_NT>()][8];
-  prefetch_block_keys<DEC_NT>(kp, bk, max_blocks, -1, may_score);
+  prefetch_block_keys_raw<DEC_NT>(kp, bk, max_blocks, may_score);
   // every block-key load issued before the wait for the position
   __builtin_amdgcn_sched_barrier(0);
   const int j_new = ((p + 1) & (ratio - 1)) == 0 ? p >> ratio_log2 : -1;

@@ -93,9 +93,20 @@ __device__ __forceinline__ float div_rn(float a, float b) {
 __device__ __forceinline__ float rsqrt_rn(float x) { return div_rn(1.0f, __builtin_sqrtf(x)); }
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
-// torch.nn.functional.softplus with beta 1, threshold 20
-__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+// torch.nn.functional.softplus (beta 1, threshold 20) in a short chain of
+// hardware exponentials and a logarithm, for the DeltaNet log-decay
+// g = a softplus(x) (a = -exp(A_log)): e^x as 2^(x log2 e); log1p(t) as the
+// series t - t^2/2 + t^3/3 - t^4/4 below t = 2^-5 (truncation below 2e-7
+// relative), else as log(1 + t) with 1 + t rounded to float (below 2e-6
+// relative, 1e-7 once t is above 1/2). The library chain (three dependent
+// precise calls) takes most of a microsecond in one lane; the decay's error
+// stays far inside the state's tolerance.
+__device__ __forceinline__ float softplus_fast(float x) {
+  if (x > 20.0f) return x;
+  const float t = __expf(x);
+  return t < 0.03125f ? t * (1.0f - t * (0.5f - t * (0.33333334f - t * 0.25f))) : __logf(1.0f + t);
+}
 
 // ---------------------------------------------------------------------------
 // Hand-off between the workgroups of one launch, on any die. The data crosses

@@ -89,22 +89,6 @@ __device__ __forceinline__ float conv_finish4(const ConvIn<T>& c, int pos) {
   return Act<T>::round(silu_f(Act<T>::round(acc)));
 }
 
-// The decay e^g, g = a * softplus(x) (a = -exp(A_log) < 0), in a short chain
-// of hardware exponentials and a logarithm: e^x and the final exponential as
-// 2^(y log2 e); log1p(t) as a series t - t^2/2 + t^3/3 - t^4/4 below t = 2^-5
-// (truncation below 2e-7 relative), else as log(1 + t) (1 + t rounded to
-// float: below 2e-6 relative). The decay's relative error stays below about
-// 2e-6 |g|, far inside the state's tolerance; the precise library chain (three
-// dependent calls) took most of a microsecond on the step's critical path.
-__device__ __forceinline__ float decay_fast(float a_neg, float x) {
-  float sp = x;
-  if (x <= 20.0f) {
-    const float t = __expf(x);
-    sp = t < 0.03125f ? t * (1.0f - t * (0.5f - t * (0.33333334f - t * 0.25f))) : __logf(1.0f + t);
-  }
-  return __expf(a_neg * sp);
-}
-
 // Hides a value's origin from the optimiser, so that work on it is not moved
 // up to where it was loaded.
 __device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
@@ -230,7 +214,7 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   const float a_neg = uniform_load(a_neg_p + h), dtb = uniform_load(dt_bias_p + h);
   QM_PHASE(6);
   // the decay, in every wave while its conv inputs are in flight
-  const float decay = decay_fast(a_neg, gate_a + dtb);
+  const float decay = __expf(a_neg * softplus_fast(gate_a + dtb));
 
   // ---- conv of the q/k channels and the slice's v channels (the q/k ring
   // slots have one writer: slice 0 of the value head h == hk). With K = 4 the
@@ -263,10 +247,13 @@ __global__ __launch_bounds__(DN_DEC_NT) void dn_decode_kernel(
   const float sq = wave_sum(fmaf(q1, q1, q0 * q0));
   const float sk = wave_sum(fmaf(k1, k1, k0 * k0));
   const float sqk = wave_sum(fmaf(q1, k1, q0 * k0));
-  const float rq = rsqrt_rn(sq + 1e-6f), rk = rsqrt_rn(sk + 1e-6f);
-  const float sqrt_d = 11.313708498984761f;
-  const float qk = div_rn(sqk * rq * rk, sqrt_d);       // q^ . k^
-  const float rqd = div_rn(rq, sqrt_d);                 // q's scale, one division for the four rows
+  // hardware reciprocal square roots and 1/sqrt(d) as a product (about an
+  // ulp from the reference's rsqrt and division, far inside the tolerance of
+  // the state and outputs)
+  const float rq = __builtin_amdgcn_rsqf(sq + 1e-6f), rk = __builtin_amdgcn_rsqf(sk + 1e-6f);
+  const float inv_sqrt_d = 0.08838834764831845f;
+  const float qk = sqk * rq * rk * inv_sqrt_d;          // q^ . k^
+  const float rqd = rq * inv_sqrt_d;                    // q's scale for the four rows
 
   QM_PHASE(2);
   // ---- per column S^T k^ and S^T q^ of the state before its decay (which

@@ -100,7 +100,7 @@ __global__ __launch_bounds__(CONV_CH) void dn_conv_chunk_kernel(ConvChunkArgs<T>
     const float beta = Act<T>::round(sigmoid_f(Act<T>::load(A.b, gg)));
     const float ga = Act<T>::load(A.a, gg) + A.dt_bias[h];
     A.beta_out[gg] = beta;
-    A.g_out[gg] = A.a_neg[h] * softplus_f(ga);
+    A.g_out[gg] = A.a_neg[h] * softplus_fast(ga);
   }
 }
 

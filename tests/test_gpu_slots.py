@@ -79,13 +79,16 @@ def _rows(xs, rows):
     return [x[rows].contiguous() for x in xs]
 
 
-def _decode(qm, model, cache, positions, qsa_in, dn_in):
-    """One decode step through the preplanned layers; every row at its own position."""
+def _decode(qm, model, cache, positions, qsa_in, dn_in, plan_position=None):
+    """One decode step through the preplanned layers; every row at its own
+    position. The QSA plan is sized for plan_position (default: the largest
+    row position), which also picks its kernel: plans of at most 512 keys take
+    the short-context kernel, larger ones the long-context kernel."""
     from importlib import import_module
     plan = import_module(qm.__name__ + ".plan")
     for b, p in enumerate(positions):
         cache.ensure_capacity(b, p + 1)
-    qp = plan.QsaDecodePlan(model, cache, 3, max(positions), BF)
+    qp = plan.QsaDecodePlan(model, cache, 3, max(positions) if plan_position is None else plan_position, BF)
     dp = plan.DnDecodePlan(model, cache, 0, BF)
     pos = torch.tensor(positions, dtype=torch.int32, device=DEV)
     qp.positions.copy_(pos)
@@ -101,8 +104,9 @@ def _decode(qm, model, cache, positions, qsa_in, dn_in):
 @pytest.mark.parametrize("p0, p1", [(2300, 130), (700, 64)])
 def test_rows_at_different_positions_match_single_sequences(gpu, p0, p1):
     """Slot 0 at p0 and slot 1 at p1 decode in one launch of each kernel; each
-    row equals its sequence decoded alone (pos 2300 scores 35 blocks and picks
-    the top 32; 130 and 64 are below the budget)."""
+    row equals its sequence decoded alone by a plan of the same size, so by the
+    same kernel (pos 2300 scores 35 blocks and picks the top 32; 130 and 64 are
+    below the budget)."""
     qm = gpu
     max_ctx = 4096
     model = _model(qm, max_ctx)
@@ -119,7 +123,7 @@ def test_rows_at_different_positions_match_single_sequences(gpu, p0, p1):
     qsa_in, dn_in = _step_inputs(13, 2)
     got_q, got_d = _decode(qm, model, both, [p0, p1], qsa_in, dn_in)
     for b, (c, p) in enumerate(zip(alone, (p0, p1))):
-        want_q, want_d = _decode(qm, model, c, [p], _rows(qsa_in, [b]), _rows(dn_in, [b]))
+        want_q, want_d = _decode(qm, model, c, [p], _rows(qsa_in, [b]), _rows(dn_in, [b]), plan_position=p0)
         assert torch.equal(got_q[b], want_q[0]), f"QSA row {b}"
         assert torch.equal(got_d[b], want_d[0]), f"DeltaNet row {b}"
         assert torch.equal(both[0].recurrent_state[b], c[0].recurrent_state[0])

@@ -2673,6 +2673,377 @@ __global__ __launch_bounds__(DEC_NT) void qsa_decode_kernel(const int* positions
   QM_PHASE_FLUSH();
 }
 
+// Hides a value's origin from the optimiser, so that its conversion is not
+// moved up to where it is loaded (which would wait for the load there).
+__device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void opaque(bf16_t& v) {
+  unsigned u = v.bits;
+  asm volatile("" : "+v"(u));
+  v.bits = static_cast<uint16_t>(u);
+}
+
+// ---------------------------------------------------------------------------
+// Short-context decode: selection off and at most SL_MAX_TOK keys, with no
+// hand-off between workgroups. Workgroup x < 64 of (kv head g, sequence b)
+// owns output slice x = (query head h = x / 8, channels 32 (x % 8) .. + 31): it
+// scores every key 0..p against query head h (K tiles on bf16 MFMA, the query
+// as its hi and lo columns), takes the softmax over them in LDS, and
+// multiplies the weights by its 32 value channels (two PV MFMAs per 32-key
+// group), so neither partials nor flags cross workgroups. Sixteen waves: wave
+// w holds 16-key tiles w and w + 16 and 32-key group w, all requested as soon
+// as the page-table row is in, so the keys and values cost one round trip.
+// Each workgroup reads every key of its kv head (576 bytes per key with its
+// value channels, from L2 after the first), which is why the path stops at
+// SL_MAX_TOK keys. Workgroup 0 of each kv head also appends the token's key and
+// value; workgroup 64 of kv head 0 stores the raw indexer key, pools the block
+// the token completes and writes the optional inspection outputs. The
+// arithmetic is the long-context kernel's (its scores, the bf16 softmax
+// weights of the PV product, fp32 sums), with one softmax over all keys
+// instead of a merge of per-item softmaxes.
+constexpr int SL_MAX_TOK = 512;
+// Plans up to this many 32-key items take it: each of its workgroups reads
+// every key (the long-context kernel's fixed cost is reached near 448 keys)
+constexpr int SL_FAST_ITEMS = 10;
+constexpr int SL_MAX_PAGES = SL_MAX_TOK / 32;   // pages hold at least 32 rows
+constexpr int SL_WAVES = 16;
+constexpr int SL_NT = 64 * SL_WAVES;
+
+struct SliceShared {
+  alignas(16) uint16_t qb[2][QSA_D];            // query head h: bf16 hi and lo
+  alignas(16) uint16_t knb[QSA_D];              // the token's roped key, bf16
+  alignas(16) uint16_t vnb[QSA_D];              // the token's value, bf16
+  float s[SL_MAX_TOK];                          // scores, then softmax weights
+  float red[SL_WAVES][32];                      // the waves' output sums
+  float wred[SL_WAVES];                         // the waves' score maxima
+  float wsum[SL_WAVES];                         // the waves' weight sums
+  int pages[SL_MAX_PAGES];
+  float chunk[DEC_MAX_RATIO / 16][IDX_D];       // side workgroup: 16-row sums
+};
+
+// The sequence's side work (threads 0..255 of workgroup 64, kv head 0).
+template <typename T>
+__device__ void slices_side_work(const DecArgs<T>& D, SliceShared& sh, int b, int p) {
+  const PrepArgs<T>& A = D.P;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int e128 = tid & 127, hh = tid >> 7;
+  const bool act = tid < DEC_NT;
+  const int rope = A.rope, ratio = A.ratio, topk = D.topk;
+  const int j_new = (p + 1) % ratio == 0 ? p / ratio : -1;
+  const float ikv = Act<T>::load(A.ik, (long)b * IDX_D + e128);
+  auto nrm = [&](float xv, float ri, float w) { return Act<T>::round(mul_rn(mul_rn(xv, ri), w)); };
+  if (tid < IDX_D) Act<T>::store(A.raw_keys, ((long)b * A.max_ctx + p) * IDX_D + tid, ikv);
+  if (j_new >= 0) {
+    // the block's mean (16-row chunk sums in order, then divided by the count),
+    // cast, normed and roped at the block's first position; the token's own row
+    // is ik (its store above may not be visible to these loads)
+    if (act) {
+      const T* raw = A.raw_keys + ((long)b * A.max_ctx + (long)j_new * ratio) * IDX_D + e128;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int ch = hh + 2 * c;
+        if (16 * ch < ratio) {
+          float acc = 0.f;
+          for (int i = 0; i < 16 && 16 * ch + i < ratio; ++i) {
+            const int r = 16 * ch + i;
+            acc = add_rn(acc, j_new * ratio + r == p ? ikv : Act<T>::load(raw, (long)r * IDX_D));
+          }
+          sh.chunk[ch][e128] = acc;
+        }
+      }
+    }
+    __syncthreads();
+    if (wv == 0) {
+      float x[2], cs0[2], sn0[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        float total = sh.chunk[0][lane + 64 * k];
+        for (int ch = 1; 16 * ch < ratio; ++ch) total = add_rn(total, sh.chunk[ch][lane + 64 * k]);
+        x[k] = Act<T>::round(div_rn(total, (float)ratio));
+        const int ec = min(lane + 64 * k, rope - 1);
+        cs0[k] = A.cos[(long)j_new * ratio * rope + ec];
+        sn0[k] = A.sin[(long)j_new * ratio * rope + ec];
+      }
+      const float ri = wave_rinv<2>(x, A.eps);
+      float y[2] = {nrm(x[0], ri, A.ik_norm[lane]), nrm(x[1], ri, A.ik_norm[lane + 64])};
+      wave_rope<2>(y, rope, cs0, sn0);
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        A.block_keys[((long)b * A.max_blocks + j_new) * IDX_D + bk_index(lane + 64 * k)] = y[k];
+    }
+  }
+  if (D.iq_out && wv < A.idx_heads) {
+    const int n_iq = A.idx_heads * IDX_D;
+    float x[2], cs[2], sn[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      x[k] = Act<T>::load(A.iq, (long)b * n_iq + wv * IDX_D + lane + 64 * k);
+      const int ec = min(lane + 64 * k, rope - 1);
+      cs[k] = A.cos[(long)p * rope + ec];
+      sn[k] = A.sin[(long)p * rope + ec];
+    }
+    const float ri = wave_rinv<2>(x, A.eps);
+    float y[2] = {nrm(x[0], ri, A.iq_norm[lane]), nrm(x[1], ri, A.iq_norm[lane + 64])};
+    wave_rope<2>(y, rope, cs, sn);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) D.iq_out[(long)b * n_iq + wv * IDX_D + lane + 64 * k] = y[k];
+  }
+  const ItemCount ic(p, ratio, topk, A.max_blocks);
+  if (D.ids) {
+    for (int i = tid; i < ic.n_sel; i += SL_NT) D.ids[(long)b * topk + i] = i;
+    if (tid == 0) D.n_sel[b] = ic.n_sel;
+  }
+  if (D.items) {
+    int2* items = D.items + (long)b * D.max_items;
+    for (int it = tid; it < ic.n_items; it += SL_NT) {
+      int u0, ulo, uhi;
+      item_span_blk(it, ic.n_blk_items, ic.gpb, ratio, ic.ts, p, it / ic.gpb, u0, ulo, uhi);
+      const int pg = A.page_table[(long)b * A.max_pages + min(u0 / A.page_size, A.max_pages - 1)];
+      items[1 + it] = make_item(pg * A.page_size + u0 % A.page_size, ulo, uhi);
+    }
+    if (tid == 0) items[0] = make_int2(ic.n_items, 0);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(SL_NT) void qsa_decode_slices_kernel(DecArgs<T> D) {
+  __shared__ SliceShared sh;
+  QM_PHASE_DECL
+  QM_PHASE(0);
+  const PrepArgs<T>& A = D.P;
+  const int x = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int col = lane & 15, quad = lane >> 4;
+  const int p = A.positions[b];
+  if (x == DEC_SLICES) {
+    // the side work belongs to the sequence, not to a kv head
+    if (g == 0 && p + 1 <= SL_MAX_TOK) slices_side_work<T>(D, sh, b, p);
+    QM_PHASE(8);
+    QM_PHASE_FLUSH();
+    return;
+  }
+  const int h = x >> 3, cb = x & 7, qh = g * GQA + h;
+  const int hq = A.hq, rope = A.rope;
+  const int bg = b * A.hkv + g;
+  T* out = D.out + ((long)b * hq + qh) * QSA_D + 32 * cb;
+  if (p + 1 > SL_MAX_TOK) {
+    // a position past the short range (a plan sized for smaller positions)
+    // cannot be attended: its output is poisoned and counted in word 2
+    if (x == 0 && tid == 0)
+      __hip_atomic_fetch_add(D.gen + (long)bg * DEC_GEN_STRIDE + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < 32) Act<T>::store(out, tid, __builtin_nanf(""));
+    return;
+  }
+
+  // ---- loads, every one unconditional (indices clamped) and none converted
+  // where it is loaded, so that no wait comes before the last is issued: the
+  // page-table row first (the key and value loads need it), the query head
+  // (wave 0) or the token's key (the other waves; wave 1 uses it) with their
+  // norm weights, the token's value, the gate of the slice's channels, then
+  // the rope row once the position is in
+  const int pgv = A.page_table[(long)b * A.max_pages + min(tid & (SL_MAX_PAGES - 1), A.max_pages - 1)];
+  T xt[4], vt_raw, gt_raw;
+  float wr[4], cs[2], sn[2];
+  {
+    const T* src = wv == 0 ? A.qg + ((long)b * hq + qh) * (2 * QSA_D) : A.k_new + (long)bg * QSA_D;
+    const float* wsrc = wv == 0 ? A.q_norm : A.k_norm;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      xt[k] = src[lane + 64 * k];
+      wr[k] = wsrc[lane + 64 * k];
+    }
+  }
+  vt_raw = A.v_new[(long)bg * QSA_D + (tid & (QSA_D - 1))];
+  gt_raw = A.qg[((long)b * hq + qh) * (2 * QSA_D) + QSA_D + 32 * cb + (tid & 31)];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int ec = min(lane + 64 * k, rope - 1);
+    cs[k] = A.cos[(long)p * rope + ec];
+    sn[k] = A.sin[(long)p * rope + ec];
+  }
+  if (tid < SL_MAX_PAGES) sh.pages[tid] = pgv;
+  __syncthreads();                        // the page-table row in LDS
+  QM_PHASE(1);
+
+  // ---- the wave's keys and values, requested now so that they travel while
+  // the query and key are normed: 16-key tiles wv and wv + 16, 32-key group wv
+  // (a wave past the keys loads nothing; the branches are uniform per wave)
+  const int n_tok = p + 1, n_tiles = (n_tok + 15) >> 4, n_grp = (n_tok + 31) >> 5;
+  const long head_base = (long)g * A.page_size * QSA_D;
+  const long page_stride = (long)A.hkv * A.page_size * QSA_D;
+  bf16x8_t kf[2][8], vf[2];              // set only where used
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (wv + SL_WAVES * i < n_tiles) {
+      const int r16 = 16 * (wv + SL_WAVES * i);
+      const uint16_t* kt = A.k_pool + sh.pages[r16 / A.page_size] * page_stride + head_base +
+                           ((r16 % A.page_size) >> 4) * 8 * 512 + lane * 8;
+#pragma unroll
+      for (int sk = 0; sk < 8; ++sk) kf[i][sk] = load_bf16x8(kt + sk * 512);
+    }
+  }
+  if (wv < n_grp) {
+    const int r32 = 32 * wv;
+    const uint16_t* vt = A.v_pool + sh.pages[r32 / A.page_size] * page_stride + head_base +
+                         (((r32 % A.page_size) >> 5) * 16 + 2 * cb) * 512 + lane * 8;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) vf[j] = load_bf16x8(vt + j * 512);
+  }
+  QM_PHASE(2);
+
+  auto nrm = [&](float xv, float ri, float w) { return Act<T>::round(mul_rn(mul_rn(xv, ri), w)); };
+  float xr[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    opaque(xt[k]);
+    xr[k] = Act<T>::load(&xt[k], 0);
+  }
+  if (wv == 0) {
+    // the query head: fused sum of squares and the hardware reciprocal square
+    // root (as the long-context kernel), then bf16 hi and lo
+    const float ri = wave_rinv_fast(xr, A.eps);
+    float y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y[k] = nrm(xr[k], ri, wr[k]);
+    wave_rope<4>(y, rope, cs, sn);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint16_t qhi = f32_to_bf16(y[k]);
+      sh.qb[0][lane + 64 * k] = qhi;
+      sh.qb[1][lane + 64 * k] = f32_to_bf16(y[k] - bf16_to_f32(qhi));
+    }
+  } else if (wv == 1) {
+    // the token's key, in the bits appended to the cache
+    const float ri = wave_rinv<4>(xr, A.eps);
+    float y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y[k] = nrm(xr[k], ri, wr[k]);
+    wave_rope<4>(y, rope, cs, sn);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sh.knb[lane + 64 * k] = f32_to_bf16(y[k]);
+  }
+  if (tid < QSA_D) {
+    opaque(vt_raw);
+    sh.vnb[tid] = f32_to_bf16(Act<T>::load(&vt_raw, 0));
+  }
+  __syncthreads();
+  QM_PHASE(3);
+
+  // ---- scores of keys 0..p: S^T = K Q^T with column 0 the query's hi part
+  // and column 1 its lo part (the other columns zero); lane col 0 adds lane
+  // col 1 (DPP row shift by 1)
+  bf16x8_t qf[8];
+#pragma unroll
+  for (int sk = 0; sk < 8; ++sk) {
+    const bf16x8_t z = {};
+    qf[sk] = col < 2 ? *reinterpret_cast<const bf16x8_t*>(&sh.qb[col & 1][32 * sk + 8 * quad]) : z;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int t = wv + SL_WAVES * i, r16 = 16 * t;
+    if (t < n_tiles) {
+      if (p >= r16 && p < r16 + 16) {
+        // the token's key (not yet in its page) replaces its row
+        const bool krow = col == (p & 15);
+#pragma unroll
+        for (int sk = 0; sk < 8; ++sk) {
+          const bf16x8_t kv = *reinterpret_cast<const bf16x8_t*>(&sh.knb[32 * sk + 8 * quad]);
+          kf[i][sk] = krow ? kv : kf[i][sk];
+        }
+      }
+      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sk = 0; sk < 8; ++sk) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[i][sk], qf[sk], c, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float full = c[v] + row_shl<1>(c[v]);
+        const int tok = r16 + 4 * quad + v;
+        if (col == 0) sh.s[tok] = tok < n_tok ? full * (1.0f / 16.0f) : -INFINITY;
+      }
+    }
+  }
+  QM_PHASE(4);
+  __syncthreads();
+  QM_PHASE(5);
+
+  // ---- softmax over the n_tok scores (at most one key per thread): the
+  // maximum behind one barrier; each thread's weight e^(s - max) goes into its
+  // wave's sum, and the PV operand forms the same weights from the scores
+  const float sv = tid < n_tok ? sh.s[tid] : -INFINITY;
+  float mx = wave_max(sv);
+  if (lane == 0) sh.wred[wv] = mx;
+  __syncthreads();
+  mx = sh.wred[0];
+#pragma unroll
+  for (int w = 1; w < SL_WAVES; ++w) mx = fmaxf(mx, sh.wred[w]);
+  const float lw = wave_sum(tid < n_tok ? __expf(sv - mx) : 0.f);
+  QM_PHASE(6);
+
+  // ---- O^T[d][0] = V^T[d][tok] P^T[tok][0] for the slice's two 16-channel
+  // blocks over the wave's 32-key group; the weights as bf16 in the PV MFMA's
+  // k order (e < 4: key 4 quad + e, else 16 + 4 quad + e - 4)
+  f32x4_t o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  if (wv < n_grp) {
+    const int r32 = 32 * wv;
+    if (p >= r32 && p < r32 + 32) {
+      // the token's value replaces its slot (one element of the lanes whose
+      // octet holds the slot)
+      const int kappa = v_slot(p - r32);
+      const int dw = (kappa & 7) >> 1, sh16 = 16 * (kappa & 1);
+      const bool vcol = quad == (kappa >> 3);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const unsigned val = sh.vnb[16 * (2 * cb + j) + col];
+        u32x4_t u = __builtin_bit_cast(u32x4_t, vf[j]);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          if (vcol && jj == dw) u[jj] = (u[jj] & ~(0xffffu << sh16)) | (val << sh16);
+        vf[j] = __builtin_bit_cast(bf16x8_t, u);
+      }
+    }
+    float pw[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = r32 + (e < 4 ? 4 * quad + e : 16 + 4 * quad + e - 4);
+      pw[e] = col == 0 && tok < n_tok ? __expf(sh.s[tok] - mx) : 0.f;
+    }
+    u32x4_t pu;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) pu[k] = pack_bf16x2(pw[2 * k], pw[2 * k + 1]);
+    const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, pu);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[j], pf, o[j], 0, 0, 0);
+  }
+  QM_PHASE(7);
+  // lane (0, quad) holds channels 16 j + 4 quad + v of the slice
+  if (col == 0) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sh.red[wv][16 * j + 4 * quad + v] = o[j][v];
+  }
+  if (lane == 0) sh.wsum[wv] = lw;
+  __syncthreads();
+  if (tid < 32) {
+    float num = 0.f, lsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < SL_WAVES; ++w) {
+      num += sh.red[w][tid];
+      lsum += sh.wsum[w];
+    }
+    const float gate = Act<T>::load(&gt_raw, 0);
+    Act<T>::store(out, tid, Act<T>::round(num / lsum) * Act<T>::round(sigmoid_f(gate)));
+  }
+  if (x == 0 && tid < QSA_D) {
+    // the token's key and value into its page slot
+    const int pg_cur = sh.pages[p / A.page_size], prow = p % A.page_size;
+    const long cbase = pg_cur * page_stride + head_base;
+    A.k_pool[cbase + k_page_index(prow, tid)] = sh.knb[tid];
+    A.v_pool[cbase + v_page_index(prow, tid)] = sh.vnb[tid];
+  }
+  QM_PHASE(8);
+  QM_PHASE_FLUSH();
+}
+
 int check_geom(const qm_qsa_geom* g, const char* who) {
   if (!g) return qm_fail(QM_ERR_ARG, who);
   if (g->head_dim != QSA_D || g->idx_dim != IDX_D)
@@ -3224,6 +3595,28 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
   if (g->batch > 65535) return qm_fail(QM_ERR_ARG, "qm_qsa_decode: batch above 65535");
   if (!workspace || workspace_bytes < qm_qsa_decode_workspace(g, splits))
     return qm_fail(QM_ERR_WORKSPACE, "qm_qsa_decode: workspace too small");
+  char* ws = static_cast<char*>(workspace);
+  unsigned* gen = reinterpret_cast<unsigned*>(ws);
+  // Short contexts (a plan of at most SL_FAST_ITEMS attention items, so at most
+  // 32 SL_FAST_ITEMS keys, with a budget that keeps the selection off for all
+  // of them) take the slice kernel: no workgroup waits for another.
+  if (splits <= SL_FAST_ITEMS && g->budget >= SL_MAX_TOK) {
+    const dim3 grid(DEC_SLICES + 1, g->n_kv_heads, g->batch);
+    auto run_slices = [&](auto* tag) -> int {
+      using T = std::remove_pointer_t<decltype(tag)>;
+      DecArgs<T> D{};
+      D.P = prep_args<T>(g, 1, qg, k_new, v_new, iq, ik, q_norm, k_norm, iq_norm, ik_norm, cos, sin, positions,
+                         page_table, k_pool, v_pool, raw_keys, block_keys, nullptr, nullptr);
+      D.gen = gen; D.out = static_cast<T*>(out);
+      D.ids = ids; D.n_sel = n_sel; D.items = static_cast<int2*>(items); D.iq_out = iq_out;
+      D.splits = splits; D.topk = g->budget / g->ratio; D.max_items = item_stride(g);
+      hipLaunchKernelGGL(qsa_decode_slices_kernel<T>, grid, dim3(SL_NT), 0, stream, D);
+      QM_CHECK_LAUNCH();
+      return QM_OK;
+    };
+    if (g->act_dtype == QM_ACT_F32) return run_slices(static_cast<float*>(nullptr));
+    return run_slices(static_cast<bf16_t*>(nullptr));
+  }
   // every workgroup of a (sequence, kv head) group waits for the others: the
   // group must fit on the device at once (groups are dispatched in order, so
   // one group at a time is enough)
@@ -3231,8 +3624,6 @@ extern "C" int qm_qsa_decode(const qm_qsa_geom* g, const void* qg, const void* k
   if (resident < 0) return resident;
   rc = qm_qsa_decode_fits(splits, resident);
   if (rc) return rc;
-  char* ws = static_cast<char*>(workspace);
-  unsigned* gen = reinterpret_cast<unsigned*>(ws);
   unsigned* flags = reinterpret_cast<unsigned*>(ws + dec_gen_bytes(g));
   float* part_ml = reinterpret_cast<float*>(ws + dec_gen_bytes(g) + dec_flag_bytes(g, splits));
   uint16_t* part_o = reinterpret_cast<uint16_t*>(ws + dec_gen_bytes(g) + dec_flag_bytes(g, splits) + dec_ml_bytes(g, splits));

@@ -418,3 +418,89 @@ def test_fused_decode_front_equals_prep_then_select(gpu, pos):
     k = int(n1.max())
     assert torch.equal(ids1[..., :k].sort(-1).values, ids2[..., :k].sort(-1).values)
     assert torch.equal(kp1, kp2)
+
+
+def _decode_both_kernels(gpu, monkeypatch, pos, seed):
+    """One decode step at `pos` twice on identical caches: through the plan the
+    position asks for (at most 10 attention items: the short-context slice
+    kernel) and through a plan sized for position 2000 (the long-context
+    kernel, whose grid is sized by the plan). Returns (oracle output, chosen
+    sets, [(output, cache) per kernel])."""
+    qm = gpu
+    cfg = OracleConfig()
+    dtype = torch.bfloat16
+    store = gi.FakeStore(gi.qsa_weights(3, seed, dtype))
+    keys, values, idx_keys = gi.qsa_past(seed + 1, pos, dtype)
+    hidden = gi.normal(gi.rng(seed + 2), (1, 1, gi.HIDDEN)).to(dtype)
+    cos, sin = tables(pos + 1)
+    want, _, _, chosen = _oracle_core(cfg, store, hidden, cos, sin, keys if pos else None,
+                                      values if pos else None, idx_keys, pos)
+    lib = qm.native.load()
+    real_splits = lib.qm_qsa_decode_splits
+    runs = []
+    for plan_pos in (pos, 2000):
+        # the model sizes its decode plan with qm_qsa_decode_splits
+        monkeypatch.setattr(lib, "qm_qsa_decode_splits", lambda g, p, pp=plan_pos: real_splits(g, pp))
+        model, cache = _model_and_cache(gpu, store, dtype, 2048 + 64)
+        if pos:
+            cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
+        qg, k, v, iq, ik = (t.to(DEV) for t in _projections(store, hidden))
+        got = model.qsa_core(qg, k, v, iq, ik, 3, cache, pos, cos.to(DEV), sin.to(DEV))
+        torch.cuda.synchronize()
+        runs.append((got, cache, model))
+    monkeypatch.setattr(lib, "qm_qsa_decode_splits", real_splits)
+    return want, chosen, runs
+
+
+@pytest.mark.parametrize("pos", [0, 31, 63, 64, 191, 192, 300])
+def test_short_context_kernel_matches_long_context_kernel(gpu, monkeypatch, pos):
+    """Below 320 keys (selection off) the slice kernel scores every key per
+    query head in one workgroup (no hand-off); the long-context kernel splits
+    the keys into 32-key items and merges their partials. Both are within the
+    bar of the oracle; they round the softmax differently (one softmax against
+    a merge of per-item ones), so their outputs agree to the bar, while the
+    appended key/value bits, the pooled block keys (63 and 191 complete a
+    block), the indexer query and the selected set agree bit for bit."""
+    print(f"short vs long context kernel pos={pos}", flush=True)
+    want, chosen, runs = _decode_both_kernels(gpu, monkeypatch, pos, 90)
+    (o_s, c_s, m_s), (o_l, c_l, m_l) = runs
+    for o, c in ((o_s, c_s), (o_l, c_l)):
+        assert _got_sets(c[3]) == chosen
+        assert rel_err(o, want, OUT_TOL) < OUT_TOL
+    assert rel_err(o_s, o_l, OUT_TOL) < OUT_TOL
+    ls, ll = c_s[3], c_l[3]
+    assert torch.equal(ls.k_pool, ll.k_pool) and torch.equal(ls.v_pool, ll.v_pool)
+    assert torch.equal(ls.raw_keys, ll.raw_keys)
+    assert torch.equal(ls.block_keys, ll.block_keys)
+    assert torch.equal(ls.last_iq, ll.last_iq)
+    for m in (m_s, m_l):
+        m.check_handoffs()
+
+
+def test_short_context_kernel_poisons_a_position_past_its_range(gpu, monkeypatch):
+    """A plan of the slice kernel (sized for position 100) launched at position
+    600, past the 512 keys its workgroups hold: every output is NaN, the
+    launch is counted in the group's overflow word, and nothing is appended
+    (no workgroup reads or writes a page)."""
+    qm = gpu
+    dtype = torch.bfloat16
+    pos = 600
+    store = gi.FakeStore(gi.qsa_weights(3, 95, dtype))
+    keys, values, idx_keys = gi.qsa_past(96, pos, dtype)
+    hidden = gi.normal(gi.rng(97), (1, 1, gi.HIDDEN)).to(dtype)
+    cos, sin = tables(pos + 1)
+    lib = qm.native.load()
+    real_splits = lib.qm_qsa_decode_splits
+    monkeypatch.setattr(lib, "qm_qsa_decode_splits", lambda g, p: real_splits(g, 100))
+    model, cache = _model_and_cache(gpu, store, dtype, 1024)
+    cache[3].keys, cache[3].values, cache[3].indexer_keys = keys.to(DEV), values.to(DEV), idx_keys.to(DEV)
+    k_before = cache[3].k_pool.clone()
+    qg, k, v, iq, ik = (t.to(DEV) for t in _projections(store, hidden))
+    print("short context kernel at pos 600 (past its range)", flush=True)
+    got = model.qsa_core(qg, k, v, iq, ik, 3, cache, pos, cos.to(DEV), sin.to(DEV))
+    torch.cuda.synchronize()
+    monkeypatch.setattr(lib, "qm_qsa_decode_splits", real_splits)
+    assert torch.isnan(got.float()).all()
+    assert torch.equal(cache[3].k_pool, k_before)
+    words = model._ws["qsa_decode_3_1"].view(torch.int32).cpu()[: 2 * 32].reshape(2, 32)
+    assert words[:, 2].tolist() == [1, 1]     # counted once per (sequence, kv head) group

@@ -346,10 +346,11 @@ size_t qm_qsa_attend_chunk_workspace(const qm_qsa_geom* g, int seq);
  *   q (qm_qsa_prep's q_out) and qg [B, S, Hq, 2*d] act as qm_qsa_attend;
  *   positions [B] = position of row 0; ids [B, S, budget/ratio] and n_sel
  *   [B, S] from qm_qsa_select; out [B, S, Hq*d] act.
- * The workspace keeps per-block entry counts between calls (double-buffered
- * by a parity word it also holds): zero-fill it before its first use, keep
- * it for one (batch, max_blocks) geometry (a larger `seq` may reuse a
- * workspace sized for it), and do not let two calls on it overlap. */
+ * The workspace holds a slot table per (block, row), filed on the way in and
+ * cleared by the merge, so every call leaves it zero: zero-fill it before its
+ * first use, keep it for one (batch, max_blocks) geometry (a workspace sized
+ * for a longer chunk serves a shorter one), and do not let two calls on it
+ * overlap. */
 int qm_qsa_attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void* qg, const void* k_pool,
                         const void* v_pool, const int* positions, const int* page_table, const int* ids,
                         const int* n_sel, void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);

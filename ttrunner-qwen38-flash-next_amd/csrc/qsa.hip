@@ -1054,12 +1054,26 @@ __device__ void rank_topk(const unsigned long long* keys, int n, int topk, int* 
   }
 }
 
+// File one selected entry: row s of sequence b took block j as its slot-th selection.
+__device__ __forceinline__ void file_entry(uint16_t* tab, int b, int max_blocks, int seq, int j, int s, int slot) {
+  tab[((long)b * max_blocks + j) * seq + s] = static_cast<uint16_t>(slot + 1);
+}
+
+// The (max, sum) pairs of a row's slot that holds no partial.
+__device__ __forceinline__ void empty_partial(float* part_ml, long row, int hkv, int nslot, int slot) {
+  for (int g = 0; g < hkv; ++g) {
+    float4* ml = reinterpret_cast<float4*>(part_ml + (((long)row * hkv + g) * nslot + slot) * GQA * 2);
+#pragma unroll
+    for (int h = 0; h < GQA / 2; ++h) ml[h] = make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
+  }
+}
+
 struct SelArgs {
   const float* iq; const float* block_keys; const int* positions; const int* page_table;
   int* ids; int* n_sel; int2* items; float* scores_out;
   int batch, seq, idx_heads, ratio, topk, max_blocks, page_size, max_pages, max_items;
-  // the chunk path's entry lists (qm_qsa_select_chunk), or null
-  unsigned* cnt = nullptr; unsigned* list = nullptr; float* part_ml = nullptr; const int* parity = nullptr;
+  // the chunk path's slot table (qm_qsa_select_chunk files into it), or null
+  uint16_t* tab = nullptr; float* part_ml = nullptr;
   int hkv = 0;
   // the rows' block scores from qsa_score_rows_kernel ([row][max_blocks]), or
   // null when the selection scores the blocks itself
@@ -1130,38 +1144,22 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
     for (int i = tid; i < A.topk; i += NT) out_ids[i] = S.sel[i];
   }
   if (tid == 0) A.n_sel[row] = n_sel;
-  if (A.cnt) {
-    // the chunk path's entry lists, as qsa_chunk_bucket_kernel files them:
-    // every selected block files (row, slot) under the block, the slots this
-    // row leaves empty get (max, sum) = (-inf, 0), and the previous call's
-    // counts (the other parity) are cleared, spread over the rows
+  if (A.tab) {
+    // the chunk path's slot table, as qsa_chunk_bucket_kernel fills it: every
+    // selected block files the row's slot, and the slots this row leaves
+    // empty get (max, sum) = (-inf, 0)
     __syncthreads();
     const int s = row % A.seq;
-    const int par = *A.parity;
-    unsigned* cnt_in = A.cnt + ((long)par * A.batch + b) * A.max_blocks;
-    unsigned* cnt_old = A.cnt + ((long)(par ^ 1) * A.batch + b) * A.max_blocks;
-    for (int j = s * NT + tid; j < A.max_blocks; j += A.seq * NT) cnt_old[j] = 0u;
     const int nslot = A.topk + 1;
     for (int i = tid; i < nslot; i += NT) {
       bool empty;
       if (i < A.topk) {
         empty = i >= n_sel;
-        if (!empty) {
-          const int j = S.sel[i];
-          // a block is at most once among a row's selections: at < seq
-          const unsigned at = atomicAdd(&cnt_in[j], 1u);
-          if (at < static_cast<unsigned>(A.seq))
-            A.list[((long)b * A.max_blocks + j) * A.seq + at] = (static_cast<unsigned>(s) << 16) | static_cast<unsigned>(i);
-        }
+        if (!empty) file_entry(A.tab, b, A.max_blocks, A.seq, S.sel[i], s, i);
       } else {
         empty = ((p + 1) / A.ratio) * A.ratio > p;      // the row completes its block: no tail
       }
-      if (empty)
-        for (int g = 0; g < A.hkv; ++g) {
-          float4* ml = reinterpret_cast<float4*>(A.part_ml + (((long)row * A.hkv + g) * nslot + i) * GQA * 2);
-#pragma unroll
-          for (int h = 0; h < GQA / 2; ++h) ml[h] = make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
-        }
+      if (empty) empty_partial(A.part_ml, row, A.hkv, nslot, i);
     }
   }
   if (!A.items) return;
@@ -1556,7 +1554,10 @@ template <typename T, typename PO = float>
 struct CombineArgs {
   const PO* part_o; const float* part_ml; const T* qg; T* out;
   int hq, hkv, splits;
-  int* flip = nullptr;      // the chunk path's entry-list parity, flipped once the merge is done
+  // the chunk path's slot table, cleared here once the attention has read
+  // it: its length in 16-byte words
+  uint16_t* tab = nullptr;
+  long tab_words = 0;
 };
 
 __device__ __forceinline__ float part_value(const float* p, long i) { return p[i]; }
@@ -1574,7 +1575,12 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T, PO> A
   __shared__ float s_w[MAX_SPLITS];
   __shared__ float s_red[QSA_D / 64];
   const float gate = Act<T>::load(A.qg, ((long)row * A.hq + hq) * (2 * QSA_D) + QSA_D + d);
-  if (A.flip && hq == 0 && row == 0 && d == 0) *A.flip ^= 1;
+  if (A.tab) {
+    // each workgroup clears 4 KB stretches of the table, spread over the grid
+    const long wg = blockIdx.x + (long)gridDim.x * blockIdx.y, n_wg = (long)gridDim.x * gridDim.y;
+    for (long w = wg * QSA_D + d; w < A.tab_words; w += n_wg * QSA_D)
+      reinterpret_cast<u32x4_t*>(A.tab)[w] = u32x4_t{0u, 0u, 0u, 0u};
+  }
   // every split's (max, sum) in parallel, then the weights in LDS
   float m = -INFINITY, l = 0.f;
   for (int s = d; s < A.splits; s += QSA_D) {
@@ -1621,111 +1627,132 @@ __global__ __launch_bounds__(QSA_D) void qsa_combine_kernel(CombineArgs<T, PO> A
 // The attention of a chunk of query rows reads each key/value block once. A
 // row's entries are its (row, slot) pairs: slot i < n_sel its i-th selected
 // block, slot topk its tail block (keys ts..p, when the row does not complete
-// its block). qm_qsa_attend_chunk is three launches:
-//   qsa_chunk_bucket   one 64-thread workgroup per row: files each selected
-//                      entry under its block (an atomic count and a list of
-//                      capacity seq per block, in the workspace) and writes the
-//                      empty partials (max -inf) of the row's unused slots;
+// its block). The entries are filed in a slot table, [B][max_blocks][seq]
+// uint16 in the workspace: entry (b, j, s) holds slot + 1 when row s selected
+// block j, else 0. Plain stores fill it (no atomics, so no round trip holds up
+// the filing), the attention reads a block's row of it, and the merge clears
+// it, so every call leaves the table zero. qm_qsa_attend_chunk is three
+// launches:
+//   qsa_chunk_bucket   one 64-thread workgroup per row: files the row's
+//                      selected entries and writes the empty partials (max
+//                      -inf) of its unused slots (qm_qsa_select_chunk does the
+//                      same inside the selection);
 //   qsa_chunk_attend   grid (blocks + tail workgroups, kv head, sequence): the
-//                      workgroup of block j reads its count and list with its
-//                      first loads, then the block's 64 tokens of key and value
-//                      pieces (16 KB of key and 16 KB of value per 32 tokens,
-//                      contiguous in the page's lane order) through registers
-//                      into LDS; each wave scores two entries x 8 query heads
-//                      on bf16 MFMA and writes one partial per (row, slot,
-//                      head): fp32 max and sum, and the output normalised by the
-//                      sum, in bf16. A tail workgroup takes the tail entries of
-//                      8 rows (one or two blocks), which would otherwise pile
-//                      onto two blocks' workgroups;
-//   qsa_combine        merges a row's topk + 1 slots and applies the gate.
-// The counts are double-buffered by a parity word: the bucket kernel files
-// into set p and clears set p ^ 1 (the previous call's), the merge flips p. The
-// workspace is zero-filled before its first use and left consistent by every
-// call.
+//                      workgroup of block j reads its table row and the page
+//                      with its first loads, then the block's 64 tokens of key
+//                      pieces straight into LDS (16 KB per 32 tokens) and of
+//                      value pieces into registers; each wave scores two
+//                      entries x 8 query heads on bf16 MFMA and writes one
+//                      partial per (row, slot, head): fp32 max and sum, and the
+//                      output normalised by the sum, in bf16. Every wave finds
+//                      the entries it needs from the table row by ballot, so
+//                      the workgroup's LDS is the keys and the softmax weights
+//                      alone (40 KB: four workgroups per compute unit). A tail
+//                      workgroup takes the tail entries of 8 rows (one or two
+//                      blocks), which would otherwise pile onto two blocks'
+//                      workgroups;
+//   qsa_combine        merges a row's topk + 1 slots, applies the gate and
+//                      clears the slot table.
+// The workspace is zero-filled before its first use; the selection (or the
+// bucket kernel) and the attention of one call use the same seq.
 constexpr int CA_MAX_BLOCKS = 4096;
 constexpr int CA_NT = 256;        // attention workgroup: four waves
 constexpr int CA_TAIL_ROWS = 8;   // rows per tail workgroup
-constexpr int CA_MAX_BPW = 4;     // blocks per workgroup
 
 struct ChunkAttnArgs {
   const uint16_t* q;                      // [rows, 2 (hi, lo), hq, 256] bf16
   const uint16_t* k_pool; const uint16_t* v_pool;
-  const int* positions; const int* page_table; const int* ids; const int* n_sel;
+  const int* positions; const int* page_table;
   uint16_t* part_o; float* part_ml;      // part_o: bf16, normalised by l
-  unsigned* cnt;                          // [2][B][max_blocks] entry counts
-  const unsigned* list;                   // [B][max_blocks][seq]: row << 16 | slot
-  const int* parity;
-  int batch, seq, hq, hkv, page_size, max_pages, ratio, topk, max_blocks, bpw, nwg_sel;
+  const uint16_t* tab;                    // [B][max_blocks][seq]: slot + 1, or 0
+  int batch, seq, hq, hkv, page_size, max_pages, ratio, topk, max_blocks, nwg_sel;
   float scale;
 };
 
 struct ChunkBucketArgs {
   const int* positions; const int* ids; const int* n_sel;
-  float* part_ml; unsigned* cnt; unsigned* list; const int* parity;
+  float* part_ml; uint16_t* tab;
   int batch, seq, hkv, ratio, topk, max_blocks;
 };
 
 __global__ __launch_bounds__(64) void qsa_chunk_bucket_kernel(ChunkBucketArgs A) {
   const int row = blockIdx.x, lane = threadIdx.x;
   const int b = row / A.seq, s = row % A.seq;
-  const int par = *A.parity;
   const int nslot = A.topk + 1;
   const int nsel = A.n_sel[row];
   const int p = A.positions[b] + s;
-  unsigned* cnt_in = A.cnt + ((long)par * A.batch + b) * A.max_blocks;
-  // the previous call's counts, cleared for the next call
-  unsigned* cnt_old = A.cnt + ((long)(par ^ 1) * A.batch + b) * A.max_blocks;
-  for (int j = s * 64 + lane; j < A.max_blocks; j += A.seq * 64) cnt_old[j] = 0u;
   for (int i = lane; i < nslot; i += 64) {
     bool empty;
     if (i < A.topk) {
       empty = i >= nsel;
-      if (!empty) {
-        const int j = A.ids[(long)row * A.topk + i];
-        // a block is at most once among a row's selections: at < seq
-        const unsigned at = atomicAdd(&cnt_in[j], 1u);
-        if (at < static_cast<unsigned>(A.seq))
-          A.list[((long)b * A.max_blocks + j) * A.seq + at] = (static_cast<unsigned>(s) << 16) | static_cast<unsigned>(i);
-      }
+      if (!empty) file_entry(A.tab, b, A.max_blocks, A.seq, A.ids[(long)row * A.topk + i], s, i);
     } else {
       empty = ((p + 1) / A.ratio) * A.ratio > p;      // the row completes its block: no tail
     }
-    if (empty)
-      for (int g = 0; g < A.hkv; ++g) {
-        float4* ml = reinterpret_cast<float4*>(A.part_ml + (((long)row * A.hkv + g) * nslot + i) * GQA * 2);
-#pragma unroll
-        for (int h = 0; h < GQA / 2; ++h) ml[h] = make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
-      }
+    if (empty) empty_partial(A.part_ml, row, A.hkv, nslot, i);
   }
 }
 
-// Workgroup LDS of the chunk attention: the block's keys, the softmax weights
-// and sums every wave hands to the others, where each column's partial goes,
-// and a per-wave tile through which partial rows leave as whole lines.
-constexpr int CA_TROW = 144;     // bytes per row of the transpose tile (padded: the writes spread over the banks)
+// Workgroup LDS of the chunk attention: the block's keys and the softmax
+// weights every wave hands to the others.
 struct ChunkShared {
   uint16_t k[2][16][64 * 8];     // per 32-token group: 16 key pieces of 1 KB (16 tokens x 32 channels)
-  bf16x8_t p[2][4][64];          // softmax weights: [group][column block = wave that formed it][lane]
-  float rl[64];                  // 1 / sum per column (entry, query head)
-  long pb[64];                   // partial row of each column, -1 for none
-  u32x4_t tbuf[CA_NT / 64][16 * CA_TROW / 16];
+  bf16x8_t p[2][4][64];          // softmax weights / sum: [group][column block = wave that formed it][lane]
 };
+static_assert(sizeof(ChunkShared) == 40960, "four workgroups per compute unit");
+
+// The next 8 entries of a 128-row span of a block's table row, in row order:
+// lane l holds rows (span base + l) and (span base + 64 + l) as `ma` / `mb` =
+// row << 16 | slot, and `ra` / `rb` are the rows of the span not yet taken
+// (bit l: lane l's row is an entry). Scalar work: the first set bits, read out
+// of their lanes; entry 2 cw + odd goes to pko[cw] of the lanes of that
+// parity. Entries past the span's last repeat the group's first.
+__device__ __forceinline__ void next_group(unsigned long long& ra, unsigned long long& rb, unsigned ma, unsigned mb,
+                                           bool odd, unsigned (&pko)[4]) {
+  unsigned first = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    unsigned v;
+    if (ra != 0ull) {
+      v = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(ma), __builtin_ctzll(ra)));
+      ra &= ra - 1ull;
+    } else if (rb != 0ull) {
+      v = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(mb), __builtin_ctzll(rb)));
+      rb &= rb - 1ull;
+    } else {
+      v = first;
+    }
+    if (i == 0) first = v;
+    if ((i & 1) == 0) pko[i >> 1] = v;
+    else pko[i >> 1] = odd ? v : pko[i >> 1];
+  }
+}
+
+// pko[w] for a wave-uniform w
+__device__ __forceinline__ unsigned pick4(const unsigned (&v)[4], int w) {
+  return w == 0 ? v[0] : w == 1 ? v[1] : w == 2 ? v[2] : v[3];
+}
+
+// Where a column's partial row goes: entry pk (row << 16 | tail << 9 | slot), query head hh.
+__device__ __forceinline__ long chunk_partial_row(const ChunkAttnArgs& A, unsigned pk, long row_b, int g, int nslot,
+                                                  int hh) {
+  return (((row_b + (pk >> 16)) * A.hkv + g) * nslot + (pk & 511)) * GQA + hh;
+}
 
 // One wave's scores over the block for its two entries x 8 query heads (lane
 // column il = which entry, hh = query head): the softmax weights of its 16
-// columns go to S.p as the PV product's operands, their sums' reciprocals and
-// partial rows to S.rl / S.pb, the (max, sum) pairs to the workspace.
+// columns, divided by their sums, go to S.p as the PV product's operands; the
+// (max, sum) pairs go to the workspace.
 __device__ __forceinline__ void chunk_scores(const ChunkAttnArgs& A, ChunkShared& S, const bf16x8_t (&qhi)[8],
                                              int j, unsigned pk, bool ok, long row_b, int pos0, int g, int nslot,
                                              bool mark = false) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, quad = lane >> 4, col = lane & 15, hh = lane & 7;
   const int gpb = A.ratio / 32;
-  const int s = pk >> 16, slot = pk & 511;
   const bool tail = (pk >> 9) & 1u;
-  const long row = row_b + s;
-  const int p = pos0 + s;
-  // a tile's eight key fragments are read from LDS before its products, so
-  // that their latencies overlap
+  const int p = pos0 + static_cast<int>(pk >> 16);
+  // a tile's key fragments are read from LDS four at a time before their
+  // products, so that their latencies overlap (eight at a time would not
+  // leave registers for four waves per SIMD)
   f32x4_t sc[2][2];
 #pragma unroll
   for (int gi = 0; gi < 2; ++gi) {
@@ -1733,11 +1760,15 @@ __device__ __forceinline__ void chunk_scores(const ChunkAttnArgs& A, ChunkShared
     for (int t = 0; t < 2; ++t) {
       f32x4_t c = {0.f, 0.f, 0.f, 0.f};
       if (gi < gpb) {
-        bf16x8_t kf[8];
 #pragma unroll
-        for (int sk = 0; sk < 8; ++sk) kf[sk] = *reinterpret_cast<const bf16x8_t*>(&S.k[gi][t * 8 + sk][lane * 8]);
+        for (int h = 0; h < 2; ++h) {
+          bf16x8_t kf[4];
 #pragma unroll
-        for (int sk = 0; sk < 8; ++sk) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[sk], qhi[sk], c, 0, 0, 0);
+          for (int u = 0; u < 4; ++u)
+            kf[u] = *reinterpret_cast<const bf16x8_t*>(&S.k[gi][t * 8 + 4 * h + u][lane * 8]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[u], qhi[4 * h + u], c, 0, 0, 0);
+        }
       }
       sc[gi][t] = c;
     }
@@ -1760,52 +1791,53 @@ __device__ __forceinline__ void chunk_scores(const ChunkAttnArgs& A, ChunkShared
   if (mark) QM_PHASE(9);
   float lsum = 0.f;
 #pragma unroll
+  for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float e = sc[gi][t][v] == -INFINITY ? 0.f : __expf(sc[gi][t][v] - mx);
+        sc[gi][t][v] = e;
+        lsum += e;
+      }
+  const float l = xor32_sum(xor16_sum(lsum));
+  // a column of no entry has l = 0: its weights are 0
+  const float rl = ok ? 1.0f / l : 0.f;
+#pragma unroll
   for (int gi = 0; gi < 2; ++gi) {
     unsigned pw[4];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      float pv[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        pv[v] = sc[gi][t][v] == -INFINITY ? 0.f : __expf(sc[gi][t][v] - mx);
-        lsum += pv[v];
-      }
-      pw[2 * t] = pack_bf16x2(pv[0], pv[1]);
-      pw[2 * t + 1] = pack_bf16x2(pv[2], pv[3]);
+      pw[2 * t] = pack_bf16x2(sc[gi][t][0] * rl, sc[gi][t][1] * rl);
+      pw[2 * t + 1] = pack_bf16x2(sc[gi][t][2] * rl, sc[gi][t][3] * rl);
     }
     S.p[gi][wv][lane] = __builtin_bit_cast(bf16x8_t, u32x4_t{pw[0], pw[1], pw[2], pw[3]});
   }
-  const float l = xor32_sum(xor16_sum(lsum));
   if (mark) QM_PHASE(10);
-  const long pb = ((row * A.hkv + g) * nslot + slot) * GQA + hh;
-  if (quad == 0) {
-    S.rl[wv * 16 + col] = ok ? 1.0f / l : 0.f;
-    S.pb[wv * 16 + col] = ok ? pb : -1;
-    if (ok) *reinterpret_cast<float2*>(A.part_ml + pb * 2) = make_float2(mx, l);
-  }
+  if (quad == 0 && ok)
+    *reinterpret_cast<float2*>(A.part_ml + chunk_partial_row(A, pk, row_b, g, nslot, hh) * 2) = make_float2(mx, l);
+  (void)col;
 }
 
-// A wave with no entry in the group: its columns hold no partial.
+// A wave with no entry in the group: its columns' weights are zero.
 __device__ __forceinline__ void chunk_no_scores(ChunkShared& S) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const bf16x8_t zero = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
   S.p[0][wv][lane] = zero;
   S.p[1][wv][lane] = zero;
-  if (lane < 16) {
-    S.rl[wv * 16 + lane] = 0.f;
-    S.pb[wv * 16 + lane] = -1;
-  }
 }
 
 // The outputs of a group's 64 columns (4 waves' entries x 8 query heads) in
-// this wave's 64 channels (16 wv ..: value blocks 4 wv .. 4 wv + 3, whose
-// pieces `vr` the wave holds), divided by the sums and written out: per column
-// block the lanes' fragments pass through the wave's LDS tile, and each lane
-// writes 16 contiguous bytes of a 128-byte line.
+// this wave's 64 channels (64 wv ..: value blocks 4 wv .. 4 wv + 3, whose
+// pieces `vr` the wave holds), written straight from the product's lanes
+// (two 16-byte stores per lane and column block, each of the four quads'
+// stores together 64 contiguous bytes of a partial row). pko/oko: the entries
+// of column block cw's lanes (entry il of wave cw) and whether they exist.
 __device__ __forceinline__ void chunk_outputs(const ChunkAttnArgs& A, ChunkShared& S, const bf16x8_t (&vr)[2][4],
-                                              int gpb, bool mark = false) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, quad = lane >> 4, col = lane & 15;
-  unsigned char* tb = reinterpret_cast<unsigned char*>(&S.tbuf[wv][0]);
+                                              const unsigned (&pko)[4], const bool (&oko)[4], long row_b, int g,
+                                              int nslot, bool mark = false) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, quad = lane >> 4, hh = lane & 7;
+  const int gpb = A.ratio / 32;
 #pragma unroll
   for (int cw = 0; cw < 4; ++cw) {
     f32x4_t acc[4];
@@ -1818,25 +1850,31 @@ __device__ __forceinline__ void chunk_outputs(const ChunkAttnArgs& A, ChunkShare
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vr[gi][cb], pf, acc[cb], 0, 0, 0);
       }
-    // acc[cb][v]: channel 64 wv + 16 cb + 4 quad + v of column 16 cw + col
-    const float rl = S.rl[cw * 16 + col];
+    // acc[cb][v]: channel 64 wv + 16 cb + 4 quad + v of column 16 cw + col.
+    // Channel blocks pair up (0, 1), (2, 3) by one 16-lane row swap: an even
+    // quad then holds channels 4 quad .. + 7 of the pair's first block (its
+    // own and the next quad's), an odd quad channels 4 (quad - 1) .. + 7 of
+    // the second, so every lane stores 16 contiguous bytes
+    uint16_t* dst = A.part_o + chunk_partial_row(A, pko[cw], row_b, g, nslot, hh) * QSA_D + 64 * wv +
+                    16 * (quad & 1) + 4 * (quad & 2);
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
-      *reinterpret_cast<u32x2_t*>(tb + col * CA_TROW + (16 * cb + 4 * quad) * 2) =
-          u32x2_t{pack_bf16x2(acc[cb][0] * rl, acc[cb][1] * rl), pack_bf16x2(acc[cb][2] * rl, acc[cb][3] * rl)};
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int f = lane + 64 * i, r = f >> 3, seg = f & 7;
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(tb + r * CA_TROW + seg * 16);
-      const long pbr = S.pb[cw * 16 + r];
-      if (pbr >= 0) *reinterpret_cast<u32x4_t*>(A.part_o + pbr * QSA_D + 64 * wv + 8 * seg) = v;
+    for (int cp = 0; cp < 4; cp += 2) {
+      const auto lo = __builtin_amdgcn_permlane16_swap(pack_bf16x2(acc[cp][0], acc[cp][1]),
+                                                       pack_bf16x2(acc[cp + 1][0], acc[cp + 1][1]), false, false);
+      const auto hi = __builtin_amdgcn_permlane16_swap(pack_bf16x2(acc[cp][2], acc[cp][3]),
+                                                       pack_bf16x2(acc[cp + 1][2], acc[cp + 1][3]), false, false);
+      if (oko[cw]) *reinterpret_cast<u32x4_t*>(dst + 16 * cp) = u32x4_t{lo[0], hi[0], lo[1], hi[1]};
     }
   }
   if (mark) QM_PHASE(11);
 }
 
-// Three workgroups per compute unit (about 50 KB of LDS each).
-__global__ __launch_bounds__(CA_NT, 3) void qsa_chunk_attend_kernel(ChunkAttnArgs A) {
+// vmcnt(0) alone (expcnt and lgkmcnt at their maxima): the keys that went
+// straight to LDS have landed before the barrier that hands them to the
+// other waves
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+__global__ __launch_bounds__(CA_NT, 4) void qsa_chunk_attend_kernel(ChunkAttnArgs A) {
   QM_PHASE_DECL
   QM_PHASE(0);
   const int x = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
@@ -1852,31 +1890,38 @@ __global__ __launch_bounds__(CA_NT, 3) void qsa_chunk_attend_kernel(ChunkAttnArg
 
   __shared__ ChunkShared S;
 
-  // A block's keys pass through registers into LDS (the thread's 8 of the 32
-  // pieces); the wave's value pieces (channel blocks 4 wv .. 4 wv + 3 of each
-  // 32-token group) stay in registers. A block of one 32-token group loads
-  // its pieces twice; the second copy is not used.
-  u32x4_t kr[8];
-  bf16x8_t vr[2][4];
-  auto kv_load = [&](int j, int page0, int page1) __attribute__((always_inline)) {
+  // A block's key pieces go straight to LDS (the wave's 4 of the 16 pieces of
+  // each 32-token group, 1 KB each, lane l's 16 bytes at byte 16 l); the
+  // wave's value pieces (channel blocks 4 wv .. 4 wv + 3 of each group) stay
+  // in registers.
+  bf16x8_t vr[2][4];   // set for the groups the block has
+  // addressed through a buffer resource per group (a scalar base) and one
+  // lane offset shared by every piece, the piece's offset scalar or immediate
+  const int k_off = lane * 16 + wv * 1024, v_off = lane * 16 + wv * 4096;
+  auto k_load = [&](int j, int page0, int page1) __attribute__((always_inline)) {
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
-      const int gg = gi < gpb ? gi : 0;
-      const int rowg = (j * A.ratio + 32 * gg) % A.page_size;
-      const long pbase = ((long)(gg ? page1 : page0) * A.hkv + g) * head_stride;
-      const uint16_t* ks = A.k_pool + pbase + (rowg >> 4) * 8 * 512 + lane * 8;
-      const uint16_t* vs = A.v_pool + pbase + (rowg >> 5) * 16 * 512 + lane * 8;
+      if (gi >= gpb) continue;
+      const int rowg = (j * A.ratio + 32 * gi) % A.page_size;
+      const long pbase = ((long)(gi ? page1 : page0) * A.hkv + g) * head_stride;
+      const auto kr = dev_rsrc(A.k_pool + pbase + (rowg >> 4) * 8 * 512, 16 * 1024);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kr[4 * gi + i] = *reinterpret_cast<const u32x4_t*>(ks + (wv + 4 * i) * 512);
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb) vr[gi][cb] = *reinterpret_cast<const bf16x8_t*>(vs + (4 * wv + cb) * 512);
+      for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (__attribute__((address_space(3))) void*)&S.k[gi][wv + 4 * i][0],
+                                                 16, k_off, 4096 * i, 0, 0);
     }
   };
-  auto k_store = [&]() __attribute__((always_inline)) {
+  auto v_load = [&](int j, int page0, int page1) __attribute__((always_inline)) {
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi)
+    for (int gi = 0; gi < 2; ++gi) {
+      if (gi >= gpb) continue;
+      const int rowg = (j * A.ratio + 32 * gi) % A.page_size;
+      const long pbase = ((long)(gi ? page1 : page0) * A.hkv + g) * head_stride;
+      const auto vrs = dev_rsrc(A.v_pool + pbase + (rowg >> 5) * 16 * 512, 16 * 1024);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(&S.k[gi][wv + 4 * i][lane * 8]) = kr[4 * gi + i];
+      for (int cb = 0; cb < 4; ++cb)
+        vr[gi][cb] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(vrs, v_off + 1024 * cb, 0, 0));
+    }
   };
   // the chunk path scores with the query's bf16 part (hi) alone: the keys
   // are bf16 too, and the softmax of these 64-key blocks is far inside the
@@ -1894,62 +1939,55 @@ __global__ __launch_bounds__(CA_NT, 3) void qsa_chunk_attend_kernel(ChunkAttnArg
   };
 
   if (x < A.nwg_sel) {
-    // ---- blocks x bpw .. x bpw + bpw - 1: their counts (both parities' words,
-    // one of them current), first entries and pages, and the position, in one
-    // round trip; then block by block
-    const int j0 = x * A.bpw;
-    const int par = *A.parity;
-    // (the per-block arrays are indexed by compile-time constants only, so
-    // they stay in registers; a runtime k reads them through a select chain)
-    unsigned cw[CA_MAX_BPW], pk0[CA_MAX_BPW];
-    int pg0[CA_MAX_BPW], pg1[CA_MAX_BPW];
-    static_for<CA_MAX_BPW>([&](auto k) {
-      const int j = min(j0 + k, A.max_blocks - 1);
-      const unsigned c0 = A.cnt[(long)b * A.max_blocks + j];
-      const unsigned c1 = A.cnt[((long)A.batch + b) * A.max_blocks + j];
-      cw[k] = k < A.bpw && j0 + k < A.max_blocks ? (par ? c1 : c0) : 0u;
-      pk0[k] = A.list[((long)b * A.max_blocks + j) * A.seq + min(e_w, A.seq - 1)];
-      int a0, a1;
-      pages_of(j, a0, a1);
-      pg0[k] = a0;
-      pg1[k] = a1;
-    });
+    // ---- block j = x: the first 128 rows of its table row, its pages and
+    // the position in one round trip; then its entries in groups of 8
+    const int j = x;
+    const uint16_t* trow = A.tab + ((long)b * A.max_blocks + j) * A.seq;
+    const int ta = lane < A.seq ? trow[lane] : 0;
+    const int tb = 64 + lane < A.seq ? trow[64 + lane] : 0;
+    int page0, page1;
+    pages_of(j, page0, page1);
     const int pos0 = A.positions[b];
-    // the nonempty blocks, as a bit mask taken lowest first
-    unsigned rem = 0u;
-    static_for<CA_MAX_BPW>([&](auto k) { rem |= cw[k] != 0u ? 1u << k : 0u; });
-    if (rem == 0u) {
-      QM_PHASE_FLUSH();
-      return;
-    }
-    auto pick = [&](const auto& v, int k) __attribute__((always_inline)) {
-      auto r = v[0];
-      static_for<CA_MAX_BPW>([&](auto i) { r = k == i ? v[i] : r; });
-      return r;
-    };
-    for (int t = 0; rem != 0u; ++t) {
-      const int k = __builtin_ctz(rem), j = j0 + k;
-      rem &= rem - 1u;
-      const int n = static_cast<int>(pick(cw, k));
-      const unsigned* lst = A.list + ((long)b * A.max_blocks + j) * A.seq;
-      kv_load(j, pick(pg0, k), pick(pg1, k));
-      unsigned pk = n > e_w ? pick(pk0, k) : lst[0];
-      q_load(pk);
-      if (t > 0) __syncthreads();   // every wave is done with the previous block's keys
-      k_store();
-      __syncthreads();
-      if (t == 0) QM_PHASE(3);
-      for (int g0 = 0; g0 < n; g0 += 8) {
-        const int e = g0 + e_w;
-        if (g0 > 0) {
-          pk = lst[min(e, n - 1)];
-          q_load(pk);
+    bool loaded = false, first = true;
+    for (int c = 0; 128 * c < A.seq; ++c) {
+      // rows 128 c + lane and 128 c + 64 + lane of the table row
+      const int ra = 128 * c + lane, rb = ra + 64;
+      const int tva = c == 0 ? ta : ra < A.seq ? trow[ra] : 0;
+      const int tvb = c == 0 ? tb : rb < A.seq ? trow[rb] : 0;
+      unsigned long long la = __ballot(tva != 0), lb = __ballot(tvb != 0);
+      if ((la | lb) == 0ull) continue;
+      const int nc = __popcll(la) + __popcll(lb);
+      const unsigned ma = (static_cast<unsigned>(ra) << 16) | static_cast<unsigned>(tva - 1);
+      const unsigned mb = (static_cast<unsigned>(rb) << 16) | static_cast<unsigned>(tvb - 1);
+      bool fresh = false;
+      if (!loaded) {
+        // every wave is done with the keys of an earlier span (the barrier
+        // between its last group's scores and outputs)
+        k_load(j, page0, page1);
+        v_load(j, page0, page1);
+        loaded = fresh = true;
+      }
+      for (int g0 = 0; g0 < nc; g0 += 8) {
+        // the group's entries: pko[cw] = entry 2 cw + il
+        unsigned pko[4];
+        next_group(la, lb, ma, mb, il, pko);
+        const bool ok = g0 + e_w < nc;
+        const unsigned pk = pick4(pko, wv);
+        q_load(pk);
+        if (fresh) {
+          wait_loads();
+          fresh = false;
         }
-        if (g0 + 2 * wv < n) chunk_scores(A, S, qhi, j, pk, e < n, row_b, pos0, g, nslot, t == 0 && g0 == 0);
+        __syncthreads();   // the block's keys are in LDS (and the previous group's weights read)
+        if (first) QM_PHASE(3);
+        if (g0 + 2 * wv < nc) chunk_scores(A, S, qhi, j, pk, ok, row_b, pos0, g, nslot, first);
         else chunk_no_scores(S);
+        bool oko[4];
+#pragma unroll
+        for (int cw = 0; cw < 4; ++cw) oko[cw] = g0 + 2 * cw + il < nc;
         __syncthreads();
-        chunk_outputs(A, S, vr, gpb, t == 0 && g0 == 0);
-        __syncthreads();   // every wave is done with the weights before the next group's
+        chunk_outputs(A, S, vr, pko, oko, row_b, g, nslot, first);
+        first = false;
       }
     }
   } else {
@@ -1958,28 +1996,45 @@ __global__ __launch_bounds__(CA_NT, 3) void qsa_chunk_attend_kernel(ChunkAttnArg
     const int tr0 = (x - A.nwg_sel) * CA_TAIL_ROWS;
     const int pos0 = A.positions[b];
     const int jt = (pos0 + tr0) / A.ratio;
-    const int r = tr0 + e_w, p = pos0 + r;
-    const bool has_tail = r < A.seq && ((p + 1) / A.ratio) * A.ratio <= p;
-    const int jr = has_tail ? p / A.ratio : -1;
-    const unsigned pk = (static_cast<unsigned>(min(r, A.seq - 1)) << 16) | (1u << 9) | static_cast<unsigned>(A.topk);
+    // entry e of the workgroup (row tr0 + e): its packed (row, tail, slot) and
+    // whether its tail lies in block j
+    auto tail_entry = [&](int e, int j, unsigned& pk) __attribute__((always_inline)) {
+      const int r = tr0 + e, p = pos0 + r;
+      pk = (static_cast<unsigned>(min(r, A.seq - 1)) << 16) | (1u << 9) | static_cast<unsigned>(A.topk);
+      return r < A.seq && ((p + 1) / A.ratio) * A.ratio <= p && p / A.ratio == j;
+    };
     int pa0, pa1, pb0, pb1;
     pages_of(jt, pa0, pa1);
     pages_of(jt + 1, pb0, pb1);
+    unsigned pk;
+    tail_entry(e_w, jt, pk);
     q_load(pk);
     for (int bi = 0; bi < 2; ++bi) {
       const int j = jt + bi;
-      // whether any of the 8 rows has its tail in block j (every thread sees
-      // the rows of its wave's entries; the waves agree through LDS)
-      const bool mine = jr == j;
-      if (!__syncthreads_or(mine ? 1 : 0)) continue;
-      kv_load(j, bi ? pb0 : pa0, bi ? pb1 : pa1);
-      k_store();
+      unsigned pko[4];
+      bool oko[4];
+#pragma unroll
+      for (int cw = 0; cw < 4; ++cw) oko[cw] = tail_entry(2 * cw + il, j, pko[cw]);
+      unsigned pk_j;
+      const bool mine = tail_entry(e_w, j, pk_j);
+      // whether any of the 8 rows has its tail in block j (every lane tests
+      // them all, so the answer is uniform without an exchange)
+      bool any = false;
+#pragma unroll
+      for (int e = 0; e < CA_TAIL_ROWS; ++e) {
+        unsigned pe;
+        any |= tail_entry(e, j, pe);
+      }
+      if (!any) continue;
+      __syncthreads();   // every wave is done with the previous block's keys and weights
+      k_load(j, bi ? pb0 : pa0, bi ? pb1 : pa1);
+      v_load(j, bi ? pb0 : pa0, bi ? pb1 : pa1);
+      wait_loads();
       __syncthreads();
       if (__builtin_amdgcn_ballot_w64(mine) != 0ull) chunk_scores(A, S, qhi, j, pk, mine, row_b, pos0, g, nslot);
       else chunk_no_scores(S);
       __syncthreads();
-      chunk_outputs(A, S, vr, gpb);
-      __syncthreads();     // every wave is done with the keys and weights before the next block's
+      chunk_outputs(A, S, vr, pko, oko, row_b, g, nslot);
     }
   }
   QM_PHASE(4);
@@ -3278,19 +3333,18 @@ extern "C" int qm_qsa_attend(const qm_qsa_geom* g, int seq, const void* q, const
 
 namespace {
 struct ChunkWs {
-  size_t parity, cnt, list, o, ml, total;
+  size_t tab, tab_bytes, o, ml, total;
 };
 
-// the parity word and the counts first, at offsets independent of seq (a
-// workspace sized for a longer chunk serves a shorter one)
+// the slot table first: every call leaves it zero, so a workspace sized for
+// a longer chunk serves a shorter one
 ChunkWs chunk_ws_layout(const qm_qsa_geom* g, int seq) {
   const int nslot = g->budget / g->ratio + 1;
   const size_t rows = (size_t)g->batch * seq;
   ChunkWs w;
-  w.parity = 0;
-  w.cnt = 256;
-  w.list = w.cnt + qm_align256((size_t)2 * g->batch * g->max_blocks * sizeof(unsigned));
-  w.o = w.list + qm_align256((size_t)g->batch * g->max_blocks * seq * sizeof(unsigned));
+  w.tab = 0;
+  w.tab_bytes = qm_align256((size_t)g->batch * g->max_blocks * seq * sizeof(uint16_t));
+  w.o = w.tab + w.tab_bytes;
   // the partials' space first holds the rows' block scores, which the
   // selection reads before the attention writes partials over them
   const size_t o_bytes = rows * g->n_kv_heads * nslot * GQA * QSA_D * sizeof(uint16_t);
@@ -3333,15 +3387,12 @@ int attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void* qg, c
   char* base = static_cast<char*>(workspace);
   const int topk = g->budget / g->ratio;
   const int nslot = topk + 1;
-  int* parity = reinterpret_cast<int*>(base + L.parity);
-  unsigned* cnt = reinterpret_cast<unsigned*>(base + L.cnt);
-  unsigned* list = reinterpret_cast<unsigned*>(base + L.list);
+  uint16_t* tab = reinterpret_cast<uint16_t*>(base + L.tab);
   uint16_t* part_o = reinterpret_cast<uint16_t*>(base + L.o);
   float* part_ml = reinterpret_cast<float*>(base + L.ml);
 
   if (!filed) {
-    ChunkBucketArgs K{positions, ids, n_sel, part_ml, cnt, list, parity, g->batch, seq, g->n_kv_heads, g->ratio, topk,
-                      g->max_blocks};
+    ChunkBucketArgs K{positions, ids, n_sel, part_ml, tab, g->batch, seq, g->n_kv_heads, g->ratio, topk, g->max_blocks};
     hipLaunchKernelGGL(qsa_chunk_bucket_kernel, dim3(g->batch * seq), dim3(64), 0, stream, K);
     QM_CHECK_LAUNCH();
   }
@@ -3349,29 +3400,25 @@ int attend_chunk(const qm_qsa_geom* g, int seq, const void* q, const void* qg, c
   ChunkAttnArgs A;
   A.q = static_cast<const uint16_t*>(q); A.k_pool = static_cast<const uint16_t*>(k_pool);
   A.v_pool = static_cast<const uint16_t*>(v_pool); A.positions = positions; A.page_table = page_table;
-  A.ids = ids; A.n_sel = n_sel; A.part_o = part_o; A.part_ml = part_ml;
-  A.cnt = cnt; A.list = list; A.parity = parity;
+  A.part_o = part_o; A.part_ml = part_ml; A.tab = tab;
   A.batch = g->batch; A.seq = seq; A.hq = g->n_heads; A.hkv = g->n_kv_heads; A.page_size = g->page_size;
   A.max_pages = g->max_pages; A.ratio = g->ratio; A.topk = topk; A.max_blocks = g->max_blocks;
   A.scale = 1.0f / 16.0f;   // 1/sqrt(256), exact
-  // blocks per workgroup: one while the grid stays within about eight
-  // workgroups per compute unit (measured at 1024 blocks x kv heads: one block
-  // per workgroup 45.0 us, two with the second's pieces loading while the
-  // first is scored 49.5 us: more workgroups in flight beat the overlap)
-  const long want = ((long)g->max_blocks * g->n_kv_heads * g->batch + 2047) / 2048;
-  A.bpw = (int)(want < 1 ? 1 : want > CA_MAX_BPW ? CA_MAX_BPW : want);
-  A.nwg_sel = (g->max_blocks + A.bpw - 1) / A.bpw;
+  // one block per workgroup: more workgroups in flight beat blocks
+  // pipelined within one (measured at 512 blocks x 2 kv heads: 31.5 us, two
+  // blocks per workgroup 33.4 us, four 47.0 us)
+  A.nwg_sel = g->max_blocks;
   const int n_tail = (seq + CA_TAIL_ROWS - 1) / CA_TAIL_ROWS;
   hipLaunchKernelGGL(qsa_chunk_attend_kernel, dim3(A.nwg_sel + n_tail, g->n_kv_heads, g->batch), dim3(CA_NT),
                      0, stream, A);
   QM_CHECK_LAUNCH();
   if (g->act_dtype == QM_ACT_F32) {
     CombineArgs<float, uint16_t> C{part_o, part_ml, static_cast<const float*>(qg), static_cast<float*>(out), g->n_heads,
-                         g->n_kv_heads, nslot, parity};
+                         g->n_kv_heads, nslot, tab, (long)(L.tab_bytes / 16)};
     hipLaunchKernelGGL((qsa_combine_kernel<float, uint16_t>), dim3(g->n_heads, g->batch * seq), dim3(QSA_D), 0, stream, C);
   } else {
     CombineArgs<bf16_t, uint16_t> C{part_o, part_ml, static_cast<const bf16_t*>(qg), static_cast<bf16_t*>(out), g->n_heads,
-                          g->n_kv_heads, nslot, parity};
+                          g->n_kv_heads, nslot, tab, (long)(L.tab_bytes / 16)};
     hipLaunchKernelGGL((qsa_combine_kernel<bf16_t, uint16_t>), dim3(g->n_heads, g->batch * seq), dim3(QSA_D), 0, stream, C);
   }
   QM_CHECK_LAUNCH();
@@ -3408,9 +3455,7 @@ extern "C" int qm_qsa_select_chunk(const qm_qsa_geom* g, int seq, const float* i
     if (rc) return rc;
     A.scores_in = scores;
   }
-  A.parity = reinterpret_cast<const int*>(base + L.parity);
-  A.cnt = reinterpret_cast<unsigned*>(base + L.cnt);
-  A.list = reinterpret_cast<unsigned*>(base + L.list);
+  A.tab = reinterpret_cast<uint16_t*>(base + L.tab);
   A.part_ml = reinterpret_cast<float*>(base + L.ml);
   A.hkv = g->n_kv_heads;
   hipLaunchKernelGGL(qsa_select_kernel, dim3(g->batch * seq), dim3(SELP_NT), 0, stream, A);

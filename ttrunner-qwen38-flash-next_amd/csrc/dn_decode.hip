@@ -22,11 +22,12 @@
 // are issued at the start, before any of them is waited for, and stores wait
 // for the end (loads and stores share one in-order counter).
 //
-// Measured (MI355X, batch 1, 32 heads, HIP graph replay): about 5.0 us per
-// step with the state in the Infinity Cache, 5.8 us with it in HBM only. A
-// workgroup's own work is about 3.5 us of that; the rest is the launch's fixed
-// cost. A single 1024-thread workgroup per head needs no hand-off but moves
-// 64 KB through one compute unit, and measured 0.5 us slower.
+// Measured (MI355X, batch 1, 32 heads): about 4.2 us per launch back to back
+// from a HIP graph, 4.5 us with the state coming from HBM (caches flushed
+// before the launch). A workgroup's own span is about 3.6 us of that; the rest
+// is the launch's fixed cost. A single 1024-thread workgroup per head needs no
+// hand-off but moves 64 KB through one compute unit, and measured 0.5 us
+// slower.
 //
 // The conv window is a ring of K slots per channel: the input of the token at
 // position p lives in slot p % K, so the K-1 history slots read by this step are

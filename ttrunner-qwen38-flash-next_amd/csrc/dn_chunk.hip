@@ -225,10 +225,13 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   QM_PHASE_DECL
   QM_PHASE(0);
   // A.parts workgroups per chunk: each forms L and T, then writes its share
-  // (all of it, or a quarter) of the record
-  const int part = blockIdx.x % A.parts;
-  const int c = (blockIdx.x / A.parts) % A.n_chunks;
-  const int bh = blockIdx.x / A.parts / A.n_chunks;
+  // (all of it, or a quarter) of the record. The parts of a chunk read the
+  // same q, k and v rows: consecutive workgroups in this order run on one die
+  // (xcd_remap), so the rows come from memory once per chunk, not per part
+  const int wg = xcd_remap(blockIdx.x, gridDim.x);
+  const int part = wg % A.parts;
+  const int c = (wg / A.parts) % A.n_chunks;
+  const int bh = wg / A.parts / A.n_chunks;
   const int span = CK_PARTS / A.parts;       // quarters this workgroup writes
   const int h = bh % A.heads, b = bh / A.heads;
   const int t0 = c * CK_C;

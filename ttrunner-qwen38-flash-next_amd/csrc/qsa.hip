@@ -194,8 +194,10 @@ __device__ __forceinline__ float2 rope_cs(const float* cos, const float* sin, lo
 // the key dtype, RMS-normed with k_norm, and roped at the block's first
 // position. Rows at or after `new0` come from `fresh` (row t - new0), earlier
 // ones from `cache`. Called by a whole block; threads 0..127 own a channel.
+// Inlined into its callers: as a call its pointers would be generic, so every
+// row would be a flat load with its address formed in between.
 template <typename T>
-__device__ float pool_block(int j, int ratio, int rope, float eps, const float* k_norm, const float* cos,
+__device__ __forceinline__ float pool_block(int j, int ratio, int rope, float eps, const float* k_norm, const float* cos,
                            const float* sin, const T* cache, const T* fresh, int new0, float* blocks, float* s_x,
                            float* s_y, float* s_scr) {
   const int tid = threadIdx.x;
@@ -206,20 +208,25 @@ __device__ float pool_block(int j, int ratio, int rope, float eps, const float* 
     // address, and rows past the block are clamped and not added
     float total = 0.f;
     for (int r0 = 0; r0 < ratio; r0 += 64) {
-      float v[64];
+      // the rows as loaded (no conversion: a conversion next to its load
+      // would wait for that load before the next is issued)
+      T v[64];
 #pragma unroll
       for (int i = 0; i < 64; ++i) {
         const int tok = t0 + min(r0 + i, ratio - 1);
         const T* src = tok >= new0 ? fresh + (long)(tok - new0) * IDX_D : cache + (long)tok * IDX_D;
-        v[i] = Act<T>::load(src, tid);
+        v[i] = src[tid];
       }
+      // every row requested before the first sum (the scheduler would
+      // otherwise start the chain early and wait for each row in turn)
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int c0 = r0 + 16 * c;
         if (c0 < ratio) {
           float acc = 0.f;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) acc = c0 + i < ratio ? add_rn(acc, v[16 * c + i]) : acc;
+          for (int i = 0; i < 16; ++i) acc = c0 + i < ratio ? add_rn(acc, Act<T>::load(&v[16 * c + i], 0)) : acc;
           total = c0 == 0 ? acc : add_rn(total, acc);
         }
       }

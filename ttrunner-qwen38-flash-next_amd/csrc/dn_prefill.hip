@@ -45,35 +45,48 @@ __global__ __launch_bounds__(CONV_CH) void dn_conv_chunk_kernel(ConvChunkArgs<T>
     const int cb = blockIdx.x % n_cb, tb = (blockIdx.x / n_cb) % n_tb, b = blockIdx.x / (n_cb * n_tb);
     const int ch = cb * CONV_CH + tid;
     if (ch >= A.conv_dim) return;
+    // the position first (a scalar load, waited for only where the ring
+    // slots are chosen, after every vector load below is issued)
     const int pos0 = A.positions[b];
     const int t0 = tb * CONV_TOK;
     const int nt = min(CONV_TOK, A.seq - t0);
     T* ring = A.ring + ((long)b * A.conv_dim + ch) * K;
     const T* x = A.qkv + (long)b * A.seq * A.conv_dim + ch;
-    // every load is unconditional (clamped index, then a select), so the
-    // compiler issues them all before the first wait
-    float w[K], hist[K - 1], win[CONV_TOK + K - 1];
-#pragma unroll
-    for (int j = 0; j < K; ++j) w[j] = Act<T>::load(A.conv_w, (long)ch * K + j);
-#pragma unroll
-    for (int j = 0; j < K - 1; ++j) {
-      int slot = (pos0 - (K - 1) + j) % K;
-      if (slot < 0) slot += K;
-      hist[j] = Act<T>::load(ring, slot);
-    }
-    // win[i] = input of token t0 - (K-1) + i; tokens before the chunk come
-    // from the ring (only in the first token block)
+    // every load is unconditional (clamped index, then a select) and none
+    // depends on the position, so all are issued before the first wait: the
+    // window, the weights and all K ring slots (the history is chosen from
+    // them once the position is in)
+    float w[K], slots[K], win[CONV_TOK + K - 1];
 #pragma unroll
     for (int i = 0; i < CONV_TOK + K - 1; ++i) {
       const int t = t0 - (K - 1) + i;
-      const int tc = min(max(t, 0), A.seq - 1);
-      const float val = Act<T>::load(x, (long)tc * A.conv_dim);
-      win[i] = (i < K - 1 && t < 0) ? hist[i < K - 1 ? i : 0] : val;
+      win[i] = Act<T>::load(x, (long)min(max(t, 0), A.seq - 1) * A.conv_dim);
     }
-    // the chunk's last K-1 inputs, for the ring (used by the first token block)
+#pragma unroll
+    for (int j = 0; j < K; ++j) w[j] = Act<T>::load(A.conv_w, (long)ch * K + j);
+    // the first token block alone reads the ring (the others load their own
+    // column's first input in its place, so none reads a slot it rewrites),
+    // and keeps the chunk's last K-1 inputs for it; unconditional, so that
+    // these loads go out with the window's
+    const T* rsrc = t0 == 0 ? ring : x;
+#pragma unroll
+    for (int j = 0; j < K; ++j) slots[j] = Act<T>::load(rsrc, t0 == 0 ? j : 0);
     T last[K - 1];
 #pragma unroll
     for (int i = 0; i < K - 1; ++i) last[i] = x[(long)max(A.seq - (K - 1) + i, 0) * A.conv_dim];
+    // win[i] = input of token t0 - (K-1) + i; tokens before the chunk come
+    // from the ring slots (pos0 - (K-1) + i) mod K (first token block)
+    // (a select, not a branch: the slot loads then stay with the window's
+    // instead of being moved into the branch that uses them)
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i) {
+      int slot = (pos0 - (K - 1) + i) % K;
+      if (slot < 0) slot += K;
+      float h = slots[0];
+#pragma unroll
+      for (int u = 1; u < K; ++u) h = slot == u ? slots[u] : h;
+      win[i] = t0 == 0 ? h : win[i];
+    }
 #pragma unroll
     for (int i = 0; i < CONV_TOK; ++i) {
       if (i < nt) {
@@ -94,13 +107,17 @@ __global__ __launch_bounds__(CONV_CH) void dn_conv_chunk_kernel(ConvChunkArgs<T>
     }
     return;
   }
-  const long gg = (long)(blockIdx.x - A.n_conv_wg) * CONV_CH + tid;
-  if (gg < (long)A.batch * A.seq * A.hv) {
+  // (token, head) pairs: the host keeps batch * seq * hv below 2^31
+  const int gg = (static_cast<int>(blockIdx.x) - A.n_conv_wg) * CONV_CH + tid;
+  if (gg < A.batch * A.seq * A.hv) {
     const int h = gg % A.hv;
-    const float beta = Act<T>::round(sigmoid_f(Act<T>::load(A.b, gg)));
-    const float ga = Act<T>::load(A.a, gg) + A.dt_bias[h];
-    A.beta_out[gg] = beta;
-    A.g_out[gg] = A.a_neg[h] * softplus_fast(ga);
+    // all four loads before either value is formed (the activations as
+    // loaded: a conversion next to its load would wait for it there)
+    const T braw = A.b[gg], araw = A.a[gg];
+    const float dtb = A.dt_bias[h], an = A.a_neg[h];
+    __builtin_amdgcn_sched_barrier(0);
+    A.beta_out[gg] = Act<T>::round(sigmoid_f(Act<T>::load(&braw, 0)));
+    A.g_out[gg] = an * softplus_fast(Act<T>::load(&araw, 0) + dtb);
   }
 }
 
@@ -156,6 +173,8 @@ int launch_prefill(const qm_dn_geom* g, int seq, const void* qkv, const void* z,
   C.batch = g->batch; C.seq = seq; C.conv_dim = conv_dim; C.hv = g->n_v_heads;
   C.n_conv_wg = g->batch * ((conv_dim + CONV_CH - 1) / CONV_CH) * ((seq + CONV_TOK - 1) / CONV_TOK);
   const long n_gate = (long)g->batch * seq * g->n_v_heads;
+  if (n_gate > 0x7fffffffL - CONV_CH)
+    return qm_fail(QM_ERR_UNSUPPORTED, "qm_dn_prefill: batch * seq * value heads must stay below 2^31");
   const dim3 grid(C.n_conv_wg + (unsigned)((n_gate + CONV_CH - 1) / CONV_CH));
   switch (g->conv_kernel) {
     case 2: hipLaunchKernelGGL((dn_conv_chunk_kernel<T, 2>), grid, dim3(CONV_CH), 0, stream, C); break;

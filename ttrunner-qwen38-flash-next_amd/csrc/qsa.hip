@@ -195,27 +195,34 @@ __device__ __forceinline__ float2 rope_cs(const float* cos, const float* sin, lo
 // position. Rows at or after `new0` come from `fresh` (row t - new0), earlier
 // ones from `cache`. Called by a whole block; threads 0..127 own a channel.
 // Inlined into its callers: as a call its pointers would be generic, so every
-// row would be a flat load with its address formed in between.
+// row would be a flat load with its address formed in between. `v`, when
+// `use_pre`, holds the block's first 64 rows as loaded already (the prep
+// kernel requests them before the position arrives); it is the rows' buffer
+// either way.
 template <typename T>
-__device__ __forceinline__ float pool_block(int j, int ratio, int rope, float eps, const float* k_norm, const float* cos,
-                           const float* sin, const T* cache, const T* fresh, int new0, float* blocks, float* s_x,
-                           float* s_y, float* s_scr) {
+__device__ __forceinline__ float pool_block_rows(T (&v)[64], bool use_pre, bool store, int j, int ratio, int rope,
+                                                 float eps, const float* k_norm, const float* cos, const float* sin,
+                                                 const T* cache, const T* fresh, int new0, float* blocks, float* s_x,
+                                                 float* s_y, float* s_scr) {
   const int tid = threadIdx.x;
   const int t0 = j * ratio;
-  const float2 csv = rope_cs(cos, sin, t0, rope);
+  // (a workgroup that does not store may hold no block: its rope row is row 0)
+  const float2 csv = rope_cs(cos, sin, store ? t0 : 0, rope);
   if (tid < IDX_D) {
     // 64 rows' loads are issued together: each row's source is chosen by
     // address, and rows past the block are clamped and not added
     float total = 0.f;
     for (int r0 = 0; r0 < ratio; r0 += 64) {
       // the rows as loaded (no conversion: a conversion next to its load
-      // would wait for that load before the next is issued)
-      T v[64];
+      // would wait for that load before the next is issued), into v unless
+      // it holds them already
+      if (!(use_pre && r0 == 0)) {
 #pragma unroll
-      for (int i = 0; i < 64; ++i) {
-        const int tok = t0 + min(r0 + i, ratio - 1);
-        const T* src = tok >= new0 ? fresh + (long)(tok - new0) * IDX_D : cache + (long)tok * IDX_D;
-        v[i] = src[tid];
+        for (int i = 0; i < 64; ++i) {
+          const int tok = t0 + min(r0 + i, ratio - 1);
+          const T* src = tok >= new0 ? fresh + (long)(tok - new0) * IDX_D : cache + (long)tok * IDX_D;
+          v[i] = src[tid];
+        }
       }
       // every row requested before the first sum (the scheduler would
       // otherwise start the chain early and wait for each row in turn)
@@ -234,8 +241,17 @@ __device__ __forceinline__ float pool_block(int j, int ratio, int rope, float ep
     s_x[tid] = Act<T>::round(div_rn(total, (float)ratio));
   }
   const float y = norm_rope_row<T>(s_x, s_y, s_scr, IDX_D, k_norm, eps, rope, csv.x, csv.y);
-  if (tid < IDX_D) blocks[(long)j * IDX_D + bk_index(tid)] = y;
+  if (store && tid < IDX_D) blocks[(long)j * IDX_D + bk_index(tid)] = y;
   return y;
+}
+
+template <typename T>
+__device__ __forceinline__ float pool_block(int j, int ratio, int rope, float eps, const float* k_norm, const float* cos,
+                                            const float* sin, const T* cache, const T* fresh, int new0, float* blocks,
+                                            float* s_x, float* s_y, float* s_scr) {
+  T v[64];
+  return pool_block_rows<T>(v, false, true, j, ratio, rope, eps, k_norm, cos, sin, cache, fresh, new0, blocks, s_x,
+                            s_y, s_scr);
 }
 
 template <typename T>
@@ -355,18 +371,47 @@ __global__ __launch_bounds__(PREP_NT) void qsa_prep_kernel(PrepArgs<T> A) {
   if (x < n_pool) {
     // the blocks j whose last row (j + 1) ratio - 1 lies in [pos0, pos0 + seq)
     __shared__ float s_x[IDX_D], s_y[IDX_D], s_scr[32];
-    const int b = x / per;
-    const int pos0 = A.positions[b];
-    const int j = pos0 / A.ratio + x % per;
-    if ((j + 1) * A.ratio > pos0 + A.seq) return;
-    pool_block<T>(j, A.ratio, A.rope, A.eps, A.ik_norm, A.cos, A.sin, A.raw_keys + (long)b * A.max_ctx * IDX_D,
-                  A.ik + (long)b * A.seq * IDX_D, pos0, A.block_keys + (long)b * A.max_blocks * IDX_D, s_x, s_y,
-                  s_scr);
+    const int b = x / per, xr = x % per;
+    const T* fresh = A.ik + (long)b * A.seq * IDX_D;
+    const T* cache = A.raw_keys + (long)b * A.max_ctx * IDX_D;
+    float* blocks = A.block_keys + (long)b * A.max_blocks * IDX_D;
+    if (A.ratio > 64) {
+      const int pos0 = A.positions[b];
+      const int j = pos0 / A.ratio + xr;
+      if ((j + 1) * A.ratio > pos0 + A.seq) return;
+      pool_block<T>(j, A.ratio, A.rope, A.eps, A.ik_norm, A.cos, A.sin, cache, fresh, pos0, blocks, s_x, s_y, s_scr);
+      return;
+    }
+    // When the chunk starts on a block boundary (prefill chunks do), block
+    // pos0 / ratio + xr is chunk rows xr ratio .. xr ratio + ratio - 1: those
+    // rows are requested before the position is known (one round trip
+    // instead of two); otherwise the block is loaded once the position is in.
+    // The position by a vector load issued first (a scalar load would be
+    // waited for together with the kernel's argument loads, before the rows);
+    // the rows by every thread (those past 128 repeat a column), so that no
+    // load sits in a branch of its own.
+    const int pos0 = __builtin_amdgcn_readfirstlane(
+        (int)__builtin_amdgcn_raw_buffer_load_b32(dev_rsrc(A.positions + b, 4), 0, 0, 0));
+    T pre[64];
+    const int col = threadIdx.x & (IDX_D - 1);
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const int r = min(xr * A.ratio + min(i, A.ratio - 1), A.seq - 1);
+      pre[i] = fresh[(long)r * IDX_D + col];
+    }
+    const int j = pos0 / A.ratio + xr;
+    // A workgroup past the chunk's completed blocks has nothing to store; it
+    // still runs on its (in-bounds) requested rows rather than returning here,
+    // which would let the compiler move those loads after the position's wait
+    const bool has = (j + 1) * A.ratio <= pos0 + A.seq;
+    pool_block_rows<T>(pre, !has || pos0 % A.ratio == 0, has, j, A.ratio, A.rope, A.eps, A.ik_norm, A.cos, A.sin,
+                       cache, fresh, pos0, blocks, s_x, s_y, s_scr);
     return;
   }
-  const int roles = A.hq + A.hkv + A.idx_heads;
-  const long wid = (long)(x - n_pool) * (PREP_NT / 64) + (threadIdx.x >> 6);
-  if (wid >= (long)A.batch * A.seq * roles) return;
+  // (row, role) waves: 32-bit arithmetic, the host keeps their count below 2^31
+  const unsigned roles = static_cast<unsigned>(A.hq + A.hkv + A.idx_heads);
+  const unsigned wid = static_cast<unsigned>(x - n_pool) * (PREP_NT / 64) + (threadIdx.x >> 6);
+  if (wid >= static_cast<unsigned>(A.batch * A.seq) * roles) return;
   prep_wave<T>(A, static_cast<int>(wid / roles), static_cast<int>(wid % roles));
 }
 
@@ -3162,7 +3207,7 @@ int launch_prep(const qm_qsa_geom* g, int seq, const void* qg, const void* k_new
                                positions, page_table, k_pool, v_pool, raw_keys, block_keys, q_out, iq_out);
   const long waves = (long)g->batch * seq * (g->n_heads + g->n_kv_heads + g->idx_heads);
   const long n_wg = (long)g->batch * prep_pool_per_seq(seq, g->ratio) + (waves + PREP_NT / 64 - 1) / (PREP_NT / 64);
-  if (n_wg > 0x7fffffffL) return qm_fail(QM_ERR_ARG, "qm_qsa_prep: too many rows");
+  if (n_wg > 0x7fffffffL || waves > 0x7fffffffL) return qm_fail(QM_ERR_ARG, "qm_qsa_prep: too many rows");
   hipLaunchKernelGGL(qsa_prep_kernel<T>, dim3(static_cast<unsigned>(n_wg)), dim3(PREP_NT), 0, stream, A);
   QM_CHECK_LAUNCH();
   return QM_OK;

@@ -156,6 +156,32 @@ __device__ __forceinline__ void load8(const bf16_t* p, float* o) {
   }
 }
 
+// eight consecutive activations loaded raw (get() converts them), so that a
+// run of loads can be issued before any conversion waits on one of them
+template <typename T> struct Raw8;
+template <> struct Raw8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const float4*>(p);
+    b = *reinterpret_cast<const float4*>(p + 4);
+  }
+  __device__ __forceinline__ void get(float* o) const {
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  }
+};
+template <> struct Raw8<bf16_t> {
+  uint4 u;
+  __device__ __forceinline__ void load(const bf16_t* p) { u = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ void get(float* o) const {
+    const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = bf16_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+      o[2 * i + 1] = bf16_to_f32(static_cast<uint16_t>(w[i] >> 16));
+    }
+  }
+};
+
 // lower 16x16 tiles (I, J), J <= I, numbered (0,0) (1,0) (1,1) (2,0) ... (3,3)
 __device__ __forceinline__ void tile_ij(int t, int& I, int& J) {
   I = t < 1 ? 0 : t < 3 ? 1 : t < 6 ? 2 : 3;
@@ -246,25 +272,37 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   const bool tok_ok = t < n_valid;
   float qn[32];
   {
+    // every load at once, the gates first (the cumulative decay is the
+    // longest chain); indices are clamped so that no load sits in a branch
+    const bool ok = lane < n_valid;
+    const long gi = ((long)b * A.seq + t0 + (ok ? lane : 0)) * A.heads + h;
+    const float g_raw = A.g[gi], b_raw = A.beta[gi];
     const long tok = (long)b * A.seq + t0 + (tok_ok ? t : 0);
+    const float bv_raw = A.beta[tok * A.heads + h];
     const long qo = tok * A.q_stride + (long)(h % A.hk) * CK_D;
     const long vo = tok * A.v_stride + (long)h * CK_D;
-    const float bv = tok_ok ? A.beta[tok * A.heads + h] : 0.f;
-    float kv[32], vv[32];
+    Raw8<T> xq[4], xk[4], xv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int d = 8 * (p + 4 * j);
-      load8(A.q + qo + d, qn + 8 * j);
-      load8(A.k + qo + d, kv + 8 * j);
-      load8(A.v + vo + d, vv + 8 * j);
+      xq[j].load(A.q + qo + d);
+      xk[j].load(A.k + qo + d);
+      xv[j].load(A.v + vo + d);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    float kv[32], vv[32];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xq[j].get(qn + 8 * j);
+      xk[j].get(kv + 8 * j);
+      xv[j].get(vv + 8 * j);
+    }
+    const float bv = tok_ok ? bv_raw : 0.f;
 
     // gates; padding tokens carry g = 0 and beta = 0
     if (wid == 0) {
-      const bool ok = lane < n_valid;
-      const long gi = ((long)b * A.seq + t0 + (ok ? lane : 0)) * A.heads + h;
-      const float gv = ok ? A.g[gi] : 0.f;
-      const float bl = ok ? A.beta[gi] : 0.f;
+      const float gv = ok ? g_raw : 0.f;
+      const float bl = ok ? b_raw : 0.f;
       double s = gv;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
@@ -563,11 +601,6 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
   const int g4 = lane >> 4, r16 = lane & 15;
   const float* recs = A.ws + (long)bh * A.n_chunks * CK_REC;
 
-  // operands two chunks ahead: three register sets, the loop unrolled by
-  // three so that no set is copied while its loads are in flight
-  ScanOps o0, o1, o2;
-  load_scan_ops(recs, wid, lane, r16, g4, col0, o0);
-  load_scan_ops(recs + (long)min(1, A.n_chunks - 1) * CK_REC, wid, lane, r16, g4, col0, o1);
   // wave wid keeps dk rows 32 wid .. 32 wid + 31 of the slice as two result
   // tiles of S^T: st[t][i] = S[dk 32 wid + 16 t + r16][column 4 g4 + i]
   float* S = A.state + (long)bh * CK_D * CK_D + col0 + 4 * g4;
@@ -576,14 +609,25 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
   for (int t = 0; t < 2; ++t) {
     const float4 x = *reinterpret_cast<const float4*>(S + (long)(32 * wid + 16 * t + r16) * CK_D);
     st[t] = f32x4_t{x.x, x.y, x.z, x.w};
+  }
+  // operands two chunks ahead: three register sets, the loop unrolled by
+  // three so that no set is copied while its loads are in flight. The state
+  // and the first two chunks' operands are requested together: the state
+  // first, so that its wait leaves the operand loads in flight
+  ScanOps o0, o1, o2;
+  load_scan_ops(recs, wid, lane, r16, g4, col0, o0);
+  load_scan_ops(recs + (long)min(1, A.n_chunks - 1) * CK_REC, wid, lane, r16, g4, col0, o1);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
     put2(sSh, sSl, SC_SS, 4 * g4, 32 * wid + 16 * t + r16, st[t][0], st[t][1]);
     put2(sSh, sSl, SC_SS, 4 * g4 + 2, 32 * wid + 16 * t + r16, st[t][2], st[t][3]);
   }
   QM_PHASE(1);
 
   auto chunk = [&](int ci, const ScanOps& cur, ScanOps& ahead) {
-    // chunk ci + 2's operands fly during this one (clamped at the last chunk)
-    load_scan_ops(recs + (long)min(ci + 2, A.n_chunks - 1) * CK_REC, wid, lane, r16, g4, col0, ahead);
+    // chunk ci + 2's operands fly during this one
+    if (ci + 2 < A.n_chunks) load_scan_ops(recs + (long)(ci + 2) * CK_REC, wid, lane, r16, g4, col0, ahead);
     __syncthreads();
     // (w S)^T and (q_dec S)^T for tokens 16 wid ..: rows = columns 4 g4 + i,
     // column = token 16 wid + r16
@@ -624,11 +668,15 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_scan_kernel(ChunkScanArgs<T> A
     if (ci < 12) QM_PHASE(2 + ci);
   };
 
-  for (int ci = 0; ci < A.n_chunks; ci += 3) {
+  // at least one chunk (the host sends no empty sequence here): no zero-trip
+  // test for the compiler to sink the first operand loads behind
+  int ci = 0;
+  do {
     chunk(ci, o0, o2);
     if (ci + 1 < A.n_chunks) chunk(ci + 1, o1, o0);
     if (ci + 2 < A.n_chunks) chunk(ci + 2, o2, o1);
-  }
+    ci += 3;
+  } while (ci < A.n_chunks);
 
 #pragma unroll
   for (int t = 0; t < 2; ++t)

@@ -265,7 +265,8 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int g4 = lane >> 4, r16 = lane & 15;
   float* rec = A.ws + ((long)bh * A.n_chunks + c) * CK_REC;
-  auto mine = [&](int quarter) __attribute__((always_inline)) { return quarter / span == part; };
+  const int span_sh = span == 1 ? 0 : 2;     // span is 1 or 4
+  auto mine = [&](int quarter) __attribute__((always_inline)) { return (quarter >> span_sh) == part; };
 
   // q, k, v rows: four threads per token, 32 dims each as four runs of 8
   const int t = tid >> 2, p = tid & 3;
@@ -350,10 +351,18 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
       *reinterpret_cast<bf16x8_t*>(&sh.u.q.l[t * CK_HS + d]) = fq.lo;
       *reinterpret_cast<bf16x8_t*>(&sh.kh[t * CK_HS + d]) = fk.hi;
       *reinterpret_cast<bf16x8_t*>(&sh.kl[t * CK_HS + d]) = fk.lo;
+      // the [dim][token] copies only where this workgroup reads them: dims
+      // 32 j .. 32 j + 31 of k for its k_dec quarter (j == part) and, with
+      // parts, the w columns of parts 0-1 (k dims 64 part ..) and the u
+      // columns of parts 2-3 (v dims 64 (part - 2) ..); uniform per j
+      const bool all = A.parts == 1;
+      if (all || j == part || (part < 2 && j / 2 == part)) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        sh.kT[d + e][t] = kv[8 * j + e];
-        sh.vT[d + e][t] = vv[8 * j + e];
+        for (int e = 0; e < 8; ++e) sh.kT[d + e][t] = kv[8 * j + e];
+      }
+      if (all || (part >= 2 && j / 2 == part - 2)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sh.vT[d + e][t] = vv[8 * j + e];
       }
     }
   }
@@ -380,10 +389,10 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   // diagonal that the scan's 32-wide k-steps read. Tile ti belongs to quarter
   // ti % 4; this workgroup's tiles go round-robin to its waves
   {
-    int k = 0;
-    for (int ti = 0; ti < 12; ++ti) {
-      if (!mine(ti & 3)) continue;
-      if (k++ % 4 != wid) continue;
+    // this workgroup's tiles in order: ti = part, part + 4, part + 8 (one
+    // quarter) or all 12; the k-th goes to wave k % 4
+    for (int k = wid; k < 3 * span; k += 4) {
+      const int ti = span == 1 ? part + 4 * k : k;
       int I, J;
       if (ti < 10) tile_ij(ti, I, J);
       else { I = ti == 10 ? 0 : 2; J = I + 1; }
@@ -434,14 +443,26 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   if (wid == 0) {
     // (I + L_II)^-1 for the four diagonal blocks; lane = (block, column):
     // x_i = [i == col] - sum_{k<i} L_ik x_k
+    // the block's lower triangle is read first (rows in runs of 4, the
+    // zeros above the diagonal included), so that the substitution's
+    // dependent chain waits on no LDS read
     const int I = g4, col = r16;
+    float4 lr[15][4];
+#pragma unroll
+    for (int i = 1; i < 16; ++i)
+#pragma unroll
+      for (int k4 = 0; k4 < (i + 3) / 4; ++k4) lr[i - 1][k4] = lds4(&L[16 * I + i][16 * I + 4 * k4]);
+    __builtin_amdgcn_sched_barrier(0);
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float* Lr = &L[16 * I + i][16 * I];
       float acc = i == col ? 1.f : 0.f;
 #pragma unroll
-      for (int kk = 0; kk < i; ++kk) acc = fmaf(-Lr[kk], x[kk], acc);
+      for (int kk = 0; kk < i; ++kk) {
+        const float4 v = lr[i - 1][kk / 4];
+        const float l = kk % 4 == 0 ? v.x : kk % 4 == 1 ? v.y : kk % 4 == 2 ? v.z : v.w;
+        acc = fmaf(-l, x[kk], acc);
+      }
       x[i] = acc;
     }
 #pragma unroll
@@ -454,13 +475,12 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
       Tm[32 * blk + r][32 * blk + 16 + cc] = 0.f;
     }
     // k_dec fragments (KD: dk blocks 2 quarter, 2 quarter + 1, token steps
-    // 0..1): lane (dk 16 D + r16, tokens 32 s + 8 g4 ..), round-robin over
-    // waves 1-3
-    int k = 0;
-    for (int f = 0; f < 16; ++f) {
+    // 0..1): lane (dk 16 D + r16, tokens 32 s + 8 g4 ..); this workgroup's
+    // fragments are f0 .. f0 + 4 span, the i-th to wave 1 + i % 3
+    const int f0 = 4 * span * part;
+    for (int i = wid - 1; i < 4 * span; i += 3) {
+      const int f = f0 + i;
       const int D = f >> 1, s = f & 1;
-      if (!mine(D >> 1)) continue;
-      if (k++ % 3 != wid - 1) continue;
       const int c0 = 32 * s + 8 * g4;
       const float* row = &sh.kT[16 * D + r16][0];
       const float4 x0 = lds4(row + c0), x1 = lds4(row + c0 + 4);

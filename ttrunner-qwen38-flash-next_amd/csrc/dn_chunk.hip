@@ -60,6 +60,17 @@ constexpr long CK_ECL = CK_U + CK_C * CK_D;
 constexpr long CK_REC = CK_ECL + 64;
 static_assert((CK_REC * 4) % 256 == 0, "records stay 256-byte aligned");
 
+// a double moved by DPP (both halves); lanes without a source, or in rows
+// outside ROW_MASK, read 0.0
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_d(double v) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(b), CTRL, ROW_MASK, 0xF, true);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(b >> 32), CTRL, ROW_MASK, 0xF, true);
+  return __builtin_bit_cast(double, (static_cast<unsigned long long>(static_cast<unsigned>(hi)) << 32) |
+                                        static_cast<unsigned>(lo));
+}
+
 // An fp32 MFMA operand as bf16 high and low parts.
 struct Frag {
   bf16x8_t hi, lo;
@@ -200,23 +211,19 @@ __device__ __forceinline__ Frag tile_frag(const uint16_t* hi, const uint16_t* lo
 // rows xr + l%16 of X and yr + l%16 of Y
 __device__ __forceinline__ f32x4_t gram16(const uint16_t* xh, const uint16_t* xl, int xr, const uint16_t* yh,
                                           const uint16_t* yl, int yr, int g4) {
+  // every operand read before the first product, so that the reads' LDS
+  // latencies overlap instead of each product waiting on its own
+  Frag a[4], b[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    a[s] = tile_frag(xh, xl, xr, s, g4);
+    b[s] = tile_frag(yh, yl, yr, s, g4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < 4; ++s) acc = mfma3(tile_frag(xh, xl, xr, s, g4), tile_frag(yh, yl, yr, s, g4), acc);
+  for (int s = 0; s < 4; ++s) acc = mfma3(a[s], b[s], acc);
   return acc;
-}
-
-// a lane's operand of an fp32 LDS row: elements 32 s + 8 g4 .. + 7, each times
-// scale[element] when SCALED
-template <bool SCALED>
-__device__ __forceinline__ Frag row_frag(const float* row, int s, int g4, const float* scale) {
-  const int c = 32 * s + 8 * g4;
-  const float4 a = lds4(row + c), b = lds4(row + c + 4);
-  float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  if (SCALED)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] *= scale[c + e];
-  return split8(x);
 }
 
 template <typename T>
@@ -304,14 +311,18 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
     if (wid == 0) {
       const float gv = ok ? g_raw : 0.f;
       const float bl = ok ? b_raw : 0.f;
+      // inclusive scan over the 64 lanes in double on DPP (no LDS round
+      // trips): row shifts by 1, 2, 4, 8, then lane 15 of each row to the
+      // next row (rows 1, 3), then lane 31 to rows 2 and 3
       double s = gv;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const double o = __shfl_up(s, off, 64);
-        if (lane >= off) s += o;
-      }
+      s += dpp_d<0x111, 0xF>(s);
+      s += dpp_d<0x112, 0xF>(s);
+      s += dpp_d<0x114, 0xF>(s);
+      s += dpp_d<0x118, 0xF>(s);
+      s += dpp_d<0x142, 0xA>(s);
+      s += dpp_d<0x143, 0xC>(s);
       const float cum = static_cast<float>(s);
-      const float last = __shfl(cum, 63, 64);
+      const float last = readlane_f(cum, 63);
       const float ec = expf(cum);
       sh.cum[lane] = cum;
       sh.beta[lane] = bl;
@@ -327,10 +338,10 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
       sq = fmaf(qn[i], qn[i], sq);
       sk = fmaf(kv[i], kv[i], sk);
     }
-    sq += __shfl_xor(sq, 1, 64);
-    sk += __shfl_xor(sk, 1, 64);
-    sq += __shfl_xor(sq, 2, 64);
-    sk += __shfl_xor(sk, 2, 64);
+    sq += dpp_f<0xB1>(sq);    // lane ^ 1
+    sk += dpp_f<0xB1>(sk);
+    sq += dpp_f<0x4E>(sq);    // lane ^ 2
+    sk += dpp_f<0x4E>(sk);
     const float rq = tok_ok ? rsqrt_rn(sq + 1e-6f) : 0.f;
     const float rk = tok_ok ? rsqrt_rn(sk + 1e-6f) : 0.f;
     const float qscale = 0.08838834764831845f;  // 128^-1/2
@@ -422,10 +433,43 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
   float (&L)[CK_C][CK_LT] = sh.u.t.L;
   float (&Tm)[CK_C][CK_LT] = sh.u.t.Tm;
   // L = (k k^T) * beta_i * exp(cum_i - cum_j) for j < i
-  for (int ti = wid; ti < 10; ti += 4) {
-    int I, J;
-    tile_ij(ti, I, J);
-    const f32x4_t acc = gram16(sh.kh, sh.kl, 16 * I + r16, sh.kh, sh.kl, 16 * J + r16, g4);
+  // three tile slots per wave, all fragments read before the first MFMA.
+  // Waves 0-2 take tiles (I, wid) for I = max(wid, 1) .. 3, so that block
+  // wid's fragments serve every slot as the B operand; wave 3 takes (3, 3)
+  // and (0, 0). Slots past a wave's tiles (wave 2's third, wave 3's third)
+  // repeat a tile and store nothing.
+  const int wu = __builtin_amdgcn_readfirstlane(wid);
+  const int ib = wu < 3 ? max(wu, 1) : 0;
+  int tI[3], tJ[3];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    tI[r] = wu < 3 ? min(ib + r, 3) : (r == 0 ? 3 : 0);
+    tJ[r] = wu < 3 ? wu : tI[r];
+  }
+  Frag fb[4], fa[3][4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) fb[st] = tile_frag(sh.kh, sh.kl, 16 * tJ[0] + r16, st, g4);
+#pragma unroll
+  for (int r = 0; r < 3; ++r)
+#pragma unroll
+    for (int st = 0; st < 4; ++st) fa[r][st] = tile_frag(sh.kh, sh.kl, 16 * tI[r] + r16, st, g4);
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4_t lacc[3];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) lacc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+      // wave 3's (0, 0) tile takes its own block as the B operand
+      const Frag& b = (wu == 3 && r > 0) ? fa[r][st] : fb[st];
+      lacc[r] = mfma3(fa[r][st], b, lacc[r]);
+    }
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    if (wu < 3 ? ib + r > 3 : r == 2) break;
+    const int I = tI[r], J = tJ[r];
+    const f32x4_t acc = lacc[r];
     const int j = 16 * J + r16;
     const float cj = sh.cum[j];
     const float4 ci = lds4(&sh.cum[16 * I + 4 * g4]), bi = lds4(&sh.beta[16 * I + 4 * g4]);
@@ -524,15 +568,47 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
     const bool is_u = tile >= 8;
     const int D = tile & 7;
     const float* arow = is_u ? &sh.vT[16 * D + r16][0] : &sh.kT[16 * D + r16][0];
+    // every LDS read first (the A row and its scales, the T rows of the four
+    // row blocks), then the splits and products
+    float4 ar[2][2], sc[2][2], tr[4][2][2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int c = 32 * s2 + 8 * g4;
+      ar[s2][0] = lds4(arow + c);
+      ar[s2][1] = lds4(arow + c + 4);
+      sc[s2][0] = lds4(&sh.bec[c]);
+      sc[s2][1] = lds4(&sh.bec[c + 4]);
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int s2 = 0; s2 <= I / 2; ++s2) {
+        const int c = 32 * s2 + 8 * g4;
+        tr[I][s2][0] = lds4(&Tm[16 * I + r16][c]);
+        tr[I][s2][1] = lds4(&Tm[16 * I + r16][c + 4]);
+      }
+    __builtin_amdgcn_sched_barrier(0);
     Frag a[2];
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-      a[s2] = is_u ? row_frag<false>(arow, s2, g4, nullptr) : row_frag<true>(arow, s2, g4, sh.bec);
+    for (int s2 = 0; s2 < 2; ++s2) {
+      float x[8] = {ar[s2][0].x, ar[s2][0].y, ar[s2][0].z, ar[s2][0].w,
+                    ar[s2][1].x, ar[s2][1].y, ar[s2][1].z, ar[s2][1].w};
+      const float y[8] = {sc[s2][0].x, sc[s2][0].y, sc[s2][0].z, sc[s2][0].w,
+                          sc[s2][1].x, sc[s2][1].y, sc[s2][1].z, sc[s2][1].w};
+      if (!is_u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= y[e];
+      a[s2] = split8(x);
+    }
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s2 = 0; s2 <= I / 2; ++s2) acc = mfma3(a[s2], row_frag<false>(&Tm[16 * I + r16][0], s2, g4, nullptr), acc);
+      for (int s2 = 0; s2 <= I / 2; ++s2) {
+        const float x[8] = {tr[I][s2][0].x, tr[I][s2][0].y, tr[I][s2][0].z, tr[I][s2][0].w,
+                            tr[I][s2][1].x, tr[I][s2][1].y, tr[I][s2][1].z, tr[I][s2][1].w};
+        acc = mfma3(a[s2], split8(x), acc);
+      }
       // acc[v]: dim 16 D + 4 g4 + v of token 16 I + r16
       if (is_u) {
         *reinterpret_cast<float4*>(rec + CK_U + (16 * I + r16) * CK_D + 16 * D + 4 * g4) =

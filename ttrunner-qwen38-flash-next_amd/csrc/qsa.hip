@@ -1267,7 +1267,28 @@ __global__ __launch_bounds__(64 * SCR_ROWS) void qsa_score_rows_kernel(ScoreRows
   const int b = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j0 = blockIdx.x * SCR_BLK, s0 = blockIdx.y * SCR_ROWS;
-  const int pos0 = A.positions[b];
+  // the position by a vector load issued first, then the tile's block rows
+  // and the group's query rows before it is known (block rows clamped to the
+  // cache's max_blocks, query rows to the sequence, so that every load is
+  // in bounds and none waits behind the position); the zeros past the
+  // eligible blocks and the group's rows are applied after
+  const unsigned pos_raw = __builtin_amdgcn_raw_buffer_load_b32(dev_rsrc(A.positions + b, 4), 0, 0, 0);
+  const float4* src = reinterpret_cast<const float4*>(A.block_keys + (long)b * A.max_blocks * IDX_D);
+  const float4* qsrc = reinterpret_cast<const float4*>(A.iq + (long)b * A.seq * A.idx_heads * IDX_D);
+  constexpr int F4 = SCR_BLK * IDX_D / 4 / (64 * SCR_ROWS);
+  const int q4 = A.idx_heads * IDX_D / 4;     // float4 per query row
+  float4 kv[F4], qv[SCR_ROWS];
+#pragma unroll
+  for (int i = 0; i < F4; ++i) {
+    const int f = tid + 64 * SCR_ROWS * i;
+    kv[i] = src[(long)min(j0 + (f >> 5), A.max_blocks - 1) * (IDX_D / 4) + (f & 31)];
+  }
+  // the group's query rows: thread t < 128 takes float4 t of each row's
+  // idx_heads x 128 (zeros past them)
+#pragma unroll
+  for (int r = 0; r < SCR_ROWS; ++r) qv[r] = qsrc[(long)min(s0 + r, A.seq - 1) * q4 + min(tid, q4 - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  const int pos0 = __builtin_amdgcn_readfirstlane((int)pos_raw);
   const int s_last = min(s0 + SCR_ROWS, A.seq) - 1;
   const int elig_max = min((pos0 + s_last + 1) / A.ratio, A.max_blocks);   // the group's last row sees the most
   const int s = s0 + wv, j = j0 + lane;
@@ -1277,21 +1298,12 @@ __global__ __launch_bounds__(64 * SCR_ROWS) void qsa_score_rows_kernel(ScoreRows
     if (A.fill && s < A.seq && j < A.max_blocks) out[j] = -INFINITY;
     return;
   }
-  const float4* src = reinterpret_cast<const float4*>(A.block_keys + ((long)b * A.max_blocks + j0) * IDX_D);
-  const float4* qsrc = reinterpret_cast<const float4*>(A.iq + ((long)b * A.seq + s0) * A.idx_heads * IDX_D);
-  constexpr int F4 = SCR_BLK * IDX_D / 4 / (64 * SCR_ROWS);
-  float4 kv[F4], qv[SCR_ROWS];
 #pragma unroll
-  for (int i = 0; i < F4; ++i) {
-    const int f = tid + 64 * SCR_ROWS * i, r = f >> 5;
-    kv[i] = j0 + r < elig_max ? src[(long)r * (IDX_D / 4) + (f & 31)] : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  // the group's query rows: thread t < 128 takes float4 t of each row's
-  // idx_heads x 128 (zeros past them)
+  for (int i = 0; i < F4; ++i)
+    if (j0 + ((tid + 64 * SCR_ROWS * i) >> 5) >= elig_max) kv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int r = 0; r < SCR_ROWS; ++r)
-    qv[r] = s0 + r < A.seq && tid < A.idx_heads * IDX_D / 4 ? qsrc[(long)r * A.idx_heads * (IDX_D / 4) + tid]
-                                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (s0 + r >= A.seq || tid >= q4) qv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int i = 0; i < F4; ++i) {
     const int f = tid + 64 * SCR_ROWS * i;

@@ -241,11 +241,9 @@ struct alignas(16) PrepShared {
     struct {
       uint16_t h[CK_C * CK_HS], l[CK_C * CK_HS];   // normalised q * d^-1/2, split
     } q;
-    struct {
-      float L[CK_C][CK_LT];    // (k beta k^T) * decay, strictly lower
-      float Tm[CK_C][CK_LT];   // (I + L)^-1, lower
-    } t;                       // after the q k^T tiles are done with q
+    float Tm[CK_C][CK_LT];     // (I + L)^-1, lower: after the q k^T tiles are done with q
   } u;
+  float L[CK_C][CK_LT];        // (k beta k^T) * decay, strictly lower (formed beside the q k^T tiles)
   uint16_t kh[CK_C * CK_HS], kl[CK_C * CK_HS];     // normalised k, split
   float kT[CK_D][CK_LT];       // normalised k, [dim][token]
   float vT[CK_D][CK_LT];       // v * beta, [dim][token]
@@ -427,11 +425,12 @@ __global__ __launch_bounds__(CK_NT) void dn_chunk_prep_kernel(ChunkPrepArgs<T> A
     }
   }
   QM_PHASE(3);
-  __syncthreads();   // q is done with: L and T take its space
+  // L has its own LDS, so its tiles follow the q k^T tiles with no barrier
+  // (T takes q's space after the barrier below)
   QM_PHASE(9);
 
-  float (&L)[CK_C][CK_LT] = sh.u.t.L;
-  float (&Tm)[CK_C][CK_LT] = sh.u.t.Tm;
+  float (&L)[CK_C][CK_LT] = sh.L;
+  float (&Tm)[CK_C][CK_LT] = sh.u.Tm;
   // L = (k k^T) * beta_i * exp(cum_i - cum_j) for j < i
   // three tile slots per wave, all fragments read before the first MFMA.
   // Waves 0-2 take tiles (I, wid) for I = max(wid, 1) .. 3, so that block

@@ -929,27 +929,39 @@ __device__ __forceinline__ int wave_incl_sum(int x) {
 // single-precision quotient, whose rounding the margin covers): monotone in the
 // key and below 256. Waves exchange partial results through LDS only at the
 // four barriers; within a wave, DPP and lane reads.
+// Each wave's range of the keys' score bits to wtot (lows, then highs), and
+// the histogram and counters cleared: the first pass of bucket_topk, which a
+// caller that forms the keys itself (lo / hi over its own keys) runs before
+// the barrier that publishes them.
+template <int NT>
+__device__ __forceinline__ void bucket_range(unsigned lo, unsigned hi, int* scr) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  lo = wave_minmax_u<false>(lo);
+  hi = wave_minmax_u<true>(hi);
+  if (tid < 256) scr[tid] = 0;             // hist
+  if (tid < 8) scr[256 + 32 + tid] = 0;    // state
+  if (lane == 0) {
+    scr[256 + wv] = static_cast<int>(lo);        // wtot[0..15] lows, [16..31] highs
+    scr[256 + 16 + wv] = static_cast<int>(hi);
+  }
+}
+
 template <int NT>
 __device__ bool bucket_topk(const unsigned long long* keys, int n, int topk, int* sel, int* hist, int* wtot,
-                            int* state, int* cand) {
+                            int* state, int* cand, bool range_in) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int NW = NT / 64;
   static_assert(NW <= 16 && NT >= 256, "wave totals in 16 slots; one bucket per thread");
-  unsigned lo = 0xffffffffu, hi = 0u;
-  for (int j = tid; j < n; j += NT) {
-    const unsigned v = static_cast<unsigned>(keys[j] >> 32);
-    lo = min(lo, v);
-    hi = max(hi, v);
+  if (!range_in) {
+    unsigned lo = 0xffffffffu, hi = 0u;
+    for (int j = tid; j < n; j += NT) {
+      const unsigned v = static_cast<unsigned>(keys[j] >> 32);
+      lo = min(lo, v);
+      hi = max(hi, v);
+    }
+    bucket_range<NT>(lo, hi, hist);
+    __syncthreads();
   }
-  lo = wave_minmax_u<false>(lo);
-  hi = wave_minmax_u<true>(hi);
-  if (tid < 256) hist[tid] = 0;
-  if (tid < 8) state[tid] = 0;
-  if (lane == 0) {
-    wtot[wv] = static_cast<int>(lo);        // wtot[0..15] lows, [16..31] highs
-    wtot[16 + wv] = static_cast<int>(hi);
-  }
-  __syncthreads();
   QM_PHASE(6);
   const unsigned glo = wave_minmax_u<false>(lane < NW ? static_cast<unsigned>(wtot[lane]) : 0xffffffffu);
   const unsigned ghi = wave_minmax_u<true>(lane < NW ? static_cast<unsigned>(wtot[16 + lane]) : 0u);
@@ -1026,8 +1038,11 @@ __device__ bool bucket_topk(const unsigned long long* keys, int n, int topk, int
   return true;
 }
 
+// range_in: the caller ran bucket_range<NT> over all n keys behind the
+// barrier that published them (used only when the bucket threshold runs)
 template <int NT, int MAXK>
-__device__ void rank_topk(const unsigned long long* keys, int n, int topk, int* sel, int* scr) {
+__device__ void rank_topk(const unsigned long long* keys, int n, int topk, int* sel, int* scr,
+                          bool range_in = false) {
   static_assert(NT >= 256 && NT % 64 == 0 && NT <= 1024, "one digit per thread");
   const int tid = threadIdx.x;
   const int npad = (n + 31) & ~31;
@@ -1052,7 +1067,7 @@ __device__ void rank_topk(const unsigned long long* keys, int n, int topk, int* 
   int* cand = scr + 256 + 40;             // [topk]
   const int lane = tid & 63, wv = tid >> 6;
   if constexpr (NT >= 1024)
-    if (topk <= RANK_CAND && bucket_topk<NT>(keys, n, topk, sel, hist, wtot, state, cand)) return;
+    if (topk <= RANK_CAND && bucket_topk<NT>(keys, n, topk, sel, hist, wtot, state, cand, range_in)) return;
   unsigned long long prefix = 0ull;
   int r = topk;
   for (int shift = 56; shift >= 0; shift -= 8) {
@@ -1161,12 +1176,24 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
     for (int j = tid; j < A.max_blocks; j += NT)
       if (j >= n_elig) A.scores_out[(long)row * A.max_blocks + j] = -INFINITY;
 
+  bool range_in = false;
   if (A.scores_in) {
     if (n_elig > A.topk) {
       const float* sc = A.scores_in + (long)row * A.max_blocks;
-      for (int j = tid; j < n_elig; j += NT) S.key[j] = sel_key(sc[j], j);
+      unsigned lo = 0xffffffffu, hi = 0u;
+      for (int j = tid; j < n_elig; j += NT) {
+        const unsigned long long k = sel_key(sc[j], j);
+        S.key[j] = k;
+        lo = min(lo, static_cast<unsigned>(k >> 32));
+        hi = max(hi, static_cast<unsigned>(k >> 32));
+      }
       const int npad = (n_elig + 31) & ~31;
       for (int j = n_elig + tid; j < npad; j += NT) S.key[j] = 0ull;
+      // the bucket threshold's key range, published by the barrier below
+      if constexpr (NT >= 1024) {
+        bucket_range<NT>(lo, hi, S.rscr);
+        range_in = true;
+      }
     }
   } else if (n_elig > A.topk || A.scores_out) {
     const float* bk = A.block_keys + (long)b * A.max_blocks * IDX_D;
@@ -1190,7 +1217,7 @@ __device__ void select_row(const SelArgs& A, SelShared& S, int row, int b, int p
   if (n_elig <= A.topk) {
     for (int i = tid; i < n_elig; i += NT) { out_ids[i] = i; S.sel[i] = i; }
   } else {
-    rank_topk<NT, SEL_MAX_BLOCKS / 2>(S.key, n_elig, A.topk, S.sel, S.rscr);
+    rank_topk<NT, SEL_MAX_BLOCKS / 2>(S.key, n_elig, A.topk, S.sel, S.rscr, range_in);
     __syncthreads();
     QM_PHASE(2);
     for (int i = tid; i < A.topk; i += NT) out_ids[i] = S.sel[i];

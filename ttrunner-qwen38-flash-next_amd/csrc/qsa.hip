@@ -974,19 +974,22 @@ __device__ bool bucket_topk(const unsigned long long* keys, int n, int topk, int
   for (int j = tid; j < n; j += NT) atomicAdd(&hist[bucket(keys[j])], 1);
   __syncthreads();                        // every wave has read the range: wtot is free
   QM_PHASE(7);
-  // suffix sums over the buckets: thread t takes bucket 255 - t
-  int h = 0, incl = 0;
-  if (tid < 256) {
-    h = hist[255 - tid];
-    incl = wave_incl_sum(h);
-    if (lane == 63) wtot[wv] = incl;
-  }
-  __syncthreads();
-  if (tid < 256) {
-    for (int w = 0; w < wv; ++w) incl += wtot[w];
-    if (incl - h < topk && incl >= topk) {   // the bucket of the topk-th largest key
-      state[0] = 255 - tid;
-      state[1] = incl;                       // keys in it and above
+  // suffix sums over the buckets in one wave (no exchange of wave totals):
+  // lane l takes buckets 255 - 4 l .. 252 - 4 l, the keys above them are the
+  // exclusive scan of the lanes' sums, then the lane walks its four downwards
+  if (wv == 0) {
+    const int4 hv = *reinterpret_cast<const int4*>(&hist[252 - 4 * lane]);
+    const int s4 = (hv.x + hv.y) + (hv.z + hv.w);
+    int above = wave_incl_sum(s4) - s4;
+    const int hb[4] = {hv.w, hv.z, hv.y, hv.x};     // buckets 255 - 4 l - i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int incl = above + hb[i];
+      if (above < topk && incl >= topk) {    // the bucket of the topk-th largest key
+        state[0] = 255 - 4 * lane - i;
+        state[1] = incl;                     // keys in it and above
+      }
+      above = incl;
     }
   }
   __syncthreads();
